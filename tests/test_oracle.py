@@ -1,0 +1,290 @@
+"""Pins the CPU oracle (oracle/cpu_gemm.c) before it is trusted as the checker.
+
+Each check is independent of the restatement being tested: the reference's
+own known-answer tests, exact integer arithmetic (numpy int64 matmul), the
+transpose identities linking NN/TN/NT, a vectorised float32 statement of the
+sequential-K definition, fp64 error bounds, and closed forms for epilogues,
+im2col and attention.  `test_checks_catch_planted_mistakes` plants plausible
+mistakes in oracle outputs (on the CPU) and shows these checks reject them.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from _parity import uniform, tol, abs_denominator, componentwise_error
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+U = np.float64(2.0 ** -24)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    if not os.path.exists(oracle.LIB_PATH):
+        oracle.build()
+
+
+@pytest.fixture(scope="module")
+def kats():
+    return np.load(os.path.join(GOLDEN, "reference_kats.npz"))
+
+
+def seq_nn(a, b, c0=None):
+    """Vectorised float32 statement of the sequential definition: for p
+    ascending, C = fl(C + fl(a[:,p] * b[p,:])) (numpy float32 ops are single
+    IEEE operations, never fused)."""
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.zeros((m, n), np.float32) if c0 is None else c0.copy()
+    for p in range(k):
+        c = (c + (a[:, p:p + 1] * b[p:p + 1, :]).astype(np.float32)).astype(np.float32)
+    return c
+
+
+def gamma_bound(a, b, k):
+    """Deterministic fp32 summation bound gamma_k (|A||B|), gamma_k = k u / (1 - k u)."""
+    g = k * U / (1 - k * U)
+    return g * abs_denominator(a, b)
+
+
+# ---------------------------------------------------------------- reference KATs
+def test_kat_backend_matmul_correctness(kats):
+    m, n, k = kats["correctness_mnk"]
+    c = oracle.matmul_batch(kats["correctness_a"], kats["correctness_b"], m, n, k)
+    np.testing.assert_array_equal(c.ravel(), kats["correctness_c"])
+
+
+def test_kat_backend_matmul_large_ones(kats):
+    ones = np.ones(64 * 64, np.float32)
+    for branch in ("auto", "unblocked", "blocked"):
+        c = oracle.matmul(ones, ones, 64, 64, 64, branch=branch)
+        np.testing.assert_array_equal(c.ravel(), kats["ones64_c"])
+    np.testing.assert_array_equal(oracle.matmul_batch(ones, ones, 64, 64, 64).ravel(), kats["ones64_c"])
+
+
+def test_kat_backend_matmul_cpu_small(kats):
+    m, n, k = kats["cpu_small_mnk"]
+    c = oracle.matmul_batch(kats["cpu_small_a"], kats["cpu_small_b"], m, n, k)
+    assert c.ravel()[0] == kats["cpu_small_c0"][0]
+
+
+@pytest.mark.parametrize("tag", ["small64", "medium256", "nonsquare", "accum64"])
+def test_kat_integer_matmuls_exact_every_layout(kats, tag):
+    m, n, k = (int(x) for x in kats[f"{tag}_mnk"])
+    a, b = kats[f"{tag}_a"].reshape(m, k), kats[f"{tag}_b"].reshape(k, n)
+    want = kats[f"{tag}_c"].reshape(m, n)
+    if tag == "accum64":  # first call overwrites, second accumulates
+        c = oracle.matmul(a, b, m, n, k)
+        c = oracle.matmul(a, b, m, n, k, accumulate=True, c_init=c)
+        np.testing.assert_array_equal(c, 2 * want)
+        return
+    np.testing.assert_array_equal(oracle.matmul(a, b, m, n, k), want)
+    np.testing.assert_array_equal(oracle.matmul(a, b, m, n, k, branch="unblocked"), want)
+    np.testing.assert_array_equal(oracle.matmul_batch(a, b, m, n, k), want)
+    np.testing.assert_array_equal(oracle.matmul_tn(a.T.copy(), b, m, n, k), want)
+    np.testing.assert_array_equal(oracle.matmul_nt(a, b.T.copy(), m, n, k), want)
+
+
+def test_kat_dense_layer_forward_backward(kats):
+    """src/test/unit/layer.zig:16-55,169-241 through the oracle's Dense steps."""
+    for act, row in zip(kats["dense_fwd_act"], kats["dense_fwd"]):
+        w0, w1, bias, x0, x1, want = row
+        y = oracle.matmul_batch(np.float32([x0, x1]), np.float32([w0, w1]), 1, 1, 2)
+        y = oracle.add_bias(y, np.float32([bias]))
+        y = oracle.activation_forward(str(act), y)
+        assert abs(float(y[0, 0]) - float(want)) <= 1e-4
+    for act, row in zip(kats["dense_bwd_act"], kats["dense_bwd"]):
+        w0, w1, x0, x1, yv, g0, g1 = row
+        gaa = oracle.activation_backward(str(act), np.float32([yv]), np.float32([1.0]))
+        gx = oracle.matmul_nt(gaa, np.float32([w0, w1]), 1, 2, 1)
+        np.testing.assert_allclose(gx.ravel(), [g0, g1], atol=1e-4)
+
+
+def test_kat_activations(kats):
+    x = kats["act_relu_x"]
+    np.testing.assert_array_equal(oracle.activation_forward("relu", x), kats["act_relu_y"])
+    s = oracle.activation_forward("sigmoid", kats["act_sigmoid_x"])
+    assert np.all((s >= 0) & (s <= 1)) and abs(float(s[2]) - 0.5) <= 1e-4
+    g = oracle.activation_backward("sigmoid", s, np.ones_like(s))
+    np.testing.assert_allclose(g, s * (1 - s), atol=1e-4)
+
+
+# ------------------------------------------------------------ structural checks
+SHAPES = [(1, 1, 1), (3, 5, 7), (31, 33, 32), (32, 32, 32), (37, 45, 29), (64, 96, 70), (70, 33, 129)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_branches_and_layouts_bit_identical(m, n, k):
+    rng = np.random.default_rng(m * 10007 + n * 101 + k)
+    a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+    ref = seq_nn(a, b)
+    for branch in ("auto", "unblocked", "blocked"):
+        np.testing.assert_array_equal(oracle.matmul(a, b, m, n, k, branch=branch), ref)
+    np.testing.assert_array_equal(oracle.matmul(a, b, m, n, k, branch="blocked", threads=4), ref)
+    np.testing.assert_array_equal(oracle.matmul_batch(a, b, m, n, k), ref)
+    # C = A B computed as (A^T)^T B and A (B^T)^T: same products, same order.
+    np.testing.assert_array_equal(oracle.matmul_tn(a.T.copy(), b, m, n, k), ref)
+    np.testing.assert_array_equal(oracle.matmul_nt(a, b.T.copy(), m, n, k), ref)
+    np.testing.assert_array_equal(oracle.matmul_tn(a.T.copy(), b, m, n, k, threads=3), ref)
+    np.testing.assert_array_equal(oracle.matmul_nt(a, b.T.copy(), m, n, k, threads=3), ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(5, 6, 7), (40, 33, 35)])
+def test_accumulate_semantics(m, n, k):
+    """NN accumulates in sequence into C (src/backend.zig:2521); TN/NT form the
+    sum from zero and then add it (src/backend.zig:2623-2627, 2640-2644)."""
+    rng = np.random.default_rng(7)
+    a, b, c0 = uniform(rng, (m, k)), uniform(rng, (k, n)), uniform(rng, (m, n))
+    np.testing.assert_array_equal(oracle.matmul(a, b, m, n, k, True, c0), seq_nn(a, b, c0))
+    np.testing.assert_array_equal(oracle.matmul_batch(a, b, m, n, k, True, c0), seq_nn(a, b, c0))
+    want = (c0 + seq_nn(a, b)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.matmul_tn(a.T.copy(), b, m, n, k, True, c0), want)
+    np.testing.assert_array_equal(oracle.matmul_nt(a, b.T.copy(), m, n, k, True, c0), want)
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 16, 16), (50, 70, 300), (8, 9, 2000)])
+def test_fp64_error_bound(m, n, k):
+    rng = np.random.default_rng(k)
+    a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+    c = oracle.matmul(a, b, m, n, k).astype(np.float64)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.all(np.abs(c - exact) <= gamma_bound(a, b, k))
+
+
+def test_identity_and_linearity():
+    rng = np.random.default_rng(3)
+    a = uniform(rng, (40, 40))
+    eye = np.eye(40, dtype=np.float32)
+    np.testing.assert_array_equal(oracle.matmul(a, eye, 40, 40, 40), a)
+    np.testing.assert_array_equal(oracle.matmul(eye, a, 40, 40, 40), a)
+    # scaling by a power of two is exact in every step
+    b = uniform(rng, (40, 40))
+    np.testing.assert_array_equal(oracle.matmul(a * 4, b, 40, 40, 40), 4 * oracle.matmul(a, b, 40, 40, 40))
+
+
+# ----------------------------------------------------------------- epilogues
+def test_epilogue_closed_forms():
+    rng = np.random.default_rng(11)
+    m, n, k = 23, 17, 41
+    a, b, bias = uniform(rng, (m, k)), uniform(rng, (k, n)), uniform(rng, (n,))
+    pre = (seq_nn(a, b) + bias[None, :]).astype(np.float32)  # bias after the full K sum
+    np.testing.assert_array_equal(oracle.matmul_bias_act(a, b, bias, m, n, k, "linear"), pre)
+    np.testing.assert_array_equal(oracle.matmul_bias_act(a, b, bias, m, n, k, "relu"), np.maximum(pre, 0))
+    p64 = pre.astype(np.float64)
+    sig = oracle.matmul_bias_act(a, b, bias, m, n, k, "sigmoid")
+    assert np.all(np.abs(sig - 1 / (1 + np.exp(-p64))) <= 4 * np.spacing(np.abs(sig)))
+    th = oracle.matmul_bias_act(a, b, bias, m, n, k, "tanh")
+    assert np.all(np.abs(th - np.tanh(p64)) <= 4 * np.spacing(np.abs(th)) + 1e-45)
+
+
+def test_activation_forward_backward_closed_forms():
+    x = np.linspace(-30, 30, 2001).astype(np.float32)
+    x64 = x.astype(np.float64)
+    s = oracle.activation_forward("sigmoid", x)
+    assert np.all(np.abs(s - 1 / (1 + np.exp(-x64))) <= 4 * np.spacing(np.abs(s)))
+    t = oracle.activation_forward("tanh", x)
+    assert np.all(np.abs(t - np.tanh(x64)) <= 4 * np.spacing(np.abs(t)) + 1e-45)
+    np.testing.assert_array_equal(oracle.activation_forward("relu", x), np.maximum(x, 0))
+    np.testing.assert_array_equal(oracle.activation_forward("linear", x), x)
+    g = np.linspace(-2, 2, x.size).astype(np.float32)
+    np.testing.assert_array_equal(oracle.activation_backward("relu", x, g), np.where(x > 0, g, 0).astype(np.float32))
+    np.testing.assert_array_equal(oracle.activation_backward("tanh", t, g), (g * (1 - t * t)).astype(np.float32))
+    np.testing.assert_array_equal(oracle.activation_backward("sigmoid", s, g), ((g * s) * (1 - s)).astype(np.float32))
+    np.testing.assert_array_equal(oracle.activation_backward("linear", s, g), g)
+
+
+def test_bias_helpers():
+    rng = np.random.default_rng(5)
+    out, bias = uniform(rng, (7, 9)), uniform(rng, (9,))
+    np.testing.assert_array_equal(oracle.add_bias(out, bias), (out + bias[None, :]).astype(np.float32))
+    gb0 = uniform(rng, (9,))
+    want = gb0.copy()
+    for r in range(7):  # rows accumulate in batch order
+        want = (want + out[r]).astype(np.float32)
+    np.testing.assert_array_equal(oracle.accumulate_bias(gb0, out), want)
+
+
+# ------------------------------------------------------ im2col, conv, attention
+def test_im2col_conv_matches_direct_convolution():
+    rng = np.random.default_rng(21)
+    B, C, H, W, OC, KH, KW, pad, stride = 2, 3, 6, 5, 4, 3, 3, 1, 1
+    x = uniform(rng, (B, C, H, W))
+    col = oracle.im2col(x, B, C, H, W, KH, KW, stride=stride, pad=pad)
+    OH, OW = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    assert col.shape == (B * OH * OW, KH * KW * C)
+    w_oihw = uniform(rng, (OC, C, KH, KW))
+    w_col = np.ascontiguousarray(w_oihw.transpose(0, 2, 3, 1).reshape(OC, KH * KW * C))  # (kh,kw,ic) order
+    bias = uniform(rng, (OC,))
+    out = oracle.conv2d_im2col_gemm(col, w_col, bias, B, OC, OH * OW, KH * KW * C)
+    xp = np.pad(x.astype(np.float64), ((0, 0), (0, 0), (pad, pad), (pad, pad)))
+    ref = np.zeros((B, OC, OH, OW))
+    for oh in range(OH):
+        for ow in range(OW):
+            patch = xp[:, :, oh * stride:oh * stride + KH, ow * stride:ow * stride + KW]
+            ref[:, :, oh, ow] = np.einsum("bchw,ochw->bo", patch, w_oihw.astype(np.float64))
+    ref += bias[None, :, None, None]
+    assert np.abs(out.reshape(B, OC, OH, OW) - ref).max() <= 1e-5
+    # the GEMM contract is C = col . W^T (NT): compare against the NT oracle + bias
+    nt = oracle.matmul_nt(col, w_col, B * OH * OW, OC, KH * KW * C) + bias[None, :]
+    gemm = out.transpose(0, 2, 1).reshape(B * OH * OW, OC)
+    assert np.abs(gemm - nt).max() <= 1e-5
+
+
+def test_attention_matches_fp64_softmax():
+    rng = np.random.default_rng(8)
+    S, D = 33, 16
+    q, k, v = (rng.standard_normal((S, D)).astype(np.float32) for _ in range(3))
+    scale = 1.0 / np.sqrt(D)
+    out = oracle.attention(q, k, v, S, D, scale)
+    s = (q.astype(np.float64) @ k.astype(np.float64).T) * scale
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    assert np.abs(out - p @ v.astype(np.float64)).max() <= 1e-5
+
+
+# --------------------------------------------------------------- golden drift
+def test_oracle_matches_committed_cases():
+    z = np.load(os.path.join(GOLDEN, "oracle_cases.npz"))
+    for name in z["names"]:
+        layout, m, n, k, acc, act = z[f"{name}_meta"]
+        m, n, k, acc = int(m), int(n), int(k), bool(int(acc))
+        a, b, bias, c0 = z[f"{name}_a"], z[f"{name}_b"], z[f"{name}_bias"], z[f"{name}_c0"]
+        if act != "none":
+            c = oracle.matmul_bias_act(a, b, bias, m, n, k, str(act))
+        elif layout == "nn":
+            c = oracle.matmul(a, b, m, n, k, acc, c0)
+        elif layout == "tn":
+            c = oracle.matmul_tn(a, b, m, n, k, acc, c0)
+        else:
+            c = oracle.matmul_nt(a, b, m, n, k, acc, c0)
+        np.testing.assert_array_equal(c, z[f"{name}_c"], err_msg=str(name))
+
+
+# ------------------------------------------------- the checks are discriminating
+def test_checks_catch_planted_mistakes(kats):
+    """Plant plausible mistakes in oracle outputs; the pinning checks reject each."""
+    rng = np.random.default_rng(99)
+    m, n, k = 37, 45, 29
+    a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+    good = oracle.matmul(a, b, m, n, k)
+    den = abs_denominator(a, b)
+    assert componentwise_error(good, seq_nn(a, b), den) == 0.0
+    # dropped last K term
+    dropped = oracle.matmul(a[:, :-1], b[:-1, :], m, n, k - 1)
+    assert componentwise_error(dropped, seq_nn(a, b), den) > tol(k)
+    # transposed operand (B^T used as B, square case)
+    sq = uniform(rng, (32, 32))
+    wrong_t = oracle.matmul(sq, sq.T.copy(), 32, 32, 32)
+    assert not np.array_equal(wrong_t, seq_nn(sq, sq))
+    # wrong sign on the bias epilogue
+    bias = uniform(rng, (n,))
+    fused = oracle.matmul_bias_act(a, b, bias, m, n, k, "linear")
+    assert componentwise_error(fused - 2 * bias[None, :], seq_nn(a, b) + bias, den + np.abs(bias)) > tol(k)
+    # swapped NT index (reading B as [k x n] instead of [n x k]) fails the integer KAT
+    mm, nn, kk = (int(x) for x in kats["small64_mnk"])
+    ai, bi = kats["small64_a"].reshape(mm, kk), kats["small64_b"].reshape(kk, nn)
+    swapped = oracle.matmul_nt(ai, bi, mm, nn, kk)  # B passed without the transpose
+    assert not np.array_equal(swapped, kats["small64_c"].reshape(mm, nn))
