@@ -1,0 +1,275 @@
+"""Benchmark of the MI355X fp32 GEMM backend (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-configs] [--no-cpu]
+
+A step is one pass of the hot path over one batch of synthetic input: one
+8192 x 8192 x 8192 row-major NN fp32 GEMM (the
+north-star target), inputs U[-1,1) already resident in HBM.  `value` is
+TFLOP/s = 2 M N K / (time per step) over exactly K timed steps, bracketed by
+a device synchronisation on both sides; the kernel's average duration comes
+from HIP events recorded on the context stream (the stream the kernels run
+on).  The other BASELINE configurations are timed too and reported under
+"configs" (parity for every one of them is checked by tests/).
+
+The CPU baseline is the oracle (a restatement of the reference CPU tiled
+matmul, src/backend.zig:2523-2570) timed on a bounded row sample of the same
+8192^3 workload, single-threaded and on all host cores (OpenMP over row
+blocks, bit-identical to the sequential order).
+
+One GPU only: --gpus N with N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_F32_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+PEAK_HBM_GBS = 8000.0
+METRIC = "fp32 GEMM TFLOP/s and % of MFMA peak; MLP train-step GEMM time, 1 MI355X"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_sgemm_nn_8192.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def uniform(rng, shape, lo=-1.0, hi=1.0):
+    return (rng.random(shape, dtype=np.float32) * np.float32(hi - lo) + np.float32(lo)).astype(np.float32)
+
+
+def time_launches(ctx, fn, steps, warmup):
+    """Average milliseconds per call from HIP events on the context stream."""
+    for _ in range(warmup):
+        fn()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    ms = e0.elapsed_ms(e1) / steps
+    e0.close()
+    e1.close()
+    return ms
+
+
+def gemm_bytes(m, n, k, batch=1, bias=False, acc=False):
+    return 4 * (m * k + k * n + m * n) * batch + (4 * n if bias else 0) + (4 * m * n * batch if acc else 0)
+
+
+def config_entry(name, layout, m, n, k, batch, ms, extra=None):
+    flops = 2.0 * m * n * k * batch
+    byts = gemm_bytes(m, n, k, batch, bias=bool(extra and extra.get("bias")))
+    t_roof = max(flops / (PEAK_F32_TFLOPS * 1e12), byts / (PEAK_HBM_GBS * 1e9))
+    e = {"name": name, "layout": layout, "m": m, "n": n, "k": k, "batch": batch, "kernel_ms": round(ms, 5),
+         "tflops": round(flops / (ms * 1e-3) / 1e12, 3), "pct_f32_peak": round(100 * flops / (ms * 1e-3) / 1e12 /
+                                                                                 PEAK_F32_TFLOPS, 2),
+         "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "roofline_frac": round(t_roof / (ms * 1e-3), 4)}
+    if extra:
+        e.update(extra)
+    return e
+
+
+def bench_configs(ctx, rng, reps=10, warmup=3):
+    """Kernel time of every BASELINE configuration (device-resident inputs)."""
+    out = []
+
+    def run(name, layout, m, n, k, batch=1, a_shape=None, b_shape=None, bias=None, act="linear", lo=-1.0):
+        lda = m if layout == "tn" else k
+        ldb = k if layout == "nt" else n
+        a_shape = a_shape or ((k, m) if layout == "tn" else (m, k))
+        b_shape = b_shape or ((n, k) if layout == "nt" else (k, n))
+        a = ctx.to_device(uniform(rng, (batch,) + a_shape, lo=lo))
+        b = ctx.to_device(uniform(rng, (batch,) + b_shape))
+        c = ctx.alloc(batch * m * n)
+        db = ctx.to_device(bias) if bias is not None else None
+        if batch == 1:
+            fn = lambda: ctx.sgemm(layout, m, n, k, a, lda, b, ldb, c, n, False, db, act)  # noqa: E731
+        else:
+            fn = lambda: ctx.sgemm_strided_batched(layout, m, n, k, a, lda, a_shape[0] * a_shape[1], b, ldb,  # noqa
+                                                   b_shape[0] * b_shape[1], c, n, m * n, batch)
+        ms = time_launches(ctx, fn, reps, warmup)
+        for buf in (a, b, c, db):
+            if buf is not None:
+                buf.close()
+        e = config_entry(name, layout, m, n, k, batch, ms, {"bias": bias is not None, "act": act})
+        log(f"  {name:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s  {e['pct_f32_peak']:5.1f}% peak")
+        out.append(e)
+        return ms
+
+    run("C1 NN 512^3", "nn", 512, 512, 512)
+    run("C3 dW TN 1024x1024x4096", "tn", 1024, 1024, 4096)
+    run("C3 dX NT 4096x1024x1024", "nt", 4096, 1024, 1024)
+    run("C4 NN 1000^3", "nn", 1000, 1000, 1000)
+    run("C4 NN 4097x1023x777", "nn", 4097, 1023, 777)
+    run("C5 attn QK^T NT x128", "nt", 1024, 1024, 64, batch=128)
+    run("C5 attn PV NN x128", "nn", 1024, 64, 1024, batch=128)
+    run("C5 conv NT 100352x128x576", "nt", 100352, 128, 576)
+    out.append(bench_mlp_step(ctx, rng, reps, warmup))
+    return out
+
+
+def bench_mlp_step(ctx, rng, reps, warmup):
+    """C2: the six GEMMs of one Dense 784-128-10 training step at batch 256 (plus the
+    relu-mask and bias-gradient kernels between them), device resident, one stream."""
+    from zigneuron_amd import DenseDevice
+    batch = 256
+    x = ctx.to_device(uniform(rng, (batch, 784), 0.0, 1.0))
+    dy = ctx.to_device(uniform(rng, (batch, 10)))
+    l1 = DenseDevice(ctx, 784, 128, "relu", batch, seed=1)
+    l2 = DenseDevice(ctx, 128, 10, "linear", batch, seed=2)
+
+    def step():
+        h = l1.forward(x)
+        l2.forward(h)
+        g = l2.backward(h, dy)
+        l1.backward(x, g)
+
+    ms = time_launches(ctx, step, reps * 5, warmup)
+    flops = 2.0 * batch * (784 * 128 + 128 * 10) * 3
+    e = {"name": "C2 MLP train step (6 GEMMs + 4 helpers)", "step_ms": round(ms, 5),
+         "gemm_gflop": round(flops / 1e9, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 3)}
+    log(f"  {e['name']:28s} {ms * 1e3:9.1f} us per step")
+    return e
+
+
+def cpu_baseline(target_s=5.0):
+    """Oracle (reference CPU tiled matmul restated) on a row sample of the 8192^3 workload."""
+    from oracle import oracle
+    rng = np.random.default_rng(1)
+    n = k = 8192
+    b = uniform(rng, (k, n))
+    threads = max(1, min(16, oracle.cpu_count()))
+    res = {}
+    for label, th in (("single", 1), ("all", threads)):
+        rows = 32 * th
+        a = uniform(rng, (rows, k))
+        t = time.perf_counter()
+        oracle.matmul(a, b, rows, n, k, branch="blocked", threads=th)
+        dt = time.perf_counter() - t
+        rows = int(min(8192, max(32, 32 * round(rows * target_s / dt / 32))))
+        a = uniform(rng, (rows, k))
+        t = time.perf_counter()
+        oracle.matmul(a, b, rows, n, k, branch="blocked", threads=th)
+        dt = time.perf_counter() - t
+        res[label] = {"tflops": 2.0 * rows * n * k / dt / 1e12, "rows": rows, "seconds": dt, "threads": th}
+        log(f"  cpu {label}: {rows} rows x 8192 x 8192 in {dt:.2f} s = {res[label]['tflops'] * 1e3:.2f} GFLOP/s")
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    allc = res["all"]
+    return {"value": round(allc["tflops"], 5), "unit": "TFLOP/s", "cores": allc["threads"], "kind": "port",
+            "sample": (f"oracle blocked NN (src/backend.zig:2523-2570 restated) on {allc['rows']} of 8192 rows of "
+                       f"the 8192^3 workload, {allc['threads']} OpenMP threads; single-thread on "
+                       f"{res['single']['rows']} rows: {res['single']['tflops']:.5f} TFLOP/s"),
+            "single_thread_tflops": round(res["single"]["tflops"], 5), "cpu_model": cpu_model}
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return float(t["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is "
+              "design-only here.", file=sys.stderr)
+        return 2
+
+    from zigneuron_amd import Context
+    ctx = Context(0)
+    log(f"device {ctx.arch}, {ctx.compute_units} CUs, {ctx.clock_khz / 1e3:.0f} MHz")
+    rng = np.random.default_rng(42)
+    m = n = k = 8192
+    log("allocating 8192^3 operands")
+    a_h, b_h = uniform(rng, (m, k)), uniform(rng, (k, n))
+    a, b, c = ctx.to_device(a_h), ctx.to_device(b_h), ctx.alloc(m * n)
+    step = lambda: ctx.sgemm("nn", m, n, k, a, k, b, n, c, n)  # noqa: E731
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.sync()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    kernel_ms = e0.elapsed_ms(e1) / args.steps
+    ms_per_step = wall * 1e3 / args.steps
+    flops = 2.0 * m * n * k
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    log(f"8192^3 NN: {ms_per_step:.3f} ms/step wall, {kernel_ms:.3f} ms kernel (events) -> {achieved:.2f} TFLOP/s")
+
+    # sanity: 4 sampled rows against an fp64 dot product
+    rows = [0, 1234, 5000, m - 1]
+    full = c.download(m * n).reshape(m, n)
+    ref = a_h[rows].astype(np.float64) @ b_h.astype(np.float64)
+    den = np.abs(a_h[rows].astype(np.float64)) @ np.abs(b_h.astype(np.float64))
+    rel = float((np.abs(full[rows] - ref) / den).max())
+    del full
+    for buf in (a, b, c):
+        buf.close()
+
+    configs = []
+    if not args.no_configs:
+        log("per-config kernel times:")
+        configs = bench_configs(ctx, rng)
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle):")
+        cpu = cpu_baseline()
+
+    traffic = load_traffic()
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic U[-1,1) operands, seed 42, resident in HBM",
+        "config": {"workload": "NN fp32 GEMM 8192x8192x8192 row-major (BASELINE configs[3], C4 large)",
+                   "m": m, "n": n, "k": k, "layout": "nn", "kernel": "zn_sgemm_nn_l",
+                   "pct_f32_peak": round(100 * value / PEAK_F32_TFLOPS, 2),
+                   "sampled_rows_max_componentwise_err": rel, "tolerance": 1e-5 * np.sqrt(k),
+                   "device": ctx.arch, "compute_units": ctx.compute_units},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_F32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_F32_TFLOPS, 4), "traffic": traffic,
+                     "kernel_ms": round(kernel_ms, 4), "algorithmic_flops_per_launch": flops},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    ctx.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,224 @@
+/*
+ * zn_hip.h -- C ABI of the MI355X (gfx950) fp32 GEMM backend for ZigNeuron.
+ *
+ * This is the drop-in boundary a Zig `HipBackend` binds with `extern fn`
+ * declarations (the binding stub is shown in INTEGRATION.md).  It replaces the
+ * reference's CUDA stack for the GEMM path: the driver binding
+ * (src/cuda_driver.zig:632-931), NVRTC (src/cuda_nvrtc.zig), the device
+ * context (src/cuda_context.zig:382-1820) and the CudaBackend GEMM wrappers
+ * (src/cuda.zig:521-797, 1008-1071, 2255-2338).  All citations are to the
+ * reference tree.
+ *
+ * Conventions
+ *  - Every function returns an int status: ZN_OK (0) or a negative ZN_ERR_*.
+ *    Nothing aborts or throws across the boundary.
+ *  - Matrices are row-major fp32.  The host-slice entry points take the
+ *    reference's implicit leading dimensions (glossary of src/backend.zig:
+ *    NN lda=K ldb=N; TN A stored [K x M]; NT B stored [N x K]; ldc=N); the
+ *    device entry points take explicit leading dimensions and batch strides.
+ *  - One context serves one host thread (the reference's Backend is not
+ *    thread-safe, src/backend.zig:25).  Work is ordered on the context's one
+ *    HIP stream.  Device-pointer entry points are asynchronous; host-slice
+ *    entry points return only after the result is in host memory, like
+ *    CudaBackend.matMul's final download (src/cuda.zig:617).
+ *  - GEMM kernels are loaded from offline-built gfx950 code objects
+ *    (zn_gemm_gfx950.hsaco); there is no runtime compilation and no CPU
+ *    fallback: a missing device or code object is an error.
+ */
+#ifndef ZN_HIP_H
+#define ZN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZN_HIP_ABI_VERSION 1
+
+/* Status codes; zn_hip_status_string() names them.  Mapped to a Zig error set
+ * the way checkCuda maps CUresult (src/cuda_driver.zig:1119-1160). */
+#define ZN_OK 0
+#define ZN_ERR_NO_DEVICE (-1)   /* no HIP device / not a gfx950 device */
+#define ZN_ERR_CODE_OBJECT (-2) /* code object missing, unreadable or not loadable */
+#define ZN_ERR_SYMBOL (-3)      /* a kernel symbol is missing from the code object */
+#define ZN_ERR_INVALID_ARG (-4) /* null pointer, bad enum, short slice, bad leading dim */
+#define ZN_ERR_OOM (-5)         /* device allocation failed */
+#define ZN_ERR_LAUNCH (-6)      /* kernel launch failed */
+#define ZN_ERR_HIP (-7)         /* other HIP runtime error; see zn_hip_last_hip_error */
+#define ZN_ERR_OVERFLOW (-8)    /* a size product overflows, or exceeds the 32-bit index range */
+
+/* Operand layouts (row-major storage). */
+typedef enum zn_layout {
+    ZN_LAYOUT_NN = 0, /* C[MxN] = A[MxK] . B[KxN]           (Backend.matMul)          */
+    ZN_LAYOUT_NT = 1, /* C[MxN] = A[MxK] . B^T, B is [NxK]  (Backend.matMulTransposeB) */
+    ZN_LAYOUT_TN = 2  /* C[MxN] = A^T . B[KxN], A is [KxM]  (Backend.matMulTransposeA) */
+} zn_layout;
+
+/* Epilogue activations, applied after the full K sum and the bias
+ * (src/backend.zig:200-295; src/activation.zig:97-120). */
+typedef enum zn_act {
+    ZN_ACT_LINEAR = 0,  /* identity                                   */
+    ZN_ACT_RELU = 1,    /* v > 0 ? v : 0                              */
+    ZN_ACT_SIGMOID = 2, /* 1/(1+exp(-v)) fused; branch-stable elementwise */
+    ZN_ACT_TANH = 3     /* tanh(v)                                    */
+} zn_act;
+
+typedef struct zn_ctx zn_ctx;
+typedef struct zn_event zn_event;
+
+typedef struct zn_device_info {
+    char name[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int32_t compute_units;  /* multiProcessorCount */
+    int32_t clock_khz;      /* max engine clock */
+    int64_t total_mem;      /* bytes of HBM */
+} zn_device_info;
+
+/* ---------------------------------------------------------------- context */
+
+/* ABI version of the loaded library (ZN_HIP_ABI_VERSION). */
+int zn_hip_abi_version(void);
+
+/* 1 when at least one HIP device is visible, else 0.  Replaces
+ * CudaBackend.isAvailable (src/cuda.zig:317-328) for Backend.detect
+ * (src/backend.zig:84-94). */
+int zn_hip_available(void);
+
+/* Create a context on `device`: select the device, create one stream, load
+ * the gfx950 code object from `code_object_dir` (NULL: $ZN_HIP_CODE_OBJECT_DIR,
+ * else the directory holding this library) and resolve every kernel symbol.
+ * Replaces CudaBackend.init -> CudaContext.init -> loadBuiltinKernels
+ * (src/cuda.zig:163-300, src/cuda_context.zig:382-497, 1325-1414). */
+int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out);
+
+/* Synchronize, release cached device memory, unload the module, destroy the
+ * stream and free the context (CudaBackend.deinit).  NULL is a no-op. */
+int zn_hip_destroy(zn_ctx *ctx);
+
+/* Static string naming a status code. */
+const char *zn_hip_status_string(int status);
+
+/* The hipError_t behind the last ZN_ERR_HIP / ZN_ERR_OOM / ZN_ERR_LAUNCH on ctx. */
+int zn_hip_last_hip_error(const zn_ctx *ctx);
+
+/* Device properties (CudaContext.queryDeviceProperties, src/cuda_context.zig:713). */
+int zn_hip_device_info(const zn_ctx *ctx, zn_device_info *out);
+
+/* The context's hipStream_t, for callers that order their own work with it. */
+void *zn_hip_stream(const zn_ctx *ctx);
+
+/* ----------------------------------------------------------------- memory */
+
+/* Caller-owned device buffers (256-byte aligned).  Replace
+ * CudaContext.getBuffer / returnBuffer for device-resident callers
+ * (src/cuda_context.zig:773-852). */
+int zn_hip_alloc(zn_ctx *ctx, size_t bytes, void **out);
+int zn_hip_free(zn_ctx *ctx, void *ptr);
+/* Blocking copies (CudaContext.upload / download, src/cuda_context.zig:882-920). */
+int zn_hip_h2d(zn_ctx *ctx, void *dst, const void *src, size_t bytes);
+int zn_hip_d2h(zn_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Stream-ordered copies; host memory must stay valid until zn_hip_sync. */
+int zn_hip_h2d_async(zn_ctx *ctx, void *dst, const void *src, size_t bytes);
+int zn_hip_d2h_async(zn_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Fill `count` floats with `value` using a kernel (safe under graph capture). */
+int zn_hip_fill_f32(zn_ctx *ctx, float *dst, float value, int64_t count);
+/* Device-to-device copy of `count` floats with a plain streaming kernel. */
+int zn_hip_copy_f32(zn_ctx *ctx, float *dst, const float *src, int64_t count);
+/* Wait for all work on the context's stream. */
+int zn_hip_sync(zn_ctx *ctx);
+
+/* ----------------------------------------------------------------- events */
+
+/* HIP events on the context's stream, for kernel timing (the role of the
+ * cuEvent timing in CudaContext.launchKernel, src/cuda_context.zig:1711-1772). */
+int zn_hip_event_create(zn_ctx *ctx, zn_event **out);
+int zn_hip_event_record(zn_ctx *ctx, zn_event *ev);
+/* Milliseconds between two recorded events; waits for `end`. */
+int zn_hip_event_elapsed_ms(zn_event *start, zn_event *end, float *ms);
+int zn_hip_event_destroy(zn_event *ev);
+
+/* ------------------------------------------------ GEMM on device pointers */
+
+/* C = act((accumulate ? C : 0) + op(A).op(B) + bias) for one problem.
+ * `bias` (length N) may be NULL.  Leading dimensions are in elements and must
+ * be >= the stored row length.  m, n >= 0; k >= 0 (k == 0 gives the epilogue
+ * of a zero sum).  Asynchronous on the context stream.
+ * Generalises CudaBackend.matMul(a,b,c,m,n,k,transpose_a,transpose_b,accumulate)
+ * (src/cuda.zig:540-618) and matMulBiasActivation (src/cuda.zig:1008-1071). */
+int zn_hip_sgemm(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
+                 const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias, int act);
+
+/* `batch` independent problems; operand p of problem i starts at
+ * p + i*stride_p (elements).  stride_a or stride_b may be 0 (a shared
+ * operand, as in CudaBackend.matMulBatch's shared B, src/cuda.zig:729-797).
+ * Attention QK^T / PV and im2col convolution GEMMs use this entry
+ * (src/cuda.zig:2255-2281, 3026-3100). */
+int zn_hip_sgemm_strided_batched(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a,
+                                 int64_t lda, int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b,
+                                 float *c, int64_t ldc, int64_t stride_c, int64_t batch, int accumulate,
+                                 const float *bias, int act);
+
+/* ------------------------------------ Dense helpers on device pointers */
+
+/* out[r*n + i] += bias[i]  (Backend.addBias, src/backend.zig:658-671). */
+int zn_hip_add_bias(zn_ctx *ctx, float *out, const float *bias, int64_t rows, int64_t n);
+/* Activation.forward per element (Backend.activationForward, src/backend.zig:367-386). */
+int zn_hip_activation_forward(zn_ctx *ctx, int act, const float *in, float *out, int64_t len);
+/* grad_in = grad_out * act'(y) from the activated output y
+ * (Backend.activationBackward, src/backend.zig:390-399, src/optimization.zig:229-303). */
+int zn_hip_activation_backward(zn_ctx *ctx, int act, const float *y, const float *grad_out, float *grad_in,
+                               int64_t len);
+/* grad_bias[i] += sum over rows r (ascending) of gaa[r*n + i]
+ * (Backend.accumulateBias, src/backend.zig:649-655, 706-713). */
+int zn_hip_accumulate_bias(zn_ctx *ctx, float *grad_bias, const float *gaa, int64_t rows, int64_t n);
+
+/* ------------------------------- Backend drop-ins on host slices (sync) */
+/* Each takes the reference method's slices as (pointer, length) pairs and its
+ * scalar arguments unchanged, stages through the context's cached device
+ * buffers, and returns when `c` holds the result.  A slice shorter than the
+ * shape requires is ZN_ERR_INVALID_ARG. */
+
+/* Backend.matMul (src/backend.zig:169-182): C[m x n] (+)= A[m x k] . B[k x n]. */
+int zn_hip_mat_mul(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c,
+                   size_t c_len, size_t m, size_t n, size_t k, int accumulate);
+/* Backend.matMulBatch (src/backend.zig:186-195): rows of A against a shared B. */
+int zn_hip_mat_mul_batch(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c,
+                         size_t c_len, size_t batch_size, size_t n, size_t k, int accumulate);
+/* Backend.matMulTransposeA (src/backend.zig:298-307): C = A^T . B, A is [k x m]. */
+int zn_hip_mat_mul_transpose_a(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c,
+                               size_t c_len, size_t m, size_t n, size_t k, int accumulate);
+/* Backend.matMulTransposeB (src/backend.zig:310-325): C = A . B^T, B is [n x k]. */
+int zn_hip_mat_mul_transpose_b(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c,
+                               size_t c_len, size_t m, size_t n, size_t k, int accumulate);
+/* Backend.matMulBias (src/backend.zig:200-222). */
+int zn_hip_mat_mul_bias(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, const float *bias,
+                        size_t bias_len, float *c, size_t c_len, size_t batch_size, size_t n, size_t k);
+/* Backend.matMulBiasRelu (src/backend.zig:225-247). */
+int zn_hip_mat_mul_bias_relu(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len,
+                             const float *bias, size_t bias_len, float *c, size_t c_len, size_t batch_size, size_t n,
+                             size_t k);
+/* Backend.matMulBiasSigmoid (src/backend.zig:250-272). */
+int zn_hip_mat_mul_bias_sigmoid(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len,
+                                const float *bias, size_t bias_len, float *c, size_t c_len, size_t batch_size,
+                                size_t n, size_t k);
+/* Backend.matMulBiasTanh (src/backend.zig:275-295). */
+int zn_hip_mat_mul_bias_tanh(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len,
+                             const float *bias, size_t bias_len, float *c, size_t c_len, size_t batch_size, size_t n,
+                             size_t k);
+/* Backend.addBias (src/backend.zig:658-671): rows = out_len / bias_len. */
+int zn_hip_add_bias_host(zn_ctx *ctx, float *out, size_t out_len, const float *bias, size_t bias_len);
+/* Backend.activationForward (src/backend.zig:367-386) for linear/relu/sigmoid/tanh. */
+int zn_hip_activation_forward_host(zn_ctx *ctx, int act, const float *in, size_t in_len, float *out,
+                                   size_t out_len);
+/* Backend.activationBackward (src/backend.zig:390-399) for linear/relu/sigmoid/tanh. */
+int zn_hip_activation_backward_host(zn_ctx *ctx, int act, const float *y, size_t y_len, const float *grad_out,
+                                    size_t grad_out_len, float *grad_in, size_t grad_in_len);
+/* Backend.accumulateBias (src/backend.zig:649-655): rows = gaa_len / grad_bias_len. */
+int zn_hip_accumulate_bias_host(zn_ctx *ctx, float *grad_bias, size_t grad_bias_len, const float *gaa,
+                                size_t gaa_len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZN_HIP_H */

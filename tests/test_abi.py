@@ -1,0 +1,115 @@
+"""CPU-side tests of the C ABI (no GPU needed): the library loads, exports every
+symbol include/zn_hip.h declares, the ctypes table matches the header, the
+code objects hold every kernel the runtime resolves, and argument/device
+errors come back as status codes."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "zn_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(zn_hip_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from zigneuron_amd import _lib
+    return _lib.load()
+
+
+def test_header_declares_the_boundary():
+    fns = header_functions()
+    assert len(fns) >= 35
+    for must in ("zn_hip_create", "zn_hip_sgemm", "zn_hip_sgemm_strided_batched", "zn_hip_mat_mul",
+                 "zn_hip_mat_mul_transpose_a", "zn_hip_mat_mul_transpose_b", "zn_hip_mat_mul_bias_relu"):
+        assert must in fns
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from zigneuron_amd import _lib
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\sT\s(zn_hip_\w+)", out.stdout))
+    missing = [f for f in header_functions() if f not in exported]
+    assert not missing, missing
+    for f in header_functions():
+        assert hasattr(lib, f)
+
+
+def test_ctypes_table_matches_header():
+    from zigneuron_amd import _lib
+    assert sorted(_lib.SIGNATURES) == header_functions()
+
+
+def test_code_objects_hold_every_kernel():
+    from zigneuron_amd import _lib
+    gemm = open(os.path.join(_lib.LIB_DIR, "zn_gemm_gfx950.hsaco"), "rb").read()
+    elt = open(os.path.join(_lib.LIB_DIR, "zn_elementwise_gfx950.hsaco"), "rb").read()
+    for blob in (gemm, elt):  # an offload bundle (hipcc --genco) or a bare ELF code object
+        assert blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or blob[:4] == b"\x7fELF"
+    for lay in ("nn", "nt", "tn"):
+        for t in ("l", "m", "s"):
+            assert f"zn_sgemm_{lay}_{t}".encode() in gemm
+    for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",
+              "zn_accumulate_bias"):
+        assert k.encode() in elt
+    assert b"gfx950" in gemm
+
+
+def test_abi_version_and_status_strings(lib):
+    from zigneuron_amd import _lib
+    assert lib.zn_hip_abi_version() == 1
+    names = {lib.zn_hip_status_string(s).decode().split(":")[0] for s in range(-8, 1)}
+    assert len(names) == 9
+    assert lib.zn_hip_status_string(-99).decode() == "ZN_ERR_UNKNOWN"
+
+
+def test_null_and_bad_arguments_without_device(lib):
+    """Argument checks that run before any device call."""
+    from zigneuron_amd import _lib
+    assert lib.zn_hip_create(0, None, None) == _lib.ZN_ERR_INVALID_ARG
+    assert lib.zn_hip_destroy(None) == _lib.ZN_OK
+    assert lib.zn_hip_sgemm(None, 0, 1, 1, 1, None, 1, None, 1, None, 1, 0, None, 0) == _lib.ZN_ERR_INVALID_ARG
+    assert lib.zn_hip_mat_mul(None, None, 0, None, 0, None, 0, 1, 1, 1, 0) == _lib.ZN_ERR_INVALID_ARG
+    assert lib.zn_hip_sync(None) == _lib.ZN_ERR_INVALID_ARG
+    assert lib.zn_hip_event_destroy(None) == _lib.ZN_OK
+    assert lib.zn_hip_stream(None) is None
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is present")
+def test_no_device_is_a_clean_error():
+    import zigneuron_amd as zn
+    assert zn.available() is False
+    with pytest.raises(zn.NoDeviceError):
+        zn.Context(0)
+    with pytest.raises(zn.NoDeviceError):
+        zn.Backend.init()
+
+
+def test_backend_rejects_non_gemm_activation():
+    from zigneuron_amd import InvalidArgumentError
+    from zigneuron_amd.backend import act_id
+    assert act_id("relu") == 1 and act_id("tanh") == 3
+    with pytest.raises(InvalidArgumentError):
+        act_id("softmax")
+
+
+def test_dense_init_scales_match_reference():
+    """src/layer.zig:330-334: He for relu, Xavier for sigmoid/tanh, sqrt(1/in) for linear."""
+    from zigneuron_amd.layer import init_scale, init_weights
+    assert init_scale("relu", 784, 128) == pytest.approx((2 / 784) ** 0.5)
+    assert init_scale("sigmoid", 128, 10) == pytest.approx((2 / 138) ** 0.5)
+    assert init_scale("linear", 128, 10) == pytest.approx((1 / 128) ** 0.5)
+    w = init_weights(784, 128, "relu", seed=1)
+    assert w.dtype == np.float32 and w.shape == (784, 128)
+    assert np.abs(w).max() <= (2 / 784) ** 0.5

@@ -1,0 +1,191 @@
+"""GPU parity at BASELINE.json's configurations (C1-C5).
+
+Where the oracle finishes in seconds the whole output is compared; at full
+scale (8192^3, the attention and convolution batches) a sample of rows or
+problems is compared exactly against the oracle and every output is covered
+by row/column checksums (C.1 = A.(B.1), 1^T.C = (1^T.A).B in fp64), a
+size-independent property bounded by the same componentwise tolerance.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from _parity import abs_denominator, normal, tol, uniform
+from gpu_common import THREADS, announce, assert_close, ref_gemm, run_gemm
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from zigneuron_amd import Context
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def checksum_property(c, a_mk, b_kn, k, what):
+    """Row and column sums of C against A.(B.1) and (1^T.A).B in fp64."""
+    A, B = a_mk.astype(np.float64), b_kn.astype(np.float64)
+    absA, absB = np.abs(A), np.abs(B)
+    row = c.astype(np.float64).sum(axis=1)
+    row_ref = A @ B.sum(axis=1)
+    row_den = absA @ absB.sum(axis=1)
+    col = c.astype(np.float64).sum(axis=0)
+    col_ref = A.sum(axis=0) @ B
+    col_den = absA.sum(axis=0) @ absB
+    slack = 1e-12
+    assert np.all(np.abs(row - row_ref) <= tol(k) * row_den + slack * row_den + 1e-30), f"{what}: row checksum"
+    assert np.all(np.abs(col - col_ref) <= tol(k) * col_den + slack * col_den + 1e-30), f"{what}: column checksum"
+
+
+def test_c1_nn_512(ctx):
+    rng = np.random.default_rng(42)
+    m = n = k = 512
+    a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+    announce("C1 NN 512^3")
+    c = run_gemm(ctx, "nn", a, b, m, n, k)
+    assert_close(c, ref_gemm("nn", a, b, m, n, k), "nn", a, b, m, n, k)
+
+
+def test_c2_mlp_training_step(ctx):
+    """X[256x784] U[0,1) -> W1 He + b1(0) + ReLU -> W2 Xavier + b2(0) linear; dY2 U[-1,1).
+    Each of the six GEMMs is checked against the oracle on the GPU's own inputs."""
+    from zigneuron_amd import DenseDevice
+    batch, d_in, d_h, d_out = 256, 784, 128, 10
+    rng = np.random.default_rng(42)
+    x = uniform(rng, (batch, d_in), 0.0, 1.0)
+    dy = uniform(rng, (batch, d_out))
+    announce("C2 MLP step")
+    l1 = DenseDevice(ctx, d_in, d_h, "relu", batch, seed=1)
+    l2 = DenseDevice(ctx, d_h, d_out, "linear", batch, seed=2)
+    dx, ddy = ctx.to_device(x), ctx.to_device(dy)
+    h1 = l1.forward(dx)
+    logits = l2.forward(h1)
+    g_h1 = l2.backward(h1, ddy)
+    g_x = l1.backward(dx, g_h1)
+    ctx.sync()
+    W1 = l1.weights.download().reshape(d_in, d_h)
+    W2 = l2.weights.download().reshape(d_h, d_out)
+    b1, b2 = np.zeros(d_h, np.float32), np.zeros(d_out, np.float32)
+    H1 = h1.download().reshape(batch, d_h)
+    assert_close(H1, oracle.matmul_bias_act(x, W1, b1, batch, d_h, d_in, "relu"), "nn", x, W1, batch, d_h, d_in,
+                 bias=b1, act="relu", what="L1 forward")
+    L = logits.download().reshape(batch, d_out)
+    assert_close(L, oracle.matmul_bias_act(H1, W2, b2, batch, d_out, d_h, "linear"), "nn", H1, W2, batch, d_out,
+                 d_h, bias=b2, what="L2 forward")
+    # L2 backward: gaa2 = dY (linear), dX2 = gaa2 . W2^T (NT), dW2 = H1^T . gaa2 (TN)
+    gaa2 = l2.gaa.download().reshape(batch, d_out)
+    np.testing.assert_array_equal(gaa2, dy)
+    GH1 = g_h1.download().reshape(batch, d_h)
+    assert_close(GH1, oracle.matmul_nt(gaa2, W2, batch, d_h, d_out), "nt", gaa2, W2, batch, d_h, d_out,
+                 what="L2 dX (NT)")
+    dW2 = l2.grad_weights.download().reshape(d_h, d_out)
+    assert_close(dW2, oracle.matmul_tn(H1, gaa2, d_h, d_out, batch), "tn", H1, gaa2, d_h, d_out, batch,
+                 what="L2 dW (TN)")
+    np.testing.assert_array_equal(l2.grad_bias.download(), oracle.accumulate_bias(np.zeros(d_out, np.float32), gaa2))
+    # L1 backward: gaa1 = relu'(H1) * GH1, dX1 = gaa1 . W1^T (NT), dW1 = X^T . gaa1 (TN)
+    gaa1 = l1.gaa.download().reshape(batch, d_h)
+    np.testing.assert_array_equal(gaa1, oracle.activation_backward("relu", H1, GH1).reshape(batch, d_h))
+    GX = g_x.download().reshape(batch, d_in)
+    assert_close(GX, oracle.matmul_nt(gaa1, W1, batch, d_in, d_h), "nt", gaa1, W1, batch, d_in, d_h,
+                 what="L1 dX (NT)")
+    dW1 = l1.grad_weights.download().reshape(d_in, d_h)
+    assert_close(dW1, oracle.matmul_tn(x, gaa1, d_in, d_h, batch, threads=THREADS), "tn", x, gaa1, d_in, d_h, batch,
+                 what="L1 dW (TN)")
+    np.testing.assert_array_equal(l1.grad_bias.download(), oracle.accumulate_bias(np.zeros(d_h, np.float32), gaa1))
+
+
+@pytest.mark.parametrize("which", ["dW_TN", "dX_NT"])
+def test_c3_dense_backward_gemms(ctx, which):
+    rng = np.random.default_rng(3)
+    s = np.float32(1.0 / 32.0)
+    X = (normal(rng, (4096, 1024)) * s).astype(np.float32)
+    W = (normal(rng, (1024, 1024)) * s).astype(np.float32)
+    dY = (normal(rng, (4096, 1024)) * s).astype(np.float32)
+    announce(f"C3 {which}")
+    if which == "dW_TN":  # dW[1024x1024] = X^T . dY, K = 4096
+        c = run_gemm(ctx, "tn", X, dY, 1024, 1024, 4096)
+        assert_close(c, ref_gemm("tn", X, dY, 1024, 1024, 4096), "tn", X, dY, 1024, 1024, 4096)
+    else:  # dX[4096x1024] = dY . W^T, K = 1024
+        c = run_gemm(ctx, "nt", dY, W, 4096, 1024, 1024)
+        assert_close(c, ref_gemm("nt", dY, W, 4096, 1024, 1024), "nt", dY, W, 4096, 1024, 1024)
+
+
+@pytest.mark.parametrize("m,n,k", [(1000, 1000, 1000), (4097, 1023, 777)])
+def test_c4_ragged_full(ctx, m, n, k):
+    rng = np.random.default_rng(m + k)
+    a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+    announce(f"C4 NN {m}x{n}x{k}")
+    c = run_gemm(ctx, "nn", a, b, m, n, k)
+    assert_close(c, ref_gemm("nn", a, b, m, n, k), "nn", a, b, m, n, k)
+
+
+def test_c4_large_8192(ctx):
+    """8192^3 NN: 64 sampled rows exact against the oracle, all rows/cols by checksum."""
+    rng = np.random.default_rng(8192)
+    m = n = k = 8192
+    a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+    announce("C4 NN 8192^3")
+    c = run_gemm(ctx, "nn", a, b, m, n, k)
+    rows = np.sort(rng.choice(m, 64, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    a_s = np.ascontiguousarray(a[rows])
+    ref = oracle.matmul(a_s, b, len(rows), n, k, branch="blocked", threads=THREADS)
+    assert_close(c[rows], ref, "nn", a_s, b, len(rows), n, k, what="8192 sampled rows")
+    checksum_property(c, a, b, k, "8192^3")
+
+
+def _softmax_rows_fp64(s):
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    return (p / p.sum(axis=-1, keepdims=True)).astype(np.float32)
+
+
+def test_c5_attention_batched(ctx):
+    """[B=8,H=16,S=1024,D=64]: QK^T (NT, batch 128) then P.V (NN, batch 128)."""
+    rng = np.random.default_rng(5)
+    BH, S, D = 128, 1024, 64
+    q, kk, v = normal(rng, (BH, S, D)), normal(rng, (BH, S, D)), normal(rng, (BH, S, D))
+    dq, dk, dv = ctx.to_device(q), ctx.to_device(kk), ctx.to_device(v)
+    ds = ctx.alloc(BH * S * S)
+    announce("C5 QK^T strided batched")
+    ctx.sgemm_strided_batched("nt", S, S, D, dq, D, S * D, dk, D, S * D, ds, S, S * S, BH)
+    scores = ds.download().reshape(BH, S, S)
+    for i in (0, 57, BH - 1):
+        assert_close(scores[i], oracle.matmul_nt(q[i], kk[i], S, S, D, threads=THREADS), "nt", q[i], kk[i], S, S,
+                     D, what=f"QK^T batch {i}")
+    for i in range(0, BH, 16):
+        checksum_property(scores[i], q[i], kk[i].T, D, f"QK^T checksum {i}")
+    # P = row softmax of N(0,1) scores (fp64 on the host), then P.V
+    p = _softmax_rows_fp64(rng.standard_normal((BH, S, S)))
+    dp = ctx.to_device(p)
+    do = ctx.alloc(BH * S * D)
+    announce("C5 PV strided batched")
+    ctx.sgemm_strided_batched("nn", S, D, S, dp, S, S * S, dv, D, S * D, do, D, S * D, BH)
+    out = do.download().reshape(BH, S, D)
+    for i in (0, 77, BH - 1):
+        assert_close(out[i], oracle.matmul(p[i], v[i], S, D, S, branch="blocked", threads=THREADS), "nn", p[i],
+                     v[i], S, D, S, what=f"PV batch {i}")
+    for i in range(0, BH, 16):
+        checksum_property(out[i], p[i], v[i], S, f"PV checksum {i}")
+    for buf in (dq, dk, dv, ds, dp, do):
+        buf.close()
+
+
+def test_c5_im2col_conv_gemm(ctx):
+    """batch 32, 64->128 channels, 3x3, 56x56, pad 1: C[100352x128] = col[100352x576] . W^T."""
+    rng = np.random.default_rng(6)
+    Bn, C, H, W, OC = 32, 64, 56, 56, 128
+    x = uniform(rng, (Bn, C, H, W))
+    col = oracle.im2col(x, Bn, C, H, W, 3, 3, stride=1, pad=1)  # K order (kh, kw, ic)
+    w = uniform(rng, (OC, 9 * C))  # weights generated directly in the col K order
+    M, K = col.shape
+    announce("C5 conv NT 100352x128x576")
+    c = run_gemm(ctx, "nt", col, w, M, OC, K)
+    rows = np.sort(rng.choice(M, 512, replace=False))
+    col_s = np.ascontiguousarray(col[rows])
+    assert_close(c[rows], oracle.matmul_nt(col_s, w, len(rows), OC, K, threads=THREADS), "nt", col_s, w, len(rows),
+                 OC, K, what="conv sampled rows")
+    checksum_property(c, col, w.T, K, "conv")

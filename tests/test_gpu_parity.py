@@ -1,0 +1,307 @@
+"""GPU parity: the HIP path against the oracle and the committed fixtures.
+
+Bar: bit-exact where the reference's own known answers are exact (integer
+inputs), otherwise max componentwise relative error <= 1e-5 * sqrt(K) in
+fp64 (tests/_parity.py).  Every call goes through the C ABI.
+"""
+from __future__ import annotations
+
+import os
+import zlib
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from _parity import uniform, normal, tol
+from gpu_common import announce, assert_close, ref_gemm, run_gemm, stored_shapes
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from zigneuron_amd import Context
+    c = Context(0)
+    assert c.arch.startswith("gfx950"), c.arch
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def backend(ctx):
+    from zigneuron_amd import Backend
+    return Backend(ctx)
+
+
+@pytest.fixture(scope="module")
+def kats():
+    return np.load(os.path.join(GOLDEN, "reference_kats.npz"))
+
+
+# ------------------------------------------------- reference known answers
+def test_kat_matmul_correctness(backend, kats):
+    announce("kat correctness 2x2x3")
+    m, n, k = (int(x) for x in kats["correctness_mnk"])
+    c = np.zeros(m * n, np.float32)
+    backend.matMul(kats["correctness_a"], kats["correctness_b"], c, m, n, k, False)
+    np.testing.assert_array_equal(c, kats["correctness_c"])
+
+
+def test_kat_matmul_large_ones(backend, kats):
+    announce("kat ones 64^3")
+    ones = np.ones(64 * 64, np.float32)
+    c = np.zeros(64 * 64, np.float32)
+    backend.matMul(ones, ones, c, 64, 64, 64, False)
+    np.testing.assert_array_equal(c, kats["ones64_c"])
+
+
+def test_kat_matmul_cpu_small(backend, kats):
+    announce("kat cpu small")
+    m, n, k = (int(x) for x in kats["cpu_small_mnk"])
+    c = np.zeros(m * n, np.float32)
+    backend.matMul(kats["cpu_small_a"], kats["cpu_small_b"], c, m, n, k, False)
+    assert abs(float(c[0]) - float(kats["cpu_small_c0"][0])) < 1e-4  # the reference test's tolerance
+
+
+@pytest.mark.parametrize("tag", ["small64", "medium256", "nonsquare", "accum64"])
+def test_kat_integer_matmuls_bit_exact(backend, kats, tag):
+    """Integer inputs keep every product and partial sum exact: all layouts must match exactly."""
+    m, n, k = (int(x) for x in kats[f"{tag}_mnk"])
+    a, b = kats[f"{tag}_a"].reshape(m, k), kats[f"{tag}_b"].reshape(k, n)
+    want = kats[f"{tag}_c"]
+    announce(f"kat integer {tag}")
+    c = np.zeros(m * n, np.float32)
+    backend.matMul(a, b, c, m, n, k, False)
+    if tag == "accum64":
+        backend.matMul(a, b, c, m, n, k, True)
+        np.testing.assert_array_equal(c, 2 * want)
+        return
+    np.testing.assert_array_equal(c, want)
+    c[:] = np.nan
+    backend.matMulTransposeA(a.T.copy(), b, c, m, n, k, False)
+    np.testing.assert_array_equal(c, want)
+    c[:] = np.nan
+    backend.matMulTransposeB(a, b.T.copy(), c, m, n, k, False)
+    np.testing.assert_array_equal(c, want)
+
+
+def test_kat_dense_layer(backend, kats):
+    """src/test/unit/layer.zig:16-55,169-241 through the Dense mirror."""
+    from zigneuron_amd import Dense
+    announce("kat dense layer")
+    for act, row in zip(kats["dense_fwd_act"], kats["dense_fwd"]):
+        w0, w1, bias, x0, x1, want = (float(v) for v in row)
+        lyr = Dense(backend, 2, 1, str(act))
+        lyr.weights[:] = [w0, w1]
+        lyr.bias[:] = [bias]
+        out = np.zeros(1, np.float32)
+        lyr.forward(np.float32([x0, x1]), out)
+        assert abs(float(out[0]) - want) <= 1e-4, (act, row)
+    for act, row in zip(kats["dense_bwd_act"], kats["dense_bwd"]):
+        w0, w1, x0, x1, yv, g0, g1 = (float(v) for v in row)
+        lyr = Dense(backend, 2, 1, str(act))
+        lyr.weights[:] = [w0, w1]
+        gi = np.zeros(2, np.float32)
+        lyr.backward(np.float32([x0, x1]), np.float32([1.0]), gi, np.float32([yv]))
+        np.testing.assert_allclose(gi, [g0, g1], atol=1e-4)
+
+
+def test_kat_activations(backend, kats):
+    announce("kat activations")
+    x = kats["act_relu_x"]
+    y = np.empty_like(x)
+    backend.activationForward("relu", x, y)
+    np.testing.assert_array_equal(y, kats["act_relu_y"])
+    xs = kats["act_sigmoid_x"]
+    s = np.empty_like(xs)
+    backend.activationForward("sigmoid", xs, s)
+    assert np.all((s >= 0) & (s <= 1)) and abs(float(s[2]) - 0.5) <= 1e-4
+    g = np.empty_like(s)
+    backend.activationBackward("sigmoid", s, np.ones_like(s), g)
+    np.testing.assert_allclose(g, s * (1 - s), atol=1e-4)
+
+
+# ---------------------------------------------------- committed fixtures
+def test_committed_oracle_cases(ctx):
+    z = np.load(os.path.join(GOLDEN, "oracle_cases.npz"))
+    for name in z["names"]:
+        layout, m, n, k, acc, act = (str(v) for v in z[f"{name}_meta"])
+        m, n, k, acc = int(m), int(n), int(k), bool(int(acc))
+        a, b, bias, c0, want = (z[f"{name}_{s}"] for s in ("a", "b", "bias", "c0", "c"))
+        announce(f"fixture {name}")
+        if act != "none":
+            c = run_gemm(ctx, layout, a, b, m, n, k, bias=bias, act=act)
+            assert_close(c, want, layout, a, b, m, n, k, bias=bias, act=act, what=str(name))
+        else:
+            c = run_gemm(ctx, layout, a, b, m, n, k, c0=c0 if acc else None, accumulate=acc)
+            assert_close(c, want, layout, a, b, m, n, k, c0=c0, accumulate=acc, what=str(name))
+
+
+# ------------------------------------------------------- seeded shapes
+SHAPES = [(1, 1, 1), (1, 9, 13), (5, 7, 3), (31, 33, 17), (37, 45, 29), (64, 64, 64), (96, 80, 72),
+          (127, 129, 130), (200, 300, 100), (257, 255, 33), (300, 520, 260), (129, 1030, 16)]
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_layouts_against_oracle(ctx, layout, m, n, k):
+    rng = np.random.default_rng(zlib.crc32(f"{layout}-{m}-{n}-{k}".encode()))
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    announce(f"{layout} {m}x{n}x{k}")
+    c = run_gemm(ctx, layout, a, b, m, n, k)
+    assert_close(c, ref_gemm(layout, a, b, m, n, k), layout, a, b, m, n, k)
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+@pytest.mark.parametrize("m,n,k", [(33, 47, 29), (130, 260, 70)])
+def test_accumulate_against_oracle(ctx, layout, m, n, k):
+    rng = np.random.default_rng(17)
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b, c0 = uniform(rng, a_shape), uniform(rng, b_shape), uniform(rng, (m, n))
+    announce(f"accumulate {layout} {m}x{n}x{k}")
+    c = run_gemm(ctx, layout, a, b, m, n, k, c0=c0, accumulate=True)
+    ref = ref_gemm(layout, a, b, m, n, k, c0=c0, accumulate=True)
+    assert_close(c, ref, layout, a, b, m, n, k, c0=c0, accumulate=True)
+
+
+def test_k_zero_and_empty(ctx):
+    announce("k=0 and empty shapes")
+    rng = np.random.default_rng(2)
+    bias = uniform(rng, (5,))
+    c = run_gemm(ctx, "nn", np.zeros(0, np.float32), np.zeros(0, np.float32), 3, 5, 0, bias=bias, act="relu")
+    np.testing.assert_array_equal(c, np.broadcast_to(np.maximum(bias, 0), (3, 5)))
+    c0 = uniform(rng, (3, 5))
+    c = run_gemm(ctx, "nt", np.zeros(0, np.float32), np.zeros(0, np.float32), 3, 5, 0, c0=c0, accumulate=True)
+    np.testing.assert_array_equal(c, c0)
+    ctx.sgemm("nn", 0, 5, 7, None, 7, None, 5, None, 5)  # m == 0: no-op, no launch
+
+
+# ---------------------------------------------------------- epilogues
+@pytest.mark.parametrize("act", ["linear", "relu", "sigmoid", "tanh"])
+@pytest.mark.parametrize("m,n,k", [(256, 128, 784), (256, 10, 128), (45, 33, 70), (300, 257, 129)])
+def test_fused_epilogues(ctx, act, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    a, b, bias = uniform(rng, (m, k)), uniform(rng, (k, n)), uniform(rng, (n,))
+    announce(f"epilogue {act} {m}x{n}x{k}")
+    c = run_gemm(ctx, "nn", a, b, m, n, k, bias=bias, act=act)
+    ref = ref_gemm("nn", a, b, m, n, k, bias=bias, act=act)
+    assert_close(c, ref, "nn", a, b, m, n, k, bias=bias, act=act)
+
+
+@pytest.mark.parametrize("name", ["matMulBias", "matMulBiasRelu", "matMulBiasSigmoid", "matMulBiasTanh"])
+def test_backend_bias_methods(backend, name):
+    act = {"matMulBias": "linear", "matMulBiasRelu": "relu", "matMulBiasSigmoid": "sigmoid",
+           "matMulBiasTanh": "tanh"}[name]
+    rng = np.random.default_rng(4)
+    m, n, k = 64, 50, 90
+    a, b, bias = uniform(rng, (m, k)), uniform(rng, (k, n)), uniform(rng, (n,))
+    c = np.zeros(m * n, np.float32)
+    announce(f"Backend.{name}")
+    getattr(backend, name)(a, b, bias, c, m, n, k)
+    ref = oracle.matmul_bias_act(a, b, bias, m, n, k, act)
+    assert_close(c.reshape(m, n), ref, "nn", a, b, m, n, k, bias=bias, act=act)
+
+
+def test_backend_elementwise_helpers(backend):
+    rng = np.random.default_rng(12)
+    out, bias = uniform(rng, (13, 37)), uniform(rng, (37,))
+    announce("addBias / activation / accumulateBias")
+    o = out.ravel().copy()
+    backend.addBias(o, bias)
+    np.testing.assert_array_equal(o, oracle.add_bias(out, bias).ravel())
+    x = np.linspace(-12, 12, 3001).astype(np.float32)
+    for act in ("linear", "relu", "sigmoid", "tanh"):
+        y = np.empty_like(x)
+        backend.activationForward(act, x, y)
+        ref = oracle.activation_forward(act, x)
+        assert np.all(np.abs(y - ref) <= 2 * np.spacing(np.abs(ref)) + 1e-45), act
+        g = uniform(rng, x.shape)
+        gi = np.empty_like(x)
+        backend.activationBackward(act, ref, g, gi)
+        np.testing.assert_array_equal(gi, oracle.activation_backward(act, ref, g))
+    gb0 = uniform(rng, (37,))
+    gb = gb0.copy()
+    backend.accumulateBias(gb, out.ravel())
+    np.testing.assert_array_equal(gb, oracle.accumulate_bias(gb0, out))  # same row order: bit-exact
+
+
+# ------------------------------------------------------ strided batched
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+def test_strided_batched_against_oracle(ctx, layout):
+    rng = np.random.default_rng(31)
+    batch, m, n, k = 6, 70, 40, 33
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a = uniform(rng, (batch,) + a_shape)
+    b = uniform(rng, (batch,) + b_shape)
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    dc = ctx.alloc(batch * m * n).fill(np.nan)
+    announce(f"strided batched {layout}")
+    ctx.sgemm_strided_batched(layout, m, n, k, da, lda, m * k, db, ldb, k * n, dc, n, m * n, batch)
+    c = dc.download().reshape(batch, m, n)
+    for i in range(batch):
+        assert_close(c[i], ref_gemm(layout, a[i], b[i], m, n, k), layout, a[i], b[i], m, n, k, what=f"batch {i}")
+    # stride 0 shares B across the batch (CudaBackend.matMulBatch's shared B)
+    ctx.sgemm_strided_batched(layout, m, n, k, da, lda, m * k, db, ldb, 0, dc, n, m * n, batch)
+    c = dc.download().reshape(batch, m, n)
+    for i in range(batch):
+        assert_close(c[i], ref_gemm(layout, a[i], b[0], m, n, k), layout, a[i], b[0], m, n, k, what=f"shared B {i}")
+    for buf in (da, db, dc):
+        buf.close()
+
+
+# ------------------------------------------- unaligned pointers / leading dims
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+def test_padded_and_unaligned_operands(ctx, layout):
+    """Leading dims larger than the row and 4-byte-offset base pointers take the scalar-load path."""
+    rng = np.random.default_rng(5)
+    m, n, k = 150, 90, 70
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    lda, ldb, ldc = a_shape[1] + 3, b_shape[1] + 5, n + 7
+    a_full = uniform(rng, (a_shape[0], lda))
+    b_full = uniform(rng, (b_shape[0], ldb))
+    da, db = ctx.to_device(np.concatenate([[0.0], a_full.ravel()])), ctx.to_device(b_full)
+    dc = ctx.alloc(1 + m * ldc).fill(-7.0)
+    announce(f"padded/unaligned {layout}")
+    ctx.sgemm(layout, m, n, k, da.offset(1), lda, db, ldb, dc.offset(1), ldc)
+    c_full = dc.download()[1:].reshape(m, ldc)
+    a = np.ascontiguousarray(a_full[:, :a_shape[1]])
+    b = np.ascontiguousarray(b_full[:, :b_shape[1]])
+    assert_close(c_full[:, :n], ref_gemm(layout, a, b, m, n, k), layout, a, b, m, n, k)
+    assert np.all(c_full[:, n:] == -7.0), "wrote outside the n columns of a padded C row"
+    for buf in (da, db, dc):
+        buf.close()
+
+
+# ----------------------------------------------------------- determinism
+def test_deterministic_bitwise(ctx):
+    rng = np.random.default_rng(9)
+    m, n, k = 300, 260, 500
+    a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+    announce("determinism")
+    c1 = run_gemm(ctx, "nn", a, b, m, n, k)
+    c2 = run_gemm(ctx, "nn", a, b, m, n, k)
+    np.testing.assert_array_equal(c1, c2)
+
+
+# ------------------------------------------------------- argument errors
+def test_invalid_arguments_are_errors(ctx, backend):
+    from zigneuron_amd import InvalidArgumentError
+    announce("argument errors")
+    d = ctx.alloc(64)
+    with pytest.raises(InvalidArgumentError):
+        ctx.sgemm(7, 4, 4, 4, d, 4, d, 4, d, 4)  # bad layout
+    with pytest.raises(InvalidArgumentError):
+        ctx.sgemm("nn", 4, 4, 4, d, 3, d, 4, d, 4)  # lda < k
+    with pytest.raises(InvalidArgumentError):
+        ctx.sgemm("nn", 4, 4, 4, d, 4, d, 4, d, 4, act=9)
+    with pytest.raises(InvalidArgumentError):
+        backend.matMul(np.zeros(3, np.float32), np.zeros(4, np.float32), np.zeros(4, np.float32), 2, 2, 2)
+    with pytest.raises(InvalidArgumentError):
+        backend.activationBackward("relu", np.zeros(3, np.float32), np.zeros(4, np.float32),
+                                   np.zeros(3, np.float32))
+    d.close()

@@ -1,0 +1,12 @@
+"""zigneuron_amd -- MI355X (gfx950) fp32 GEMM backend for ZigNeuron.
+
+The product is the C-ABI library ``lib/libzn_hip.so`` (include/zn_hip.h) and
+its offline-built gfx950 code objects; this package is the host-side mirror
+of the reference ``Backend``/``Dense`` interfaces over that ABI.
+"""
+from ._lib import ZnError, NoDeviceError, CodeObjectError, InvalidArgumentError  # noqa: F401
+from .backend import Backend, Context, DeviceBuffer, available  # noqa: F401
+from .layer import Dense, DenseDevice  # noqa: F401
+
+__all__ = ["Backend", "Context", "DeviceBuffer", "Dense", "DenseDevice", "available", "ZnError",
+           "NoDeviceError", "CodeObjectError", "InvalidArgumentError"]

@@ -1,0 +1,303 @@
+// fp32 GEMM for gfx950 (CDNA4) on the fp32 matrix cores.
+//
+// One MFMA core serves the three layouts of ZigNeuron's Backend.matMul family
+// (NN: src/backend.zig:169, TN: :298, NT: :310), the fused bias+activation
+// epilogues (:200-295) and a strided-batched grid (blockIdx.y = problem).
+//
+// Structure of one workgroup (BM x BN macro tile, WM x WN waves):
+//  * Global -> registers -> LDS staging, double buffered, one barrier per
+//    BK slice.  Each operand keeps its global layout in LDS: a K-contiguous
+//    operand (A of NN/NT, B of NT) is stored [x][BK+4], an X-contiguous one
+//    (A of TN, B of NN/TN) [BK][X].  No transposing LDS writes are needed;
+//    the layout only changes how lanes read fragments.
+//  * v_mfma_f32_32x32x2f32: a 32x32 fp32 block per instruction, K = 2 split
+//    over the two lane halves.  The K order inside a group of 8 is permuted
+//    so that lane half h, step t covers k = 8g + 4h + t; a K-contiguous
+//    fragment is then one 16-byte LDS read per block.
+//  * For an X-contiguous operand the 32 lanes of a block own FX consecutive
+//    tile rows/cols (row = FX*i + f), so their fragment is one FX-wide LDS
+//    read and, for B, their output columns are FX-wide vector stores.
+//  * Edges (ragged M, N, K) are zero-filled in LDS; zero products leave the
+//    sums unchanged, and stores are predicated.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../zn_kernel_args.h"
+
+typedef float zn_f32x16 __attribute__((ext_vector_type(16)));
+typedef float zn_f32x4 __attribute__((ext_vector_type(4)));
+typedef float zn_f32x2 __attribute__((ext_vector_type(2)));
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kKPad = 4;  // floats of padding per K-contiguous LDS row (conflict-free 16-byte reads)
+
+template <int N> struct FVec;
+template <> struct FVec<1> { typedef float type; };
+template <> struct FVec<2> { typedef zn_f32x2 type; };
+template <> struct FVec<4> { typedef zn_f32x4 type; };
+
+__device__ __forceinline__ float zn_activate(float v, int act) {
+    switch (act) {
+    case 1: return v > 0.0f ? v : 0.0f;               // relu   (src/backend.zig:239-240)
+    case 2: return 1.0f / (1.0f + expf(-v));          // sigmoid (src/backend.zig:264-265)
+    case 3: return tanhf(v);                          // tanh   (src/backend.zig:289-290)
+    default: return v;
+    }
+}
+
+// One operand's BX x BK slice: global -> registers -> LDS.
+//   KC: element (x, k) at g[x*ld + k]; LDS row x, stride BK + kKPad.
+//  !KC: element (x, k) at g[k*ld + x]; LDS row k, stride BX.
+template <int BX, int BK, int NT, bool KC>
+struct Stage {
+    static constexpr int kChunksPerRow = KC ? BK / 4 : BX / 4;  // float4 chunks along the contiguous dim
+    static constexpr int kLoads = (BX * BK / 4) / NT;            // chunks per thread
+    static constexpr int kRowsPerPass = NT / kChunksPerRow;
+    static constexpr int kLdsStride = KC ? BK + kKPad : BX;
+    static constexpr int kLdsFloats = KC ? BX * (BK + kKPad) : BK * BX;
+    static_assert((BX * BK / 4) % NT == 0, "tile must split evenly over threads");
+    static_assert(NT % kChunksPerRow == 0, "rows per pass must be whole");
+
+    zn_f32x4 r[kLoads];
+
+    // Fetch slice k0 of the tile starting at x0.  `xmax`/`kmax` bound the
+    // problem; `vec` allows 16-byte loads (aligned rows).
+    __device__ __forceinline__ void load(const float *__restrict__ g, int64_t ld, int x0, int k0, int xmax, int kmax,
+                                         bool vec, int tid) {
+        const int row0 = tid / kChunksPerRow;
+        const int col = (tid % kChunksPerRow) * 4;
+        const bool interior = x0 + BX <= xmax && k0 + BK <= kmax;
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int row = row0 + j * kRowsPerPass;
+            // (outer, inner) coordinates in the problem: KC -> (x, k), !KC -> (k, x)
+            const int outer = (KC ? x0 : k0) + row;
+            const int inner = (KC ? k0 : x0) + col;
+            const int outer_max = KC ? xmax : kmax;
+            const int inner_max = KC ? kmax : xmax;
+            const float *src = g + (int64_t)outer * ld + inner;
+            if (interior && vec) {
+                r[j] = *reinterpret_cast<const zn_f32x4 *>(src);
+            } else if (interior) {
+                r[j] = zn_f32x4{src[0], src[1], src[2], src[3]};
+            } else {
+                zn_f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (outer < outer_max) {
+                    if (inner + 0 < inner_max) v[0] = src[0];
+                    if (inner + 1 < inner_max) v[1] = src[1];
+                    if (inner + 2 < inner_max) v[2] = src[2];
+                    if (inner + 3 < inner_max) v[3] = src[3];
+                }
+                r[j] = v;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(float *lds, int tid) const {
+        const int row0 = tid / kChunksPerRow;
+        const int col = (tid % kChunksPerRow) * 4;
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int row = row0 + j * kRowsPerPass;
+            *reinterpret_cast<zn_f32x4 *>(lds + row * kLdsStride + col) = r[j];
+        }
+    }
+};
+
+// Fragments for the four MFMA steps of one K group of 8:
+// frag[f][t] = operand value of lane (i = lane % 32, h = lane / 32) for block
+// f at k = kg + 4h + t.
+template <int BX, int BK, int FX, bool KC>
+__device__ __forceinline__ void read_frags(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
+    const int i = lane & 31;
+    const int h = lane >> 5;
+    if constexpr (KC) {
+        // LDS [BX][BK + pad]: block f covers rows w0 + 32 f + i; one 16-byte read each.
+#pragma unroll
+        for (int f = 0; f < FX; ++f) {
+            const zn_f32x4 v =
+                *reinterpret_cast<const zn_f32x4 *>(lds + (w0 + 32 * f + i) * (BK + kKPad) + kg + 4 * h);
+            frag[f][0] = v[0];
+            frag[f][1] = v[1];
+            frag[f][2] = v[2];
+            frag[f][3] = v[3];
+        }
+    } else {
+        // LDS [BK][BX]: lane i owns rows w0 + FX*i + f, f < FX; one FX-wide read per step.
+        typedef typename FVec<FX>::type VT;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const VT v = *reinterpret_cast<const VT *>(lds + (kg + 4 * h + t) * BX + w0 + FX * i);
+            if constexpr (FX == 1) {
+                frag[0][t] = v;
+            } else {
+#pragma unroll
+                for (int f = 0; f < FX; ++f) frag[f][t] = v[f];
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
+__device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
+    constexpr int NT = WM * WN * kWave;
+    constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+    constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 blocks per wave
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+    static_assert(BK % 8 == 0, "BK must be a multiple of the K group");
+    static_assert(FM == 1 || FM == 2 || FM == 4, "FM");
+    static_assert(FN == 1 || FN == 2 || FN == 4, "FN");
+    typedef Stage<BM, BK, NT, AK> StageA;
+    typedef Stage<BN, BK, NT, BKC> StageB;
+
+    __shared__ __attribute__((aligned(16))) float lds_a[2][StageA::kLdsFloats];
+    __shared__ __attribute__((aligned(16))) float lds_b[2][StageB::kLdsFloats];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int wm0 = (wave / WN) * WTM;
+    const int wn0 = (wave % WN) * WTN;
+
+    // ---- tile raster: XCD-contiguous ranges, then GROUP_M-row groups
+    int pid = blockIdx.x;
+    const int ntiles = p.tiles_m * p.tiles_n;
+    if (p.xcd_remap) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+    const int group_span = p.group_m * p.tiles_n;
+    const int first_m = (pid / group_span) * p.group_m;
+    const int gsize = min(p.tiles_m - first_m, p.group_m);
+    const int in_group = pid % group_span;
+    const int tm = first_m + in_group % gsize;
+    const int tn = in_group / gsize;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int64_t bz = blockIdx.y;
+    const float *__restrict__ ga = p.a + bz * p.stride_a;
+    const float *__restrict__ gb = p.b + bz * p.stride_b;
+    float *__restrict__ gc = p.c + bz * p.stride_c;
+
+    zn_f32x16 acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+    StageA sa;
+    StageB sb;
+    const int ktiles = (p.k + BK - 1) / BK;
+    const bool va = p.vec_a != 0, vb = p.vec_b != 0;
+
+    if (ktiles > 0) {
+        sa.load(ga, p.lda, m0, 0, p.m, p.k, va, tid);
+        sb.load(gb, p.ldb, n0, 0, p.n, p.k, vb, tid);
+        sa.store(lds_a[0], tid);
+        sb.store(lds_b[0], tid);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < ktiles;
+        if (more) {
+            sa.load(ga, p.lda, m0, (kt + 1) * BK, p.m, p.k, va, tid);
+            sb.load(gb, p.ldb, n0, (kt + 1) * BK, p.n, p.k, vb, tid);
+        }
+        const float *la = lds_a[cur];
+        const float *lb = lds_b[cur];
+#pragma unroll
+        for (int kg = 0; kg < BK; kg += 8) {
+            float fa[FM][4], fb[FN][4];
+            read_frags<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
+            read_frags<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
+        }
+        if (more) {
+            sa.store(lds_a[cur ^ 1], tid);
+            sb.store(lds_b[cur ^ 1], tid);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: v = acc (+ C) (+ bias[col]) -> act -> store
+    // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
+    // holds block row 8*(r/4) + 4*h + r%4, block column j.
+    const int j = lane & 31;
+    const int h = lane >> 5;
+    const bool has_bias = p.bias != nullptr;
+    float bias_v[FN];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+        const int col = n0 + wn0 + (BKC ? 32 * fn + j : FN * j + fn);
+        bias_v[fn] = (has_bias && col < p.n) ? p.bias[col] : 0.0f;
+    }
+    const bool vec_store = !BKC && FN > 1 && p.vec_c && (n0 + wn0 + FN * j + FN <= p.n);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
+            const int row = m0 + wm0 + (AK ? 32 * fm + bi : FM * bi + fm);
+            if (row >= p.m) continue;
+            float *crow = gc + (int64_t)row * p.ldc;
+            if constexpr (!BKC && FN > 1) {
+                if (vec_store) {
+                    typedef typename FVec<FN>::type VT;
+                    VT *dst = reinterpret_cast<VT *>(crow + n0 + wn0 + FN * j);
+                    VT v;
+                    if (p.accumulate) v = *dst;
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn) {
+                        float x = acc[fm][fn][r];
+                        if (p.accumulate) x = v[fn] + x;
+                        if (has_bias) x = x + bias_v[fn];
+                        v[fn] = zn_activate(x, p.act);
+                    }
+                    *dst = v;
+                    continue;
+                }
+            }
+            {
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    const int col = n0 + wn0 + (BKC ? 32 * fn + j : FN * j + fn);
+                    if (col >= p.n) continue;
+                    float x = acc[fm][fn][r];
+                    if (p.accumulate) x = crow[col] + x;
+                    if (has_bias) x = x + bias_v[fn];
+                    crow[col] = zn_activate(x, p.act);
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+// Exported kernels: zn_sgemm_<layout>_<tile>.  Layout letters follow the
+// reference: nn = Backend.matMul, nt = matMulTransposeB, tn = matMulTransposeA.
+// Tiles: l = 128x128 (4 waves of 64x64), m = 64x64 (4 waves of 32x32),
+// s = 32x32 (1 wave) for small problems.
+#define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC)                                       \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64) void NAME(ZnGemmArgs p) {              \
+        gemm_tile<BM, BN, BK, WM, WN, AK, BKC>(p);                                               \
+    }
+
+ZN_GEMM_KERNEL(zn_sgemm_nn_l, 128, 128, 16, 2, 2, true, false)
+ZN_GEMM_KERNEL(zn_sgemm_nt_l, 128, 128, 16, 2, 2, true, true)
+ZN_GEMM_KERNEL(zn_sgemm_tn_l, 128, 128, 16, 2, 2, false, false)
+ZN_GEMM_KERNEL(zn_sgemm_nn_m, 64, 64, 16, 2, 2, true, false)
+ZN_GEMM_KERNEL(zn_sgemm_nt_m, 64, 64, 16, 2, 2, true, true)
+ZN_GEMM_KERNEL(zn_sgemm_tn_m, 64, 64, 16, 2, 2, false, false)
+ZN_GEMM_KERNEL(zn_sgemm_nn_s, 32, 32, 16, 1, 1, true, false)
+ZN_GEMM_KERNEL(zn_sgemm_nt_s, 32, 32, 16, 1, 1, true, true)
+ZN_GEMM_KERNEL(zn_sgemm_tn_s, 32, 32, 16, 1, 1, false, false)

@@ -1,0 +1,707 @@
+// zn_hip.cpp -- host runtime of the MI355X fp32 GEMM backend (C ABI in
+// include/zn_hip.h).
+//
+// Replaces, for the GEMM path, the reference's CUDA driver binding, NVRTC
+// and device context (src/cuda_driver.zig, src/cuda_nvrtc.zig,
+// src/cuda_context.zig) and the CudaBackend GEMM wrappers (src/cuda.zig).
+// Design:
+//  * one context = one device + one HIP stream + the two offline-built gfx950
+//    code objects (zn_gemm_gfx950.hsaco, zn_elementwise_gfx950.hsaco) loaded
+//    with hipModuleLoad; no runtime compilation, no CPU fallback;
+//  * a size-bucketed device-buffer cache for the host-slice entry points
+//    (the role of the pow2 pool in src/cuda_context.zig:773-852);
+//  * the launch policy (tile choice, raster, vector-load eligibility) lives
+//    here, so it is testable without touching device code.
+#include <hip/hip_runtime.h>
+
+#include <dlfcn.h>
+#include <sys/stat.h>
+
+#include <climits>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../../include/zn_hip.h"
+#include "../zn_kernel_args.h"
+
+namespace {
+
+enum Tile { kTileL = 0, kTileM = 1, kTileS = 2, kNumTiles = 3 };
+struct TileShape {
+    int bm, bn, threads;
+    const char *suffix;
+};
+constexpr TileShape kTiles[kNumTiles] = {{128, 128, 256, "l"}, {64, 64, 256, "m"}, {32, 32, 64, "s"}};
+constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
+
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kNumElt };
+constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",           "zn_copy_f32",
+                                           "zn_add_bias",           "zn_activation_forward",
+                                           "zn_activation_backward", "zn_accumulate_bias"};
+
+constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
+constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
+
+}  // namespace
+
+struct zn_ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    hipModule_t gemm_module = nullptr;
+    hipModule_t elt_module = nullptr;
+    hipFunction_t gemm[3][kNumTiles] = {};
+    hipFunction_t elt[kNumElt] = {};
+    int last_hip_error = 0;
+    zn_device_info info = {};
+    // Cached device buffers for the host-slice entry points, keyed by
+    // power-of-two byte size.
+    std::map<size_t, std::vector<void *>> pool;
+};
+
+struct zn_event {
+    hipEvent_t ev = nullptr;
+};
+
+namespace {
+
+int fail_hip(zn_ctx *ctx, hipError_t e, int status = ZN_ERR_HIP) {
+    if (ctx) ctx->last_hip_error = (int)e;
+    return status;
+}
+
+#define ZN_HIP_TRY(ctx, expr)                          \
+    do {                                               \
+        hipError_t zn_e_ = (expr);                     \
+        if (zn_e_ != hipSuccess) return fail_hip((ctx), zn_e_); \
+    } while (0)
+
+bool mul_ok(size_t a, size_t b, size_t *out) {
+    if (a != 0 && b > SIZE_MAX / a) return false;
+    *out = a * b;
+    return true;
+}
+
+bool file_exists(const std::string &path) {
+    struct stat st;
+    return stat(path.c_str(), &st) == 0 && S_ISREG(st.st_mode);
+}
+
+// Directory holding this shared library (the default code-object location).
+std::string library_dir() {
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void *>(&zn_hip_abi_version), &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        const size_t slash = p.find_last_of('/');
+        if (slash != std::string::npos) return p.substr(0, slash);
+    }
+    return ".";
+}
+
+int select_device(zn_ctx *ctx) {
+    ZN_HIP_TRY(ctx, hipSetDevice(ctx->device));
+    return ZN_OK;
+}
+
+size_t bucket_of(size_t bytes) {
+    size_t b = 256;
+    while (b < bytes) b <<= 1;
+    return b;
+}
+
+int pool_get(zn_ctx *ctx, size_t bytes, float **out) {
+    const size_t b = bucket_of(bytes ? bytes : 4);
+    auto &list = ctx->pool[b];
+    if (!list.empty()) {
+        *out = static_cast<float *>(list.back());
+        list.pop_back();
+        return ZN_OK;
+    }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, b);
+    if (e != hipSuccess) {
+        // release cached buffers and retry once
+        (void)hipGetLastError();
+        for (auto &kv : ctx->pool)
+            for (void *q : kv.second) (void)hipFree(q);
+        ctx->pool.clear();
+        e = hipMalloc(&p, b);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail_hip(ctx, e, ZN_ERR_OOM);
+        }
+    }
+    *out = static_cast<float *>(p);
+    return ZN_OK;
+}
+
+void pool_put(zn_ctx *ctx, float *p, size_t bytes) {
+    if (p) ctx->pool[bucket_of(bytes ? bytes : 4)].push_back(p);
+}
+
+// RAII lease of pooled staging buffers (returned to the cache on scope exit).
+struct Lease {
+    zn_ctx *ctx;
+    float *ptr = nullptr;
+    size_t bytes = 0;
+    explicit Lease(zn_ctx *c) : ctx(c) {}
+    int get(size_t n_floats) {
+        bytes = n_floats * sizeof(float);
+        return pool_get(ctx, bytes, &ptr);
+    }
+    ~Lease() { pool_put(ctx, ptr, bytes); }
+};
+
+// Every kernel takes one argument block by value; the runtime copies it into
+// the kernarg segment using the kernel's own metadata.
+int launch(zn_ctx *ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned threads, void *args) {
+    void *params[] = {args};
+    hipError_t e = hipModuleLaunchKernel(f, gx, gy, 1, threads, 1, 1, 0, ctx->stream, params, nullptr);
+    if (e != hipSuccess) return fail_hip(ctx, e, ZN_ERR_LAUNCH);
+    return ZN_OK;
+}
+
+// ------------------------------------------------------------ GEMM policy
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Largest tile that still gives enough workgroups to occupy the chip.
+Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t batch) {
+    const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+    const int64_t l = cdiv(m, 128) * cdiv(n, 128) * batch;
+    if (l >= cus) return kTileL;
+    const int64_t md = cdiv(m, 64) * cdiv(n, 64) * batch;
+    if (md >= cus / 2) return kTileM;
+    return kTileS;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
+                int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
+                int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act) {
+    if (!ctx) return ZN_ERR_INVALID_ARG;
+    if (layout < ZN_LAYOUT_NN || layout > ZN_LAYOUT_TN) return ZN_ERR_INVALID_ARG;
+    if (act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
+    if (m < 0 || n < 0 || k < 0 || batch < 0 || stride_a < 0 || stride_b < 0 || stride_c < 0)
+        return ZN_ERR_INVALID_ARG;
+    if (m > INT_MAX || n > INT_MAX || k > INT_MAX) return ZN_ERR_OVERFLOW;
+    if (m == 0 || n == 0 || batch == 0) return ZN_OK;
+    if (!c || (k > 0 && (!a || !b))) return ZN_ERR_INVALID_ARG;
+    // stored row lengths: A is [m x k] (nn, nt) or [k x m] (tn); B is [k x n] (nn, tn) or [n x k] (nt)
+    const int64_t a_row = layout == ZN_LAYOUT_TN ? m : k;
+    const int64_t b_row = layout == ZN_LAYOUT_NT ? k : n;
+    if (k > 0 && (lda < a_row || ldb < b_row || lda < 1 || ldb < 1)) return ZN_ERR_INVALID_ARG;
+    if (ldc < n) return ZN_ERR_INVALID_ARG;
+
+    const Tile tile = choose_tile(ctx, m, n, batch);
+    const TileShape &ts = kTiles[tile];
+    const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
+    if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
+
+    ZnGemmArgs args;
+    std::memset(&args, 0, sizeof(args));
+    args.a = a;
+    args.b = b;
+    args.c = c;
+    args.bias = bias;
+    args.lda = lda;
+    args.ldb = ldb;
+    args.ldc = ldc;
+    args.stride_a = stride_a;
+    args.stride_b = stride_b;
+    args.stride_c = stride_c;
+    args.m = (int32_t)m;
+    args.n = (int32_t)n;
+    args.k = (int32_t)k;
+    args.tiles_m = (int32_t)tiles_m;
+    args.tiles_n = (int32_t)tiles_n;
+    args.accumulate = accumulate ? 1 : 0;
+    args.act = act;
+    args.vec_a = aligned16(a) && lda % 4 == 0 && stride_a % 4 == 0;
+    args.vec_b = aligned16(b) && ldb % 4 == 0 && stride_b % 4 == 0;
+    args.vec_c = aligned16(c) && ldc % 4 == 0 && stride_c % 4 == 0;
+    args.group_m = 8;
+    const int64_t ntiles = tiles_m * tiles_n;
+    args.xcd_remap = (ntiles % 8 == 0) ? 1 : 0;
+
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    hipFunction_t f = ctx->gemm[layout][tile];
+    constexpr int64_t kMaxGridY = 65535;
+    for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
+        const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
+        ZnGemmArgs part = args;
+        part.a = a ? a + b0 * stride_a : nullptr;
+        part.b = b ? b + b0 * stride_b : nullptr;
+        part.c = c + b0 * stride_c;
+        rc = launch(ctx, f, (unsigned)ntiles, (unsigned)nb, (unsigned)ts.threads, &part);
+        if (rc) return rc;
+    }
+    return ZN_OK;
+}
+
+int elt_launch(zn_ctx *ctx, EltKernel kernel, int64_t work_items, const ZnEltArgs &args) {
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    const int64_t threads = 256;
+    int64_t blocks = cdiv(work_items, threads);
+    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+    if (blocks > cap) blocks = cap;  // grid-stride loops cover the rest
+    if (blocks < 1) blocks = 1;
+    ZnEltArgs a = args;
+    return launch(ctx, ctx->elt[kernel], (unsigned)blocks, 1, (unsigned)threads, &a);
+}
+
+int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n) {
+    if (n == 0) return ZN_OK;
+    ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    return ZN_OK;
+}
+
+int copy_out_and_wait(zn_ctx *ctx, float *dst, const float *src, size_t n) {
+    if (n) ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return ZN_OK;
+}
+
+// Host-slice GEMM: stage A, B (and C when accumulating), run, download C.
+int host_gemm(zn_ctx *ctx, int layout, const float *a, size_t a_len, const float *b, size_t b_len, const float *bias,
+              size_t bias_len, float *c, size_t c_len, size_t m, size_t n, size_t k, int accumulate, int act) {
+    if (!ctx) return ZN_ERR_INVALID_ARG;
+    size_t mk, kn, mn;
+    if (!mul_ok(m, k, &mk) || !mul_ok(k, n, &kn) || !mul_ok(m, n, &mn)) return ZN_ERR_OVERFLOW;
+    if (m > INT_MAX || n > INT_MAX || k > INT_MAX) return ZN_ERR_OVERFLOW;
+    if (a_len < mk || b_len < kn || c_len < mn) return ZN_ERR_INVALID_ARG;
+    if ((mk && !a) || (kn && !b) || (mn && !c)) return ZN_ERR_INVALID_ARG;
+    if (bias && bias_len < n) return ZN_ERR_INVALID_ARG;
+    if (mn == 0) return ZN_OK;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease da(ctx), db(ctx), dc(ctx), dbias(ctx);
+    if ((rc = da.get(mk)) || (rc = db.get(kn)) || (rc = dc.get(mn))) return rc;
+    if (bias && (rc = dbias.get(n))) return rc;
+    if ((rc = copy_in(ctx, da.ptr, a, mk)) || (rc = copy_in(ctx, db.ptr, b, kn))) return rc;
+    if (accumulate && (rc = copy_in(ctx, dc.ptr, c, mn))) return rc;
+    if (bias && (rc = copy_in(ctx, dbias.ptr, bias, n))) return rc;
+    const int64_t lda = layout == ZN_LAYOUT_TN ? (int64_t)m : (int64_t)k;
+    const int64_t ldb = layout == ZN_LAYOUT_NT ? (int64_t)k : (int64_t)n;
+    rc = gemm_launch(ctx, layout, (int64_t)m, (int64_t)n, (int64_t)k, da.ptr, lda > 0 ? lda : 1, 0, db.ptr,
+                     ldb > 0 ? ldb : 1, 0, dc.ptr, (int64_t)n, 0, 1, accumulate, bias ? dbias.ptr : nullptr, act);
+    if (rc) return rc;
+    return copy_out_and_wait(ctx, c, dc.ptr, mn);
+}
+
+}  // namespace
+
+// =================================================================== C ABI
+extern "C" {
+
+int zn_hip_abi_version(void) { return ZN_HIP_ABI_VERSION; }
+
+int zn_hip_available(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return count > 0 ? 1 : 0;
+}
+
+const char *zn_hip_status_string(int status) {
+    switch (status) {
+    case ZN_OK: return "ZN_OK";
+    case ZN_ERR_NO_DEVICE: return "ZN_ERR_NO_DEVICE: no usable gfx950 HIP device";
+    case ZN_ERR_CODE_OBJECT: return "ZN_ERR_CODE_OBJECT: gfx950 code object missing or not loadable";
+    case ZN_ERR_SYMBOL: return "ZN_ERR_SYMBOL: kernel symbol missing from the code object";
+    case ZN_ERR_INVALID_ARG: return "ZN_ERR_INVALID_ARG: invalid argument";
+    case ZN_ERR_OOM: return "ZN_ERR_OOM: device allocation failed";
+    case ZN_ERR_LAUNCH: return "ZN_ERR_LAUNCH: kernel launch failed";
+    case ZN_ERR_HIP: return "ZN_ERR_HIP: HIP runtime error";
+    case ZN_ERR_OVERFLOW: return "ZN_ERR_OVERFLOW: size overflow or beyond 32-bit index range";
+    default: return "ZN_ERR_UNKNOWN";
+    }
+}
+
+int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
+    if (!out) return ZN_ERR_INVALID_ARG;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        return ZN_ERR_NO_DEVICE;
+    }
+    if (device < 0 || device >= count) return ZN_ERR_INVALID_ARG;
+
+    std::string dir;
+    if (code_object_dir && *code_object_dir)
+        dir = code_object_dir;
+    else if (const char *env = std::getenv("ZN_HIP_CODE_OBJECT_DIR"))
+        dir = env;
+    else
+        dir = library_dir();
+    const std::string gemm_path = dir + "/" + kGemmObject;
+    const std::string elt_path = dir + "/" + kEltObject;
+
+    zn_ctx *ctx = new (std::nothrow) zn_ctx();
+    if (!ctx) return ZN_ERR_OOM;
+    ctx->device = device;
+    auto bail = [&](int rc) {
+        zn_hip_destroy(ctx);
+        return rc;
+    };
+
+    if (hipSetDevice(device) != hipSuccess) return bail(ZN_ERR_NO_DEVICE);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return bail(ZN_ERR_NO_DEVICE);
+    std::snprintf(ctx->info.name, sizeof(ctx->info.name), "%s", prop.gcnArchName);
+    ctx->info.compute_units = prop.multiProcessorCount;
+    ctx->info.clock_khz = prop.clockRate;
+    ctx->info.total_mem = (int64_t)prop.totalGlobalMem;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return bail(ZN_ERR_NO_DEVICE);
+
+    if (!file_exists(gemm_path) || !file_exists(elt_path)) return bail(ZN_ERR_CODE_OBJECT);
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return bail(fail_hip(ctx, e));
+    if (hipModuleLoad(&ctx->gemm_module, gemm_path.c_str()) != hipSuccess) {
+        ctx->gemm_module = nullptr;
+        return bail(ZN_ERR_CODE_OBJECT);
+    }
+    if (hipModuleLoad(&ctx->elt_module, elt_path.c_str()) != hipSuccess) {
+        ctx->elt_module = nullptr;
+        return bail(ZN_ERR_CODE_OBJECT);
+    }
+    for (int l = 0; l < 3; ++l)
+        for (int t = 0; t < kNumTiles; ++t) {
+            char name[64];
+            std::snprintf(name, sizeof(name), "zn_sgemm_%s_%s", kLayoutName[l], kTiles[t].suffix);
+            if (hipModuleGetFunction(&ctx->gemm[l][t], ctx->gemm_module, name) != hipSuccess)
+                return bail(ZN_ERR_SYMBOL);
+        }
+    for (int i = 0; i < kNumElt; ++i)
+        if (hipModuleGetFunction(&ctx->elt[i], ctx->elt_module, kEltName[i]) != hipSuccess) return bail(ZN_ERR_SYMBOL);
+    *out = ctx;
+    return ZN_OK;
+}
+
+int zn_hip_destroy(zn_ctx *ctx) {
+    if (!ctx) return ZN_OK;
+    if (ctx->device >= 0) (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto &kv : ctx->pool)
+        for (void *p : kv.second) (void)hipFree(p);
+    ctx->pool.clear();
+    if (ctx->gemm_module) (void)hipModuleUnload(ctx->gemm_module);
+    if (ctx->elt_module) (void)hipModuleUnload(ctx->elt_module);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    (void)hipGetLastError();
+    delete ctx;
+    return ZN_OK;
+}
+
+int zn_hip_last_hip_error(const zn_ctx *ctx) { return ctx ? ctx->last_hip_error : 0; }
+
+int zn_hip_device_info(const zn_ctx *ctx, zn_device_info *out) {
+    if (!ctx || !out) return ZN_ERR_INVALID_ARG;
+    *out = ctx->info;
+    return ZN_OK;
+}
+
+void *zn_hip_stream(const zn_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+// ----------------------------------------------------------------- memory
+int zn_hip_alloc(zn_ctx *ctx, size_t bytes, void **out) {
+    if (!ctx || !out) return ZN_ERR_INVALID_ARG;
+    *out = nullptr;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    hipError_t e = hipMalloc(out, bytes ? bytes : 4);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *out = nullptr;
+        return fail_hip(ctx, e, ZN_ERR_OOM);
+    }
+    return ZN_OK;
+}
+
+int zn_hip_free(zn_ctx *ctx, void *ptr) {
+    if (!ctx) return ZN_ERR_INVALID_ARG;
+    if (!ptr) return ZN_OK;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    ZN_HIP_TRY(ctx, hipFree(ptr));
+    return ZN_OK;
+}
+
+static int zn_copy(zn_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind, bool wait) {
+    if (!ctx) return ZN_ERR_INVALID_ARG;
+    if (bytes == 0) return ZN_OK;
+    if (!dst || !src) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
+    if (wait) ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return ZN_OK;
+}
+
+int zn_hip_h2d(zn_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return zn_copy(ctx, dst, src, bytes, hipMemcpyHostToDevice, true);
+}
+int zn_hip_d2h(zn_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return zn_copy(ctx, dst, src, bytes, hipMemcpyDeviceToHost, true);
+}
+int zn_hip_h2d_async(zn_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return zn_copy(ctx, dst, src, bytes, hipMemcpyHostToDevice, false);
+}
+int zn_hip_d2h_async(zn_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return zn_copy(ctx, dst, src, bytes, hipMemcpyDeviceToHost, false);
+}
+
+int zn_hip_fill_f32(zn_ctx *ctx, float *dst, float value, int64_t count) {
+    if (!ctx || count < 0) return ZN_ERR_INVALID_ARG;
+    if (count == 0) return ZN_OK;
+    if (!dst) return ZN_ERR_INVALID_ARG;
+    ZnEltArgs a = {};
+    a.out = dst;
+    a.rows = 1;
+    a.n = count;
+    a.value = value;
+    return elt_launch(ctx, kFill, count, a);
+}
+
+int zn_hip_copy_f32(zn_ctx *ctx, float *dst, const float *src, int64_t count) {
+    if (!ctx || count < 0) return ZN_ERR_INVALID_ARG;
+    if (count == 0) return ZN_OK;
+    if (!dst || !src) return ZN_ERR_INVALID_ARG;
+    ZnEltArgs a = {};
+    a.out = dst;
+    a.in0 = src;
+    a.rows = 1;
+    a.n = count;
+    return elt_launch(ctx, kCopy, (count + 3) / 4, a);
+}
+
+int zn_hip_sync(zn_ctx *ctx) {
+    if (!ctx) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return ZN_OK;
+}
+
+// ----------------------------------------------------------------- events
+int zn_hip_event_create(zn_ctx *ctx, zn_event **out) {
+    if (!ctx || !out) return ZN_ERR_INVALID_ARG;
+    *out = nullptr;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    zn_event *ev = new (std::nothrow) zn_event();
+    if (!ev) return ZN_ERR_OOM;
+    hipError_t e = hipEventCreate(&ev->ev);
+    if (e != hipSuccess) {
+        delete ev;
+        return fail_hip(ctx, e);
+    }
+    *out = ev;
+    return ZN_OK;
+}
+
+int zn_hip_event_record(zn_ctx *ctx, zn_event *ev) {
+    if (!ctx || !ev) return ZN_ERR_INVALID_ARG;
+    ZN_HIP_TRY(ctx, hipEventRecord(ev->ev, ctx->stream));
+    return ZN_OK;
+}
+
+int zn_hip_event_elapsed_ms(zn_event *start, zn_event *end, float *ms) {
+    if (!start || !end || !ms) return ZN_ERR_INVALID_ARG;
+    if (hipEventSynchronize(end->ev) != hipSuccess) return ZN_ERR_HIP;
+    if (hipEventElapsedTime(ms, start->ev, end->ev) != hipSuccess) return ZN_ERR_HIP;
+    return ZN_OK;
+}
+
+int zn_hip_event_destroy(zn_event *ev) {
+    if (!ev) return ZN_OK;
+    (void)hipEventDestroy(ev->ev);
+    delete ev;
+    return ZN_OK;
+}
+
+// ------------------------------------------------------------------ GEMM
+int zn_hip_sgemm(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
+                 const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias, int act) {
+    return gemm_launch(ctx, layout, m, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias, act);
+}
+
+int zn_hip_sgemm_strided_batched(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a,
+                                 int64_t lda, int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b,
+                                 float *c, int64_t ldc, int64_t stride_c, int64_t batch, int accumulate,
+                                 const float *bias, int act) {
+    return gemm_launch(ctx, layout, m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch, accumulate,
+                       bias, act);
+}
+
+// ---------------------------------------------------------- Dense helpers
+int zn_hip_add_bias(zn_ctx *ctx, float *out, const float *bias, int64_t rows, int64_t n) {
+    if (!ctx || rows < 0 || n < 0) return ZN_ERR_INVALID_ARG;
+    if (rows == 0 || n == 0) return ZN_OK;
+    if (!out || !bias) return ZN_ERR_INVALID_ARG;
+    ZnEltArgs a = {};
+    a.out = out;
+    a.in0 = bias;
+    a.rows = rows;
+    a.n = n;
+    return elt_launch(ctx, kAddBias, rows * n, a);
+}
+
+int zn_hip_activation_forward(zn_ctx *ctx, int act, const float *in, float *out, int64_t len) {
+    if (!ctx || len < 0 || act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
+    if (len == 0) return ZN_OK;
+    if (!in || !out) return ZN_ERR_INVALID_ARG;
+    ZnEltArgs a = {};
+    a.out = out;
+    a.in0 = in;
+    a.rows = 1;
+    a.n = len;
+    a.act = act;
+    return elt_launch(ctx, kActFwd, len, a);
+}
+
+int zn_hip_activation_backward(zn_ctx *ctx, int act, const float *y, const float *grad_out, float *grad_in,
+                               int64_t len) {
+    if (!ctx || len < 0 || act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
+    if (len == 0) return ZN_OK;
+    if (!y || !grad_out || !grad_in) return ZN_ERR_INVALID_ARG;
+    ZnEltArgs a = {};
+    a.out = grad_in;
+    a.in0 = y;
+    a.in1 = grad_out;
+    a.rows = 1;
+    a.n = len;
+    a.act = act;
+    return elt_launch(ctx, kActBwd, len, a);
+}
+
+int zn_hip_accumulate_bias(zn_ctx *ctx, float *grad_bias, const float *gaa, int64_t rows, int64_t n) {
+    if (!ctx || rows < 0 || n < 0) return ZN_ERR_INVALID_ARG;
+    if (rows == 0 || n == 0) return ZN_OK;
+    if (!grad_bias || !gaa) return ZN_ERR_INVALID_ARG;
+    ZnEltArgs a = {};
+    a.out = grad_bias;
+    a.in0 = gaa;
+    a.rows = rows;
+    a.n = n;
+    return elt_launch(ctx, kAccBias, n, a);
+}
+
+// ------------------------------------------------ host-slice drop-ins
+int zn_hip_mat_mul(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c, size_t c_len,
+                   size_t m, size_t n, size_t k, int accumulate) {
+    return host_gemm(ctx, ZN_LAYOUT_NN, a, a_len, b, b_len, nullptr, 0, c, c_len, m, n, k, accumulate, ZN_ACT_LINEAR);
+}
+
+int zn_hip_mat_mul_batch(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c,
+                         size_t c_len, size_t batch_size, size_t n, size_t k, int accumulate) {
+    return host_gemm(ctx, ZN_LAYOUT_NN, a, a_len, b, b_len, nullptr, 0, c, c_len, batch_size, n, k, accumulate,
+                     ZN_ACT_LINEAR);
+}
+
+int zn_hip_mat_mul_transpose_a(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c,
+                               size_t c_len, size_t m, size_t n, size_t k, int accumulate) {
+    return host_gemm(ctx, ZN_LAYOUT_TN, a, a_len, b, b_len, nullptr, 0, c, c_len, m, n, k, accumulate, ZN_ACT_LINEAR);
+}
+
+int zn_hip_mat_mul_transpose_b(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c,
+                               size_t c_len, size_t m, size_t n, size_t k, int accumulate) {
+    return host_gemm(ctx, ZN_LAYOUT_NT, a, a_len, b, b_len, nullptr, 0, c, c_len, m, n, k, accumulate, ZN_ACT_LINEAR);
+}
+
+static int host_bias_gemm(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, const float *bias,
+                          size_t bias_len, float *c, size_t c_len, size_t batch_size, size_t n, size_t k, int act) {
+    if (!bias && n) return ZN_ERR_INVALID_ARG;
+    return host_gemm(ctx, ZN_LAYOUT_NN, a, a_len, b, b_len, bias, bias_len, c, c_len, batch_size, n, k, 0, act);
+}
+
+int zn_hip_mat_mul_bias(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, const float *bias,
+                        size_t bias_len, float *c, size_t c_len, size_t batch_size, size_t n, size_t k) {
+    return host_bias_gemm(ctx, a, a_len, b, b_len, bias, bias_len, c, c_len, batch_size, n, k, ZN_ACT_LINEAR);
+}
+int zn_hip_mat_mul_bias_relu(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len,
+                             const float *bias, size_t bias_len, float *c, size_t c_len, size_t batch_size, size_t n,
+                             size_t k) {
+    return host_bias_gemm(ctx, a, a_len, b, b_len, bias, bias_len, c, c_len, batch_size, n, k, ZN_ACT_RELU);
+}
+int zn_hip_mat_mul_bias_sigmoid(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len,
+                                const float *bias, size_t bias_len, float *c, size_t c_len, size_t batch_size,
+                                size_t n, size_t k) {
+    return host_bias_gemm(ctx, a, a_len, b, b_len, bias, bias_len, c, c_len, batch_size, n, k, ZN_ACT_SIGMOID);
+}
+int zn_hip_mat_mul_bias_tanh(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len,
+                             const float *bias, size_t bias_len, float *c, size_t c_len, size_t batch_size, size_t n,
+                             size_t k) {
+    return host_bias_gemm(ctx, a, a_len, b, b_len, bias, bias_len, c, c_len, batch_size, n, k, ZN_ACT_TANH);
+}
+
+int zn_hip_add_bias_host(zn_ctx *ctx, float *out, size_t out_len, const float *bias, size_t bias_len) {
+    if (!ctx || bias_len == 0) return ZN_ERR_INVALID_ARG;  // the reference divides by bias.len
+    if (out_len && (!out || !bias)) return ZN_ERR_INVALID_ARG;
+    const size_t rows = out_len / bias_len;
+    if (rows == 0) return ZN_OK;
+    const size_t used = rows * bias_len;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease dout(ctx), dbias(ctx);
+    if ((rc = dout.get(used)) || (rc = dbias.get(bias_len))) return rc;
+    if ((rc = copy_in(ctx, dout.ptr, out, used)) || (rc = copy_in(ctx, dbias.ptr, bias, bias_len))) return rc;
+    if ((rc = zn_hip_add_bias(ctx, dout.ptr, dbias.ptr, (int64_t)rows, (int64_t)bias_len))) return rc;
+    return copy_out_and_wait(ctx, out, dout.ptr, used);
+}
+
+int zn_hip_activation_forward_host(zn_ctx *ctx, int act, const float *in, size_t in_len, float *out, size_t out_len) {
+    if (!ctx || act < ZN_ACT_LINEAR || act > ZN_ACT_TANH || out_len < in_len) return ZN_ERR_INVALID_ARG;
+    if (in_len == 0) return ZN_OK;
+    if (!in || !out) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease din(ctx), dout(ctx);
+    if ((rc = din.get(in_len)) || (rc = dout.get(in_len))) return rc;
+    if ((rc = copy_in(ctx, din.ptr, in, in_len))) return rc;
+    if ((rc = zn_hip_activation_forward(ctx, act, din.ptr, dout.ptr, (int64_t)in_len))) return rc;
+    return copy_out_and_wait(ctx, out, dout.ptr, in_len);
+}
+
+int zn_hip_activation_backward_host(zn_ctx *ctx, int act, const float *y, size_t y_len, const float *grad_out,
+                                    size_t grad_out_len, float *grad_in, size_t grad_in_len) {
+    if (!ctx || act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
+    if (y_len != grad_out_len || y_len != grad_in_len) return ZN_ERR_INVALID_ARG;
+    if (y_len == 0) return ZN_OK;
+    if (!y || !grad_out || !grad_in) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease dy(ctx), dgo(ctx), dgi(ctx);
+    if ((rc = dy.get(y_len)) || (rc = dgo.get(y_len)) || (rc = dgi.get(y_len))) return rc;
+    if ((rc = copy_in(ctx, dy.ptr, y, y_len)) || (rc = copy_in(ctx, dgo.ptr, grad_out, y_len))) return rc;
+    if ((rc = zn_hip_activation_backward(ctx, act, dy.ptr, dgo.ptr, dgi.ptr, (int64_t)y_len))) return rc;
+    return copy_out_and_wait(ctx, grad_in, dgi.ptr, y_len);
+}
+
+int zn_hip_accumulate_bias_host(zn_ctx *ctx, float *grad_bias, size_t grad_bias_len, const float *gaa,
+                                size_t gaa_len) {
+    if (!ctx || grad_bias_len == 0) return ZN_ERR_INVALID_ARG;
+    if (gaa_len && (!grad_bias || !gaa)) return ZN_ERR_INVALID_ARG;
+    const size_t rows = gaa_len / grad_bias_len;
+    if (rows == 0) return ZN_OK;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease dgb(ctx), dgaa(ctx);
+    if ((rc = dgb.get(grad_bias_len)) || (rc = dgaa.get(rows * grad_bias_len))) return rc;
+    if ((rc = copy_in(ctx, dgb.ptr, grad_bias, grad_bias_len)) || (rc = copy_in(ctx, dgaa.ptr, gaa, rows * grad_bias_len)))
+        return rc;
+    if ((rc = zn_hip_accumulate_bias(ctx, dgb.ptr, dgaa.ptr, (int64_t)rows, (int64_t)grad_bias_len))) return rc;
+    return copy_out_and_wait(ctx, grad_bias, dgb.ptr, grad_bias_len);
+}
+
+}  // extern "C"

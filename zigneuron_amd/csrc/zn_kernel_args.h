@@ -1,0 +1,38 @@
+// Kernel argument blocks shared by the host runtime (zn_hip.cpp) and the
+// gfx950 code objects (kernels/*.hip).  Each kernel takes one of these structs
+// by value, so the host passes a single kernel parameter whose layout is fixed
+// here.  Plain C layout; no HIP types.
+#ifndef ZN_KERNEL_ARGS_H
+#define ZN_KERNEL_ARGS_H
+
+#include <stdint.h>
+
+// One (possibly batched) fp32 GEMM: C = act((acc ? C : 0) + op(A) op(B) + bias).
+struct ZnGemmArgs {
+    const float *a;
+    const float *b;
+    float *c;
+    const float *bias;   // length n, or null
+    int64_t lda, ldb, ldc;
+    int64_t stride_a, stride_b, stride_c;  // batch strides (elements); batch = blockIdx.y
+    int32_t m, n, k;
+    int32_t tiles_m, tiles_n;  // macro-tile grid of one problem; gridDim.x == tiles_m * tiles_n
+    int32_t accumulate;        // 1: add the existing C
+    int32_t act;               // zn_act
+    int32_t vec_a, vec_b;      // 1: 16-byte aligned rows, use dwordx4 loads
+    int32_t vec_c;             // 1: ldc and C allow vector stores
+    int32_t group_m;           // tile rows per raster group
+    int32_t xcd_remap;         // 1: gridDim.x % 8 == 0, give each XCD a contiguous tile range
+};
+
+// Elementwise helpers (fill, copy, bias, activations, bias gradient).
+struct ZnEltArgs {
+    float *out;
+    const float *in0;
+    const float *in1;
+    int64_t rows, n;   // n = row length; for flat ops rows*n = element count
+    float value;
+    int32_t act;
+};
+
+#endif

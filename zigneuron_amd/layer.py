@@ -1,0 +1,112 @@
+"""Mirror of ZigNeuron's ``Dense`` layer (src/layer.zig:291-476) on the HIP arm.
+
+Shapes and call sequence follow the reference:
+  * weights [input_size x output_size] row-major, bias [output_size]
+    (src/layer.zig:311-314), initialised U[-1,1) * scale with He / Xavier /
+    linear scales (src/layer.zig:330-338); the bias starts at zero;
+  * forward: NN GEMM + bias + activation (src/layer.zig:380-409).  On this
+    backend the three steps run as one fused kernel through
+    ``Backend.matMulBias{,Relu,Sigmoid,Tanh}`` (src/backend.zig:200-295);
+  * backward: activationBackward -> NT GEMM for grad_input -> accumulateBias
+    -> TN GEMM for grad_weights (src/layer.zig:411-475).
+
+``DenseDevice`` is the same layer with every tensor resident in HBM (the
+device-pointer C ABI), used for the MLP training-step workload.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+from .backend import Backend, Context, DeviceBuffer, act_id
+
+_FUSED = {"linear": "matMulBias", "relu": "matMulBiasRelu", "sigmoid": "matMulBiasSigmoid",
+          "tanh": "matMulBiasTanh"}
+
+
+def init_scale(act: str, input_size: int, output_size: int) -> float:
+    """Weight scale of Dense.init (src/layer.zig:330-334)."""
+    if act in ("relu", "leaky_relu"):
+        return math.sqrt(2.0 / input_size)
+    if act == "linear":
+        return math.sqrt(1.0 / input_size)
+    return math.sqrt(2.0 / (input_size + output_size))
+
+
+def init_weights(input_size: int, output_size: int, act: str, seed: int) -> np.ndarray:
+    """U[-1,1) * scale from a seeded PCG64 stream (the reference's Zig PRNG
+    stream is not reproduced; parity tests feed the same arrays to both sides)."""
+    rng = np.random.default_rng(seed)
+    u = rng.random((input_size, output_size), dtype=np.float32)
+    return ((u * np.float32(2.0) - np.float32(1.0)) * np.float32(init_scale(act, input_size, output_size))).astype(
+        np.float32)
+
+
+class Dense:
+    def __init__(self, backend: Backend, input_size: int, output_size: int, act: str = "relu", seed: int = 1):
+        if input_size == 0:
+            raise _lib.InvalidArgumentError(_lib.ZN_ERR_INVALID_ARG, "Dense.init", "InvalidInputSize")
+        if output_size == 0:
+            raise _lib.InvalidArgumentError(_lib.ZN_ERR_INVALID_ARG, "Dense.init", "InvalidOutputSize")
+        act_id(act)  # validates
+        self.backend = backend
+        self.input_size, self.output_size, self.act = input_size, output_size, act
+        self.weights = init_weights(input_size, output_size, act, seed).ravel()
+        self.bias = np.zeros(output_size, np.float32)
+        self.grad_weights = np.zeros(input_size * output_size, np.float32)
+        self.grad_bias = np.zeros(output_size, np.float32)
+
+    def forward(self, inp, output) -> None:
+        inp = np.ascontiguousarray(inp, dtype=np.float32)
+        batch = inp.size // self.input_size
+        if output.size != batch * self.output_size:
+            raise _lib.InvalidArgumentError(_lib.ZN_ERR_INVALID_ARG, "Dense.forward", "InvalidOutputSize")
+        getattr(self.backend, _FUSED[self.act])(inp, self.weights, self.bias, output, batch, self.output_size,
+                                                self.input_size)
+
+    def backward(self, inp, grad_output, grad_input, activated_output) -> None:
+        inp = np.ascontiguousarray(inp, dtype=np.float32)
+        batch = inp.size // self.input_size if self.input_size > 0 else 1
+        gaa = np.empty(batch * self.output_size, np.float32)
+        self.backend.activationBackward(self.act, activated_output, grad_output, gaa)
+        self.backend.matMulTransposeB(gaa, self.weights, grad_input, batch, self.input_size, self.output_size,
+                                      False)
+        self.backend.accumulateBias(self.grad_bias, gaa)
+        self.backend.matMulTransposeA(inp, gaa, self.grad_weights, self.input_size, self.output_size, batch, False)
+
+
+class DenseDevice:
+    """Dense with weights, gradients and activations resident in HBM."""
+
+    def __init__(self, ctx: Context, input_size: int, output_size: int, act: str, batch: int,
+                 weights: Optional[np.ndarray] = None, bias: Optional[np.ndarray] = None, seed: int = 1):
+        self.ctx, self.input_size, self.output_size, self.act, self.batch = ctx, input_size, output_size, act, batch
+        w = init_weights(input_size, output_size, act, seed) if weights is None else weights
+        b = np.zeros(output_size, np.float32) if bias is None else bias
+        self.weights = ctx.to_device(w)
+        self.bias = ctx.to_device(b)
+        self.grad_weights = ctx.alloc(input_size * output_size).fill(0.0)
+        self.grad_bias = ctx.alloc(output_size).fill(0.0)
+        self.out = ctx.alloc(batch * output_size)
+        self.gaa = ctx.alloc(batch * output_size)
+        self.grad_input = ctx.alloc(batch * input_size)
+
+    def forward(self, x: DeviceBuffer) -> DeviceBuffer:
+        """Fused NN + bias + activation into self.out (asynchronous)."""
+        self.ctx.sgemm("nn", self.batch, self.output_size, self.input_size, x, self.input_size, self.weights,
+                       self.output_size, self.out, self.output_size, False, self.bias, self.act)
+        return self.out
+
+    def backward(self, x: DeviceBuffer, grad_out: DeviceBuffer) -> DeviceBuffer:
+        """activationBackward -> NT (grad_input) -> accumulateBias -> TN (grad_weights)."""
+        n_out = self.batch * self.output_size
+        self.ctx.activation_backward(self.act, self.out, grad_out, self.gaa, n_out)
+        self.ctx.sgemm("nt", self.batch, self.input_size, self.output_size, self.gaa, self.output_size,
+                       self.weights, self.output_size, self.grad_input, self.input_size)
+        self.ctx.accumulate_bias(self.grad_bias, self.gaa, self.batch, self.output_size)
+        self.ctx.sgemm("tn", self.input_size, self.output_size, self.batch, x, self.input_size, self.gaa,
+                       self.output_size, self.grad_weights, self.output_size)
+        return self.grad_input
