@@ -180,6 +180,21 @@ def cpu_baseline(target_s=5.0):
             "single_thread_tflops": round(res["single"]["tflops"], 5), "cpu_model": cpu_model}
 
 
+def copy_calibration(ctx, steps, warmup) -> int:
+    """1 GiB read + 1 GiB write per launch with the plain streaming copy kernel."""
+    count = (1 << 30) // 4
+    src, dst = ctx.alloc(count).fill(1.0), ctx.alloc(count)
+    ms = time_launches(ctx, lambda: ctx.copy(dst.ptr, src.ptr, count), steps, warmup)
+    gbs = 2 * count * 4 / (ms * 1e-3) / 1e9
+    log(f"copy 1 GiB: {ms:.3f} ms -> {gbs:.1f} GB/s (read+write)")
+    print(json.dumps({"workload": "zn_copy_f32 1 GiB", "bytes_read_per_launch": count * 4,
+                      "bytes_written_per_launch": count * 4, "kernel_ms": round(ms, 4), "gbs": round(gbs, 1)}))
+    src.close()
+    dst.close()
+    ctx.close()
+    return 0
+
+
 def load_traffic():
     try:
         with open(TRAFFIC_FILE) as f:
@@ -196,6 +211,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="time only a 1 GiB device-to-device copy (zn_copy_f32): the known-size reference "
+                         "for scaling FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is "
@@ -205,6 +223,8 @@ def main() -> int:
     from zigneuron_amd import Context
     ctx = Context(0)
     log(f"device {ctx.arch}, {ctx.compute_units} CUs, {ctx.clock_khz / 1e3:.0f} MHz")
+    if args.copy_calibration:
+        return copy_calibration(ctx, args.steps, args.warmup)
     rng = np.random.default_rng(42)
     m = n = k = 8192
     log("allocating 8192^3 operands")

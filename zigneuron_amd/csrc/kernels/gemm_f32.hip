@@ -17,8 +17,10 @@
 //  * For an X-contiguous operand the 32 lanes of a block own FX consecutive
 //    tile rows/cols (row = FX*i + f), so their fragment is one FX-wide LDS
 //    read and, for B, their output columns are FX-wide vector stores.
-//  * Edges (ragged M, N, K) are zero-filled in LDS; zero products leave the
-//    sums unchanged, and stores are predicated.
+//  * Edges (ragged M, N, K) are zero-filled in LDS: staging uses raw buffer
+//    loads whose masked lanes carry an out-of-range offset and read zero, so
+//    the load path has no branches; zero products leave the sums unchanged,
+//    and stores are predicated.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -47,10 +49,21 @@ __device__ __forceinline__ float zn_activate(float v, int act) {
     }
 }
 
+// Raw buffer descriptor over one operand of one problem: loads at byte
+// offsets >= `bytes` return zero, so masked elements use an out-of-range
+// offset instead of a branch.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 // One operand's BX x BK slice: global -> registers -> LDS.
 //   KC: element (x, k) at g[x*ld + k]; LDS row x, stride BK + kKPad.
 //  !KC: element (x, k) at g[k*ld + x]; LDS row k, stride BX.
-template <int BX, int BK, int NT, bool KC>
+// VEC: rows are 16-byte aligned and the contiguous extent is a multiple of 4,
+// so a float4 chunk is either wholly inside the problem or wholly outside.
+template <int BX, int BK, int NT, bool KC, bool VEC>
 struct Stage {
     static constexpr int kChunksPerRow = KC ? BK / 4 : BX / 4;  // float4 chunks along the contiguous dim
     static constexpr int kLoads = (BX * BK / 4) / NT;            // chunks per thread
@@ -62,35 +75,30 @@ struct Stage {
 
     zn_f32x4 r[kLoads];
 
-    // Fetch slice k0 of the tile starting at x0.  `xmax`/`kmax` bound the
-    // problem; `vec` allows 16-byte loads (aligned rows).
-    __device__ __forceinline__ void load(const float *__restrict__ g, int64_t ld, int x0, int k0, int xmax, int kmax,
-                                         bool vec, int tid) {
+    // Fetch slice k0 of the tile starting at x0; `xmax`/`kmax` bound the
+    // problem.  Branch-free: out-of-problem elements read as zero.
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rsrc, int ld, int x0, int k0, int xmax, int kmax,
+                                         int tid) {
         const int row0 = tid / kChunksPerRow;
         const int col = (tid % kChunksPerRow) * 4;
-        const bool interior = x0 + BX <= xmax && k0 + BK <= kmax;
 #pragma unroll
         for (int j = 0; j < kLoads; ++j) {
             const int row = row0 + j * kRowsPerPass;
             // (outer, inner) coordinates in the problem: KC -> (x, k), !KC -> (k, x)
             const int outer = (KC ? x0 : k0) + row;
             const int inner = (KC ? k0 : x0) + col;
-            const int outer_max = KC ? xmax : kmax;
+            const bool ok_outer = outer < (KC ? xmax : kmax);
             const int inner_max = KC ? kmax : xmax;
-            const float *src = g + (int64_t)outer * ld + inner;
-            if (interior && vec) {
-                r[j] = *reinterpret_cast<const zn_f32x4 *>(src);
-            } else if (interior) {
-                r[j] = zn_f32x4{src[0], src[1], src[2], src[3]};
+            const uint32_t base = (uint32_t)(outer * ld + inner) * 4u;
+            if constexpr (VEC) {
+                const uint32_t off = (ok_outer && inner < inner_max) ? base : kOutOfRange;
+                r[j] = __builtin_bit_cast(zn_f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
             } else {
-                zn_f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (outer < outer_max) {
-                    if (inner + 0 < inner_max) v[0] = src[0];
-                    if (inner + 1 < inner_max) v[1] = src[1];
-                    if (inner + 2 < inner_max) v[2] = src[2];
-                    if (inner + 3 < inner_max) v[3] = src[3];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t off = (ok_outer && inner + e < inner_max) ? base + 4u * e : kOutOfRange;
+                    r[j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
                 }
-                r[j] = v;
             }
         }
     }
@@ -140,7 +148,7 @@ __device__ __forceinline__ void read_frags(const float *lds, int w0, int kg, int
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, bool VEC>
 __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
@@ -149,8 +157,8 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     static_assert(BK % 8 == 0, "BK must be a multiple of the K group");
     static_assert(FM == 1 || FM == 2 || FM == 4, "FM");
     static_assert(FN == 1 || FN == 2 || FN == 4, "FN");
-    typedef Stage<BM, BK, NT, AK> StageA;
-    typedef Stage<BN, BK, NT, BKC> StageB;
+    typedef Stage<BM, BK, NT, AK, VEC> StageA;
+    typedef Stage<BN, BK, NT, BKC, VEC> StageB;
 
     __shared__ __attribute__((aligned(16))) float lds_a[2][StageA::kLdsFloats];
     __shared__ __attribute__((aligned(16))) float lds_b[2][StageB::kLdsFloats];
@@ -189,11 +197,16 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     StageA sa;
     StageB sb;
     const int ktiles = (p.k + BK - 1) / BK;
-    const bool va = p.vec_a != 0, vb = p.vec_b != 0;
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    // operand extents in bytes (the host keeps each below 2^31)
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
+    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
 
     if (ktiles > 0) {
-        sa.load(ga, p.lda, m0, 0, p.m, p.k, va, tid);
-        sb.load(gb, p.ldb, n0, 0, p.n, p.k, vb, tid);
+        sa.load(ra, lda, m0, 0, p.m, p.k, tid);
+        sb.load(rb, ldb, n0, 0, p.n, p.k, tid);
         sa.store(lds_a[0], tid);
         sb.store(lds_b[0], tid);
     }
@@ -203,8 +216,8 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
         const int cur = kt & 1;
         const bool more = kt + 1 < ktiles;
         if (more) {
-            sa.load(ga, p.lda, m0, (kt + 1) * BK, p.m, p.k, va, tid);
-            sb.load(gb, p.ldb, n0, (kt + 1) * BK, p.n, p.k, vb, tid);
+            sa.load(ra, lda, m0, (kt + 1) * BK, p.m, p.k, tid);
+            sb.load(rb, ldb, n0, (kt + 1) * BK, p.n, p.k, tid);
         }
         const float *la = lds_a[cur];
         const float *lb = lds_b[cur];
@@ -283,21 +296,25 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
 
 }  // namespace
 
-// Exported kernels: zn_sgemm_<layout>_<tile>.  Layout letters follow the
-// reference: nn = Backend.matMul, nt = matMulTransposeB, tn = matMulTransposeA.
-// Tiles: l = 128x128 (4 waves of 64x64), m = 64x64 (4 waves of 32x32),
-// s = 32x32 (1 wave) for small problems.
-#define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC)                                       \
+// Exported kernels: zn_sgemm_<layout>_<tile>[_v].  Layout letters follow
+// the reference: nn = Backend.matMul, nt = matMulTransposeB, tn =
+// matMulTransposeA.  Tiles: l = 128x128 (4 waves of 64x64), m = 64x64
+// (4 waves of 32x32), s = 32x32 (1 wave) for small problems.  The _v variants
+// stage operands with 16-byte loads (aligned rows, contiguous extents a
+// multiple of 4); the plain ones with 4-byte loads.
+#define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC)                                  \
     extern "C" __global__ __launch_bounds__(WM *WN * 64) void NAME(ZnGemmArgs p) {              \
-        gemm_tile<BM, BN, BK, WM, WN, AK, BKC>(p);                                               \
+        gemm_tile<BM, BN, BK, WM, WN, AK, BKC, VEC>(p);                                          \
     }
 
-ZN_GEMM_KERNEL(zn_sgemm_nn_l, 128, 128, 16, 2, 2, true, false)
-ZN_GEMM_KERNEL(zn_sgemm_nt_l, 128, 128, 16, 2, 2, true, true)
-ZN_GEMM_KERNEL(zn_sgemm_tn_l, 128, 128, 16, 2, 2, false, false)
-ZN_GEMM_KERNEL(zn_sgemm_nn_m, 64, 64, 16, 2, 2, true, false)
-ZN_GEMM_KERNEL(zn_sgemm_nt_m, 64, 64, 16, 2, 2, true, true)
-ZN_GEMM_KERNEL(zn_sgemm_tn_m, 64, 64, 16, 2, 2, false, false)
-ZN_GEMM_KERNEL(zn_sgemm_nn_s, 32, 32, 16, 1, 1, true, false)
-ZN_GEMM_KERNEL(zn_sgemm_nt_s, 32, 32, 16, 1, 1, true, true)
-ZN_GEMM_KERNEL(zn_sgemm_tn_s, 32, 32, 16, 1, 1, false, false)
+#define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, VEC, SUFFIX)                                  \
+    ZN_GEMM_KERNEL(zn_sgemm_nn_##TILE##SUFFIX, BM, BN, BK, WM, WN, true, false, VEC)            \
+    ZN_GEMM_KERNEL(zn_sgemm_nt_##TILE##SUFFIX, BM, BN, BK, WM, WN, true, true, VEC)             \
+    ZN_GEMM_KERNEL(zn_sgemm_tn_##TILE##SUFFIX, BM, BN, BK, WM, WN, false, false, VEC)
+
+ZN_GEMM_LAYOUTS(l, 128, 128, 16, 2, 2, true, _v)
+ZN_GEMM_LAYOUTS(l, 128, 128, 16, 2, 2, false, )
+ZN_GEMM_LAYOUTS(m, 64, 64, 16, 2, 2, true, _v)
+ZN_GEMM_LAYOUTS(m, 64, 64, 16, 2, 2, false, )
+ZN_GEMM_LAYOUTS(s, 32, 32, 16, 1, 1, true, _v)
+ZN_GEMM_LAYOUTS(s, 32, 32, 16, 1, 1, false, )

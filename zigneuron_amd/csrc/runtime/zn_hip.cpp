@@ -54,7 +54,7 @@ struct zn_ctx {
     hipStream_t stream = nullptr;
     hipModule_t gemm_module = nullptr;
     hipModule_t elt_module = nullptr;
-    hipFunction_t gemm[3][kNumTiles] = {};
+    hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
     hipFunction_t elt[kNumElt] = {};
     int last_hip_error = 0;
     zn_device_info info = {};
@@ -196,6 +196,12 @@ int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const 
     const int64_t b_row = layout == ZN_LAYOUT_NT ? k : n;
     if (k > 0 && (lda < a_row || ldb < b_row || lda < 1 || ldb < 1)) return ZN_ERR_INVALID_ARG;
     if (ldc < n) return ZN_ERR_INVALID_ARG;
+    // The kernels address each operand of one problem with 32-bit byte
+    // offsets: keep every per-problem extent below 2 GiB.
+    const int64_t a_outer = layout == ZN_LAYOUT_TN ? k : m;
+    const int64_t b_outer = layout == ZN_LAYOUT_NT ? n : k;
+    const int64_t kLimit = (int64_t)INT_MAX / 4;
+    if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || (b_outer - 1) * ldb + b_row > kLimit)) return ZN_ERR_OVERFLOW;
 
     const Tile tile = choose_tile(ctx, m, n, batch);
     const TileShape &ts = kTiles[tile];
@@ -221,8 +227,9 @@ int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const 
     args.tiles_n = (int32_t)tiles_n;
     args.accumulate = accumulate ? 1 : 0;
     args.act = act;
-    args.vec_a = aligned16(a) && lda % 4 == 0 && stride_a % 4 == 0;
-    args.vec_b = aligned16(b) && ldb % 4 == 0 && stride_b % 4 == 0;
+    // 16-byte staging: aligned rows and contiguous extents that are whole float4s
+    const bool vec = aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0 && stride_a % 4 == 0 &&
+                     stride_b % 4 == 0 && a_row % 4 == 0 && b_row % 4 == 0;
     args.vec_c = aligned16(c) && ldc % 4 == 0 && stride_c % 4 == 0;
     args.group_m = 8;
     const int64_t ntiles = tiles_m * tiles_n;
@@ -230,7 +237,7 @@ int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const 
 
     int rc = select_device(ctx);
     if (rc) return rc;
-    hipFunction_t f = ctx->gemm[layout][tile];
+    hipFunction_t f = ctx->gemm[layout][tile][vec ? 1 : 0];
     constexpr int64_t kMaxGridY = 65535;
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
@@ -375,12 +382,14 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
         return bail(ZN_ERR_CODE_OBJECT);
     }
     for (int l = 0; l < 3; ++l)
-        for (int t = 0; t < kNumTiles; ++t) {
-            char name[64];
-            std::snprintf(name, sizeof(name), "zn_sgemm_%s_%s", kLayoutName[l], kTiles[t].suffix);
-            if (hipModuleGetFunction(&ctx->gemm[l][t], ctx->gemm_module, name) != hipSuccess)
-                return bail(ZN_ERR_SYMBOL);
-        }
+        for (int t = 0; t < kNumTiles; ++t)
+            for (int v = 0; v < 2; ++v) {
+                char name[64];
+                std::snprintf(name, sizeof(name), "zn_sgemm_%s_%s%s", kLayoutName[l], kTiles[t].suffix,
+                              v ? "_v" : "");
+                if (hipModuleGetFunction(&ctx->gemm[l][t][v], ctx->gemm_module, name) != hipSuccess)
+                    return bail(ZN_ERR_SYMBOL);
+            }
     for (int i = 0; i < kNumElt; ++i)
         if (hipModuleGetFunction(&ctx->elt[i], ctx->elt_module, kEltName[i]) != hipSuccess) return bail(ZN_ERR_SYMBOL);
     *out = ctx;

@@ -19,7 +19,6 @@ struct ZnGemmArgs {
     int32_t tiles_m, tiles_n;  // macro-tile grid of one problem; gridDim.x == tiles_m * tiles_n
     int32_t accumulate;        // 1: add the existing C
     int32_t act;               // zn_act
-    int32_t vec_a, vec_b;      // 1: 16-byte aligned rows, use dwordx4 loads
     int32_t vec_c;             // 1: ldc and C allow vector stores
     int32_t group_m;           // tile rows per raster group
     int32_t xcd_remap;         // 1: gridDim.x % 8 == 0, give each XCD a contiguous tile range
