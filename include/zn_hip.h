@@ -140,6 +140,18 @@ int zn_hip_event_destroy(zn_event *ev);
 
 /* ------------------------------------------------ GEMM on device pointers */
 
+/* Macro-tile override for the GEMM launch policy: ZN_TILE_AUTO (the default)
+ * picks by problem size; the others force one tile for every following GEMM
+ * on this context.  No counterpart in the reference: it exists for tuning and
+ * for tests that must reach every kernel variant. */
+#define ZN_TILE_AUTO (-1)
+#define ZN_TILE_256x128 0
+#define ZN_TILE_128x128 1
+#define ZN_TILE_128x64 2
+#define ZN_TILE_64x64 3
+#define ZN_TILE_32x32 4
+int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile);
+
 /* C = act((accumulate ? C : 0) + op(A).op(B) + bias) for one problem.
  * `bias` (length N) may be NULL.  Leading dimensions are in elements and must
  * be >= the stored row length.  m, n >= 0; k >= 0 (k == 0 gives the epilogue

@@ -58,8 +58,9 @@ def test_code_objects_hold_every_kernel():
     for blob in (gemm, elt):  # an offload bundle (hipcc --genco) or a bare ELF code object
         assert blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or blob[:4] == b"\x7fELF"
     for lay in ("nn", "nt", "tn"):
-        for t in ("l", "m", "s"):
-            assert f"zn_sgemm_{lay}_{t}".encode() in gemm
+        for t in ("x", "l", "n", "m", "s"):
+            for v in ("", "_v"):
+                assert f"zn_sgemm_{lay}_{t}{v}".encode() in gemm
     for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",
               "zn_accumulate_bias"):
         assert k.encode() in elt
@@ -77,6 +78,7 @@ def test_abi_version_and_status_strings(lib):
 def test_null_and_bad_arguments_without_device(lib):
     """Argument checks that run before any device call."""
     from zigneuron_amd import _lib
+    assert lib.zn_hip_set_gemm_tile(None, 0) == _lib.ZN_ERR_INVALID_ARG
     assert lib.zn_hip_create(0, None, None) == _lib.ZN_ERR_INVALID_ARG
     assert lib.zn_hip_destroy(None) == _lib.ZN_OK
     assert lib.zn_hip_sgemm(None, 0, 1, 1, 1, None, 1, None, 1, None, 1, 0, None, 0) == _lib.ZN_ERR_INVALID_ARG

@@ -305,3 +305,51 @@ def test_invalid_arguments_are_errors(ctx, backend):
         backend.activationBackward("relu", np.zeros(3, np.float32), np.zeros(4, np.float32),
                                    np.zeros(3, np.float32))
     d.close()
+
+
+# ------------------------------------------------ every kernel variant
+TILES = ["256x128", "128x128", "128x64", "64x64", "32x32"]
+
+
+@pytest.mark.parametrize("aligned", [True, False], ids=["vec16", "vec4"])
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+@pytest.mark.parametrize("tile", TILES)
+def test_every_tile_variant(ctx, tile, layout, aligned):
+    """Force each macro tile on ragged shapes, for both staging widths: plain
+    GEMM, then accumulate + bias + tanh through the same kernel."""
+    m, n, k = (300, 260, 136) if aligned else (301, 259, 133)
+    rng = np.random.default_rng(zlib.crc32(f"{tile}-{layout}-{aligned}".encode()))
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    c0, bias = uniform(rng, (m, n)), uniform(rng, (n,))
+    announce(f"tile {tile} {layout} {'vec16' if aligned else 'vec4'}")
+    ctx.set_gemm_tile(tile)
+    try:
+        c = run_gemm(ctx, layout, a, b, m, n, k)
+        assert_close(c, ref_gemm(layout, a, b, m, n, k), layout, a, b, m, n, k, what=tile)
+        c = run_gemm(ctx, layout, a, b, m, n, k, c0=c0, accumulate=True, bias=bias, act="tanh")
+    finally:
+        ctx.set_gemm_tile("auto")
+    pre = (ref_gemm(layout, a, b, m, n, k, c0=c0, accumulate=True) + bias[None, :]).astype(np.float32)
+    ref = np.tanh(pre.astype(np.float64)).astype(np.float32)
+    assert_close(c, ref, layout, a, b, m, n, k, c0=c0, accumulate=True, bias=bias, act="tanh", what=tile + " epi")
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_every_tile_strided_batched(ctx, tile):
+    rng = np.random.default_rng(77)
+    batch, m, n, k = 3, 130, 70, 40
+    a, b = uniform(rng, (batch, m, k)), uniform(rng, (batch, n, k))
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    dc = ctx.alloc(batch * m * n).fill(np.nan)
+    announce(f"tile {tile} batched nt")
+    ctx.set_gemm_tile(tile)
+    try:
+        ctx.sgemm_strided_batched("nt", m, n, k, da, k, m * k, db, k, n * k, dc, n, m * n, batch)
+        c = dc.download().reshape(batch, m, n)
+    finally:
+        ctx.set_gemm_tile("auto")
+    for i in range(batch):
+        assert_close(c[i], ref_gemm("nt", a[i], b[i], m, n, k), "nt", a[i], b[i], m, n, k, what=f"{tile} {i}")
+    for buf in (da, db, dc):
+        buf.close()

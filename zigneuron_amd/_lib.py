@@ -25,6 +25,8 @@ ZN_ERR_HIP = -7
 ZN_ERR_OVERFLOW = -8
 
 LAYOUT_NN, LAYOUT_NT, LAYOUT_TN = 0, 1, 2
+TILE_AUTO = -1
+TILES = {"auto": -1, "256x128": 0, "128x128": 1, "128x64": 2, "64x64": 3, "32x32": 4}
 ACT_LINEAR, ACT_RELU, ACT_SIGMOID, ACT_TANH = 0, 1, 2, 3
 
 
@@ -114,6 +116,7 @@ SIGNATURES = {
     "zn_hip_event_record": (I, [P, P]),
     "zn_hip_event_elapsed_ms": (I, [P, P, ctypes.POINTER(F)]),
     "zn_hip_event_destroy": (I, [P]),
+    "zn_hip_set_gemm_tile": (I, [P, I]),
     "zn_hip_sgemm": (I, [P, I, I64, I64, I64, P, I64, P, I64, P, I64, I, P, I]),
     "zn_hip_sgemm_strided_batched": (I, [P, I, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, I64, I, P, I]),
     "zn_hip_add_bias": (I, [P, P, P, I64, I64]),

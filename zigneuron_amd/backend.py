@@ -165,6 +165,11 @@ class Context:
     def copy(self, dst: int, src: int, count: int) -> None:
         check(_lib.load().zn_hip_copy_f32(self.handle, int(dst), int(src), int(count)), "zn_hip_copy_f32")
 
+    def set_gemm_tile(self, tile="auto") -> None:
+        """Force one macro tile ("256x128", "128x128", "128x64", "64x64", "32x32") or "auto"."""
+        check(_lib.load().zn_hip_set_gemm_tile(self.handle, _lib.TILES[tile] if isinstance(tile, str) else tile),
+              "zn_hip_set_gemm_tile")
+
     # --- GEMM on device pointers (asynchronous on the context stream)
     def sgemm(self, layout, m, n, k, a, lda, b, ldb, c, ldc, accumulate=False, bias=None, act="linear") -> None:
         check(_lib.load().zn_hip_sgemm(self.handle, layout_id(layout), m, n, k, _dptr(a), lda, _dptr(b), ldb,

@@ -298,23 +298,30 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
 
 // Exported kernels: zn_sgemm_<layout>_<tile>[_v].  Layout letters follow
 // the reference: nn = Backend.matMul, nt = matMulTransposeB, tn =
-// matMulTransposeA.  Tiles: l = 128x128 (4 waves of 64x64), m = 64x64
-// (4 waves of 32x32), s = 32x32 (1 wave) for small problems.  The _v variants
-// stage operands with 16-byte loads (aligned rows, contiguous extents a
-// multiple of 4); the plain ones with 4-byte loads.
-#define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC)                                  \
-    extern "C" __global__ __launch_bounds__(WM *WN * 64) void NAME(ZnGemmArgs p) {              \
+// matMulTransposeA.  Tiles (macro tile, waves x wave tile):
+//   x = 256x128, 8 waves of 64x64   large problems (two workgroups per CU)
+//   l = 128x128, 4 waves of 64x64
+//   n = 128x64,  2 waves of 64x64   narrow N (attention P.V, N = 64)
+//   m = 64x64,   4 waves of 32x32   mid-size problems
+//   s = 32x32,   1 wave             small problems
+// The _v variants stage operands with 16-byte loads (aligned rows,
+// contiguous extents a multiple of 4); the plain ones with 4-byte loads.
+#define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                            \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void NAME(ZnGemmArgs p) {        \
         gemm_tile<BM, BN, BK, WM, WN, AK, BKC, VEC>(p);                                          \
     }
 
-#define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, VEC, SUFFIX)                                  \
-    ZN_GEMM_KERNEL(zn_sgemm_nn_##TILE##SUFFIX, BM, BN, BK, WM, WN, true, false, VEC)            \
-    ZN_GEMM_KERNEL(zn_sgemm_nt_##TILE##SUFFIX, BM, BN, BK, WM, WN, true, true, VEC)             \
-    ZN_GEMM_KERNEL(zn_sgemm_tn_##TILE##SUFFIX, BM, BN, BK, WM, WN, false, false, VEC)
+#define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, VEC, SUFFIX)                            \
+    ZN_GEMM_KERNEL(zn_sgemm_nn_##TILE##SUFFIX, BM, BN, BK, WM, WN, true, false, VEC, MINB)      \
+    ZN_GEMM_KERNEL(zn_sgemm_nt_##TILE##SUFFIX, BM, BN, BK, WM, WN, true, true, VEC, MINB)       \
+    ZN_GEMM_KERNEL(zn_sgemm_tn_##TILE##SUFFIX, BM, BN, BK, WM, WN, false, false, VEC, MINB)
 
-ZN_GEMM_LAYOUTS(l, 128, 128, 16, 2, 2, true, _v)
-ZN_GEMM_LAYOUTS(l, 128, 128, 16, 2, 2, false, )
-ZN_GEMM_LAYOUTS(m, 64, 64, 16, 2, 2, true, _v)
-ZN_GEMM_LAYOUTS(m, 64, 64, 16, 2, 2, false, )
-ZN_GEMM_LAYOUTS(s, 32, 32, 16, 1, 1, true, _v)
-ZN_GEMM_LAYOUTS(s, 32, 32, 16, 1, 1, false, )
+#define ZN_GEMM_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                            \
+    ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, true, _v)                                   \
+    ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, false, )
+
+ZN_GEMM_TILE(x, 256, 128, 16, 4, 2, 1)
+ZN_GEMM_TILE(l, 128, 128, 16, 2, 2, 4)
+ZN_GEMM_TILE(n, 128, 64, 16, 2, 1, 1)
+ZN_GEMM_TILE(m, 64, 64, 16, 2, 2, 1)
+ZN_GEMM_TILE(s, 32, 32, 16, 1, 1, 1)

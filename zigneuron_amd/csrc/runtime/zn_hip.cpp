@@ -31,12 +31,14 @@
 
 namespace {
 
-enum Tile { kTileL = 0, kTileM = 1, kTileS = 2, kNumTiles = 3 };
+// Macro tiles of the GEMM code object (kernels/gemm_f32.hip).
+enum Tile { kTileX = 0, kTileL, kTileN, kTileM, kTileS, kNumTiles };
 struct TileShape {
     int bm, bn, threads;
     const char *suffix;
 };
-constexpr TileShape kTiles[kNumTiles] = {{128, 128, 256, "l"}, {64, 64, 256, "m"}, {32, 32, 64, "s"}};
+constexpr TileShape kTiles[kNumTiles] = {
+    {256, 128, 512, "x"}, {128, 128, 256, "l"}, {128, 64, 128, "n"}, {64, 64, 256, "m"}, {32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
 enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kNumElt };
@@ -57,6 +59,7 @@ struct zn_ctx {
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
     hipFunction_t elt[kNumElt] = {};
     int last_hip_error = 0;
+    int forced_tile = -1;  // ZN_TILE_AUTO
     zn_device_info info = {};
     // Cached device buffers for the host-slice entry points, keyed by
     // power-of-two byte size.
@@ -168,13 +171,17 @@ int launch(zn_ctx *ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned thre
 // ------------------------------------------------------------ GEMM policy
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Largest tile that still gives enough workgroups to occupy the chip.
+// Tile choice, from measurements on MI355X (256 CUs): the largest tiles win
+// once they give every CU two or more workgroups; below that, latency
+// hiding needs more, smaller workgroups (64x64); N <= 64 uses 128x64 so no
+// MFMA block idles; tiny problems use 32x32 to spread over more CUs.
 Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t batch) {
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
-    const int64_t l = cdiv(m, 128) * cdiv(n, 128) * batch;
-    if (l >= cus) return kTileL;
-    const int64_t md = cdiv(m, 64) * cdiv(n, 64) * batch;
-    if (md >= cus / 2) return kTileM;
+    auto tiles = [&](Tile t) { return cdiv(m, kTiles[t].bm) * cdiv(n, kTiles[t].bn) * batch; };
+    if (n <= 64 && tiles(kTileN) >= cus) return kTileN;
+    if (tiles(kTileX) >= 2 * cus) return kTileX;
+    if (tiles(kTileL) >= 4 * cus) return kTileL;
+    if (tiles(kTileM) >= cus / 2) return kTileM;
     return kTileS;
 }
 
@@ -203,7 +210,7 @@ int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const 
     const int64_t kLimit = (int64_t)INT_MAX / 4;
     if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || (b_outer - 1) * ldb + b_row > kLimit)) return ZN_ERR_OVERFLOW;
 
-    const Tile tile = choose_tile(ctx, m, n, batch);
+    const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, batch);
     const TileShape &ts = kTiles[tile];
     const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
     if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
@@ -540,6 +547,12 @@ int zn_hip_event_destroy(zn_event *ev) {
 }
 
 // ------------------------------------------------------------------ GEMM
+int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile) {
+    if (!ctx || tile < ZN_TILE_AUTO || tile >= kNumTiles) return ZN_ERR_INVALID_ARG;
+    ctx->forced_tile = tile;
+    return ZN_OK;
+}
+
 int zn_hip_sgemm(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                  const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias, int act) {
     return gemm_launch(ctx, layout, m, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias, act);
