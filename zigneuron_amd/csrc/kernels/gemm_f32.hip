@@ -184,7 +184,7 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     const int64_t bz = blockIdx.y;
     const float *__restrict__ ga = p.a + bz * p.stride_a;
     const float *__restrict__ gb = p.b + bz * p.stride_b;
-    float *__restrict__ gc = p.c + bz * p.stride_c;
+    float *gc = p.c + bz * p.stride_c;
 
     zn_f32x16 acc[FM][FN];
 #pragma unroll
@@ -196,7 +196,10 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
 
     StageA sa;
     StageB sb;
-    const int ktiles = (p.k + BK - 1) / BK;
+    // this workgroup's K range (the whole K unless split)
+    const int kbeg = (int)blockIdx.z * p.k_chunk;
+    const int kend = min(p.k, kbeg + p.k_chunk);
+    const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     // operand extents in bytes (the host keeps each below 2^31)
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
@@ -205,8 +208,8 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
 
     if (ktiles > 0) {
-        sa.load(ra, lda, m0, 0, p.m, p.k, tid);
-        sb.load(rb, ldb, n0, 0, p.n, p.k, tid);
+        sa.load(ra, lda, m0, kbeg, p.m, kend, tid);
+        sb.load(rb, ldb, n0, kbeg, p.n, kend, tid);
         sa.store(lds_a[0], tid);
         sb.store(lds_b[0], tid);
     }
@@ -216,8 +219,8 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
         const int cur = kt & 1;
         const bool more = kt + 1 < ktiles;
         if (more) {
-            sa.load(ra, lda, m0, (kt + 1) * BK, p.m, p.k, tid);
-            sb.load(rb, ldb, n0, (kt + 1) * BK, p.n, p.k, tid);
+            sa.load(ra, lda, m0, kbeg + (kt + 1) * BK, p.m, kend, tid);
+            sb.load(rb, ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, tid);
         }
         const float *la = lds_a[cur];
         const float *lb = lds_b[cur];
@@ -244,16 +247,23 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     // ---- epilogue: v = acc (+ C) (+ bias[col]) -> act -> store
     // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
     // holds block row 8*(r/4) + 4*h + r%4, block column j.
+    // A split-K slice stores its raw partial sums to the workspace instead.
+    const bool split = p.splits > 1;
+    if (split) gc = p.ws + ((int64_t)bz * p.splits + blockIdx.z) * (int64_t)p.m * p.n;
+    const int64_t ldc = split ? (int64_t)p.n : p.ldc;
+    const bool accumulate = !split && p.accumulate;
+    const int act = split ? 0 : p.act;
     const int j = lane & 31;
     const int h = lane >> 5;
-    const bool has_bias = p.bias != nullptr;
+    const bool has_bias = !split && p.bias != nullptr;
     float bias_v[FN];
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
         const int col = n0 + wn0 + (BKC ? 32 * fn + j : FN * j + fn);
         bias_v[fn] = (has_bias && col < p.n) ? p.bias[col] : 0.0f;
     }
-    const bool vec_store = !BKC && FN > 1 && p.vec_c && (n0 + wn0 + FN * j + FN <= p.n);
+    const bool vec_c = split ? (p.n % 4 == 0) : (p.vec_c != 0);
+    const bool vec_store = !BKC && FN > 1 && vec_c && (n0 + wn0 + FN * j + FN <= p.n);
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
 #pragma unroll
@@ -261,19 +271,19 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
             const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
             const int row = m0 + wm0 + (AK ? 32 * fm + bi : FM * bi + fm);
             if (row >= p.m) continue;
-            float *crow = gc + (int64_t)row * p.ldc;
+            float *crow = gc + (int64_t)row * ldc;
             if constexpr (!BKC && FN > 1) {
                 if (vec_store) {
                     typedef typename FVec<FN>::type VT;
                     VT *dst = reinterpret_cast<VT *>(crow + n0 + wn0 + FN * j);
                     VT v;
-                    if (p.accumulate) v = *dst;
+                    if (accumulate) v = *dst;
 #pragma unroll
                     for (int fn = 0; fn < FN; ++fn) {
                         float x = acc[fm][fn][r];
-                        if (p.accumulate) x = v[fn] + x;
+                        if (accumulate) x = v[fn] + x;
                         if (has_bias) x = x + bias_v[fn];
-                        v[fn] = zn_activate(x, p.act);
+                        v[fn] = zn_activate(x, act);
                     }
                     *dst = v;
                     continue;
@@ -285,9 +295,9 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
                     const int col = n0 + wn0 + (BKC ? 32 * fn + j : FN * j + fn);
                     if (col >= p.n) continue;
                     float x = acc[fm][fn][r];
-                    if (p.accumulate) x = crow[col] + x;
+                    if (accumulate) x = crow[col] + x;
                     if (has_bias) x = x + bias_v[fn];
-                    crow[col] = zn_activate(x, p.act);
+                    crow[col] = zn_activate(x, act);
                 }
             }
         }
@@ -302,8 +312,8 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
 //   x = 256x128, 8 waves of 64x64   large problems (two workgroups per CU)
 //   l = 128x128, 4 waves of 64x64
 //   n = 128x64,  2 waves of 64x64   narrow N (attention P.V, N = 64)
-//   m = 64x64,   4 waves of 32x32   mid-size problems
-//   s = 32x32,   1 wave             small problems
+//   m = 64x64,   4 waves of 32x32   mid-size problems (BK 32)
+//   s = 32x32,   1 wave             small problems (BK 32)
 // The _v variants stage operands with 16-byte loads (aligned rows,
 // contiguous extents a multiple of 4); the plain ones with 4-byte loads.
 #define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                            \
@@ -323,5 +333,43 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
 ZN_GEMM_TILE(x, 256, 128, 16, 4, 2, 1)
 ZN_GEMM_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_GEMM_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_GEMM_TILE(m, 64, 64, 16, 2, 2, 1)
-ZN_GEMM_TILE(s, 32, 32, 16, 1, 1, 1)
+ZN_GEMM_TILE(m, 64, 64, 32, 2, 2, 1)
+ZN_GEMM_TILE(s, 32, 32, 32, 1, 1, 1)
+
+// Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
+// of ws[s] + bias).  Slices are summed in ascending order, so results do not
+// depend on scheduling.  Grid-stride over batch * m * n (float4 along n when
+// n, ldc and C allow it).
+extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs p) {
+    const int64_t mn = (int64_t)p.m * p.n;
+    const int vw = p.vec ? 4 : 1;
+    const int64_t per_problem = mn / vw;
+    const int64_t total = per_problem * p.batch;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = t / per_problem;
+        const int64_t e = (t - b * per_problem) * vw;  // element index within the problem
+        const int64_t row = e / p.n, col = e - row * p.n;
+        const float *src = p.ws + b * p.splits * mn + e;
+        float *dst = p.c + b * p.stride_c + row * p.ldc + col;
+        if (p.vec) {
+            zn_f32x4 s = *reinterpret_cast<const zn_f32x4 *>(src);
+            for (int z = 1; z < p.splits; ++z) s = s + *reinterpret_cast<const zn_f32x4 *>(src + z * mn);
+            zn_f32x4 v = s;
+            if (p.accumulate) v = *reinterpret_cast<const zn_f32x4 *>(dst) + v;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float x = v[q];
+                if (p.bias) x = x + p.bias[col + q];
+                v[q] = zn_activate(x, p.act);
+            }
+            *reinterpret_cast<zn_f32x4 *>(dst) = v;
+        } else {
+            float s = src[0];
+            for (int z = 1; z < p.splits; ++z) s = s + src[z * mn];
+            float x = p.accumulate ? dst[0] + s : s;
+            if (p.bias) x = x + p.bias[col];
+            dst[0] = zn_activate(x, p.act);
+        }
+    }
+}

@@ -34,11 +34,14 @@ namespace {
 // Macro tiles of the GEMM code object (kernels/gemm_f32.hip).
 enum Tile { kTileX = 0, kTileL, kTileN, kTileM, kTileS, kNumTiles };
 struct TileShape {
-    int bm, bn, threads;
+    int bm, bn, bk, threads;
     const char *suffix;
 };
-constexpr TileShape kTiles[kNumTiles] = {
-    {256, 128, 512, "x"}, {128, 128, 256, "l"}, {128, 64, 128, "n"}, {64, 64, 256, "m"}, {32, 32, 64, "s"}};
+constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
+                                         {128, 128, 16, 256, "l"},
+                                         {128, 64, 16, 128, "n"},
+                                         {64, 64, 32, 256, "m"},
+                                         {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
 enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kNumElt };
@@ -57,6 +60,10 @@ struct zn_ctx {
     hipModule_t gemm_module = nullptr;
     hipModule_t elt_module = nullptr;
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
+    hipFunction_t splitk_reduce = nullptr;
+    // Split-K workspace (partial sums), grown on demand and kept until destroy.
+    float *ws = nullptr;
+    size_t ws_bytes = 0;
     hipFunction_t elt[kNumElt] = {};
     int last_hip_error = 0;
     int forced_tile = -1;  // ZN_TILE_AUTO
@@ -146,6 +153,27 @@ void pool_put(zn_ctx *ctx, float *p, size_t bytes) {
     if (p) ctx->pool[bucket_of(bytes ? bytes : 4)].push_back(p);
 }
 
+// Make the split-K workspace at least `bytes` long.  Growing waits for the
+// stream first, because queued kernels may still use the old buffer.
+int ensure_workspace(zn_ctx *ctx, size_t bytes) {
+    if (ctx->ws_bytes >= bytes) return ZN_OK;
+    size_t want = ctx->ws_bytes ? ctx->ws_bytes : ((size_t)1 << 22);
+    while (want < bytes) want <<= 1;
+    ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail_hip(ctx, e, ZN_ERR_OOM);
+    }
+    ctx->ws = static_cast<float *>(p);
+    ctx->ws_bytes = want;
+    return ZN_OK;
+}
+
 // RAII lease of pooled staging buffers (returned to the cache on scope exit).
 struct Lease {
     zn_ctx *ctx;
@@ -161,9 +189,9 @@ struct Lease {
 
 // Every kernel takes one argument block by value; the runtime copies it into
 // the kernarg segment using the kernel's own metadata.
-int launch(zn_ctx *ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned threads, void *args) {
+int launch(zn_ctx *ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned threads, void *args, unsigned gz = 1) {
     void *params[] = {args};
-    hipError_t e = hipModuleLaunchKernel(f, gx, gy, 1, threads, 1, 1, 0, ctx->stream, params, nullptr);
+    hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, threads, 1, 1, 0, ctx->stream, params, nullptr);
     if (e != hipSuccess) return fail_hip(ctx, e, ZN_ERR_LAUNCH);
     return ZN_OK;
 }
@@ -183,6 +211,22 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t batch) {
     if (tiles(kTileL) >= 4 * cus) return kTileL;
     if (tiles(kTileM) >= cus / 2) return kTileM;
     return kTileS;
+}
+
+// Split-K factor: problems that give fewer than ~4 workgroups per CU (the
+// latency-bound regime: few waves to hide each K slice's load round trip)
+// split K across blockIdx.z, keeping at least two BK slices per split.
+int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k, int64_t batch) {
+    const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+    const TileShape &ts = kTiles[tile];
+    const int64_t tiles = cdiv(m, ts.bm) * cdiv(n, ts.bn) * batch;
+    const int64_t target = 4 * cus;
+    if (tiles >= target / 2) return 1;
+    int64_t splits = target / tiles;
+    const int64_t max_by_k = k / (2 * ts.bk);
+    if (splits > max_by_k) splits = max_by_k;
+    if (splits > 16) splits = 16;
+    return splits < 2 ? 1 : (int)splits;
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -244,16 +288,54 @@ int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const 
 
     int rc = select_device(ctx);
     if (rc) return rc;
-    hipFunction_t f = ctx->gemm[layout][tile][vec ? 1 : 0];
     constexpr int64_t kMaxGridY = 65535;
+    const int64_t chunk_batch = batch < kMaxGridY ? batch : kMaxGridY;
+    int splits = choose_splits(ctx, tile, m, n, k, batch);
+    int64_t k_chunk = k;
+    if (splits > 1) {
+        k_chunk = cdiv(cdiv(k, splits), ts.bk) * ts.bk;
+        splits = (int)cdiv(k, k_chunk);
+        const size_t need = (size_t)splits * (size_t)chunk_batch * (size_t)m * (size_t)n * sizeof(float);
+        if (splits > 1 && ensure_workspace(ctx, need) != ZN_OK) splits = 1;  // fall back to one pass
+        if (splits <= 1) {
+            splits = 1;
+            k_chunk = k;
+        }
+    }
+    args.splits = splits;
+    args.k_chunk = (int32_t)k_chunk;
+    args.ws = ctx->ws;
+    hipFunction_t f = ctx->gemm[layout][tile][vec ? 1 : 0];
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
         ZnGemmArgs part = args;
         part.a = a ? a + b0 * stride_a : nullptr;
         part.b = b ? b + b0 * stride_b : nullptr;
         part.c = c + b0 * stride_c;
-        rc = launch(ctx, f, (unsigned)ntiles, (unsigned)nb, (unsigned)ts.threads, &part);
+        rc = launch(ctx, f, (unsigned)ntiles, (unsigned)nb, (unsigned)ts.threads, &part, (unsigned)splits);
         if (rc) return rc;
+        if (splits > 1) {
+            ZnReduceArgs r;
+            std::memset(&r, 0, sizeof(r));
+            r.ws = ctx->ws;
+            r.c = part.c;
+            r.bias = bias;
+            r.ldc = ldc;
+            r.stride_c = stride_c;
+            r.m = (int32_t)m;
+            r.n = (int32_t)n;
+            r.batch = (int32_t)nb;
+            r.splits = splits;
+            r.accumulate = accumulate ? 1 : 0;
+            r.act = act;
+            r.vec = (n % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(part.c)) ? 1 : 0;
+            const int64_t items = m * n * nb / (r.vec ? 4 : 1);
+            int64_t blocks = cdiv(items, 256);
+            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 8;
+            if (blocks > cap) blocks = cap;
+            rc = launch(ctx, ctx->splitk_reduce, (unsigned)blocks, 1, 256, &r);
+            if (rc) return rc;
+        }
     }
     return ZN_OK;
 }
@@ -397,6 +479,8 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                 if (hipModuleGetFunction(&ctx->gemm[l][t][v], ctx->gemm_module, name) != hipSuccess)
                     return bail(ZN_ERR_SYMBOL);
             }
+    if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess)
+        return bail(ZN_ERR_SYMBOL);
     for (int i = 0; i < kNumElt; ++i)
         if (hipModuleGetFunction(&ctx->elt[i], ctx->elt_module, kEltName[i]) != hipSuccess) return bail(ZN_ERR_SYMBOL);
     *out = ctx;
@@ -410,6 +494,8 @@ int zn_hip_destroy(zn_ctx *ctx) {
     for (auto &kv : ctx->pool)
         for (void *p : kv.second) (void)hipFree(p);
     ctx->pool.clear();
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    ctx->ws = nullptr;
     if (ctx->gemm_module) (void)hipModuleUnload(ctx->gemm_module);
     if (ctx->elt_module) (void)hipModuleUnload(ctx->elt_module);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

@@ -22,6 +22,22 @@ struct ZnGemmArgs {
     int32_t vec_c;             // 1: ldc and C allow vector stores
     int32_t group_m;           // tile rows per raster group
     int32_t xcd_remap;         // 1: gridDim.x % 8 == 0, give each XCD a contiguous tile range
+    // split-K: blockIdx.z = slice of K; splits > 1 writes raw partial sums to
+    // ws[(problem * splits + slice)][m][n] and a reduce kernel finishes C.
+    int32_t splits;
+    int32_t k_chunk;           // K per slice, a multiple of the tile's BK
+    float *ws;
+};
+
+// Split-K reduction: C = act((accumulate ? C : 0) + sum_s ws[s] + bias), the
+// slices summed in ascending order.
+struct ZnReduceArgs {
+    const float *ws;
+    float *c;
+    const float *bias;
+    int64_t ldc, stride_c;
+    int32_t m, n, batch, splits;
+    int32_t accumulate, act, vec;
 };
 
 // Elementwise helpers (fill, copy, bias, activations, bias gradient).
