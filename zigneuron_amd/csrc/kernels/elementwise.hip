@@ -48,7 +48,8 @@ extern "C" __global__ __launch_bounds__(256) void zn_fill_f32(ZnEltArgs p) {
     for (int64_t i = gtid(); i < total; i += gstride()) p.out[i] = p.value;
 }
 
-// out[i] = in0[i]; dwordx4 body when both pointers are 16-byte aligned.
+// out[i] = in0[i]; dwordx4 body when both pointers are 16-byte aligned,
+// four independent 16-byte loads in flight per thread before their stores.
 extern "C" __global__ __launch_bounds__(256) void zn_copy_f32(ZnEltArgs p) {
     const int64_t total = p.rows * p.n;
     const bool aligned = ((reinterpret_cast<uintptr_t>(p.out) | reinterpret_cast<uintptr_t>(p.in0)) & 15) == 0;
@@ -56,8 +57,20 @@ extern "C" __global__ __launch_bounds__(256) void zn_copy_f32(ZnEltArgs p) {
         const int64_t nv = total >> 2;
         const zn_f32x4 *src = reinterpret_cast<const zn_f32x4 *>(p.in0);
         zn_f32x4 *dst = reinterpret_cast<zn_f32x4 *>(p.out);
-        for (int64_t i = gtid(); i < nv; i += gstride()) dst[i] = src[i];
-        for (int64_t i = (nv << 2) + gtid(); i < total; i += gstride()) p.out[i] = p.in0[i];
+        const int64_t stride = gstride();
+        int64_t i = gtid();
+        for (; i + 3 * stride < nv; i += 4 * stride) {
+            const zn_f32x4 v0 = __builtin_nontemporal_load(src + i);
+            const zn_f32x4 v1 = __builtin_nontemporal_load(src + i + stride);
+            const zn_f32x4 v2 = __builtin_nontemporal_load(src + i + 2 * stride);
+            const zn_f32x4 v3 = __builtin_nontemporal_load(src + i + 3 * stride);
+            __builtin_nontemporal_store(v0, dst + i);
+            __builtin_nontemporal_store(v1, dst + i + stride);
+            __builtin_nontemporal_store(v2, dst + i + 2 * stride);
+            __builtin_nontemporal_store(v3, dst + i + 3 * stride);
+        }
+        for (; i < nv; i += stride) dst[i] = src[i];
+        for (int64_t t = (nv << 2) + gtid(); t < total; t += stride) p.out[t] = p.in0[t];
     } else {
         for (int64_t i = gtid(); i < total; i += gstride()) p.out[i] = p.in0[i];
     }
@@ -82,13 +95,21 @@ extern "C" __global__ __launch_bounds__(256) void zn_activation_backward(ZnEltAr
 
 // grad_bias[i] += sum_r gaa[r*n + i], rows ascending exactly like
 // cpuAccumulateBias (src/backend.zig:706-713): one thread per column, so the
-// result is bit-identical to the reference; loads are coalesced across the
-// threads of a row.
+// result is bit-identical to the reference.  Loads are coalesced across the
+// threads of a row and issued eight rows ahead of the (sequential) adds.
 extern "C" __global__ __launch_bounds__(256) void zn_accumulate_bias(ZnEltArgs p) {
     const int64_t col = gtid();
     if (col >= p.n) return;
     float s = p.out[col];
     const float *src = p.in0 + col;
-    for (int64_t r = 0; r < p.rows; ++r) s = s + src[r * p.n];
+    int64_t r = 0;
+    for (; r + 8 <= p.rows; r += 8) {
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = src[(r + q) * p.n];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s = s + v[q];
+    }
+    for (; r < p.rows; ++r) s = s + src[r * p.n];
     p.out[col] = s;
 }
