@@ -185,6 +185,33 @@ int zn_hip_activation_backward(zn_ctx *ctx, int act, const float *y, const float
  * (Backend.accumulateBias, src/backend.zig:649-655, 706-713). */
 int zn_hip_accumulate_bias(zn_ctx *ctx, float *grad_bias, const float *gaa, int64_t rows, int64_t n);
 
+/* ------------------------------------- conv and attention (device pointers) */
+
+/* Backend.im2col (src/backend.zig:3775-3827) on device: NCHW `input` ->
+ * col[(b*OH*OW + oh*OW + ow)][(kh*kW + kw)*C + ic], zero in the padding. */
+int zn_hip_im2col(zn_ctx *ctx, const float *input, float *col, int64_t batch, int64_t channels, int64_t in_h,
+                  int64_t in_w, int64_t k_h, int64_t k_w, int64_t out_h, int64_t out_w, int64_t stride_h,
+                  int64_t stride_w, int64_t pad_h, int64_t pad_w);
+/* cpuConv2dForwardIm2col (src/backend.zig:3881-3950) on device: im2col, then
+ * per image out[OC][OH*OW] = W . col^T + bias[oc] (NCHW output).  Like the
+ * reference, W is read as [OC][(kh*kW + kw)*C + ic], the K order of the
+ * columns.  The col buffer (batch*OH*OW*C*kH*kW floats) comes from the
+ * context's device-buffer cache. */
+int zn_hip_conv2d_forward_im2col(zn_ctx *ctx, const float *input, const float *weights, const float *bias,
+                                 float *output, int64_t batch, int64_t in_channels, int64_t out_channels, int64_t k_h,
+                                 int64_t k_w, int64_t in_h, int64_t in_w, int64_t out_h, int64_t out_w,
+                                 int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w);
+/* Row softmax of scaled scores (out may equal in): out[r,:] = exp(s - max) /
+ * sum(exp(s - max)), s = in[r,:] * scale, the softmax of cpuAttentionForward
+ * (src/backend.zig:3201-3214). */
+int zn_hip_softmax_rows(zn_ctx *ctx, const float *in, float *out, int64_t rows, int64_t n, float scale);
+/* cpuAttentionForward (src/backend.zig:3197-3222) for `batch` independent
+ * single-head problems [seq_len x d_k] laid out back to back (e.g. B*H heads
+ * of a [B,H,S,D] tensor): S = Q.K^T (NT), softmax(S * scale), O = P.V (NN).
+ * Scores (batch*seq_len^2 floats) come from the context's buffer cache. */
+int zn_hip_attention_forward(zn_ctx *ctx, const float *q, const float *k, const float *v, float *out, int64_t batch,
+                             int64_t seq_len, int64_t d_k, float scale);
+
 /* ------------------------------- Backend drop-ins on host slices (sync) */
 /* Each takes the reference method's slices as (pointer, length) pairs and its
  * scalar arguments unchanged, stages through the context's cached device
@@ -229,6 +256,23 @@ int zn_hip_activation_backward_host(zn_ctx *ctx, int act, const float *y, size_t
 /* Backend.accumulateBias (src/backend.zig:649-655): rows = gaa_len / grad_bias_len. */
 int zn_hip_accumulate_bias_host(zn_ctx *ctx, float *grad_bias, size_t grad_bias_len, const float *gaa,
                                 size_t gaa_len);
+
+/* Backend.conv2dForward (src/backend.zig:507-518 -> cpuConv2dForward :3004):
+ * batch = input_len / (C*H*W).  Keeps the reference's switch: when
+ * batch*OC*OH*OW >= 1024 and kH*kW >= 9 the weights are read in the im2col
+ * K order (cpuConv2dForwardIm2col), otherwise as [OC][C][kH][kW] (the direct
+ * branch); both run as im2col + GEMM on the device. */
+int zn_hip_conv2d_forward_host(zn_ctx *ctx, const float *input, size_t input_len, const float *weights,
+                               size_t weights_len, const float *bias, size_t bias_len, float *output,
+                               size_t output_len, size_t in_channels, size_t out_channels, size_t k_h, size_t k_w,
+                               size_t in_h, size_t in_w, size_t out_h, size_t out_w, size_t stride_h, size_t stride_w,
+                               size_t pad_h, size_t pad_w);
+/* Backend.attentionForward (src/backend.zig:631-638): one head [seq_len x
+ * d_k]; `scores` (length >= seq_len, as the reference requires) is not
+ * written: the device keeps its scores in HBM. */
+int zn_hip_attention_forward_host(zn_ctx *ctx, const float *q, size_t q_len, const float *k, size_t k_len,
+                                  const float *v, size_t v_len, float *output, size_t output_len, float *scores,
+                                  size_t scores_len, size_t seq_len, size_t d_k, float scale);
 
 #ifdef __cplusplus
 }

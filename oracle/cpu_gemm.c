@@ -25,6 +25,7 @@
 #include "cpu_gemm.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -289,6 +290,42 @@ void zno_conv2d_im2col_gemm(const float *col, const float *weights, const float 
                 out[(bi * out_channels + oc) * col_height + hw] = sum + bias[oc];
             }
         }
+}
+
+void zno_conv2d_forward(const float *input, size_t input_len, const float *weights, const float *bias, float *out,
+                        size_t channels, size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w,
+                        size_t out_h, size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w) {
+    const size_t batch = input_len / (channels * in_h * in_w);
+    const size_t total_out = batch * out_channels * out_h * out_w;
+    if (total_out >= 1024 && k_h * k_w >= 9) {
+        const size_t col_h = out_h * out_w, col_w = k_h * k_w * channels;
+        float *col = (float *)malloc(batch * col_h * col_w * sizeof(float));
+        if (!col) return;
+        zno_im2col(input, col, batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h, stride_w, pad_h,
+                   pad_w);
+        zno_conv2d_im2col_gemm(col, weights, bias, out, batch, out_channels, col_h, col_w);
+        free(col);
+        return;
+    }
+    for (size_t bi = 0; bi < batch; ++bi)
+        for (size_t oc = 0; oc < out_channels; ++oc)
+            for (size_t oh = 0; oh < out_h; ++oh)
+                for (size_t ow = 0; ow < out_w; ++ow) {
+                    float sum = 0.0f;
+                    const long h0 = (long)(oh * stride_h) - (long)pad_h;
+                    const long w0 = (long)(ow * stride_w) - (long)pad_w;
+                    for (size_t ic = 0; ic < channels; ++ic)
+                        for (size_t kh = 0; kh < k_h; ++kh)
+                            for (size_t kw = 0; kw < k_w; ++kw) {
+                                const long ih = h0 + (long)kh, iw = w0 + (long)kw;
+                                if (ih < 0 || iw < 0 || ih >= (long)in_h || iw >= (long)in_w) continue;
+                                const float prod =
+                                    input[((bi * channels + ic) * in_h + (size_t)ih) * in_w + (size_t)iw] *
+                                    weights[((oc * channels + ic) * k_h + kh) * k_w + kw];
+                                sum = sum + prod;
+                            }
+                    out[((bi * out_channels + oc) * out_h + oh) * out_w + ow] = sum + bias[oc];
+                }
 }
 
 void zno_attention(const float *q, const float *k, const float *v, float *out, float *scores, size_t seq_len,

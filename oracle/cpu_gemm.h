@@ -68,6 +68,13 @@ void zno_im2col(const float *input, float *col, size_t batch, size_t channels, s
  * a 4-lane partial-sum dot of col row with W[oc,:], plus bias, NCHW output. */
 void zno_conv2d_im2col_gemm(const float *col, const float *weights, const float *bias, float *out,
                             size_t batch, size_t out_channels, size_t col_height, size_t col_width);
+/* cpuConv2dForward (src/backend.zig:3004-3045): batch = input_len / (C*H*W);
+ * the im2col + GEMM stage when batch*OC*OH*OW >= 1024 and kH*kW >= 9 (weights
+ * then read as [OC][(kh*kW+kw)*C+ic], like the reference), otherwise the
+ * direct loop with weights [OC][C][kH][kW]. */
+void zno_conv2d_forward(const float *input, size_t input_len, const float *weights, const float *bias, float *out,
+                        size_t channels, size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w,
+                        size_t out_h, size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w);
 /* cpuAttentionForward (src/backend.zig:3197-3222), single head [S x D]. */
 void zno_attention(const float *q, const float *k, const float *v, float *out, float *scores,
                    size_t seq_len, size_t d_k, float scale);

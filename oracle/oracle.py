@@ -51,6 +51,7 @@ def lib() -> ctypes.CDLL:
             "zno_im2col": [P, P] + [S] * 12,
             "zno_conv2d_im2col_gemm": [P, P, P, P, S, S, S, S],
             "zno_attention": [P, P, P, P, P, S, S, F],
+            "zno_conv2d_forward": [P, S, P, P, P] + [S] * 12,
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -173,6 +174,18 @@ def conv2d_im2col_gemm(col, weights, bias, batch, out_channels, col_height, col_
     out = np.empty((batch, out_channels, col_height), np.float32)
     lib().zno_conv2d_im2col_gemm(_p(col), _p(w), _p(bias), _p(out), batch, out_channels,
                                  col_height, col_width)
+    return out
+
+
+def conv2d_forward(x, weights, bias, channels, out_channels, k_h, k_w, in_h, in_w, stride=1, pad=0):
+    """cpuConv2dForward with its naive / im2col switch; returns [batch, OC, OH, OW]."""
+    x, w, bias = _f32(x), _f32(weights), _f32(bias)
+    out_h = (in_h + 2 * pad - k_h) // stride + 1
+    out_w = (in_w + 2 * pad - k_w) // stride + 1
+    batch = x.size // (channels * in_h * in_w)
+    out = np.empty((batch, out_channels, out_h, out_w), np.float32)
+    lib().zno_conv2d_forward(_p(x), x.size, _p(w), _p(bias), _p(out), channels, out_channels, k_h, k_w, in_h, in_w,
+                             out_h, out_w, stride, stride, pad, pad)
     return out
 
 

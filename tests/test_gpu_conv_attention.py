@@ -1,0 +1,213 @@
+"""GPU parity of the convolution (im2col + GEMM) and attention paths.
+
+im2col is pure data movement and must be bit-exact.  The conv GEMM is held to
+the GEMM tolerance 1e-5*sqrt(K), K = C*kH*kW, componentwise against the
+oracle with denominator |col|.|W|^T + |bias|.  Attention is checked stage by
+stage (scores, softmax, P.V) and end to end with the bound derived from the
+stages: a score error e_s <= 1e-5*sqrt(D) (|Q|.|K|^T) * scale perturbs each
+softmax row by at most 2*max(e_s) relatively, and P.V adds 1e-5*sqrt(S); the
+oracle carries the same bound, hence the factor 2.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from _parity import abs_denominator, componentwise_error, normal, tol, uniform
+from gpu_common import announce
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from zigneuron_amd import Context
+    c = Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def backend(ctx):
+    from zigneuron_amd import Backend
+    return Backend(ctx)
+
+
+def out_hw(h, w, k_h, k_w, stride, pad):
+    return (h + 2 * pad - k_h) // stride + 1, (w + 2 * pad - k_w) // stride + 1
+
+
+CONV_CASES = [  # batch, C, H, W, OC, kH, kW, stride, pad
+    (2, 3, 9, 7, 5, 3, 3, 1, 1),
+    (1, 4, 8, 8, 6, 3, 3, 2, 1),
+    (3, 2, 6, 5, 4, 2, 3, 1, 0),
+    (2, 16, 12, 12, 24, 3, 3, 1, 1),
+    (1, 1, 5, 5, 1, 1, 1, 1, 0),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_im2col_bit_exact(ctx, case):
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    x = uniform(np.random.default_rng(1), (B, C, H, W))
+    announce(f"im2col {case}")
+    dx = ctx.to_device(x)
+    dcol = ctx.alloc(B * OH * OW * KH * KW * C).fill(np.nan)
+    ctx.im2col(dx, dcol, B, C, H, W, KH, KW, OH, OW, st, st, pd, pd)
+    got = dcol.download().reshape(B * OH * OW, KH * KW * C)
+    np.testing.assert_array_equal(got, oracle.im2col(x, B, C, H, W, KH, KW, stride=st, pad=pd))
+    dx.close()
+    dcol.close()
+
+
+def conv_check(out, x, w_col, bias, case, what):
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    col = oracle.im2col(x, B, C, H, W, KH, KW, stride=st, pad=pd)
+    ref = oracle.conv2d_im2col_gemm(col, w_col, bias, B, OC, OH * OW, KH * KW * C)
+    k = KH * KW * C
+    for b in range(B):
+        cb = col[b * OH * OW:(b + 1) * OH * OW]
+        den = abs_denominator(w_col, cb.T.copy()) + np.abs(bias.astype(np.float64))[:, None]
+        err = componentwise_error(out[b].reshape(OC, OH * OW), ref[b], den)
+        assert err <= tol(k), f"{what} batch {b}: {err:.3e} > {tol(k):.3e}"
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv2d_forward_im2col_device(ctx, case):
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    rng = np.random.default_rng(2)
+    x, w, bias = uniform(rng, (B, C, H, W)), uniform(rng, (OC, KH * KW * C)), uniform(rng, (OC,))
+    announce(f"conv2d im2col device {case}")
+    dx, dw, db = ctx.to_device(x), ctx.to_device(w), ctx.to_device(bias)
+    do = ctx.alloc(B * OC * OH * OW).fill(np.nan)
+    ctx.conv2d_forward_im2col(dx, dw, db, do, B, C, OC, KH, KW, H, W, OH, OW, st, st, pd, pd)
+    conv_check(do.download().reshape(B, OC, OH, OW), x, w, bias, case, "device")
+    for buf in (dx, dw, db, do):
+        buf.close()
+
+
+@pytest.mark.parametrize("case", CONV_CASES + [(4, 8, 16, 16, 16, 3, 3, 1, 1)])
+def test_backend_conv2d_forward_both_branches(backend, case):
+    """Backend.conv2dForward keeps the reference's size switch: direct semantics
+    (W as [OC][C][kH][kW]) for small problems, im2col semantics otherwise."""
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    rng = np.random.default_rng(3)
+    x, w, bias = uniform(rng, (B, C, H, W)), uniform(rng, (OC, C, KH, KW)), uniform(rng, (OC,))
+    out = np.empty(B * OC * OH * OW, np.float32)
+    announce(f"Backend.conv2dForward {case}")
+    backend.conv2dForward(x, w, bias, out, C, OC, KH, KW, H, W, OH, OW, st, st, pd, pd)
+    ref = oracle.conv2d_forward(x, w, bias, C, OC, KH, KW, H, W, stride=st, pad=pd)
+    im2col_branch = B * OC * OH * OW >= 1024 and KH * KW >= 9
+    w_col = w.reshape(OC, -1) if im2col_branch else np.ascontiguousarray(
+        w.transpose(0, 2, 3, 1).reshape(OC, KH * KW * C))
+    conv_check(out.reshape(B, OC, OH, OW), x, w_col, bias, case, "branch im2col" if im2col_branch else "branch direct")
+    # and the oracle's own switch agrees with the semantics used above
+    np.testing.assert_allclose(out.reshape(ref.shape), ref, rtol=0, atol=tol(KH * KW * C) * np.abs(ref).max() * 4
+                               + 1e-6)
+
+
+def test_softmax_rows_against_fp64(ctx):
+    rng = np.random.default_rng(4)
+    for rows, n, scale in ((7, 1, 1.0), (5, 33, 0.5), (64, 1024, 0.125), (3, 3000, 0.3)):
+        s = (rng.standard_normal((rows, n)) * 4).astype(np.float32)
+        announce(f"softmax {rows}x{n}")
+        d = ctx.to_device(s)
+        o = ctx.alloc(rows * n)
+        ctx.softmax_rows(d, o, rows, n, scale)
+        got = o.download().reshape(rows, n)
+        z = s.astype(np.float64) * np.float32(scale)
+        ref = np.exp(z - z.max(axis=1, keepdims=True))
+        ref /= ref.sum(axis=1, keepdims=True)
+        assert np.all(np.abs(got - ref) <= 8 * np.spacing(ref.astype(np.float32)) + 1e-6 * ref), (rows, n)
+        np.testing.assert_allclose(got.sum(axis=1), 1.0, atol=1e-5)
+        ctx.softmax_rows(d, d, rows, n, scale)  # in place
+        np.testing.assert_array_equal(d.download().reshape(rows, n), got)
+        d.close()
+        o.close()
+
+
+def attention_bound(q, k, v, scale):
+    """Componentwise bound on |out - out_exact| for one head (see module docstring)."""
+    S, D = q.shape
+    q64, k64, v64 = (x.astype(np.float64) for x in (q, k, v))
+    s = q64 @ k64.T * scale
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    e_s = tol(D) * (np.abs(q64) @ np.abs(k64).T) * abs(scale)
+    rel = 2 * e_s.max(axis=1, keepdims=True) + tol(S) + 1e-6
+    return p @ v64, rel * (p @ np.abs(v64))
+
+
+@pytest.mark.parametrize("batch,seq,d", [(1, 17, 8), (3, 64, 16), (2, 200, 64)])
+def test_attention_forward_device(ctx, batch, seq, d):
+    rng = np.random.default_rng(seq)
+    q, k, v = normal(rng, (batch, seq, d)), normal(rng, (batch, seq, d)), normal(rng, (batch, seq, d))
+    scale = 1.0 / np.sqrt(d)
+    announce(f"attention {batch}x{seq}x{d}")
+    dq, dk, dv = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)
+    do = ctx.alloc(batch * seq * d).fill(np.nan)
+    ctx.attention_forward(dq, dk, dv, do, batch, seq, d, scale)
+    out = do.download().reshape(batch, seq, d)
+    for i in range(batch):
+        exact, bound = attention_bound(q[i], k[i], v[i], scale)
+        ref = oracle.attention(q[i], k[i], v[i], seq, d, scale)
+        assert np.all(np.abs(ref - exact) <= bound), "oracle outside its own bound"
+        assert np.all(np.abs(out[i] - ref) <= 2 * bound), f"head {i}"
+    for buf in (dq, dk, dv, do):
+        buf.close()
+
+
+def test_backend_attention_forward_host(backend):
+    rng = np.random.default_rng(11)
+    S, D = 96, 32
+    q, k, v = normal(rng, (S, D)), normal(rng, (S, D)), normal(rng, (S, D))
+    out = np.empty(S * D, np.float32)
+    scores = np.empty(S, np.float32)
+    announce("Backend.attentionForward")
+    backend.attentionForward(q, k, v, out, scores, S, D, 1.0 / np.sqrt(D))
+    exact, bound = attention_bound(q, k, v, 1.0 / np.sqrt(D))
+    ref = oracle.attention(q, k, v, S, D, 1.0 / np.sqrt(D))
+    assert np.all(np.abs(out.reshape(S, D) - ref) <= 2 * bound)
+    from zigneuron_amd import InvalidArgumentError
+    with pytest.raises(InvalidArgumentError):
+        backend.attentionForward(q, k, v, out, np.empty(S - 1, np.float32), S, D, 1.0)
+
+
+def test_c5_attention_end_to_end(ctx):
+    """[B=8,H=16,S=1024,D=64] through the fused entry point; 4 heads checked against the bound."""
+    rng = np.random.default_rng(5)
+    BH, S, D = 128, 1024, 64
+    q, k, v = normal(rng, (BH, S, D)), normal(rng, (BH, S, D)), normal(rng, (BH, S, D))
+    scale = 1.0 / np.sqrt(D)
+    announce("C5 attention end to end")
+    dq, dk, dv = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)
+    do = ctx.alloc(BH * S * D)
+    ctx.attention_forward(dq, dk, dv, do, BH, S, D, scale)
+    out = do.download().reshape(BH, S, D)
+    assert np.all(np.isfinite(out))
+    for i in (0, 41, 90, BH - 1):
+        exact, bound = attention_bound(q[i], k[i], v[i], scale)
+        assert np.all(np.abs(out[i] - exact) <= bound), f"head {i}"
+    for buf in (dq, dk, dv, do):
+        buf.close()
+
+
+def test_c5_conv_end_to_end(ctx):
+    """batch 32, 64->128, 3x3, 56x56, pad 1 through zn_hip_conv2d_forward_im2col; 2 images checked."""
+    rng = np.random.default_rng(6)
+    B, C, H, W, OC = 32, 64, 56, 56, 128
+    x, w, bias = uniform(rng, (B, C, H, W)), uniform(rng, (OC, 9 * C)), uniform(rng, (OC,))
+    announce("C5 conv end to end")
+    dx, dw, db = ctx.to_device(x), ctx.to_device(w), ctx.to_device(bias)
+    do = ctx.alloc(B * OC * H * W)
+    ctx.conv2d_forward_im2col(dx, dw, db, do, B, C, OC, 3, 3, H, W, H, W, 1, 1, 1, 1)
+    out = do.download().reshape(B, OC, H, W)
+    case = (2, C, H, W, OC, 3, 3, 1, 1)
+    conv_check(out[[0, B - 1]], np.ascontiguousarray(x[[0, B - 1]]), w, bias, case, "C5")
+    for buf in (dx, dw, db, do):
+        buf.close()

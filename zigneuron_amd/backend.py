@@ -199,6 +199,26 @@ class Context:
         check(_lib.load().zn_hip_accumulate_bias(self.handle, _dptr(grad_bias), _dptr(gaa), rows, n),
               "zn_hip_accumulate_bias")
 
+    # --- convolution and attention on device pointers
+    def im2col(self, inp, col, batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h=1, stride_w=1,
+               pad_h=0, pad_w=0) -> None:
+        check(_lib.load().zn_hip_im2col(self.handle, _dptr(inp), _dptr(col), batch, channels, in_h, in_w, k_h, k_w,
+                                        out_h, out_w, stride_h, stride_w, pad_h, pad_w), "zn_hip_im2col")
+
+    def conv2d_forward_im2col(self, inp, weights, bias, out, batch, in_channels, out_channels, k_h, k_w, in_h,
+                              in_w, out_h, out_w, stride_h=1, stride_w=1, pad_h=0, pad_w=0) -> None:
+        check(_lib.load().zn_hip_conv2d_forward_im2col(
+            self.handle, _dptr(inp), _dptr(weights), _dptr(bias), _dptr(out), batch, in_channels, out_channels, k_h,
+            k_w, in_h, in_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w), "zn_hip_conv2d_forward_im2col")
+
+    def softmax_rows(self, inp, out, rows, n, scale=1.0) -> None:
+        check(_lib.load().zn_hip_softmax_rows(self.handle, _dptr(inp), _dptr(out), rows, n, float(scale)),
+              "zn_hip_softmax_rows")
+
+    def attention_forward(self, q, k, v, out, batch, seq_len, d_k, scale) -> None:
+        check(_lib.load().zn_hip_attention_forward(self.handle, _dptr(q), _dptr(k), _dptr(v), _dptr(out), batch,
+                                                   seq_len, d_k, float(scale)), "zn_hip_attention_forward")
+
     def close(self) -> None:
         if self.handle:
             _lib.load().zn_hip_destroy(self.handle)
@@ -317,3 +337,21 @@ class Backend:
         gb, gaa = _f32_out(grad_bias), _f32_in(grad_after_act)
         check(_lib.load().zn_hip_accumulate_bias_host(self._h, _ptr(gb), gb.size, _ptr(gaa), gaa.size),
               "zn_hip_accumulate_bias_host")
+
+    # --- convolution and attention
+    def conv2dForward(self, inp, weights, bias, output, in_channels, out_channels, kernel_h, kernel_w, input_h,
+                      input_w, output_h, output_w, stride_h, stride_w, padding_h, padding_w):
+        """Backend.conv2dForward (src/backend.zig:507-518), NCHW, batch = len(input) / (C*H*W)."""
+        x, w, b, out = _f32_in(inp), _f32_in(weights), _f32_in(bias), _f32_out(output)
+        check(_lib.load().zn_hip_conv2d_forward_host(
+            self._h, _ptr(x), x.size, _ptr(w), w.size, _ptr(b), b.size, _ptr(out), out.size, in_channels,
+            out_channels, kernel_h, kernel_w, input_h, input_w, output_h, output_w, stride_h, stride_w, padding_h,
+            padding_w), "zn_hip_conv2d_forward_host")
+
+    def attentionForward(self, q, k, v, output, scores_buffer, seq_len, d_k, scaling_factor):
+        """Backend.attentionForward (src/backend.zig:631-638), one head [seq_len x d_k]."""
+        q, k, v, out = _f32_in(q), _f32_in(k), _f32_in(v), _f32_out(output)
+        sc = _f32_out(scores_buffer)
+        check(_lib.load().zn_hip_attention_forward_host(
+            self._h, _ptr(q), q.size, _ptr(k), k.size, _ptr(v), v.size, _ptr(out), out.size, _ptr(sc), sc.size,
+            seq_len, d_k, float(scaling_factor)), "zn_hip_attention_forward_host")

@@ -113,3 +113,120 @@ extern "C" __global__ __launch_bounds__(256) void zn_accumulate_bias(ZnEltArgs p
     for (; r < p.rows; ++r) s = s + src[r * p.n];
     p.out[col] = s;
 }
+
+// Backend.im2col (src/backend.zig:3775-3827): one thread per element of
+// col[(b*OH*OW + oh*OW + ow)][(kh*KW + kw)*C + ic]; zero outside the padded
+// input.  Writes are coalesced along the col row.
+extern "C" __global__ __launch_bounds__(256) void zn_im2col(ZnIm2colArgs p) {
+    const int64_t kc = (int64_t)p.k_h * p.k_w * p.channels;
+    const int64_t hw = (int64_t)p.out_h * p.out_w;
+    const int64_t total = (int64_t)p.batch * hw * kc;
+    for (int64_t i = gtid(); i < total; i += gstride()) {
+        const int64_t row = i / kc;
+        const int colc = (int)(i - row * kc);
+        const int kpos = colc / p.channels, ic = colc - kpos * p.channels;
+        const int kh = kpos / p.k_w, kw = kpos - kh * p.k_w;
+        const int64_t b = row / hw;
+        const int r = (int)(row - b * hw);
+        const int oh = r / p.out_w, ow = r - oh * p.out_w;
+        const int ih = oh * p.stride_h - p.pad_h + kh;
+        const int iw = ow * p.stride_w - p.pad_w + kw;
+        float v = 0.0f;
+        if (ih >= 0 && iw >= 0 && ih < p.in_h && iw < p.in_w)
+            v = p.input[((b * p.channels + ic) * p.in_h + ih) * (int64_t)p.in_w + iw];
+        p.col[i] = v;
+    }
+}
+
+namespace {
+
+constexpr int kSoftmaxThreads = 256;
+constexpr int kSoftmaxPerThread = 8;  // rows up to 2048 stay in registers
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Block-wide reduction of one value per thread (max or sum).
+template <bool MAX>
+__device__ __forceinline__ float block_reduce(float v, float *red) {
+    v = MAX ? wave_max(v) : wave_sum(v);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x & 63;
+    __syncthreads();  // `red` may still be read from the previous reduction
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < kSoftmaxThreads / 64; ++w) r = MAX ? fmaxf(r, red[w]) : r + red[w];
+    return r;
+}
+
+}  // namespace
+
+// Row softmax of scaled scores, in place allowed (out may equal in0):
+// out[r, :] = exp(s - max) / sum(exp(s - max)) with s = in0[r, :] * value,
+// the steps of cpuAttentionForward (src/backend.zig:3201-3214).  One
+// workgroup per row; rows up to 2048 are read once and kept in registers.
+extern "C" __global__ __launch_bounds__(256) void zn_softmax_rows(ZnEltArgs p) {
+    __shared__ float red[kSoftmaxThreads / 64];
+    const float scale = p.value;
+    for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
+        const float *src = p.in0 + r * p.n;
+        float *dst = p.out + r * p.n;
+        if (p.n <= kSoftmaxThreads * kSoftmaxPerThread) {
+            float v[kSoftmaxPerThread];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int q = 0; q < kSoftmaxPerThread; ++q) {
+                const int64_t i = threadIdx.x + (int64_t)q * kSoftmaxThreads;
+                v[q] = i < p.n ? src[i] * scale : -INFINITY;
+                mx = fmaxf(mx, v[q]);
+            }
+            mx = block_reduce<true>(mx, red);
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kSoftmaxPerThread; ++q) {
+                const int64_t i = threadIdx.x + (int64_t)q * kSoftmaxThreads;
+                v[q] = i < p.n ? expf(v[q] - mx) : 0.0f;
+                sum += v[q];
+            }
+            sum = block_reduce<false>(sum, red);
+#pragma unroll
+            for (int q = 0; q < kSoftmaxPerThread; ++q) {
+                const int64_t i = threadIdx.x + (int64_t)q * kSoftmaxThreads;
+                if (i < p.n) dst[i] = v[q] / sum;
+            }
+        } else {
+            float mx = -INFINITY;
+            for (int64_t i = threadIdx.x; i < p.n; i += kSoftmaxThreads) mx = fmaxf(mx, src[i] * scale);
+            mx = block_reduce<true>(mx, red);
+            float sum = 0.0f;
+            for (int64_t i = threadIdx.x; i < p.n; i += kSoftmaxThreads) {
+                const float e = expf(src[i] * scale - mx);
+                dst[i] = e;
+                sum += e;
+            }
+            sum = block_reduce<false>(sum, red);
+            for (int64_t i = threadIdx.x; i < p.n; i += kSoftmaxThreads) dst[i] = dst[i] / sum;
+        }
+    }
+}
+
+// Conv weights [OC][C][kH][kW] -> [OC][(kh*kW + kw)*C + ic], the K order of
+// the im2col columns (batch = OC).  Lets the im2col GEMM compute the direct
+// convolution of cpuConv2dForward's small-problem branch
+// (src/backend.zig:3019-3041).
+extern "C" __global__ __launch_bounds__(256) void zn_permute_conv_weights(ZnIm2colArgs p) {
+    const int64_t kc = (int64_t)p.k_h * p.k_w * p.channels;
+    const int64_t total = (int64_t)p.batch * kc;
+    for (int64_t i = gtid(); i < total; i += gstride()) {
+        const int64_t oc = i / kc;
+        const int colc = (int)(i - oc * kc);
+        const int kpos = colc / p.channels, ic = colc - kpos * p.channels;
+        p.col[i] = p.input[(oc * p.channels + ic) * (int64_t)(p.k_h * p.k_w) + kpos];
+    }
+}

@@ -256,11 +256,13 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     const int j = lane & 31;
     const int h = lane >> 5;
     const bool has_bias = !split && p.bias != nullptr;
+    const bool col_bias = has_bias && !p.bias_rows;
+    const bool row_bias = has_bias && p.bias_rows;
     float bias_v[FN];
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
         const int col = n0 + wn0 + (BKC ? 32 * fn + j : FN * j + fn);
-        bias_v[fn] = (has_bias && col < p.n) ? p.bias[col] : 0.0f;
+        bias_v[fn] = (col_bias && col < p.n) ? p.bias[col] : 0.0f;
     }
     const bool vec_c = split ? (p.n % 4 == 0) : (p.vec_c != 0);
     const bool vec_store = !BKC && FN > 1 && vec_c && (n0 + wn0 + FN * j + FN <= p.n);
@@ -272,6 +274,7 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
             const int row = m0 + wm0 + (AK ? 32 * fm + bi : FM * bi + fm);
             if (row >= p.m) continue;
             float *crow = gc + (int64_t)row * ldc;
+            const float rb = row_bias ? p.bias[row] : 0.0f;
             if constexpr (!BKC && FN > 1) {
                 if (vec_store) {
                     typedef typename FVec<FN>::type VT;
@@ -282,7 +285,7 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
                     for (int fn = 0; fn < FN; ++fn) {
                         float x = acc[fm][fn][r];
                         if (accumulate) x = v[fn] + x;
-                        if (has_bias) x = x + bias_v[fn];
+                        if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
                         v[fn] = zn_activate(x, act);
                     }
                     *dst = v;
@@ -296,7 +299,7 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
                     if (col >= p.n) continue;
                     float x = acc[fm][fn][r];
                     if (accumulate) x = crow[col] + x;
-                    if (has_bias) x = x + bias_v[fn];
+                    if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
                     crow[col] = zn_activate(x, act);
                 }
             }
@@ -337,7 +340,7 @@ ZN_GEMM_TILE(m, 64, 64, 32, 2, 2, 1)
 ZN_GEMM_TILE(s, 32, 32, 32, 1, 1, 1)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
-// of ws[s] + bias).  Slices are summed in ascending order, so results do not
+// of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not
 // depend on scheduling.  Grid-stride over batch * m * n (float4 along n when
 // n, ldc and C allow it).
 extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs p) {
@@ -360,7 +363,7 @@ extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs 
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 float x = v[q];
-                if (p.bias) x = x + p.bias[col + q];
+                if (p.bias) x = x + p.bias[p.bias_rows ? row : col + q];
                 v[q] = zn_activate(x, p.act);
             }
             *reinterpret_cast<zn_f32x4 *>(dst) = v;
@@ -368,7 +371,7 @@ extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs 
             float s = src[0];
             for (int z = 1; z < p.splits; ++z) s = s + src[z * mn];
             float x = p.accumulate ? dst[0] + s : s;
-            if (p.bias) x = x + p.bias[col];
+            if (p.bias) x = x + p.bias[p.bias_rows ? row : col];
             dst[0] = zn_activate(x, p.act);
         }
     }

@@ -44,10 +44,10 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
                                          {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kNumElt };
-constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",           "zn_copy_f32",
-                                           "zn_add_bias",           "zn_activation_forward",
-                                           "zn_activation_backward", "zn_accumulate_bias"};
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kPermuteW, kNumElt };
+constexpr const char *kEltName[kNumElt] = {
+    "zn_fill_f32",        "zn_copy_f32", "zn_add_bias",     "zn_activation_forward",  "zn_activation_backward",
+    "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows", "zn_permute_conv_weights"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
@@ -134,8 +134,10 @@ int pool_get(zn_ctx *ctx, size_t bytes, float **out) {
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, b);
     if (e != hipSuccess) {
-        // release cached buffers and retry once
+        // release cached buffers (after the stream drains: queued kernels may
+        // still use buffers returned to the cache) and retry once
         (void)hipGetLastError();
+        (void)hipStreamSynchronize(ctx->stream);
         for (auto &kv : ctx->pool)
             for (void *q : kv.second) (void)hipFree(q);
         ctx->pool.clear();
@@ -231,9 +233,9 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
-                int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
-                int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act) {
+int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
+                   int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
+                   int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
     if (layout < ZN_LAYOUT_NN || layout > ZN_LAYOUT_TN) return ZN_ERR_INVALID_ARG;
     if (act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
@@ -278,6 +280,7 @@ int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const 
     args.tiles_n = (int32_t)tiles_n;
     args.accumulate = accumulate ? 1 : 0;
     args.act = act;
+    args.bias_rows = bias_rows ? 1 : 0;
     // 16-byte staging: aligned rows and contiguous extents that are whole float4s
     const bool vec = aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0 && stride_a % 4 == 0 &&
                      stride_b % 4 == 0 && a_row % 4 == 0 && b_row % 4 == 0;
@@ -328,6 +331,7 @@ int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const 
             r.splits = splits;
             r.accumulate = accumulate ? 1 : 0;
             r.act = act;
+            r.bias_rows = bias_rows ? 1 : 0;
             r.vec = (n % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(part.c)) ? 1 : 0;
             const int64_t items = m * n * nb / (r.vec ? 4 : 1);
             int64_t blocks = cdiv(items, 256);
@@ -340,7 +344,15 @@ int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const 
     return ZN_OK;
 }
 
-int elt_launch(zn_ctx *ctx, EltKernel kernel, int64_t work_items, const ZnEltArgs &args) {
+int gemm_launch(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
+                int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
+                int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act) {
+    return gemm_launch_ex(ctx, layout, m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch,
+                          accumulate, bias, act, 0);
+}
+
+template <typename Args>
+int elt_launch(zn_ctx *ctx, EltKernel kernel, int64_t work_items, const Args &args) {
     int rc = select_device(ctx);
     if (rc) return rc;
     const int64_t threads = 256;
@@ -348,7 +360,7 @@ int elt_launch(zn_ctx *ctx, EltKernel kernel, int64_t work_items, const ZnEltArg
     const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
     if (blocks > cap) blocks = cap;  // grid-stride loops cover the rest
     if (blocks < 1) blocks = 1;
-    ZnEltArgs a = args;
+    Args a = args;
     return launch(ctx, ctx->elt[kernel], (unsigned)blocks, 1, (unsigned)threads, &a);
 }
 
@@ -705,6 +717,124 @@ int zn_hip_accumulate_bias(zn_ctx *ctx, float *grad_bias, const float *gaa, int6
     return elt_launch(ctx, kAccBias, n, a);
 }
 
+// ------------------------------------------------- conv and attention
+static bool conv_dims_ok(int64_t batch, int64_t c, int64_t oc, int64_t kh, int64_t kw, int64_t h, int64_t w,
+                         int64_t oh, int64_t ow, int64_t sh, int64_t sw, int64_t ph, int64_t pw) {
+    if (batch < 0 || c < 1 || oc < 1 || kh < 1 || kw < 1 || h < 1 || w < 1 || oh < 0 || ow < 0 || sh < 1 ||
+        sw < 1 || ph < 0 || pw < 0)
+        return false;
+    const int64_t lim = INT_MAX;
+    return batch <= lim && c * kh * kw <= lim && h * w <= lim && oh * ow <= lim && oc <= lim;
+}
+
+int zn_hip_im2col(zn_ctx *ctx, const float *input, float *col, int64_t batch, int64_t channels, int64_t in_h,
+                  int64_t in_w, int64_t k_h, int64_t k_w, int64_t out_h, int64_t out_w, int64_t stride_h,
+                  int64_t stride_w, int64_t pad_h, int64_t pad_w) {
+    if (!ctx || !conv_dims_ok(batch, channels, 1, k_h, k_w, in_h, in_w, out_h, out_w, stride_h, stride_w, pad_h,
+                              pad_w))
+        return ZN_ERR_INVALID_ARG;
+    const int64_t total = batch * out_h * out_w * k_h * k_w * channels;
+    if (total == 0) return ZN_OK;
+    if (!input || !col) return ZN_ERR_INVALID_ARG;
+    ZnIm2colArgs a;
+    a.input = input;
+    a.col = col;
+    a.batch = (int32_t)batch;
+    a.channels = (int32_t)channels;
+    a.in_h = (int32_t)in_h;
+    a.in_w = (int32_t)in_w;
+    a.k_h = (int32_t)k_h;
+    a.k_w = (int32_t)k_w;
+    a.out_h = (int32_t)out_h;
+    a.out_w = (int32_t)out_w;
+    a.stride_h = (int32_t)stride_h;
+    a.stride_w = (int32_t)stride_w;
+    a.pad_h = (int32_t)pad_h;
+    a.pad_w = (int32_t)pad_w;
+    return elt_launch(ctx, kIm2col, total, a);
+}
+
+// im2col into a pooled buffer, then per image one NT GEMM
+// out_b[OC][OH*OW] = W[OC][K] . col_b^T + bias[oc] (a strided batch with W
+// shared), which writes NCHW directly.  `direct_weights` permutes W from
+// [OC][C][kH][kW] into the col K order first (cpuConv2dForward's direct
+// branch); otherwise W is read as [OC][K] like cpuConv2dForwardIm2col.
+static int conv2d_device(zn_ctx *ctx, const float *input, const float *weights, const float *bias, float *output,
+                         int64_t batch, int64_t c, int64_t oc, int64_t kh, int64_t kw, int64_t h, int64_t w,
+                         int64_t oh, int64_t ow, int64_t sh, int64_t sw, int64_t ph, int64_t pw, bool direct_weights) {
+    if (!ctx || !conv_dims_ok(batch, c, oc, kh, kw, h, w, oh, ow, sh, sw, ph, pw)) return ZN_ERR_INVALID_ARG;
+    const int64_t hw = oh * ow, kdim = c * kh * kw;
+    if (batch == 0 || hw == 0) return ZN_OK;
+    if (!input || !weights || !bias || !output) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease col(ctx), wperm(ctx);
+    if ((rc = col.get((size_t)(batch * hw * kdim)))) return rc;
+    if ((rc = zn_hip_im2col(ctx, input, col.ptr, batch, c, h, w, kh, kw, oh, ow, sh, sw, ph, pw))) return rc;
+    const float *wk = weights;
+    if (direct_weights) {
+        if ((rc = wperm.get((size_t)(oc * kdim)))) return rc;
+        ZnIm2colArgs a;
+        std::memset(&a, 0, sizeof(a));
+        a.input = weights;
+        a.col = wperm.ptr;
+        a.batch = (int32_t)oc;
+        a.channels = (int32_t)c;
+        a.k_h = (int32_t)kh;
+        a.k_w = (int32_t)kw;
+        if ((rc = elt_launch(ctx, kPermuteW, oc * kdim, a))) return rc;
+        wk = wperm.ptr;
+    }
+    // A = W [OC x K] shared (stride 0); B = col_b [HW x K] (NT); C_b = out + b*OC*HW, ldc = HW
+    return gemm_launch_ex(ctx, ZN_LAYOUT_NT, oc, hw, kdim, wk, kdim, 0, col.ptr, kdim, hw * kdim, output, hw,
+                          oc * hw, batch, 0, bias, ZN_ACT_LINEAR, 1);
+}
+
+int zn_hip_conv2d_forward_im2col(zn_ctx *ctx, const float *input, const float *weights, const float *bias,
+                                 float *output, int64_t batch, int64_t in_channels, int64_t out_channels, int64_t k_h,
+                                 int64_t k_w, int64_t in_h, int64_t in_w, int64_t out_h, int64_t out_w,
+                                 int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w) {
+    return conv2d_device(ctx, input, weights, bias, output, batch, in_channels, out_channels, k_h, k_w, in_h, in_w,
+                         out_h, out_w, stride_h, stride_w, pad_h, pad_w, false);
+}
+
+int zn_hip_softmax_rows(zn_ctx *ctx, const float *in, float *out, int64_t rows, int64_t n, float scale) {
+    if (!ctx || rows < 0 || n < 0) return ZN_ERR_INVALID_ARG;
+    if (rows == 0 || n == 0) return ZN_OK;
+    if (!in || !out) return ZN_ERR_INVALID_ARG;
+    ZnEltArgs a = {};
+    a.out = out;
+    a.in0 = in;
+    a.rows = rows;
+    a.n = n;
+    a.value = scale;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 8;
+    return launch(ctx, ctx->elt[kSoftmax], (unsigned)(rows < cap ? rows : cap), 1, 256, &a);
+}
+
+// Per problem: S = Q.K^T (NT), P = softmax_rows(S * scale), O = P.V (NN); the
+// score matrices live in a pooled buffer of batch * seq * seq floats.
+int zn_hip_attention_forward(zn_ctx *ctx, const float *q, const float *k, const float *v, float *out, int64_t batch,
+                             int64_t seq_len, int64_t d_k, float scale) {
+    if (!ctx || batch < 0 || seq_len < 0 || d_k < 0) return ZN_ERR_INVALID_ARG;
+    if (batch == 0 || seq_len == 0 || d_k == 0) return ZN_OK;
+    if (!q || !k || !v || !out) return ZN_ERR_INVALID_ARG;
+    if (seq_len > INT_MAX || d_k > INT_MAX) return ZN_ERR_OVERFLOW;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease scores(ctx);
+    if ((rc = scores.get((size_t)(batch * seq_len * seq_len)))) return rc;
+    const int64_t sd = seq_len * d_k, ss = seq_len * seq_len;
+    if ((rc = gemm_launch(ctx, ZN_LAYOUT_NT, seq_len, seq_len, d_k, q, d_k, sd, k, d_k, sd, scores.ptr, seq_len, ss,
+                          batch, 0, nullptr, ZN_ACT_LINEAR)))
+        return rc;
+    if ((rc = zn_hip_softmax_rows(ctx, scores.ptr, scores.ptr, batch * seq_len, seq_len, scale))) return rc;
+    return gemm_launch(ctx, ZN_LAYOUT_NN, seq_len, d_k, seq_len, scores.ptr, seq_len, ss, v, d_k, sd, out, d_k, sd,
+                       batch, 0, nullptr, ZN_ACT_LINEAR);
+}
+
 // ------------------------------------------------ host-slice drop-ins
 int zn_hip_mat_mul(zn_ctx *ctx, const float *a, size_t a_len, const float *b, size_t b_len, float *c, size_t c_len,
                    size_t m, size_t n, size_t k, int accumulate) {
@@ -810,6 +940,65 @@ int zn_hip_accumulate_bias_host(zn_ctx *ctx, float *grad_bias, size_t grad_bias_
         return rc;
     if ((rc = zn_hip_accumulate_bias(ctx, dgb.ptr, dgaa.ptr, (int64_t)rows, (int64_t)grad_bias_len))) return rc;
     return copy_out_and_wait(ctx, grad_bias, dgb.ptr, grad_bias_len);
+}
+
+int zn_hip_conv2d_forward_host(zn_ctx *ctx, const float *input, size_t input_len, const float *weights,
+                               size_t weights_len, const float *bias, size_t bias_len, float *output,
+                               size_t output_len, size_t in_channels, size_t out_channels, size_t k_h, size_t k_w,
+                               size_t in_h, size_t in_w, size_t out_h, size_t out_w, size_t stride_h, size_t stride_w,
+                               size_t pad_h, size_t pad_w) {
+    if (!ctx || in_channels == 0 || in_h == 0 || in_w == 0) return ZN_ERR_INVALID_ARG;
+    const int64_t lim = INT_MAX;
+    if ((int64_t)in_channels > lim || (int64_t)out_channels > lim || (int64_t)k_h > lim || (int64_t)k_w > lim ||
+        (int64_t)in_h > lim || (int64_t)in_w > lim || (int64_t)out_h > lim || (int64_t)out_w > lim)
+        return ZN_ERR_OVERFLOW;
+    const size_t plane = in_channels * in_h * in_w;
+    const size_t batch = input_len / plane;  // batch_size = input.len / (C*H*W) (src/backend.zig:3005)
+    const size_t kdim = in_channels * k_h * k_w;
+    const size_t out_count = batch * out_channels * out_h * out_w;
+    if (weights_len < out_channels * kdim || bias_len < out_channels || output_len < out_count)
+        return ZN_ERR_INVALID_ARG;
+    if (out_count == 0) return ZN_OK;
+    if (!input || !weights || !bias || !output) return ZN_ERR_INVALID_ARG;
+    // the reference's switch (src/backend.zig:3009-3016): im2col semantics for
+    // large problems with kernels of 9+ taps, direct convolution otherwise
+    const bool use_im2col = out_count >= 1024 && k_h * k_w >= 9;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease din(ctx), dw(ctx), db(ctx), dout(ctx);
+    if ((rc = din.get(batch * plane)) || (rc = dw.get(out_channels * kdim)) || (rc = db.get(out_channels)) ||
+        (rc = dout.get(out_count)))
+        return rc;
+    if ((rc = copy_in(ctx, din.ptr, input, batch * plane)) || (rc = copy_in(ctx, dw.ptr, weights, out_channels * kdim)) ||
+        (rc = copy_in(ctx, db.ptr, bias, out_channels)))
+        return rc;
+    rc = conv2d_device(ctx, din.ptr, dw.ptr, db.ptr, dout.ptr, (int64_t)batch, (int64_t)in_channels,
+                       (int64_t)out_channels, (int64_t)k_h, (int64_t)k_w, (int64_t)in_h, (int64_t)in_w, (int64_t)out_h,
+                       (int64_t)out_w, (int64_t)stride_h, (int64_t)stride_w, (int64_t)pad_h, (int64_t)pad_w,
+                       !use_im2col);
+    if (rc) return rc;
+    return copy_out_and_wait(ctx, output, dout.ptr, out_count);
+}
+
+int zn_hip_attention_forward_host(zn_ctx *ctx, const float *q, size_t q_len, const float *k, size_t k_len,
+                                  const float *v, size_t v_len, float *output, size_t output_len, float *scores,
+                                  size_t scores_len, size_t seq_len, size_t d_k, float scale) {
+    (void)scores;  // the device path keeps its scores in HBM
+    if (!ctx) return ZN_ERR_INVALID_ARG;
+    size_t sd;
+    if (!mul_ok(seq_len, d_k, &sd)) return ZN_ERR_OVERFLOW;
+    if (q_len < sd || k_len < sd || v_len < sd || output_len < sd || scores_len < seq_len) return ZN_ERR_INVALID_ARG;
+    if (sd == 0) return ZN_OK;
+    if (!q || !k || !v || !output) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease dq(ctx), dk(ctx), dv(ctx), dout(ctx);
+    if ((rc = dq.get(sd)) || (rc = dk.get(sd)) || (rc = dv.get(sd)) || (rc = dout.get(sd))) return rc;
+    if ((rc = copy_in(ctx, dq.ptr, q, sd)) || (rc = copy_in(ctx, dk.ptr, k, sd)) || (rc = copy_in(ctx, dv.ptr, v, sd)))
+        return rc;
+    if ((rc = zn_hip_attention_forward(ctx, dq.ptr, dk.ptr, dv.ptr, dout.ptr, 1, (int64_t)seq_len, (int64_t)d_k, scale)))
+        return rc;
+    return copy_out_and_wait(ctx, output, dout.ptr, sd);
 }
 
 }  // extern "C"

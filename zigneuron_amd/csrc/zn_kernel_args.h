@@ -27,6 +27,7 @@ struct ZnGemmArgs {
     int32_t splits;
     int32_t k_chunk;           // K per slice, a multiple of the tile's BK
     float *ws;
+    int32_t bias_rows;         // 1: bias is indexed by row (length m), else by column (length n)
 };
 
 // Split-K reduction: C = act((accumulate ? C : 0) + sum_s ws[s] + bias), the
@@ -38,16 +39,25 @@ struct ZnReduceArgs {
     int64_t ldc, stride_c;
     int32_t m, n, batch, splits;
     int32_t accumulate, act, vec;
+    int32_t bias_rows;
 };
 
-// Elementwise helpers (fill, copy, bias, activations, bias gradient).
+// Elementwise helpers (fill, copy, bias, activations, bias gradient, row
+// softmax).
 struct ZnEltArgs {
     float *out;
     const float *in0;
     const float *in1;
     int64_t rows, n;   // n = row length; for flat ops rows*n = element count
-    float value;
+    float value;       // fill value; softmax score scale
     int32_t act;
+};
+
+// im2col (Backend.im2col layout): col[(b*OH*OW + oh*OW + ow)][(kh*KW + kw)*C + ic].
+struct ZnIm2colArgs {
+    const float *input;  // NCHW
+    float *col;
+    int32_t batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w;
 };
 
 #endif
