@@ -115,7 +115,55 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
     run("C5 attn PV NN x128", "nn", 1024, 64, 1024, batch=128)
     run("C5 conv NT 100352x128x576", "nt", 100352, 128, 576)
     out.append(bench_mlp_step(ctx, rng, reps, warmup))
+    out.extend(bench_conv_attention(ctx, rng, reps, warmup))
     return out
+
+
+def bench_conv_attention(ctx, rng, reps, warmup):
+    """C5 through the full device paths: zn_hip_conv2d_forward_im2col (im2col +
+    NCHW GEMM) and zn_hip_attention_forward (QK^T, scale+softmax, P.V)."""
+    res = []
+    B, C, H, W, OC = 32, 64, 56, 56, 128
+    x = ctx.to_device(uniform(rng, (B, C, H, W)))
+    w = ctx.to_device(uniform(rng, (OC, 9 * C)))
+    bias = ctx.to_device(uniform(rng, (OC,)))
+    o = ctx.alloc(B * OC * H * W)
+    ms = time_launches(ctx, lambda: ctx.conv2d_forward_im2col(x, w, bias, o, B, C, OC, 3, 3, H, W, H, W, 1, 1, 1, 1),
+                       reps, warmup)
+    e = config_entry("C5 conv end-to-end (im2col + NCHW GEMM)", "nt", OC, H * W, 9 * C, B, ms, {"bias": True})
+    log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
+    res.append(e)
+    for buf in (x, w, bias, o):
+        buf.close()
+    BH, S, D = 128, 1024, 64
+    q, k, v = (ctx.to_device(uniform(rng, (BH, S, D))) for _ in range(3))
+    o = ctx.alloc(BH * S * D)
+    ms = time_launches(ctx, lambda: ctx.attention_forward(q, k, v, o, BH, S, D, 0.125), reps, warmup)
+    flops = 4.0 * BH * S * S * D
+    e = {"name": "C5 attention end-to-end (QK^T + softmax + PV)", "kernel_ms": round(ms, 5),
+         "tflops": round(flops / (ms * 1e-3) / 1e12, 3), "batch": BH, "seq_len": S, "d_k": D}
+    log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
+    res.append(e)
+    for buf in (q, k, v, o):
+        buf.close()
+    return res
+
+
+def bench_host_slice(ctx, a_h, b_h):
+    """Backend.matMul on host arrays (H2D of A and B, GEMM, D2H of C): the
+    PCIe-inclusive rate of the drop-in boundary, 8192^3."""
+    from zigneuron_amd import Backend
+    be = Backend(ctx)
+    n = a_h.shape[0]
+    c_h = np.empty(n * n, np.float32)
+    be.matMul(a_h, b_h, c_h, n, n, n, False)  # warm the staging cache
+    t = time.perf_counter()
+    be.matMul(a_h, b_h, c_h, n, n, n, False)
+    dt = time.perf_counter() - t
+    e = {"name": "host-slice Backend.matMul 8192^3 (PCIe-inclusive)", "wall_ms": round(dt * 1e3, 3),
+         "tflops": round(2.0 * n ** 3 / dt / 1e12, 3), "bytes_over_pcie": 3 * n * n * 4}
+    log(f"  {e['name']}: {dt * 1e3:.1f} ms -> {e['tflops']:.2f} TFLOP/s")
+    return e
 
 
 def bench_mlp_step(ctx, rng, reps, warmup):
@@ -265,6 +313,7 @@ def main() -> int:
     if not args.no_configs:
         log("per-config kernel times:")
         configs = bench_configs(ctx, rng)
+        configs.append(bench_host_slice(ctx, a_h, b_h))
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle):")
