@@ -325,7 +325,7 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic U[-1,1) operands, seed 42, resident in HBM",
         "config": {"workload": "NN fp32 GEMM 8192x8192x8192 row-major (BASELINE configs[3], C4 large)",
-                   "m": m, "n": n, "k": k, "layout": "nn", "kernel": "zn_sgemm_nn_l",
+                   "m": m, "n": n, "k": k, "layout": "nn", "kernel": "zn_sgemm_nn_x_v",
                    "pct_f32_peak": round(100 * value / PEAK_F32_TFLOPS, 2),
                    "sampled_rows_max_componentwise_err": rel, "tolerance": 1e-5 * np.sqrt(k),
                    "device": ctx.arch, "compute_units": ctx.compute_units},
