@@ -205,12 +205,15 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // once they give every CU two or more workgroups; below that, latency
 // hiding needs more, smaller workgroups (64x64); N <= 64 uses 128x64 so no
 // MFMA block idles; tiny problems use 32x32 to spread over more CUs.
+// A tile whose padding wastes more than a quarter of its MFMA work (for
+// example 256-row tiles over M = 128) is skipped for the next smaller one.
 Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t batch) {
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     auto tiles = [&](Tile t) { return cdiv(m, kTiles[t].bm) * cdiv(n, kTiles[t].bn) * batch; };
+    auto useful = [&](Tile t) { return 4 * m * n * batch >= 3 * tiles(t) * kTiles[t].bm * kTiles[t].bn; };
     if (n <= 64 && tiles(kTileN) >= cus) return kTileN;
-    if (tiles(kTileX) >= 2 * cus) return kTileX;
-    if (tiles(kTileL) >= 4 * cus) return kTileL;
+    if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
+    if (tiles(kTileL) >= 4 * cus && useful(kTileL)) return kTileL;
     if (tiles(kTileM) >= cus / 2) return kTileM;
     return kTileS;
 }
