@@ -115,3 +115,22 @@ def test_dense_init_scales_match_reference():
     w = init_weights(784, 128, "relu", seed=1)
     assert w.dtype == np.float32 and w.shape == (784, 128)
     assert np.abs(w).max() <= (2 / 784) ** 0.5
+
+
+def test_lds_dma_m0_use_is_confined():
+    """The 16-byte staging sets M0 right before each buffer_load ... lds; no other
+    instruction in the GEMM code object may read or write M0."""
+    from zigneuron_amd import _lib
+    path = os.path.join(_lib.LIB_DIR, "zn_gemm_gfx950.s")
+    lines = [ln.split(";")[0].strip() for ln in open(path)]
+    insts = [ln for ln in lines if ln and not ln.startswith((".", "#")) and not ln.endswith(":")]
+    m0_writes = 0
+    for i, ins in enumerate(insts):
+        if re.search(r"\bm0\b", ins):
+            assert re.match(r"s_mov_b32 m0, s\d+$", ins), ins
+            nxt = insts[i + 1]
+            assert nxt.startswith("buffer_load_dwordx4") and nxt.endswith(" lds"), (ins, nxt)
+            m0_writes += 1
+        if " lds" in ins and ins.startswith("buffer_load"):
+            assert re.match(r"s_mov_b32 m0, s\d+$", insts[i - 1]), ins
+    assert m0_writes > 0

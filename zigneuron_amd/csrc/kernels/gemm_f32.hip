@@ -148,28 +148,88 @@ __device__ __forceinline__ void read_frags(const float *lds, int w0, int kg, int
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, bool VEC>
-__device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
-    constexpr int NT = WM * WN * kWave;
-    constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
-    constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 blocks per wave
-    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    static_assert(BK % 8 == 0, "BK must be a multiple of the K group");
-    static_assert(FM == 1 || FM == 2 || FM == 4, "FM");
-    static_assert(FN == 1 || FN == 2 || FN == 4, "FN");
-    typedef Stage<BM, BK, NT, AK, VEC> StageA;
-    typedef Stage<BN, BK, NT, BKC, VEC> StageB;
+// ---- 16-byte staging straight into LDS (the _v kernels) ----------------
+// buffer_load_dwordx4 ... lds writes lane L's 16 bytes to LDS address
+// M0 + 16*L, so one wave instruction fills a contiguous 1 KB block; lanes
+// with an out-of-range offset write zeros (both behaviours checked on
+// gfx950).  The loads are issued from inline assembly so that the compiler
+// does not guard every LDS read with a wait for all outstanding loads; the
+// kernel waits explicitly (vmcnt) before each stage's barrier.  M0 is set
+// immediately before each load and is not used by any other code in these
+// kernels (the build emits the assembly and tests/test_abi.py checks it).
+typedef __attribute__((address_space(3))) void zn_lds_void;
 
-    __shared__ __attribute__((aligned(16))) float lds_a[2][StageA::kLdsFloats];
-    __shared__ __attribute__((aligned(16))) float lds_b[2][StageB::kLdsFloats];
+template <int BX, int BK, int NT, bool KC>
+struct DmaStage {
+    static constexpr int kFloats = BX * BK;
+    static constexpr int kBlocks = kFloats / 256;  // 1 KB blocks per stage
+    static constexpr int kWaves = NT / kWave;
+    static constexpr int kPerWave = kBlocks / kWaves;
+    static_assert(kBlocks % kWaves == 0 && kPerWave >= 1, "1 KB blocks must split evenly over waves");
+    static_assert(!KC || BK == 16 || BK == 32, "K-contiguous DMA staging supports BK 16 and 32");
+    static_assert(KC || BX % 4 == 0, "BX");
 
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
-    const int wm0 = (wave / WN) * WTM;
-    const int wn0 = (wave % WN) * WTN;
+    // K-contiguous operands are stored [x][BK] without padding; chunk c (4
+    // floats) of row x sits in slot c ^ swz(x), which spreads the 16-byte
+    // fragment reads of 8 consecutive rows over all banks.
+    __device__ static __forceinline__ int swz(int row) { return BK == 16 ? ((row >> 1) & 3) : (row & 7); }
 
-    // ---- tile raster: XCD-contiguous ranges, then GROUP_M-row groups
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, int ld, int x0, int k0,
+                                                 int xmax, int kmax, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int q = j * kWaves + wave;  // this wave's 1 KB block
+            int outer, inner;
+            bool ok;
+            if constexpr (KC) {
+                constexpr int cpr = BK / 4, rpb = 256 / BK;  // chunks per row, rows per block
+                const int row = q * rpb + lane / cpr;
+                const int c = (lane % cpr) ^ swz(row);
+                outer = x0 + row;
+                inner = k0 + 4 * c;
+                ok = outer < xmax && inner < kmax;
+            } else {
+                constexpr int cpr = BX / 4, rpb = 256 / BX;  // LDS rows are k, stride BX
+                const int krow = q * rpb + lane / cpr;
+                outer = k0 + krow;
+                inner = x0 + 4 * (lane % cpr);
+                ok = outer < kmax && inner < xmax;
+            }
+            const uint32_t off = ok ? (uint32_t)(outer * ld + inner) * 4u : kOutOfRange;
+            const uint32_t lds_addr =
+                __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + q * 256));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                         :
+                         : "s"(lds_addr), "v"(off), "s"(rsrc)
+                         : "memory");
+        }
+    }
+};
+
+// Fragments from DMA-staged LDS (same lane/K mapping as read_frags).
+template <int BX, int BK, int FX, bool KC>
+__device__ __forceinline__ void read_frags_dma(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
+    if constexpr (KC) {
+        const int i = lane & 31;
+        const int h = lane >> 5;
+#pragma unroll
+        for (int f = 0; f < FX; ++f) {
+            const int row = w0 + 32 * f + i;
+            const int slot = (kg / 4 + h) ^ DmaStage<BX, BK, kWave, true>::swz(row);
+            const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(lds + row * BK + 4 * slot);
+            frag[f][0] = v[0];
+            frag[f][1] = v[1];
+            frag[f][2] = v[2];
+            frag[f][3] = v[3];
+        }
+    } else {
+        read_frags<BX, BK, FX, false>(lds, w0, kg, lane, frag);  // [BK][BX] rows, identical layout
+    }
+}
+
+// Tile coordinates of this workgroup: optional XCD-contiguous remap, then
+// groups of `group_m` tile rows (group_m = 1 is plain row-major order).
+__device__ __forceinline__ void tile_coords(const ZnGemmArgs &p, int &tm, int &tn) {
     int pid = blockIdx.x;
     const int ntiles = p.tiles_m * p.tiles_n;
     if (p.xcd_remap) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
@@ -177,77 +237,20 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     const int first_m = (pid / group_span) * p.group_m;
     const int gsize = min(p.tiles_m - first_m, p.group_m);
     const int in_group = pid % group_span;
-    const int tm = first_m + in_group % gsize;
-    const int tn = in_group / gsize;
-    const int m0 = tm * BM, n0 = tn * BN;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
 
+// Epilogue of one macro tile: v = acc (+ C) (+ bias) -> act -> store.
+// 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
+// holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
+// stores its raw partial sums to the workspace instead.
+template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
+__device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+                                           int m0, int n0, int wm0, int wn0, int lane) {
+    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
     const int64_t bz = blockIdx.y;
-    const float *__restrict__ ga = p.a + bz * p.stride_a;
-    const float *__restrict__ gb = p.b + bz * p.stride_b;
     float *gc = p.c + bz * p.stride_c;
-
-    zn_f32x16 acc[FM][FN];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-
-    StageA sa;
-    StageB sb;
-    // this workgroup's K range (the whole K unless split)
-    const int kbeg = (int)blockIdx.z * p.k_chunk;
-    const int kend = min(p.k, kbeg + p.k_chunk);
-    const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-    const int lda = (int)p.lda, ldb = (int)p.ldb;
-    // operand extents in bytes (the host keeps each below 2^31)
-    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
-    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
-
-    if (ktiles > 0) {
-        sa.load(ra, lda, m0, kbeg, p.m, kend, tid);
-        sb.load(rb, ldb, n0, kbeg, p.n, kend, tid);
-        sa.store(lds_a[0], tid);
-        sb.store(lds_b[0], tid);
-    }
-    __syncthreads();
-
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < ktiles;
-        if (more) {
-            sa.load(ra, lda, m0, kbeg + (kt + 1) * BK, p.m, kend, tid);
-            sb.load(rb, ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, tid);
-        }
-        const float *la = lds_a[cur];
-        const float *lb = lds_b[cur];
-#pragma unroll
-        for (int kg = 0; kg < BK; kg += 8) {
-            float fa[FM][4], fb[FN][4];
-            read_frags<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
-            read_frags<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-                    for (int fn = 0; fn < FN; ++fn)
-                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
-        }
-        if (more) {
-            sa.store(lds_a[cur ^ 1], tid);
-            sb.store(lds_b[cur ^ 1], tid);
-        }
-        __syncthreads();
-    }
-
-    // ---- epilogue: v = acc (+ C) (+ bias[col]) -> act -> store
-    // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
-    // holds block row 8*(r/4) + 4*h + r%4, block column j.
-    // A split-K slice stores its raw partial sums to the workspace instead.
     const bool split = p.splits > 1;
     if (split) gc = p.ws + ((int64_t)bz * p.splits + blockIdx.z) * (int64_t)p.m * p.n;
     const int64_t ldc = split ? (int64_t)p.n : p.ldc;
@@ -307,6 +310,168 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     }
 }
 
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, bool VEC>
+__device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
+    constexpr int NT = WM * WN * kWave;
+    constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+    constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 blocks per wave
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+    static_assert(BK % 8 == 0, "BK must be a multiple of the K group");
+    static_assert(FM == 1 || FM == 2 || FM == 4, "FM");
+    static_assert(FN == 1 || FN == 2 || FN == 4, "FN");
+    typedef Stage<BM, BK, NT, AK, VEC> StageA;
+    typedef Stage<BN, BK, NT, BKC, VEC> StageB;
+
+    __shared__ __attribute__((aligned(16))) float lds_a[2][StageA::kLdsFloats];
+    __shared__ __attribute__((aligned(16))) float lds_b[2][StageB::kLdsFloats];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int wm0 = (wave / WN) * WTM;
+    const int wn0 = (wave % WN) * WTN;
+
+    int tm, tn;
+    tile_coords(p, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int64_t bz = blockIdx.y;
+    const float *__restrict__ ga = p.a + bz * p.stride_a;
+    const float *__restrict__ gb = p.b + bz * p.stride_b;
+
+    zn_f32x16 acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+    StageA sa;
+    StageB sb;
+    // this workgroup's K range (the whole K unless split)
+    const int kbeg = (int)blockIdx.z * p.k_chunk;
+    const int kend = min(p.k, kbeg + p.k_chunk);
+    const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    // operand extents in bytes (the host keeps each below 2^31)
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
+    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
+
+    if (ktiles > 0) {
+        sa.load(ra, lda, m0, kbeg, p.m, kend, tid);
+        sb.load(rb, ldb, n0, kbeg, p.n, kend, tid);
+        sa.store(lds_a[0], tid);
+        sb.store(lds_b[0], tid);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < ktiles;
+        if (more) {
+            sa.load(ra, lda, m0, kbeg + (kt + 1) * BK, p.m, kend, tid);
+            sb.load(rb, ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, tid);
+        }
+        const float *la = lds_a[cur];
+        const float *lb = lds_b[cur];
+#pragma unroll
+        for (int kg = 0; kg < BK; kg += 8) {
+            float fa[FM][4], fb[FN][4];
+            read_frags<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
+            read_frags<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
+        }
+        if (more) {
+            sa.store(lds_a[cur ^ 1], tid);
+            sb.store(lds_b[cur ^ 1], tid);
+        }
+        __syncthreads();
+    }
+
+    store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, m0, n0, wm0, wn0, lane);
+}
+
+// 16-byte-staged GEMM: two LDS stages filled by DMA.  Iteration kt waits
+// for its stage (vmcnt(0) + barrier), refills the other stage with slice
+// kt + 1, then computes slice kt while that load is in flight.
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
+__device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
+    constexpr int NT = WM * WN * kWave;
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int FM = WTM / 32, FN = WTN / 32;
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+    typedef DmaStage<BM, BK, NT, AK> SA;
+    typedef DmaStage<BN, BK, NT, BKC> SB;
+    __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
+    __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+    int tm, tn;
+    tile_coords(p, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int64_t bz = blockIdx.y;
+    const float *ga = p.a + bz * p.stride_a;
+    const float *gb = p.b + bz * p.stride_b;
+
+    zn_f32x16 acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+    const int kbeg = (int)blockIdx.z * p.k_chunk;
+    const int kend = min(p.k, kbeg + p.k_chunk);
+    const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
+    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
+
+    if (ktiles > 0) {
+        SA::issue(ra, lds_a[0], lda, m0, kbeg, p.m, kend, wave, lane);
+        SB::issue(rb, lds_b[0], ldb, n0, kbeg, p.n, kend, wave, lane);
+    }
+    for (int kt = 0; kt < ktiles; ++kt) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of slice kt is in LDS
+        __syncthreads();  // every wave's part is; every wave is done reading slice kt - 1
+        const int cur = kt & 1;
+        if (kt + 1 < ktiles) {
+            SA::issue(ra, lds_a[cur ^ 1], lda, m0, kbeg + (kt + 1) * BK, p.m, kend, wave, lane);
+            SB::issue(rb, lds_b[cur ^ 1], ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, wave, lane);
+        }
+        const float *la = lds_a[cur];
+        const float *lb = lds_b[cur];
+#pragma unroll
+        for (int kg = 0; kg < BK; kg += 8) {
+            float fa[FM][4], fb[FN][4];
+            read_frags_dma<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
+            read_frags_dma<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
+        }
+    }
+    store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, m0, n0, wm0, wn0, lane);
+}
+
 }  // namespace
 
 // Exported kernels: zn_sgemm_<layout>_<tile>[_v].  Layout letters follow
@@ -317,11 +482,15 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
 //   n = 128x64,  2 waves of 64x64   narrow N (attention P.V, N = 64)
 //   m = 64x64,   4 waves of 32x32   mid-size problems (BK 32)
 //   s = 32x32,   1 wave             small problems (BK 32)
-// The _v variants stage operands with 16-byte loads (aligned rows,
-// contiguous extents a multiple of 4); the plain ones with 4-byte loads.
+// The _v variants stage operands with 16-byte loads straight into LDS
+// (aligned rows, contiguous extents a multiple of 4); the plain ones with
+// 4-byte buffer loads through registers.
 #define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                            \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void NAME(ZnGemmArgs p) {        \
-        gemm_tile<BM, BN, BK, WM, WN, AK, BKC, VEC>(p);                                          \
+        if constexpr (VEC)                                                                       \
+            gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC>(p);                                       \
+        else                                                                                     \
+            gemm_tile<BM, BN, BK, WM, WN, AK, BKC, false>(p);                                    \
     }
 
 #define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, VEC, SUFFIX)                            \
