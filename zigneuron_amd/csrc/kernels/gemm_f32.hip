@@ -5,11 +5,14 @@
 // epilogues (:200-295) and a strided-batched grid (blockIdx.y = problem).
 //
 // Structure of one workgroup (BM x BN macro tile, WM x WN waves):
-//  * Global -> registers -> LDS staging, double buffered, one barrier per
-//    BK slice.  Each operand keeps its global layout in LDS: a K-contiguous
-//    operand (A of NN/NT, B of NT) is stored [x][BK+4], an X-contiguous one
-//    (A of TN, B of NN/TN) [BK][X].  No transposing LDS writes are needed;
-//    the layout only changes how lanes read fragments.
+//  * Two LDS stages, one barrier per BK slice: slice kt + 1 is loaded while
+//    slice kt is multiplied.  Aligned operands (the _v kernels) go straight
+//    from HBM into LDS with 16-byte buffer_load ... lds (no registers, no LDS
+//    stores); unaligned ones go through registers with 4-byte buffer loads.
+//  * Each operand keeps its global layout in LDS: a K-contiguous operand (A
+//    of NN/NT, B of NT) is stored by rows of x, an X-contiguous one (A of TN,
+//    B of NN/TN) by rows of k.  NN, NT and TN differ only in how lanes read
+//    fragments, so no transposing LDS writes are needed.
 //  * v_mfma_f32_32x32x2f32: a 32x32 fp32 block per instruction, K = 2 split
 //    over the two lane halves.  The K order inside a group of 8 is permuted
 //    so that lane half h, step t covers k = 8g + 4h + t; a K-contiguous
@@ -17,10 +20,12 @@
 //  * For an X-contiguous operand the 32 lanes of a block own FX consecutive
 //    tile rows/cols (row = FX*i + f), so their fragment is one FX-wide LDS
 //    read and, for B, their output columns are FX-wide vector stores.
-//  * Edges (ragged M, N, K) are zero-filled in LDS: staging uses raw buffer
-//    loads whose masked lanes carry an out-of-range offset and read zero, so
-//    the load path has no branches; zero products leave the sums unchanged,
-//    and stores are predicated.
+//  * Edges (ragged M, N, K) are zero-filled in LDS: masked lanes carry an
+//    out-of-range buffer offset and read (or DMA) zeros, so the load path has
+//    no branches; zero products leave the sums unchanged, and stores are
+//    predicated.
+//  * Split-K: blockIdx.z selects a K range; partial sums go to a workspace
+//    and zn_splitk_reduce adds them in slice order (deterministic).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -58,14 +63,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, u
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// One operand's BX x BK slice: global -> registers -> LDS.
+// One operand's BX x BK slice through registers (the 4-byte-load kernels,
+// for rows that are not 16-byte aligned): global -> registers -> LDS.
 //   KC: element (x, k) at g[x*ld + k]; LDS row x, stride BK + kKPad.
 //  !KC: element (x, k) at g[k*ld + x]; LDS row k, stride BX.
-// VEC: rows are 16-byte aligned and the contiguous extent is a multiple of 4,
-// so a float4 chunk is either wholly inside the problem or wholly outside.
-template <int BX, int BK, int NT, bool KC, bool VEC>
+template <int BX, int BK, int NT, bool KC>
 struct Stage {
-    static constexpr int kChunksPerRow = KC ? BK / 4 : BX / 4;  // float4 chunks along the contiguous dim
+    static constexpr int kChunksPerRow = KC ? BK / 4 : BX / 4;  // 4-float chunks along the contiguous dim
     static constexpr int kLoads = (BX * BK / 4) / NT;            // chunks per thread
     static constexpr int kRowsPerPass = NT / kChunksPerRow;
     static constexpr int kLdsStride = KC ? BK + kKPad : BX;
@@ -90,15 +94,10 @@ struct Stage {
             const bool ok_outer = outer < (KC ? xmax : kmax);
             const int inner_max = KC ? kmax : xmax;
             const uint32_t base = (uint32_t)(outer * ld + inner) * 4u;
-            if constexpr (VEC) {
-                const uint32_t off = (ok_outer && inner < inner_max) ? base : kOutOfRange;
-                r[j] = __builtin_bit_cast(zn_f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
-            } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t off = (ok_outer && inner + e < inner_max) ? base + 4u * e : kOutOfRange;
-                    r[j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
-                }
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t off = (ok_outer && inner + e < inner_max) ? base + 4u * e : kOutOfRange;
+                r[j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
             }
         }
     }
@@ -310,7 +309,7 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, bool VEC>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
 __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
@@ -319,8 +318,8 @@ __device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
     static_assert(BK % 8 == 0, "BK must be a multiple of the K group");
     static_assert(FM == 1 || FM == 2 || FM == 4, "FM");
     static_assert(FN == 1 || FN == 2 || FN == 4, "FN");
-    typedef Stage<BM, BK, NT, AK, VEC> StageA;
-    typedef Stage<BN, BK, NT, BKC, VEC> StageB;
+    typedef Stage<BM, BK, NT, AK> StageA;
+    typedef Stage<BN, BK, NT, BKC> StageB;
 
     __shared__ __attribute__((aligned(16))) float lds_a[2][StageA::kLdsFloats];
     __shared__ __attribute__((aligned(16))) float lds_b[2][StageB::kLdsFloats];
@@ -490,7 +489,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
         if constexpr (VEC)                                                                       \
             gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC>(p);                                       \
         else                                                                                     \
-            gemm_tile<BM, BN, BK, WM, WN, AK, BKC, false>(p);                                    \
+            gemm_tile<BM, BN, BK, WM, WN, AK, BKC>(p);                                           \
     }
 
 #define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, VEC, SUFFIX)                            \
