@@ -127,10 +127,10 @@ def test_lds_dma_m0_use_is_confined():
     m0_writes = 0
     for i, ins in enumerate(insts):
         if re.search(r"\bm0\b", ins):
-            assert re.match(r"s_mov_b32 m0, s\d+$", ins), ins
+            assert re.match(r"s_mov_b32 m0, (s\d+|vcc_lo|vcc_hi)$", ins), ins
             nxt = insts[i + 1]
-            assert nxt.startswith("buffer_load_dwordx4") and nxt.endswith(" lds"), (ins, nxt)
+            assert re.match(r"buffer_load_dword(x4)? ", nxt) and nxt.endswith(" lds"), (ins, nxt)
             m0_writes += 1
         if " lds" in ins and ins.startswith("buffer_load"):
-            assert re.match(r"s_mov_b32 m0, s\d+$", insts[i - 1]), ins
+            assert re.match(r"s_mov_b32 m0, (s\d+|vcc_lo|vcc_hi)$", insts[i - 1]), ins
     assert m0_writes > 0

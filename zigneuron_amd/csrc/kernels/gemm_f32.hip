@@ -6,9 +6,9 @@
 //
 // Structure of one workgroup (BM x BN macro tile, WM x WN waves):
 //  * Two LDS stages, one barrier per BK slice: slice kt + 1 is loaded while
-//    slice kt is multiplied.  Aligned operands (the _v kernels) go straight
-//    from HBM into LDS with 16-byte buffer_load ... lds (no registers, no LDS
-//    stores); unaligned ones go through registers with 4-byte buffer loads.
+//    slice kt is multiplied.  Operands go straight from HBM into LDS with
+//    buffer_load ... lds (no staging registers, no LDS stores): 16-byte
+//    loads for aligned operands (the _v kernels), 4-byte loads otherwise.
 //  * Each operand keeps its global layout in LDS: a K-contiguous operand (A
 //    of NN/NT, B of NT) is stored by rows of x, an X-contiguous one (A of TN,
 //    B of NN/TN) by rows of k.  NN, NT and TN differ only in how lanes read
@@ -38,7 +38,6 @@ typedef float zn_f32x2 __attribute__((ext_vector_type(2)));
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kKPad = 4;  // floats of padding per K-contiguous LDS row (conflict-free 16-byte reads)
 
 template <int N> struct FVec;
 template <> struct FVec<1> { typedef float type; };
@@ -63,149 +62,105 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, u
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// One operand's BX x BK slice through registers (the 4-byte-load kernels,
-// for rows that are not 16-byte aligned): global -> registers -> LDS.
-//   KC: element (x, k) at g[x*ld + k]; LDS row x, stride BK + kKPad.
-//  !KC: element (x, k) at g[k*ld + x]; LDS row k, stride BX.
-template <int BX, int BK, int NT, bool KC>
-struct Stage {
-    static constexpr int kChunksPerRow = KC ? BK / 4 : BX / 4;  // 4-float chunks along the contiguous dim
-    static constexpr int kLoads = (BX * BK / 4) / NT;            // chunks per thread
-    static constexpr int kRowsPerPass = NT / kChunksPerRow;
-    static constexpr int kLdsStride = KC ? BK + kKPad : BX;
-    static constexpr int kLdsFloats = KC ? BX * (BK + kKPad) : BK * BX;
-    static_assert((BX * BK / 4) % NT == 0, "tile must split evenly over threads");
-    static_assert(NT % kChunksPerRow == 0, "rows per pass must be whole");
-
-    zn_f32x4 r[kLoads];
-
-    // Fetch slice k0 of the tile starting at x0; `xmax`/`kmax` bound the
-    // problem.  Branch-free: out-of-problem elements read as zero.
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rsrc, int ld, int x0, int k0, int xmax, int kmax,
-                                         int tid) {
-        const int row0 = tid / kChunksPerRow;
-        const int col = (tid % kChunksPerRow) * 4;
-#pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int row = row0 + j * kRowsPerPass;
-            // (outer, inner) coordinates in the problem: KC -> (x, k), !KC -> (k, x)
-            const int outer = (KC ? x0 : k0) + row;
-            const int inner = (KC ? k0 : x0) + col;
-            const bool ok_outer = outer < (KC ? xmax : kmax);
-            const int inner_max = KC ? kmax : xmax;
-            const uint32_t base = (uint32_t)(outer * ld + inner) * 4u;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t off = (ok_outer && inner + e < inner_max) ? base + 4u * e : kOutOfRange;
-                r[j][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
-            }
-        }
-    }
-
-    __device__ __forceinline__ void store(float *lds, int tid) const {
-        const int row0 = tid / kChunksPerRow;
-        const int col = (tid % kChunksPerRow) * 4;
-#pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int row = row0 + j * kRowsPerPass;
-            *reinterpret_cast<zn_f32x4 *>(lds + row * kLdsStride + col) = r[j];
-        }
-    }
-};
-
-// Fragments for the four MFMA steps of one K group of 8:
-// frag[f][t] = operand value of lane (i = lane % 32, h = lane / 32) for block
-// f at k = kg + 4h + t.
-template <int BX, int BK, int FX, bool KC>
-__device__ __forceinline__ void read_frags(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
+// Fragments for the four MFMA steps of one K group of 8 from an
+// X-contiguous LDS tile [BK][BX]: frag[f][t] is the operand value of lane
+// (i = lane % 32, h = lane / 32) for block f at k = kg + 4h + t; lane i owns
+// rows w0 + FX*i + f, f < FX, so each step is one FX-wide LDS read.
+template <int BX, int BK, int FX>
+__device__ __forceinline__ void read_frags_x(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
     const int i = lane & 31;
     const int h = lane >> 5;
-    if constexpr (KC) {
-        // LDS [BX][BK + pad]: block f covers rows w0 + 32 f + i; one 16-byte read each.
+    typedef typename FVec<FX>::type VT;
 #pragma unroll
-        for (int f = 0; f < FX; ++f) {
-            const zn_f32x4 v =
-                *reinterpret_cast<const zn_f32x4 *>(lds + (w0 + 32 * f + i) * (BK + kKPad) + kg + 4 * h);
-            frag[f][0] = v[0];
-            frag[f][1] = v[1];
-            frag[f][2] = v[2];
-            frag[f][3] = v[3];
-        }
-    } else {
-        // LDS [BK][BX]: lane i owns rows w0 + FX*i + f, f < FX; one FX-wide read per step.
-        typedef typename FVec<FX>::type VT;
+    for (int t = 0; t < 4; ++t) {
+        const VT v = *reinterpret_cast<const VT *>(lds + (kg + 4 * h + t) * BX + w0 + FX * i);
+        if constexpr (FX == 1) {
+            frag[0][t] = v;
+        } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const VT v = *reinterpret_cast<const VT *>(lds + (kg + 4 * h + t) * BX + w0 + FX * i);
-            if constexpr (FX == 1) {
-                frag[0][t] = v;
-            } else {
-#pragma unroll
-                for (int f = 0; f < FX; ++f) frag[f][t] = v[f];
-            }
+            for (int f = 0; f < FX; ++f) frag[f][t] = v[f];
         }
     }
 }
 
-// ---- 16-byte staging straight into LDS (the _v kernels) ----------------
+// ---- operand staging straight into LDS -----------------------------------
 // buffer_load_dwordx4 ... lds writes lane L's 16 bytes to LDS address
-// M0 + 16*L, so one wave instruction fills a contiguous 1 KB block; lanes
-// with an out-of-range offset write zeros (both behaviours checked on
-// gfx950).  The loads are issued from inline assembly so that the compiler
+// M0 + 16*L (buffer_load_dword ... lds: 4 bytes at M0 + 4*L), so one wave
+// instruction fills a contiguous 1 KB (256 B) block; lanes with an
+// out-of-range offset write zeros (both behaviours checked on gfx950).  The loads are issued from inline assembly so that the compiler
 // does not guard every LDS read with a wait for all outstanding loads; the
 // kernel waits explicitly (vmcnt) before each stage's barrier.  M0 is set
 // immediately before each load and is not used by any other code in these
 // kernels (the build emits the assembly and tests/test_abi.py checks it).
 typedef __attribute__((address_space(3))) void zn_lds_void;
 
-template <int BX, int BK, int NT, bool KC>
+template <int BX, int BK, int NT, bool KC, int W>
 struct DmaStage {
+    static_assert(W == 16 || W == 4, "16-byte or 4-byte loads");
     static constexpr int kFloats = BX * BK;
-    static constexpr int kBlocks = kFloats / 256;  // 1 KB blocks per stage
+    static constexpr int kPerInst = W / 4 * kWave;  // floats one wave instruction writes (256 or 64)
+    static constexpr int kInsts = kFloats / kPerInst;
     static constexpr int kWaves = NT / kWave;
-    static constexpr int kPerWave = kBlocks / kWaves;
-    static_assert(kBlocks % kWaves == 0 && kPerWave >= 1, "1 KB blocks must split evenly over waves");
+    static constexpr int kPerWave = kInsts / kWaves;
+    static_assert(kInsts % kWaves == 0 && kPerWave >= 1, "load blocks must split evenly over waves");
     static_assert(!KC || BK == 16 || BK == 32, "K-contiguous DMA staging supports BK 16 and 32");
-    static_assert(KC || BX % 4 == 0, "BX");
 
     // K-contiguous operands are stored [x][BK] without padding; chunk c (4
     // floats) of row x sits in slot c ^ swz(x), which spreads the 16-byte
-    // fragment reads of 8 consecutive rows over all banks.
+    // fragment reads of 8 consecutive rows over all banks.  X-contiguous
+    // operands are stored [BK][BX].
     __device__ static __forceinline__ int swz(int row) { return BK == 16 ? ((row >> 1) & 3) : (row & 7); }
 
     __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, int ld, int x0, int k0,
                                                  int xmax, int kmax, int wave, int lane) {
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
-            const int q = j * kWaves + wave;  // this wave's 1 KB block
+            const int p0 = (j * kWaves + wave) * kPerInst;  // first LDS float this instruction writes
             int outer, inner;
             bool ok;
-            if constexpr (KC) {
-                constexpr int cpr = BK / 4, rpb = 256 / BK;  // chunks per row, rows per block
-                const int row = q * rpb + lane / cpr;
-                const int c = (lane % cpr) ^ swz(row);
-                outer = x0 + row;
-                inner = k0 + 4 * c;
-                ok = outer < xmax && inner < kmax;
+            if constexpr (W == 16) {
+                const int p = p0 + 4 * lane;  // lane writes LDS floats p .. p + 3
+                if constexpr (KC) {
+                    const int row = p / BK;
+                    const int c = ((p % BK) / 4) ^ swz(row);
+                    outer = x0 + row;
+                    inner = k0 + 4 * c;
+                } else {
+                    outer = k0 + p / BX;
+                    inner = x0 + p % BX;
+                }
+                ok = outer < (KC ? xmax : kmax) && inner < (KC ? kmax : xmax);
             } else {
-                constexpr int cpr = BX / 4, rpb = 256 / BX;  // LDS rows are k, stride BX
-                const int krow = q * rpb + lane / cpr;
-                outer = k0 + krow;
-                inner = x0 + 4 * (lane % cpr);
-                ok = outer < kmax && inner < xmax;
+                const int p = p0 + lane;  // lane writes LDS float p
+                if constexpr (KC) {
+                    const int row = p / BK, pos = p % BK;
+                    const int c = (pos / 4) ^ swz(row);
+                    outer = x0 + row;
+                    inner = k0 + 4 * c + (pos & 3);
+                } else {
+                    outer = k0 + p / BX;
+                    inner = x0 + p % BX;
+                }
+                ok = outer < (KC ? xmax : kmax) && inner < (KC ? kmax : xmax);
             }
             const uint32_t off = ok ? (uint32_t)(outer * ld + inner) * 4u : kOutOfRange;
-            const uint32_t lds_addr =
-                __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + q * 256));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(lds_addr), "v"(off), "s"(rsrc)
-                         : "memory");
+            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+            if constexpr (W == 16)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                             :
+                             : "s"(lds_addr), "v"(off), "s"(rsrc)
+                             : "memory");
+            else
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                             :
+                             : "s"(lds_addr), "v"(off), "s"(rsrc)
+                             : "memory");
         }
     }
 };
 
-// Fragments from DMA-staged LDS (same lane/K mapping as read_frags).
+// Fragments from the staged LDS tile: a K-contiguous tile gives one 16-byte
+// read per block (lane i: row w0 + 32f + i, k = kg + 4h .. kg + 4h + 3).
 template <int BX, int BK, int FX, bool KC>
 __device__ __forceinline__ void read_frags_dma(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
     if constexpr (KC) {
@@ -214,7 +169,7 @@ __device__ __forceinline__ void read_frags_dma(const float *lds, int w0, int kg,
 #pragma unroll
         for (int f = 0; f < FX; ++f) {
             const int row = w0 + 32 * f + i;
-            const int slot = (kg / 4 + h) ^ DmaStage<BX, BK, kWave, true>::swz(row);
+            const int slot = (kg / 4 + h) ^ DmaStage<BX, BK, kWave, true, 16>::swz(row);
             const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(lds + row * BK + 4 * slot);
             frag[f][0] = v[0];
             frag[f][1] = v[1];
@@ -222,7 +177,7 @@ __device__ __forceinline__ void read_frags_dma(const float *lds, int w0, int kg,
             frag[f][3] = v[3];
         }
     } else {
-        read_frags<BX, BK, FX, false>(lds, w0, kg, lane, frag);  // [BK][BX] rows, identical layout
+        read_frags_x<BX, BK, FX>(lds, w0, kg, lane, frag);
     }
 }
 
@@ -309,107 +264,18 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
-__device__ __forceinline__ void gemm_tile(const ZnGemmArgs &p) {
-    constexpr int NT = WM * WN * kWave;
-    constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
-    constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 blocks per wave
-    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    static_assert(BK % 8 == 0, "BK must be a multiple of the K group");
-    static_assert(FM == 1 || FM == 2 || FM == 4, "FM");
-    static_assert(FN == 1 || FN == 2 || FN == 4, "FN");
-    typedef Stage<BM, BK, NT, AK> StageA;
-    typedef Stage<BN, BK, NT, BKC> StageB;
-
-    __shared__ __attribute__((aligned(16))) float lds_a[2][StageA::kLdsFloats];
-    __shared__ __attribute__((aligned(16))) float lds_b[2][StageB::kLdsFloats];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
-    const int wm0 = (wave / WN) * WTM;
-    const int wn0 = (wave % WN) * WTN;
-
-    int tm, tn;
-    tile_coords(p, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
-
-    const int64_t bz = blockIdx.y;
-    const float *__restrict__ ga = p.a + bz * p.stride_a;
-    const float *__restrict__ gb = p.b + bz * p.stride_b;
-
-    zn_f32x16 acc[FM][FN];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-
-    StageA sa;
-    StageB sb;
-    // this workgroup's K range (the whole K unless split)
-    const int kbeg = (int)blockIdx.z * p.k_chunk;
-    const int kend = min(p.k, kbeg + p.k_chunk);
-    const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-    const int lda = (int)p.lda, ldb = (int)p.ldb;
-    // operand extents in bytes (the host keeps each below 2^31)
-    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
-    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
-
-    if (ktiles > 0) {
-        sa.load(ra, lda, m0, kbeg, p.m, kend, tid);
-        sb.load(rb, ldb, n0, kbeg, p.n, kend, tid);
-        sa.store(lds_a[0], tid);
-        sb.store(lds_b[0], tid);
-    }
-    __syncthreads();
-
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < ktiles;
-        if (more) {
-            sa.load(ra, lda, m0, kbeg + (kt + 1) * BK, p.m, kend, tid);
-            sb.load(rb, ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, tid);
-        }
-        const float *la = lds_a[cur];
-        const float *lb = lds_b[cur];
-#pragma unroll
-        for (int kg = 0; kg < BK; kg += 8) {
-            float fa[FM][4], fb[FN][4];
-            read_frags<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
-            read_frags<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-                    for (int fn = 0; fn < FN; ++fn)
-                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
-        }
-        if (more) {
-            sa.store(lds_a[cur ^ 1], tid);
-            sb.store(lds_b[cur ^ 1], tid);
-        }
-        __syncthreads();
-    }
-
-    store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, m0, n0, wm0, wn0, lane);
-}
-
-// 16-byte-staged GEMM: two LDS stages filled by DMA.  Iteration kt waits
+// The GEMM main loop: two LDS stages filled by DMA (W = 16: 16-byte loads
+// for aligned operands, W = 4: 4-byte loads otherwise).  Iteration kt waits
 // for its stage (vmcnt(0) + barrier), refills the other stage with slice
 // kt + 1, then computes slice kt while that load is in flight.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int W>
 __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    typedef DmaStage<BM, BK, NT, AK> SA;
-    typedef DmaStage<BN, BK, NT, BKC> SB;
+    typedef DmaStage<BM, BK, NT, AK, W> SA;
+    typedef DmaStage<BN, BK, NT, BKC, W> SB;
     __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
@@ -483,13 +349,10 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
 //   s = 32x32,   1 wave             small problems (BK 32)
 // The _v variants stage operands with 16-byte loads straight into LDS
 // (aligned rows, contiguous extents a multiple of 4); the plain ones with
-// 4-byte buffer loads through registers.
+// 4-byte loads straight into LDS.
 #define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                            \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void NAME(ZnGemmArgs p) {        \
-        if constexpr (VEC)                                                                       \
-            gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC>(p);                                       \
-        else                                                                                     \
-            gemm_tile<BM, BN, BK, WM, WN, AK, BKC>(p);                                           \
+        gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC, (VEC) ? 16 : 4>(p);                           \
     }
 
 #define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, VEC, SUFFIX)                            \
