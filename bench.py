@@ -120,8 +120,8 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
 
 
 def bench_conv_attention(ctx, rng, reps, warmup):
-    """C5 through the full device paths: zn_hip_conv2d_forward_im2col (im2col +
-    NCHW GEMM) and zn_hip_attention_forward (QK^T, scale+softmax, P.V)."""
+    """C5 through the full device paths: zn_hip_conv2d_forward_im2col (implicit
+    GEMM, NCHW output) and zn_hip_attention_forward (QK^T, scale+softmax, P.V)."""
     res = []
     B, C, H, W, OC = 32, 64, 56, 56, 128
     x = ctx.to_device(uniform(rng, (B, C, H, W)))
@@ -130,7 +130,7 @@ def bench_conv_attention(ctx, rng, reps, warmup):
     o = ctx.alloc(B * OC * H * W)
     ms = time_launches(ctx, lambda: ctx.conv2d_forward_im2col(x, w, bias, o, B, C, OC, 3, 3, H, W, H, W, 1, 1, 1, 1),
                        reps, warmup)
-    e = config_entry("C5 conv end-to-end (im2col + NCHW GEMM)", "nt", OC, H * W, 9 * C, B, ms, {"bias": True})
+    e = config_entry("C5 conv end-to-end (implicit GEMM)", "nn", OC, H * W, 9 * C, B, ms, {"bias": True})
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
     res.append(e)
     for buf in (x, w, bias, o):

@@ -192,12 +192,18 @@ int zn_hip_accumulate_bias(zn_ctx *ctx, float *grad_bias, const float *gaa, int6
 int zn_hip_im2col(zn_ctx *ctx, const float *input, float *col, int64_t batch, int64_t channels, int64_t in_h,
                   int64_t in_w, int64_t k_h, int64_t k_w, int64_t out_h, int64_t out_w, int64_t stride_h,
                   int64_t stride_w, int64_t pad_h, int64_t pad_w);
-/* cpuConv2dForwardIm2col (src/backend.zig:3881-3950) on device: im2col, then
- * per image out[OC][OH*OW] = W . col^T + bias[oc] (NCHW output).  Like the
- * reference, W is read as [OC][(kh*kW + kw)*C + ic], the K order of the
- * columns.  The col buffer (batch*OH*OW*C*kH*kW floats) comes from the
- * context's device-buffer cache. */
+/* cpuConv2dForwardIm2col (src/backend.zig:3881-3950) on device, as an
+ * implicit GEMM: per image out[OC][OH*OW] = W . im2col(input)^T + bias[oc]
+ * (NCHW output), the im2col operand gathered on the fly (no col buffer).
+ * Like the reference, W is read as [OC][(kh*kW + kw)*C + ic], the K order of
+ * the im2col columns. */
 int zn_hip_conv2d_forward_im2col(zn_ctx *ctx, const float *input, const float *weights, const float *bias,
+                                 float *output, int64_t batch, int64_t in_channels, int64_t out_channels, int64_t k_h,
+                                 int64_t k_w, int64_t in_h, int64_t in_w, int64_t out_h, int64_t out_w,
+                                 int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w);
+/* The same implicit GEMM with W read as [OC][C][kH][kW]: the convolution of
+ * the direct branch of cpuConv2dForward (src/backend.zig:3019-3041). */
+int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *weights, const float *bias,
                                  float *output, int64_t batch, int64_t in_channels, int64_t out_channels, int64_t k_h,
                                  int64_t k_w, int64_t in_h, int64_t in_w, int64_t out_h, int64_t out_w,
                                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w);
@@ -261,7 +267,7 @@ int zn_hip_accumulate_bias_host(zn_ctx *ctx, float *grad_bias, size_t grad_bias_
  * batch = input_len / (C*H*W).  Keeps the reference's switch: when
  * batch*OC*OH*OW >= 1024 and kH*kW >= 9 the weights are read in the im2col
  * K order (cpuConv2dForwardIm2col), otherwise as [OC][C][kH][kW] (the direct
- * branch); both run as im2col + GEMM on the device. */
+ * branch); both run as the implicit GEMM on the device. */
 int zn_hip_conv2d_forward_host(zn_ctx *ctx, const float *input, size_t input_len, const float *weights,
                                size_t weights_len, const float *bias, size_t bias_len, float *output,
                                size_t output_len, size_t in_channels, size_t out_channels, size_t k_h, size_t k_w,

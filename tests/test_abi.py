@@ -61,8 +61,12 @@ def test_code_objects_hold_every_kernel():
         for t in ("x", "l", "n", "m", "s"):
             for v in ("", "_v"):
                 assert f"zn_sgemm_{lay}_{t}{v}".encode() in gemm
+    for t in ("x", "l", "n", "m", "s"):
+        for v in ("", "_v"):
+            assert f"zn_conv_nn_{t}{v}".encode() in gemm
+    assert b"zn_splitk_reduce" in gemm
     for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",
-              "zn_accumulate_bias"):
+              "zn_accumulate_bias", "zn_im2col", "zn_softmax_rows"):
         assert k.encode() in elt
     assert b"gfx950" in gemm
 

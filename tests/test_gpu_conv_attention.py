@@ -90,6 +90,37 @@ def test_conv2d_forward_im2col_device(ctx, case):
         buf.close()
 
 
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "32x32"])
+@pytest.mark.parametrize("case", [(3, 5, 11, 9, 7, 3, 3, 2, 1), (2, 8, 10, 12, 40, 3, 2, 1, 1)])
+def test_conv_implicit_gemm_every_tile(ctx, case, tile):
+    """Both weight orders through every forced tile: im2col order against the
+    reference's im2col GEMM, OIHW order against the direct convolution."""
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    rng = np.random.default_rng(9)
+    x, w, bias = uniform(rng, (B, C, H, W)), uniform(rng, (OC, C, KH, KW)), uniform(rng, (OC,))
+    dx, db = ctx.to_device(x), ctx.to_device(bias)
+    do = ctx.alloc(B * OC * OH * OW)
+    announce(f"conv implicit tile {tile} {case}")
+    ctx.set_gemm_tile(tile)
+    try:
+        w_col = np.ascontiguousarray(w.transpose(0, 2, 3, 1).reshape(OC, KH * KW * C))
+        dw = ctx.to_device(w_col)
+        do.fill(np.nan)
+        ctx.conv2d_forward_im2col(dx, dw, db, do, B, C, OC, KH, KW, H, W, OH, OW, st, st, pd, pd)
+        conv_check(do.download().reshape(B, OC, OH, OW), x, w_col, bias, case, f"{tile} im2col order")
+        dw.close()
+        dw = ctx.to_device(w)  # OIHW: the same convolution, so the same reference
+        do.fill(np.nan)
+        ctx.conv2d_forward_direct(dx, dw, db, do, B, C, OC, KH, KW, H, W, OH, OW, st, st, pd, pd)
+        conv_check(do.download().reshape(B, OC, OH, OW), x, w_col, bias, case, f"{tile} OIHW order")
+        dw.close()
+    finally:
+        ctx.set_gemm_tile("auto")
+    for buf in (dx, db, do):
+        buf.close()
+
+
 @pytest.mark.parametrize("case", CONV_CASES + [(4, 8, 16, 16, 16, 3, 3, 1, 1)])
 def test_backend_conv2d_forward_both_branches(backend, case):
     """Backend.conv2dForward keeps the reference's size switch: direct semantics

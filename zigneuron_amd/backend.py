@@ -211,6 +211,13 @@ class Context:
             self.handle, _dptr(inp), _dptr(weights), _dptr(bias), _dptr(out), batch, in_channels, out_channels, k_h,
             k_w, in_h, in_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w), "zn_hip_conv2d_forward_im2col")
 
+    def conv2d_forward_direct(self, inp, weights, bias, out, batch, in_channels, out_channels, k_h, k_w, in_h,
+                              in_w, out_h, out_w, stride_h=1, stride_w=1, pad_h=0, pad_w=0) -> None:
+        """Implicit-GEMM convolution with W as [OC][C][kH][kW] (true NCHW convolution)."""
+        check(_lib.load().zn_hip_conv2d_forward_direct(
+            self.handle, _dptr(inp), _dptr(weights), _dptr(bias), _dptr(out), batch, in_channels, out_channels, k_h,
+            k_w, in_h, in_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w), "zn_hip_conv2d_forward_direct")
+
     def softmax_rows(self, inp, out, rows, n, scale=1.0) -> None:
         check(_lib.load().zn_hip_softmax_rows(self.handle, _dptr(inp), _dptr(out), rows, n, float(scale)),
               "zn_hip_softmax_rows")

@@ -215,18 +215,3 @@ extern "C" __global__ __launch_bounds__(256) void zn_softmax_rows(ZnEltArgs p) {
         }
     }
 }
-
-// Conv weights [OC][C][kH][kW] -> [OC][(kh*kW + kw)*C + ic], the K order of
-// the im2col columns (batch = OC).  Lets the im2col GEMM compute the direct
-// convolution of cpuConv2dForward's small-problem branch
-// (src/backend.zig:3019-3041).
-extern "C" __global__ __launch_bounds__(256) void zn_permute_conv_weights(ZnIm2colArgs p) {
-    const int64_t kc = (int64_t)p.k_h * p.k_w * p.channels;
-    const int64_t total = (int64_t)p.batch * kc;
-    for (int64_t i = gtid(); i < total; i += gstride()) {
-        const int64_t oc = i / kc;
-        const int colc = (int)(i - oc * kc);
-        const int kpos = colc / p.channels, ic = colc - kpos * p.channels;
-        p.col[i] = p.input[(oc * p.channels + ic) * (int64_t)(p.k_h * p.k_w) + kpos];
-    }
-}

@@ -159,6 +159,54 @@ struct DmaStage {
     }
 };
 
+// Implicit-GEMM convolution operand: the X-contiguous tile [BK][BN] of the
+// virtual im2col matrix, element (k, n) gathered with 4-byte loads from the
+// NCHW input (out-of-image taps and out-of-problem elements read zero).  One
+// wave instruction covers 64 consecutive n of one k row when BN >= 64, so
+// the filter-tap decode is uniform across the wave.
+template <int BN, int BK, int NT>
+struct ConvGatherStage {
+    static constexpr int kFloats = BN * BK;
+    static constexpr int kInsts = kFloats / kWave;
+    static constexpr int kWaves = NT / kWave;
+    static constexpr int kPerWave = kInsts / kWaves;
+    static_assert(kInsts % kWaves == 0 && kPerWave >= 1, "load blocks must split evenly over waves");
+
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
+                                                 int n0, int k0, int nmax, int kmax, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int p0 = (j * kWaves + wave) * kWave;
+            const int pos = p0 + lane;
+            const int k = k0 + pos / BN;
+            const int n = n0 + pos % BN;
+            int ic, kh, kw;
+            if (g.k_order == 0) {
+                const int kpos = k / g.channels;
+                ic = k - kpos * g.channels;
+                kh = kpos / g.k_w;
+                kw = kpos - kh * g.k_w;
+            } else {
+                const int khw = g.k_h * g.k_w;
+                ic = k / khw;
+                const int kpos = k - ic * khw;
+                kh = kpos / g.k_w;
+                kw = kpos - kh * g.k_w;
+            }
+            const int oh = n / g.out_w, ow = n - oh * g.out_w;
+            const int ih = oh * g.stride_h - g.pad_h + kh;
+            const int iw = ow * g.stride_w - g.pad_w + kw;
+            const bool ok = n < nmax && k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
+            const uint32_t off = ok ? (uint32_t)((ic * g.in_h + ih) * g.in_w + iw) * 4u : kOutOfRange;
+            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                         :
+                         : "s"(lds_addr), "v"(off), "s"(rsrc)
+                         : "memory");
+        }
+    }
+};
+
 // Fragments from the staged LDS tile: a K-contiguous tile gives one 16-byte
 // read per block (lane i: row w0 + 32f + i, k = kg + 4h .. kg + 4h + 3).
 template <int BX, int BK, int FX, bool KC>
@@ -264,18 +312,21 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
     }
 }
 
-// The GEMM main loop: two LDS stages filled by DMA (W = 16: 16-byte loads
-// for aligned operands, W = 4: 4-byte loads otherwise).  Iteration kt waits
+// The GEMM main loop: two LDS stages filled by DMA (WA/WB = 16: 16-byte
+// loads for aligned operands, 4: 4-byte loads otherwise; CONV gathers B from
+// an NCHW image).  Iteration kt waits
 // for its stage (vmcnt(0) + barrier), refills the other stage with slice
 // kt + 1, then computes slice kt while that load is in flight.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int W>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, bool CONV>
 __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    typedef DmaStage<BM, BK, NT, AK, W> SA;
-    typedef DmaStage<BN, BK, NT, BKC, W> SB;
+    static_assert(!CONV || (!BKC && WB == 4), "the convolution operand is X-contiguous and gathered");
+    typedef DmaStage<BM, BK, NT, AK, WA> SA;
+    typedef DmaStage<BN, BK, NT, BKC, WB> SB;
+    typedef ConvGatherStage<BN, BK, NT> SC;
     __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
@@ -302,13 +353,21 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
-    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
+    const uint32_t b_bytes =
+        CONV ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+             : (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
 
+    auto issue_b = [&](float *lds, int k0) {
+        if constexpr (CONV)
+            SC::issue(rb, lds, p.conv, n0, k0, p.n, kend, wave, lane);
+        else
+            SB::issue(rb, lds, ldb, n0, k0, p.n, kend, wave, lane);
+    };
     if (ktiles > 0) {
         SA::issue(ra, lds_a[0], lda, m0, kbeg, p.m, kend, wave, lane);
-        SB::issue(rb, lds_b[0], ldb, n0, kbeg, p.n, kend, wave, lane);
+        issue_b(lds_b[0], kbeg);
     }
     for (int kt = 0; kt < ktiles; ++kt) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of slice kt is in LDS
@@ -316,7 +375,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
         const int cur = kt & 1;
         if (kt + 1 < ktiles) {
             SA::issue(ra, lds_a[cur ^ 1], lda, m0, kbeg + (kt + 1) * BK, p.m, kend, wave, lane);
-            SB::issue(rb, lds_b[cur ^ 1], ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, wave, lane);
+            issue_b(lds_b[cur ^ 1], kbeg + (kt + 1) * BK);
         }
         const float *la = lds_a[cur];
         const float *lb = lds_b[cur];
@@ -352,7 +411,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
 // 4-byte loads straight into LDS.
 #define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                            \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void NAME(ZnGemmArgs p) {        \
-        gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC, (VEC) ? 16 : 4>(p);                           \
+        gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC, (VEC) ? 16 : 4, (VEC) ? 16 : 4, false>(p);    \
     }
 
 #define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, VEC, SUFFIX)                            \
@@ -369,6 +428,24 @@ ZN_GEMM_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_GEMM_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_GEMM_TILE(m, 64, 64, 32, 2, 2, 1)
 ZN_GEMM_TILE(s, 32, 32, 32, 1, 1, 1)
+
+// Implicit-GEMM convolution, per image b = blockIdx.y:
+// out_b[OC][OH*OW] = W[OC][K] . im2col(input_b)^T (+ bias[oc]), an NN GEMM
+// whose B operand is gathered from the NCHW input (ZnConvGeom).  _v: W rows
+// are 16-byte aligned.
+#define ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_conv_nn_##TILE##SUFFIX(ZnGemmArgs p) { \
+        gemm_tile_dma<BM, BN, BK, WM, WN, true, false, WA, 4, true>(p);                          \
+    }
+#define ZN_CONV_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+
+ZN_CONV_TILE(x, 256, 128, 16, 4, 2, 1)
+ZN_CONV_TILE(l, 128, 128, 16, 2, 2, 4)
+ZN_CONV_TILE(n, 128, 64, 16, 2, 1, 1)
+ZN_CONV_TILE(m, 64, 64, 32, 2, 2, 1)
+ZN_CONV_TILE(s, 32, 32, 32, 1, 1, 1)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not

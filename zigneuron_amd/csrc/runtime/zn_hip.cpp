@@ -44,10 +44,10 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
                                          {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kPermuteW, kNumElt };
-constexpr const char *kEltName[kNumElt] = {
-    "zn_fill_f32",        "zn_copy_f32", "zn_add_bias",     "zn_activation_forward",  "zn_activation_backward",
-    "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows", "zn_permute_conv_weights"};
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kNumElt };
+constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", "zn_add_bias",
+                                           "zn_activation_forward", "zn_activation_backward",
+                                           "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
@@ -60,6 +60,7 @@ struct zn_ctx {
     hipModule_t gemm_module = nullptr;
     hipModule_t elt_module = nullptr;
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
+    hipFunction_t conv[kNumTiles][2] = {};     // implicit-GEMM convolution [tile][16-byte W rows]
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -236,9 +237,13 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// `conv` (optional) turns B into the implicit im2col operand of an NCHW
+// image batch (B[k][n] gathered per ZnConvGeom, images `stride_b` apart);
+// the problem is then NN with M = out channels, N = out pixels.
 int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                    int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
-                   int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows) {
+                   int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows,
+                   const ZnConvGeom *conv = nullptr) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
     if (layout < ZN_LAYOUT_NN || layout > ZN_LAYOUT_TN) return ZN_ERR_INVALID_ARG;
     if (act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
@@ -257,7 +262,9 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     const int64_t a_outer = layout == ZN_LAYOUT_TN ? k : m;
     const int64_t b_outer = layout == ZN_LAYOUT_NT ? n : k;
     const int64_t kLimit = (int64_t)INT_MAX / 4;
-    if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || (b_outer - 1) * ldb + b_row > kLimit)) return ZN_ERR_OVERFLOW;
+    const int64_t b_extent = conv ? (int64_t)conv->channels * conv->in_h * conv->in_w : (b_outer - 1) * ldb + b_row;
+    if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || b_extent > kLimit)) return ZN_ERR_OVERFLOW;
+    if (conv && layout != ZN_LAYOUT_NN) return ZN_ERR_INVALID_ARG;
 
     const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, batch);
     const TileShape &ts = kTiles[tile];
@@ -284,9 +291,11 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     args.accumulate = accumulate ? 1 : 0;
     args.act = act;
     args.bias_rows = bias_rows ? 1 : 0;
+    if (conv) args.conv = *conv;
     // 16-byte staging: aligned rows and contiguous extents that are whole float4s
-    const bool vec = aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0 && stride_a % 4 == 0 &&
-                     stride_b % 4 == 0 && a_row % 4 == 0 && b_row % 4 == 0;
+    const bool vec = conv ? (aligned16(a) && lda % 4 == 0 && stride_a % 4 == 0 && a_row % 4 == 0)
+                          : (aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0 && stride_a % 4 == 0 &&
+                             stride_b % 4 == 0 && a_row % 4 == 0 && b_row % 4 == 0);
     args.vec_c = aligned16(c) && ldc % 4 == 0 && stride_c % 4 == 0;
     // Plain row-major tile order: on MI355X it gave the lowest L2-miss traffic
     // for multi-round problems (8192^3 NN: 5.6 GB fetched per launch against
@@ -315,7 +324,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     args.splits = splits;
     args.k_chunk = (int32_t)k_chunk;
     args.ws = ctx->ws;
-    hipFunction_t f = ctx->gemm[layout][tile][vec ? 1 : 0];
+    hipFunction_t f = conv ? ctx->conv[tile][vec ? 1 : 0] : ctx->gemm[layout][tile][vec ? 1 : 0];
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
         ZnGemmArgs part = args;
@@ -498,6 +507,12 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                 if (hipModuleGetFunction(&ctx->gemm[l][t][v], ctx->gemm_module, name) != hipSuccess)
                     return bail(ZN_ERR_SYMBOL);
             }
+    for (int t = 0; t < kNumTiles; ++t)
+        for (int v = 0; v < 2; ++v) {
+            char name[64];
+            std::snprintf(name, sizeof(name), "zn_conv_nn_%s%s", kTiles[t].suffix, v ? "_v" : "");
+            if (hipModuleGetFunction(&ctx->conv[t][v], ctx->gemm_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
+        }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess)
         return bail(ZN_ERR_SYMBOL);
     for (int i = 0; i < kNumElt; ++i)
@@ -761,40 +776,33 @@ int zn_hip_im2col(zn_ctx *ctx, const float *input, float *col, int64_t batch, in
     return elt_launch(ctx, kIm2col, total, a);
 }
 
-// im2col into a pooled buffer, then per image one NT GEMM
-// out_b[OC][OH*OW] = W[OC][K] . col_b^T + bias[oc] (a strided batch with W
-// shared), which writes NCHW directly.  `direct_weights` permutes W from
-// [OC][C][kH][kW] into the col K order first (cpuConv2dForward's direct
-// branch); otherwise W is read as [OC][K] like cpuConv2dForwardIm2col.
+// Implicit-GEMM convolution: per image one NN GEMM
+// out_b[OC][OH*OW] = W[OC][K] . im2col(input_b)^T + bias[oc], the im2col
+// operand gathered on the fly (no col buffer).  k_order 0 reads W in the
+// im2col K order (kh, kw, ic) like cpuConv2dForwardIm2col; 1 reads W as
+// [OC][C][kH][kW] like the direct branch of cpuConv2dForward.
 static int conv2d_device(zn_ctx *ctx, const float *input, const float *weights, const float *bias, float *output,
                          int64_t batch, int64_t c, int64_t oc, int64_t kh, int64_t kw, int64_t h, int64_t w,
-                         int64_t oh, int64_t ow, int64_t sh, int64_t sw, int64_t ph, int64_t pw, bool direct_weights) {
+                         int64_t oh, int64_t ow, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int k_order) {
     if (!ctx || !conv_dims_ok(batch, c, oc, kh, kw, h, w, oh, ow, sh, sw, ph, pw)) return ZN_ERR_INVALID_ARG;
     const int64_t hw = oh * ow, kdim = c * kh * kw;
     if (batch == 0 || hw == 0) return ZN_OK;
     if (!input || !weights || !bias || !output) return ZN_ERR_INVALID_ARG;
-    int rc = select_device(ctx);
-    if (rc) return rc;
-    Lease col(ctx), wperm(ctx);
-    if ((rc = col.get((size_t)(batch * hw * kdim)))) return rc;
-    if ((rc = zn_hip_im2col(ctx, input, col.ptr, batch, c, h, w, kh, kw, oh, ow, sh, sw, ph, pw))) return rc;
-    const float *wk = weights;
-    if (direct_weights) {
-        if ((rc = wperm.get((size_t)(oc * kdim)))) return rc;
-        ZnIm2colArgs a;
-        std::memset(&a, 0, sizeof(a));
-        a.input = weights;
-        a.col = wperm.ptr;
-        a.batch = (int32_t)oc;
-        a.channels = (int32_t)c;
-        a.k_h = (int32_t)kh;
-        a.k_w = (int32_t)kw;
-        if ((rc = elt_launch(ctx, kPermuteW, oc * kdim, a))) return rc;
-        wk = wperm.ptr;
-    }
-    // A = W [OC x K] shared (stride 0); B = col_b [HW x K] (NT); C_b = out + b*OC*HW, ldc = HW
-    return gemm_launch_ex(ctx, ZN_LAYOUT_NT, oc, hw, kdim, wk, kdim, 0, col.ptr, kdim, hw * kdim, output, hw,
-                          oc * hw, batch, 0, bias, ZN_ACT_LINEAR, 1);
+    if (h * w > INT_MAX || c * h * w > INT_MAX / 4) return ZN_ERR_OVERFLOW;
+    ZnConvGeom g;
+    g.channels = (int32_t)c;
+    g.in_h = (int32_t)h;
+    g.in_w = (int32_t)w;
+    g.k_h = (int32_t)kh;
+    g.k_w = (int32_t)kw;
+    g.out_w = (int32_t)ow;
+    g.stride_h = (int32_t)sh;
+    g.stride_w = (int32_t)sw;
+    g.pad_h = (int32_t)ph;
+    g.pad_w = (int32_t)pw;
+    g.k_order = k_order;
+    return gemm_launch_ex(ctx, ZN_LAYOUT_NN, oc, hw, kdim, weights, kdim, 0, input, hw, c * h * w, output, hw,
+                          oc * hw, batch, 0, bias, ZN_ACT_LINEAR, 1, &g);
 }
 
 int zn_hip_conv2d_forward_im2col(zn_ctx *ctx, const float *input, const float *weights, const float *bias,
@@ -802,7 +810,15 @@ int zn_hip_conv2d_forward_im2col(zn_ctx *ctx, const float *input, const float *w
                                  int64_t k_w, int64_t in_h, int64_t in_w, int64_t out_h, int64_t out_w,
                                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w) {
     return conv2d_device(ctx, input, weights, bias, output, batch, in_channels, out_channels, k_h, k_w, in_h, in_w,
-                         out_h, out_w, stride_h, stride_w, pad_h, pad_w, false);
+                         out_h, out_w, stride_h, stride_w, pad_h, pad_w, 0);
+}
+
+int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *weights, const float *bias,
+                                 float *output, int64_t batch, int64_t in_channels, int64_t out_channels, int64_t k_h,
+                                 int64_t k_w, int64_t in_h, int64_t in_w, int64_t out_h, int64_t out_w,
+                                 int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w) {
+    return conv2d_device(ctx, input, weights, bias, output, batch, in_channels, out_channels, k_h, k_w, in_h, in_w,
+                         out_h, out_w, stride_h, stride_w, pad_h, pad_w, 1);
 }
 
 int zn_hip_softmax_rows(zn_ctx *ctx, const float *in, float *out, int64_t rows, int64_t n, float scale) {
@@ -982,7 +998,7 @@ int zn_hip_conv2d_forward_host(zn_ctx *ctx, const float *input, size_t input_len
     rc = conv2d_device(ctx, din.ptr, dw.ptr, db.ptr, dout.ptr, (int64_t)batch, (int64_t)in_channels,
                        (int64_t)out_channels, (int64_t)k_h, (int64_t)k_w, (int64_t)in_h, (int64_t)in_w, (int64_t)out_h,
                        (int64_t)out_w, (int64_t)stride_h, (int64_t)stride_w, (int64_t)pad_h, (int64_t)pad_w,
-                       !use_im2col);
+                       use_im2col ? 0 : 1);
     if (rc) return rc;
     return copy_out_and_wait(ctx, output, dout.ptr, out_count);
 }

@@ -7,6 +7,15 @@
 
 #include <stdint.h>
 
+// Geometry of an implicit-GEMM convolution operand: B[k][n] is the im2col
+// element of output pixel n = oh*out_w + ow and filter tap k, gathered from
+// the NCHW input of one image (blockIdx.y).
+struct ZnConvGeom {
+    int32_t channels, in_h, in_w, k_h, k_w, out_w;
+    int32_t stride_h, stride_w, pad_h, pad_w;
+    int32_t k_order;  // 0: k = (kh*k_w + kw)*channels + ic (im2col order); 1: k = (ic*k_h + kh)*k_w + kw (OIHW)
+};
+
 // One (possibly batched) fp32 GEMM: C = act((acc ? C : 0) + op(A) op(B) + bias).
 struct ZnGemmArgs {
     const float *a;
@@ -28,6 +37,7 @@ struct ZnGemmArgs {
     int32_t k_chunk;           // K per slice, a multiple of the tile's BK
     float *ws;
     int32_t bias_rows;         // 1: bias is indexed by row (length m), else by column (length n)
+    ZnConvGeom conv;           // the zn_conv_* kernels only
 };
 
 // Split-K reduction: C = act((accumulate ? C : 0) + sum_s ws[s] + bias), the
