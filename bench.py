@@ -121,7 +121,7 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
 
 def bench_conv_attention(ctx, rng, reps, warmup):
     """C5 through the full device paths: zn_hip_conv2d_forward_im2col (implicit
-    GEMM, NCHW output) and zn_hip_attention_forward (QK^T, scale+softmax, P.V)."""
+    GEMM, NCHW output) and zn_hip_attention_forward (one fused kernel at d_k = 64)."""
     res = []
     B, C, H, W, OC = 32, 64, 56, 56, 128
     x = ctx.to_device(uniform(rng, (B, C, H, W)))
@@ -140,7 +140,7 @@ def bench_conv_attention(ctx, rng, reps, warmup):
     o = ctx.alloc(BH * S * D)
     ms = time_launches(ctx, lambda: ctx.attention_forward(q, k, v, o, BH, S, D, 0.125), reps, warmup)
     flops = 4.0 * BH * S * S * D
-    e = {"name": "C5 attention end-to-end (QK^T + softmax + PV)", "kernel_ms": round(ms, 5),
+    e = {"name": "C5 attention end-to-end (fused online softmax)", "kernel_ms": round(ms, 5),
          "tflops": round(flops / (ms * 1e-3) / 1e12, 3), "batch": BH, "seq_len": S, "d_k": D}
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
     res.append(e)

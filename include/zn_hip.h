@@ -213,8 +213,11 @@ int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *w
 int zn_hip_softmax_rows(zn_ctx *ctx, const float *in, float *out, int64_t rows, int64_t n, float scale);
 /* cpuAttentionForward (src/backend.zig:3197-3222) for `batch` independent
  * single-head problems [seq_len x d_k] laid out back to back (e.g. B*H heads
- * of a [B,H,S,D] tensor): S = Q.K^T (NT), softmax(S * scale), O = P.V (NN).
- * Scores (batch*seq_len^2 floats) come from the context's buffer cache. */
+ * of a [B,H,S,D] tensor): out = softmax(scale * Q.K^T) . V.  For d_k <= 128
+ * one fused kernel streams K and V past each block of queries (online
+ * softmax) and never writes the scores; larger d_k run QK^T (NT GEMM), the
+ * row softmax and P.V (NN GEMM) with batch*seq_len^2 scores taken from the
+ * context's buffer cache. */
 int zn_hip_attention_forward(zn_ctx *ctx, const float *q, const float *k, const float *v, float *out, int64_t batch,
                              int64_t seq_len, int64_t d_k, float scale);
 

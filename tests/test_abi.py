@@ -55,7 +55,8 @@ def test_code_objects_hold_every_kernel():
     from zigneuron_amd import _lib
     gemm = open(os.path.join(_lib.LIB_DIR, "zn_gemm_gfx950.hsaco"), "rb").read()
     elt = open(os.path.join(_lib.LIB_DIR, "zn_elementwise_gfx950.hsaco"), "rb").read()
-    for blob in (gemm, elt):  # an offload bundle (hipcc --genco) or a bare ELF code object
+    attn = open(os.path.join(_lib.LIB_DIR, "zn_attention_gfx950.hsaco"), "rb").read()
+    for blob in (gemm, elt, attn):  # an offload bundle (hipcc --genco) or a bare ELF code object
         assert blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or blob[:4] == b"\x7fELF"
     for lay in ("nn", "nt", "tn"):
         for t in ("x", "l", "n", "m", "s"):
@@ -68,7 +69,10 @@ def test_code_objects_hold_every_kernel():
     for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",
               "zn_accumulate_bias", "zn_im2col", "zn_softmax_rows"):
         assert k.encode() in elt
-    assert b"gfx950" in gemm
+    for d in (32, 64, 128):
+        for v in ("", "_v"):
+            assert f"zn_attention_d{d}{v}".encode() in attn
+    assert b"gfx950" in gemm and b"gfx950" in attn
 
 
 def test_abi_version_and_status_strings(lib):
@@ -121,11 +125,12 @@ def test_dense_init_scales_match_reference():
     assert np.abs(w).max() <= (2 / 784) ** 0.5
 
 
-def test_lds_dma_m0_use_is_confined():
-    """The 16-byte staging sets M0 right before each buffer_load ... lds; no other
-    instruction in the GEMM code object may read or write M0."""
+@pytest.mark.parametrize("obj", ["zn_gemm_gfx950.s", "zn_attention_gfx950.s"])
+def test_lds_dma_m0_use_is_confined(obj):
+    """The LDS-DMA staging sets M0 right before each buffer_load ... lds; no other
+    instruction in the code objects that use it may read or write M0."""
     from zigneuron_amd import _lib
-    path = os.path.join(_lib.LIB_DIR, "zn_gemm_gfx950.s")
+    path = os.path.join(_lib.LIB_DIR, obj)
     lines = [ln.split(";")[0].strip() for ln in open(path)]
     insts = [ln for ln in lines if ln and not ln.startswith((".", "#")) and not ln.endswith(":")]
     m0_writes = 0

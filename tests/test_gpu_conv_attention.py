@@ -1,14 +1,18 @@
-"""GPU parity of the convolution (im2col + GEMM) and attention paths.
+"""GPU parity of the convolution (im2col, implicit GEMM) and attention paths.
 
 im2col is pure data movement and must be bit-exact.  The conv GEMM is held to
 the GEMM tolerance 1e-5*sqrt(K), K = C*kH*kW, componentwise against the
-oracle with denominator |col|.|W|^T + |bias|.  Attention is checked stage by
-stage (scores, softmax, P.V) and end to end with the bound derived from the
-stages: a score error e_s <= 1e-5*sqrt(D) (|Q|.|K|^T) * scale perturbs each
-softmax row by at most 2*max(e_s) relatively, and P.V adds 1e-5*sqrt(S); the
-oracle carries the same bound, hence the factor 2.
+oracle with denominator |col|.|W|^T + |bias|.  Attention (the fused
+online-softmax kernel for d_k <= 128, the three-kernel path above) is checked
+stage by stage (scores, softmax) and end to end with the bound derived from
+the stages: a score error e_s <= 1e-5*sqrt(D) (|Q|.|K|^T) * scale perturbs
+each softmax row by at most 2*max(e_s) relatively, and the weighted sum over
+S keys (with the fused kernel's per-block rescaling, a few ulp) adds
+1e-5*sqrt(S) + 1e-6; the oracle carries the same bound, hence the factor 2.
 """
 from __future__ import annotations
+
+import ctypes
 
 import numpy as np
 import pytest
@@ -91,7 +95,9 @@ def test_conv2d_forward_im2col_device(ctx, case):
 
 
 @pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "32x32"])
-@pytest.mark.parametrize("case", [(3, 5, 11, 9, 7, 3, 3, 2, 1), (2, 8, 10, 12, 40, 3, 2, 1, 1)])
+@pytest.mark.parametrize("case", [(3, 5, 11, 9, 7, 3, 3, 2, 1), (2, 8, 10, 12, 40, 3, 2, 1, 1),
+                                  (2, 7, 13, 11, 20, 5, 5, 2, 2), (1, 64, 9, 9, 33, 1, 1, 1, 0),
+                                  (2, 4, 17, 19, 8, 7, 7, 3, 3), (1, 1, 70, 70, 3, 4, 4, 1, 2)])
 def test_conv_implicit_gemm_every_tile(ctx, case, tile):
     """Both weight orders through every forced tile: im2col order against the
     reference's im2col GEMM, OIHW order against the direct convolution."""
@@ -174,8 +180,11 @@ def attention_bound(q, k, v, scale):
     return p @ v64, rel * (p @ np.abs(v64))
 
 
-@pytest.mark.parametrize("batch,seq,d", [(1, 17, 8), (3, 64, 16), (2, 200, 64)])
+@pytest.mark.parametrize("batch,seq,d", [(1, 17, 8), (3, 64, 16), (2, 200, 64), (1, 1, 5), (2, 129, 32),
+                                         (2, 50, 17), (2, 77, 100), (1, 300, 128), (1, 65, 160), (1, 130, 129)])
 def test_attention_forward_device(ctx, batch, seq, d):
+    """Fused kernel for every padded head dim (32/64/128, 16-byte and 4-byte
+    I/O, ragged query and key blocks); d_k > 128 takes the three-kernel path."""
     rng = np.random.default_rng(seq)
     q, k, v = normal(rng, (batch, seq, d)), normal(rng, (batch, seq, d)), normal(rng, (batch, seq, d))
     scale = 1.0 / np.sqrt(d)
@@ -190,6 +199,50 @@ def test_attention_forward_device(ctx, batch, seq, d):
         assert np.all(np.abs(ref - exact) <= bound), "oracle outside its own bound"
         assert np.all(np.abs(out[i] - ref) <= 2 * bound), f"head {i}"
     for buf in (dq, dk, dv, do):
+        buf.close()
+
+
+@pytest.mark.parametrize("scale", [2.0, -0.7, 0.0])
+def test_attention_online_softmax_rescaling(ctx, scale):
+    """Large, negative and zero score scales: the running maximum moves across
+    key blocks (keys sorted so later blocks hold larger scores), and a zero
+    scale gives the plain mean of V."""
+    rng = np.random.default_rng(3)
+    S, D = 515, 64
+    q, k, v = normal(rng, (1, S, D)), normal(rng, (1, S, D)), normal(rng, (1, S, D))
+    order = np.argsort(k[0] @ q[0].mean(axis=0))
+    k = np.ascontiguousarray(k[:, order])
+    announce(f"attention rescaling scale={scale}")
+    dq, dk, dv = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)
+    do = ctx.alloc(S * D).fill(np.nan)
+    ctx.attention_forward(dq, dk, dv, do, 1, S, D, scale)
+    out = do.download().reshape(S, D)
+    exact, bound = attention_bound(q[0], k[0], v[0], scale)
+    assert np.all(np.abs(out - exact) <= bound)
+    if scale == 0.0:
+        np.testing.assert_allclose(out, np.broadcast_to(v[0].astype(np.float64).mean(axis=0), (S, D)), atol=1e-5)
+    for buf in (dq, dk, dv, do):
+        buf.close()
+
+
+def test_attention_unaligned_pointers(ctx):
+    """Q, K, V and O one float off 16-byte alignment select the 4-byte kernel."""
+    rng = np.random.default_rng(4)
+    S, D = 150, 64
+    q, k, v = normal(rng, (S, D)), normal(rng, (S, D)), normal(rng, (S, D))
+    bufs = [ctx.alloc(S * D + 1) for _ in range(4)]
+    for buf, x in zip(bufs[:3], (q, k, v)):
+        buf.upload(np.concatenate([np.zeros(1, np.float32), x.ravel()]))
+    bufs[3].fill(np.nan)
+    announce("attention unaligned")
+    from zigneuron_amd import _lib
+    from zigneuron_amd._lib import check
+    check(_lib.load().zn_hip_attention_forward(ctx.handle, *(b.offset(1) for b in bufs), 1, S, D,
+                                               ctypes.c_float(0.125)), "attention")
+    out = bufs[3].download()[1:].reshape(S, D)
+    exact, bound = attention_bound(q, k, v, 0.125)
+    assert np.all(np.abs(out - exact) <= bound)
+    for buf in bufs:
         buf.close()
 
 

@@ -31,18 +31,9 @@
 
 #include "../zn_kernel_args.h"
 
-typedef float zn_f32x16 __attribute__((ext_vector_type(16)));
-typedef float zn_f32x4 __attribute__((ext_vector_type(4)));
-typedef float zn_f32x2 __attribute__((ext_vector_type(2)));
+#include "zn_mfma_stage.h"
 
 namespace {
-
-constexpr int kWave = 64;
-
-template <int N> struct FVec;
-template <> struct FVec<1> { typedef float type; };
-template <> struct FVec<2> { typedef zn_f32x2 type; };
-template <> struct FVec<4> { typedef zn_f32x4 type; };
 
 __device__ __forceinline__ float zn_activate(float v, int act) {
     switch (act) {
@@ -53,117 +44,21 @@ __device__ __forceinline__ float zn_activate(float v, int act) {
     }
 }
 
-// Raw buffer descriptor over one operand of one problem: loads at byte
-// offsets >= `bytes` return zero, so masked elements use an out-of-range
-// offset instead of a branch.
-constexpr uint32_t kOutOfRange = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)bytes, 0x00020000);
+// x / d for 0 <= x < 2^31 with (mul, shift) as stored in ZnConvGeom
+// (Granlund & Montgomery 1994, Theorem 4.2, with 31-bit dividends).
+__device__ __forceinline__ int zn_udiv(int x, uint32_t mul, uint32_t shift) {
+    return (int)(((uint64_t)(uint32_t)x * mul) >> (31 + shift));
 }
-
-// Fragments for the four MFMA steps of one K group of 8 from an
-// X-contiguous LDS tile [BK][BX]: frag[f][t] is the operand value of lane
-// (i = lane % 32, h = lane / 32) for block f at k = kg + 4h + t; lane i owns
-// rows w0 + FX*i + f, f < FX, so each step is one FX-wide LDS read.
-template <int BX, int BK, int FX>
-__device__ __forceinline__ void read_frags_x(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
-    const int i = lane & 31;
-    const int h = lane >> 5;
-    typedef typename FVec<FX>::type VT;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const VT v = *reinterpret_cast<const VT *>(lds + (kg + 4 * h + t) * BX + w0 + FX * i);
-        if constexpr (FX == 1) {
-            frag[0][t] = v;
-        } else {
-#pragma unroll
-            for (int f = 0; f < FX; ++f) frag[f][t] = v[f];
-        }
-    }
-}
-
-// ---- operand staging straight into LDS -----------------------------------
-// buffer_load_dwordx4 ... lds writes lane L's 16 bytes to LDS address
-// M0 + 16*L (buffer_load_dword ... lds: 4 bytes at M0 + 4*L), so one wave
-// instruction fills a contiguous 1 KB (256 B) block; lanes with an
-// out-of-range offset write zeros (both behaviours checked on gfx950).  The loads are issued from inline assembly so that the compiler
-// does not guard every LDS read with a wait for all outstanding loads; the
-// kernel waits explicitly (vmcnt) before each stage's barrier.  M0 is set
-// immediately before each load and is not used by any other code in these
-// kernels (the build emits the assembly and tests/test_abi.py checks it).
-typedef __attribute__((address_space(3))) void zn_lds_void;
-
-template <int BX, int BK, int NT, bool KC, int W>
-struct DmaStage {
-    static_assert(W == 16 || W == 4, "16-byte or 4-byte loads");
-    static constexpr int kFloats = BX * BK;
-    static constexpr int kPerInst = W / 4 * kWave;  // floats one wave instruction writes (256 or 64)
-    static constexpr int kInsts = kFloats / kPerInst;
-    static constexpr int kWaves = NT / kWave;
-    static constexpr int kPerWave = kInsts / kWaves;
-    static_assert(kInsts % kWaves == 0 && kPerWave >= 1, "load blocks must split evenly over waves");
-    static_assert(!KC || BK == 16 || BK == 32, "K-contiguous DMA staging supports BK 16 and 32");
-
-    // K-contiguous operands are stored [x][BK] without padding; chunk c (4
-    // floats) of row x sits in slot c ^ swz(x), which spreads the 16-byte
-    // fragment reads of 8 consecutive rows over all banks.  X-contiguous
-    // operands are stored [BK][BX].
-    __device__ static __forceinline__ int swz(int row) { return BK == 16 ? ((row >> 1) & 3) : (row & 7); }
-
-    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, int ld, int x0, int k0,
-                                                 int xmax, int kmax, int wave, int lane) {
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int p0 = (j * kWaves + wave) * kPerInst;  // first LDS float this instruction writes
-            int outer, inner;
-            bool ok;
-            if constexpr (W == 16) {
-                const int p = p0 + 4 * lane;  // lane writes LDS floats p .. p + 3
-                if constexpr (KC) {
-                    const int row = p / BK;
-                    const int c = ((p % BK) / 4) ^ swz(row);
-                    outer = x0 + row;
-                    inner = k0 + 4 * c;
-                } else {
-                    outer = k0 + p / BX;
-                    inner = x0 + p % BX;
-                }
-                ok = outer < (KC ? xmax : kmax) && inner < (KC ? kmax : xmax);
-            } else {
-                const int p = p0 + lane;  // lane writes LDS float p
-                if constexpr (KC) {
-                    const int row = p / BK, pos = p % BK;
-                    const int c = (pos / 4) ^ swz(row);
-                    outer = x0 + row;
-                    inner = k0 + 4 * c + (pos & 3);
-                } else {
-                    outer = k0 + p / BX;
-                    inner = x0 + p % BX;
-                }
-                ok = outer < (KC ? xmax : kmax) && inner < (KC ? kmax : xmax);
-            }
-            const uint32_t off = ok ? (uint32_t)(outer * ld + inner) * 4u : kOutOfRange;
-            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
-            if constexpr (W == 16)
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                             :
-                             : "s"(lds_addr), "v"(off), "s"(rsrc)
-                             : "memory");
-            else
-                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-                             :
-                             : "s"(lds_addr), "v"(off), "s"(rsrc)
-                             : "memory");
-        }
-    }
-};
 
 // Implicit-GEMM convolution operand: the X-contiguous tile [BK][BN] of the
 // virtual im2col matrix, element (k, n) gathered with 4-byte loads from the
-// NCHW input (out-of-image taps and out-of-problem elements read zero).  One
-// wave instruction covers 64 consecutive n of one k row when BN >= 64, so
-// the filter-tap decode is uniform across the wave.
+// NCHW input (out-of-image taps and out-of-problem elements read zero).
+//
+// When BN is a whole number of waves wide and every wave keeps the same BN
+// columns for all of its loads (kFixedN), a lane's output pixel n is fixed
+// for the whole tile: its (oh, ow) decode is done once (Lane), and the filter
+// tap of each load is uniform across the wave, decoded on the scalar unit.
+// Otherwise (BN = 32) every element is decoded per lane.
 template <int BN, int BK, int NT>
 struct ConvGatherStage {
     static constexpr int kFloats = BN * BK;
@@ -171,63 +66,75 @@ struct ConvGatherStage {
     static constexpr int kWaves = NT / kWave;
     static constexpr int kPerWave = kInsts / kWaves;
     static_assert(kInsts % kWaves == 0 && kPerWave >= 1, "load blocks must split evenly over waves");
+    static constexpr int kRowWaves = BN / kWave;  // wave loads per k row
+    static constexpr bool kFixedN = BN % kWave == 0 && kWaves % kRowWaves == 0;
+
+    struct Lane {
+        int ih0, iw0;  // top-left input tap of this lane's output pixel
+        int base;      // ih0 * in_w + iw0
+        bool ok;       // the pixel lies inside the problem
+    };
+
+    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int wave, int lane) {
+        Lane l;
+        const int n = n0 + (kFixedN ? (wave % kRowWaves) * kWave : 0) + lane;
+        const int oh = n / g.out_w, ow = n - oh * g.out_w;
+        l.ih0 = oh * g.stride_h - g.pad_h;
+        l.iw0 = ow * g.stride_w - g.pad_w;
+        l.base = l.ih0 * g.in_w + l.iw0;
+        l.ok = n < nmax;
+        return l;
+    }
+
+    __device__ static __forceinline__ void load(__amdgpu_buffer_rsrc_t rsrc, float *lds, int p0, uint32_t off) {
+        const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                     :
+                     : "s"(lds_addr), "v"(off), "s"(rsrc)
+                     : "memory");
+    }
+
+    // Filter tap of im2col column k: input channel, kernel row and column.
+    __device__ static __forceinline__ void decode_k(const ZnConvGeom &g, int k, int &ic, int &kh, int &kw) {
+        const int q = zn_udiv(k, g.div1_mul, g.div1_shift);
+        const int r = k - q * g.div1;
+        const int kpos = g.k_order == 0 ? q : r;
+        ic = g.k_order == 0 ? r : q;
+        kh = zn_udiv(kpos, g.kw_mul, g.kw_shift);
+        kw = kpos - kh * g.k_w;
+    }
 
     __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
-                                                 int n0, int k0, int nmax, int kmax, int wave, int lane) {
+                                                 const Lane &ln, int n0, int k0, int nmax, int kmax, int wave,
+                                                 int lane) {
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
-            const int p0 = (j * kWaves + wave) * kWave;
-            const int pos = p0 + lane;
-            const int k = k0 + pos / BN;
-            const int n = n0 + pos % BN;
-            int ic, kh, kw;
-            if (g.k_order == 0) {
-                const int kpos = k / g.channels;
-                ic = k - kpos * g.channels;
-                kh = kpos / g.k_w;
-                kw = kpos - kh * g.k_w;
+            const int row = j * kWaves + wave;  // wave-uniform
+            const int p0 = row * kWave;
+            uint32_t off;
+            if constexpr (kFixedN) {
+                const int k = k0 + row / kRowWaves;  // wave-uniform
+                int ic, kh, kw;
+                decode_k(g, k, ic, kh, kw);
+                const int ih = ln.ih0 + kh, iw = ln.iw0 + kw;
+                const bool ok = ln.ok && k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
+                off = ok ? (uint32_t)(ln.base + (ic * g.in_h + kh) * g.in_w + kw) * 4u : kOutOfRange;
             } else {
-                const int khw = g.k_h * g.k_w;
-                ic = k / khw;
-                const int kpos = k - ic * khw;
-                kh = kpos / g.k_w;
-                kw = kpos - kh * g.k_w;
+                const int pos = p0 + lane;
+                const int k = k0 + pos / BN;
+                const int n = n0 + pos % BN;
+                int ic, kh, kw;
+                decode_k(g, k, ic, kh, kw);
+                const int oh = zn_udiv(n, g.ow_mul, g.ow_shift), ow = n - oh * g.out_w;
+                const int ih = oh * g.stride_h - g.pad_h + kh;
+                const int iw = ow * g.stride_w - g.pad_w + kw;
+                const bool ok = n < nmax && k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
+                off = ok ? (uint32_t)((ic * g.in_h + ih) * g.in_w + iw) * 4u : kOutOfRange;
             }
-            const int oh = n / g.out_w, ow = n - oh * g.out_w;
-            const int ih = oh * g.stride_h - g.pad_h + kh;
-            const int iw = ow * g.stride_w - g.pad_w + kw;
-            const bool ok = n < nmax && k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
-            const uint32_t off = ok ? (uint32_t)((ic * g.in_h + ih) * g.in_w + iw) * 4u : kOutOfRange;
-            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-                         :
-                         : "s"(lds_addr), "v"(off), "s"(rsrc)
-                         : "memory");
+            load(rsrc, lds, p0, off);
         }
     }
 };
-
-// Fragments from the staged LDS tile: a K-contiguous tile gives one 16-byte
-// read per block (lane i: row w0 + 32f + i, k = kg + 4h .. kg + 4h + 3).
-template <int BX, int BK, int FX, bool KC>
-__device__ __forceinline__ void read_frags_dma(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
-    if constexpr (KC) {
-        const int i = lane & 31;
-        const int h = lane >> 5;
-#pragma unroll
-        for (int f = 0; f < FX; ++f) {
-            const int row = w0 + 32 * f + i;
-            const int slot = (kg / 4 + h) ^ DmaStage<BX, BK, kWave, true, 16>::swz(row);
-            const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(lds + row * BK + 4 * slot);
-            frag[f][0] = v[0];
-            frag[f][1] = v[1];
-            frag[f][2] = v[2];
-            frag[f][3] = v[3];
-        }
-    } else {
-        read_frags_x<BX, BK, FX>(lds, w0, kg, lane, frag);
-    }
-}
 
 // Tile coordinates of this workgroup: optional XCD-contiguous remap, then
 // groups of `group_m` tile rows (group_m = 1 is plain row-major order).
@@ -359,9 +266,11 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
 
+    typename SC::Lane cl{};
+    if constexpr (CONV && SC::kFixedN) cl = SC::lane_setup(p.conv, n0, p.n, wave, lane);
     auto issue_b = [&](float *lds, int k0) {
         if constexpr (CONV)
-            SC::issue(rb, lds, p.conv, n0, k0, p.n, kend, wave, lane);
+            SC::issue(rb, lds, p.conv, cl, n0, k0, p.n, kend, wave, lane);
         else
             SB::issue(rb, lds, ldb, n0, k0, p.n, kend, wave, lane);
     };

@@ -1,0 +1,156 @@
+// Shared device helpers of the MFMA kernels (GEMM, convolution, attention):
+// vector types, raw buffer descriptors, X-contiguous fragment reads and the
+// LDS-DMA operand staging.  Included by each kernel translation unit; every
+// definition has internal linkage.
+#ifndef ZN_MFMA_STAGE_H
+#define ZN_MFMA_STAGE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef float zn_f32x16 __attribute__((ext_vector_type(16)));
+typedef float zn_f32x4 __attribute__((ext_vector_type(4)));
+typedef float zn_f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+template <int N> struct FVec;
+template <> struct FVec<1> { typedef float type; };
+template <> struct FVec<2> { typedef zn_f32x2 type; };
+template <> struct FVec<4> { typedef zn_f32x4 type; };
+
+// Raw buffer descriptor over one operand of one problem: loads at byte
+// offsets >= `bytes` return zero, so masked elements use an out-of-range
+// offset instead of a branch.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Fragments for the four MFMA steps of one K group of 8 from an
+// X-contiguous LDS tile [BK][BX]: frag[f][t] is the operand value of lane
+// (i = lane % 32, h = lane / 32) for block f at k = kg + 4h + t; lane i owns
+// rows w0 + FX*i + f, f < FX, so each step is one FX-wide LDS read.
+template <int BX, int BK, int FX>
+__device__ __forceinline__ void read_frags_x(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
+    const int i = lane & 31;
+    const int h = lane >> 5;
+    typedef typename FVec<FX>::type VT;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const VT v = *reinterpret_cast<const VT *>(lds + (kg + 4 * h + t) * BX + w0 + FX * i);
+        if constexpr (FX == 1) {
+            frag[0][t] = v;
+        } else {
+#pragma unroll
+            for (int f = 0; f < FX; ++f) frag[f][t] = v[f];
+        }
+    }
+}
+
+// ---- operand staging straight into LDS -----------------------------------
+// buffer_load_dwordx4 ... lds writes lane L's 16 bytes to LDS address
+// M0 + 16*L (buffer_load_dword ... lds: 4 bytes at M0 + 4*L), so one wave
+// instruction fills a contiguous 1 KB (256 B) block; lanes with an
+// out-of-range offset write zeros (both behaviours checked on gfx950).  The loads are issued from inline assembly so that the compiler
+// does not guard every LDS read with a wait for all outstanding loads; the
+// kernel waits explicitly (vmcnt) before each stage's barrier.  M0 is set
+// immediately before each load and is not used by any other code in these
+// kernels (the build emits the assembly and tests/test_abi.py checks it).
+typedef __attribute__((address_space(3))) void zn_lds_void;
+
+template <int BX, int BK, int NT, bool KC, int W>
+struct DmaStage {
+    static_assert(W == 16 || W == 4, "16-byte or 4-byte loads");
+    static constexpr int kFloats = BX * BK;
+    static constexpr int kPerInst = W / 4 * kWave;  // floats one wave instruction writes (256 or 64)
+    static constexpr int kInsts = kFloats / kPerInst;
+    static constexpr int kWaves = NT / kWave;
+    static constexpr int kPerWave = kInsts / kWaves;
+    static_assert(kInsts % kWaves == 0 && kPerWave >= 1, "load blocks must split evenly over waves");
+    static_assert(!KC || BK == 16 || BK == 32 || BK == 64 || BK == 128, "K-contiguous DMA staging: BK 16..128");
+
+    // K-contiguous operands are stored [x][BK] without padding; chunk c (4
+    // floats) of row x sits in slot c ^ swz(x), which spreads the 16-byte
+    // fragment reads of 8 consecutive rows over all banks (for BK >= 32 the
+    // XOR stays inside an aligned group of 8 chunks).  X-contiguous
+    // operands are stored [BK][BX].
+    __device__ static __forceinline__ int swz(int row) { return BK == 16 ? ((row >> 1) & 3) : (row & 7); }
+
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, int ld, int x0, int k0,
+                                                 int xmax, int kmax, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int p0 = (j * kWaves + wave) * kPerInst;  // first LDS float this instruction writes
+            int outer, inner;
+            bool ok;
+            if constexpr (W == 16) {
+                const int p = p0 + 4 * lane;  // lane writes LDS floats p .. p + 3
+                if constexpr (KC) {
+                    const int row = p / BK;
+                    const int c = ((p % BK) / 4) ^ swz(row);
+                    outer = x0 + row;
+                    inner = k0 + 4 * c;
+                } else {
+                    outer = k0 + p / BX;
+                    inner = x0 + p % BX;
+                }
+                ok = outer < (KC ? xmax : kmax) && inner < (KC ? kmax : xmax);
+            } else {
+                const int p = p0 + lane;  // lane writes LDS float p
+                if constexpr (KC) {
+                    const int row = p / BK, pos = p % BK;
+                    const int c = (pos / 4) ^ swz(row);
+                    outer = x0 + row;
+                    inner = k0 + 4 * c + (pos & 3);
+                } else {
+                    outer = k0 + p / BX;
+                    inner = x0 + p % BX;
+                }
+                ok = outer < (KC ? xmax : kmax) && inner < (KC ? kmax : xmax);
+            }
+            const uint32_t off = ok ? (uint32_t)(outer * ld + inner) * 4u : kOutOfRange;
+            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+            if constexpr (W == 16)
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                             :
+                             : "s"(lds_addr), "v"(off), "s"(rsrc)
+                             : "memory");
+            else
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                             :
+                             : "s"(lds_addr), "v"(off), "s"(rsrc)
+                             : "memory");
+        }
+    }
+};
+
+
+// Fragments from the staged LDS tile: a K-contiguous tile gives one 16-byte
+// read per block (lane i: row w0 + 32f + i, k = kg + 4h .. kg + 4h + 3).
+template <int BX, int BK, int FX, bool KC>
+__device__ __forceinline__ void read_frags_dma(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
+    if constexpr (KC) {
+        const int i = lane & 31;
+        const int h = lane >> 5;
+#pragma unroll
+        for (int f = 0; f < FX; ++f) {
+            const int row = w0 + 32 * f + i;
+            const int slot = (kg / 4 + h) ^ DmaStage<BX, BK, kWave, true, 16>::swz(row);
+            const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(lds + row * BK + 4 * slot);
+            frag[f][0] = v[0];
+            frag[f][1] = v[1];
+            frag[f][2] = v[2];
+            frag[f][3] = v[3];
+        }
+    } else {
+        read_frags_x<BX, BK, FX>(lds, w0, kg, lane, frag);
+    }
+}
+
+}  // namespace
+
+#endif

@@ -51,6 +51,10 @@ constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", 
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
+constexpr const char *kAttnObject = "zn_attention_gfx950.hsaco";
+// Fused attention kernels by padded head dim (zn_attention_d<dim>[_v]).
+constexpr int kAttnDims[3] = {32, 64, 128};
+constexpr int kAttnQueries = 128;  // queries per workgroup (4 waves x 32)
 
 }  // namespace
 
@@ -59,6 +63,8 @@ struct zn_ctx {
     hipStream_t stream = nullptr;
     hipModule_t gemm_module = nullptr;
     hipModule_t elt_module = nullptr;
+    hipModule_t attn_module = nullptr;
+    hipFunction_t attn[3][2] = {};             // fused attention [head dim 32/64/128][16-byte I/O]
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
     hipFunction_t conv[kNumTiles][2] = {};     // implicit-GEMM convolution [tile][16-byte W rows]
     hipFunction_t splitk_reduce = nullptr;
@@ -208,13 +214,16 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // MFMA block idles; tiny problems use 32x32 to spread over more CUs.
 // A tile whose padding wastes more than a quarter of its MFMA work (for
 // example 256-row tiles over M = 128) is skipped for the next smaller one.
-Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t batch) {
+// A gathered (implicit convolution) operand costs more per staged element, so
+// the larger l tile, which reuses each staged element over 128 rows, pays
+// off from 2 instead of 4 tiles per CU (C5 conv: l 221 us, m 227 us).
+Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t batch, bool gathered = false) {
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     auto tiles = [&](Tile t) { return cdiv(m, kTiles[t].bm) * cdiv(n, kTiles[t].bn) * batch; };
     auto useful = [&](Tile t) { return 4 * m * n * batch >= 3 * tiles(t) * kTiles[t].bm * kTiles[t].bn; };
     if (n <= 64 && tiles(kTileN) >= cus) return kTileN;
     if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
-    if (tiles(kTileL) >= 4 * cus && useful(kTileL)) return kTileL;
+    if (tiles(kTileL) >= (gathered ? 2 : 4) * cus && useful(kTileL)) return kTileL;
     if (tiles(kTileM) >= cus / 2) return kTileM;
     return kTileS;
 }
@@ -236,6 +245,16 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Multiplier and shift for x / d, 0 <= x < 2^31, d >= 1: shift = ceil(log2 d),
+// mul = ceil(2^(31 + shift) / d), which is below 2^32 (Granlund & Montgomery
+// 1994, Theorem 4.2 with N = 31).
+void udiv_magic(uint32_t d, uint32_t &mul, uint32_t &shift) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    mul = (uint32_t)(((1ull << (31 + l)) + d - 1) / d);
+    shift = l;
+}
 
 // `conv` (optional) turns B into the implicit im2col operand of an NCHW
 // image batch (B[k][n] gathered per ZnConvGeom, images `stride_b` apart);
@@ -266,7 +285,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || b_extent > kLimit)) return ZN_ERR_OVERFLOW;
     if (conv && layout != ZN_LAYOUT_NN) return ZN_ERR_INVALID_ARG;
 
-    const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, batch);
+    const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, batch, conv != nullptr);
     const TileShape &ts = kTiles[tile];
     const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
     if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
@@ -469,6 +488,7 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
         dir = library_dir();
     const std::string gemm_path = dir + "/" + kGemmObject;
     const std::string elt_path = dir + "/" + kEltObject;
+    const std::string attn_path = dir + "/" + kAttnObject;
 
     zn_ctx *ctx = new (std::nothrow) zn_ctx();
     if (!ctx) return ZN_ERR_OOM;
@@ -487,7 +507,7 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     ctx->info.total_mem = (int64_t)prop.totalGlobalMem;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return bail(ZN_ERR_NO_DEVICE);
 
-    if (!file_exists(gemm_path) || !file_exists(elt_path)) return bail(ZN_ERR_CODE_OBJECT);
+    if (!file_exists(gemm_path) || !file_exists(elt_path) || !file_exists(attn_path)) return bail(ZN_ERR_CODE_OBJECT);
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) return bail(fail_hip(ctx, e));
     if (hipModuleLoad(&ctx->gemm_module, gemm_path.c_str()) != hipSuccess) {
@@ -496,6 +516,10 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     }
     if (hipModuleLoad(&ctx->elt_module, elt_path.c_str()) != hipSuccess) {
         ctx->elt_module = nullptr;
+        return bail(ZN_ERR_CODE_OBJECT);
+    }
+    if (hipModuleLoad(&ctx->attn_module, attn_path.c_str()) != hipSuccess) {
+        ctx->attn_module = nullptr;
         return bail(ZN_ERR_CODE_OBJECT);
     }
     for (int l = 0; l < 3; ++l)
@@ -517,6 +541,12 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
         return bail(ZN_ERR_SYMBOL);
     for (int i = 0; i < kNumElt; ++i)
         if (hipModuleGetFunction(&ctx->elt[i], ctx->elt_module, kEltName[i]) != hipSuccess) return bail(ZN_ERR_SYMBOL);
+    for (int d = 0; d < 3; ++d)
+        for (int v = 0; v < 2; ++v) {
+            char name[64];
+            std::snprintf(name, sizeof(name), "zn_attention_d%d%s", kAttnDims[d], v ? "_v" : "");
+            if (hipModuleGetFunction(&ctx->attn[d][v], ctx->attn_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
+        }
     *out = ctx;
     return ZN_OK;
 }
@@ -532,6 +562,7 @@ int zn_hip_destroy(zn_ctx *ctx) {
     ctx->ws = nullptr;
     if (ctx->gemm_module) (void)hipModuleUnload(ctx->gemm_module);
     if (ctx->elt_module) (void)hipModuleUnload(ctx->elt_module);
+    if (ctx->attn_module) (void)hipModuleUnload(ctx->attn_module);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     (void)hipGetLastError();
     delete ctx;
@@ -801,6 +832,10 @@ static int conv2d_device(zn_ctx *ctx, const float *input, const float *weights, 
     g.pad_h = (int32_t)ph;
     g.pad_w = (int32_t)pw;
     g.k_order = k_order;
+    g.div1 = k_order == 0 ? g.channels : g.k_h * g.k_w;
+    udiv_magic((uint32_t)g.div1, g.div1_mul, g.div1_shift);
+    udiv_magic((uint32_t)g.k_w, g.kw_mul, g.kw_shift);
+    udiv_magic((uint32_t)g.out_w, g.ow_mul, g.ow_shift);
     return gemm_launch_ex(ctx, ZN_LAYOUT_NN, oc, hw, kdim, weights, kdim, 0, input, hw, c * h * w, output, hw,
                           oc * hw, batch, 0, bias, ZN_ACT_LINEAR, 1, &g);
 }
@@ -839,6 +874,9 @@ int zn_hip_softmax_rows(zn_ctx *ctx, const float *in, float *out, int64_t rows, 
 
 // Per problem: S = Q.K^T (NT), P = softmax_rows(S * scale), O = P.V (NN); the
 // score matrices live in a pooled buffer of batch * seq * seq floats.
+// Head dims up to 128 run the fused single-pass kernel (scores never leave
+// the CU); larger ones run QK^T (NT GEMM), the row softmax and P.V (NN GEMM)
+// with the scores in a pooled HBM buffer.
 int zn_hip_attention_forward(zn_ctx *ctx, const float *q, const float *k, const float *v, float *out, int64_t batch,
                              int64_t seq_len, int64_t d_k, float scale) {
     if (!ctx || batch < 0 || seq_len < 0 || d_k < 0) return ZN_ERR_INVALID_ARG;
@@ -847,9 +885,34 @@ int zn_hip_attention_forward(zn_ctx *ctx, const float *q, const float *k, const 
     if (seq_len > INT_MAX || d_k > INT_MAX) return ZN_ERR_OVERFLOW;
     int rc = select_device(ctx);
     if (rc) return rc;
-    Lease scores(ctx);
-    if ((rc = scores.get((size_t)(batch * seq_len * seq_len)))) return rc;
     const int64_t sd = seq_len * d_k, ss = seq_len * seq_len;
+    if (d_k <= kAttnDims[2] && sd <= (int64_t)INT_MAX / 4) {
+        const int dim = d_k <= kAttnDims[0] ? 0 : d_k <= kAttnDims[1] ? 1 : 2;
+        const int vec = d_k % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+        ZnAttnArgs a;
+        a.q = q;
+        a.k = k;
+        a.v = v;
+        a.out = out;
+        a.stride = sd;
+        a.seq_len = (int32_t)seq_len;
+        a.d_k = (int32_t)d_k;
+        a.scale_log2 = scale * 1.44269504088896340736f;
+        const int64_t gx = cdiv(seq_len, kAttnQueries);
+        constexpr int64_t kMaxGridY = 65535;
+        for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
+            const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
+            ZnAttnArgs c = a;
+            c.q = q + b0 * sd;
+            c.k = k + b0 * sd;
+            c.v = v + b0 * sd;
+            c.out = out + b0 * sd;
+            if ((rc = launch(ctx, ctx->attn[dim][vec], (unsigned)gx, (unsigned)nb, 256, &c))) return rc;
+        }
+        return ZN_OK;
+    }
+    Lease scores(ctx);
+    if ((rc = scores.get((size_t)(batch * ss)))) return rc;
     if ((rc = gemm_launch(ctx, ZN_LAYOUT_NT, seq_len, seq_len, d_k, q, d_k, sd, k, d_k, sd, scores.ptr, seq_len, ss,
                           batch, 0, nullptr, ZN_ACT_LINEAR)))
         return rc;

@@ -14,6 +14,12 @@ struct ZnConvGeom {
     int32_t channels, in_h, in_w, k_h, k_w, out_w;
     int32_t stride_h, stride_w, pad_h, pad_w;
     int32_t k_order;  // 0: k = (kh*k_w + kw)*channels + ic (im2col order); 1: k = (ic*k_h + kh)*k_w + kw (OIHW)
+    // Unsigned division by a constant for 0 <= x < 2^31: x / d ==
+    // (x * mul) >> (31 + shift) with shift = ceil(log2 d), mul = ceil(2^(31 + shift) / d).
+    // div1 splits k into its outer and inner index (channels for k_order 0,
+    // k_h*k_w for 1); the other divisors are k_w and out_w.
+    int32_t div1;
+    uint32_t div1_mul, div1_shift, kw_mul, kw_shift, ow_mul, ow_shift;
 };
 
 // One (possibly batched) fp32 GEMM: C = act((acc ? C : 0) + op(A) op(B) + bias).
@@ -61,6 +67,18 @@ struct ZnEltArgs {
     int64_t rows, n;   // n = row length; for flat ops rows*n = element count
     float value;       // fill value; softmax score scale
     int32_t act;
+};
+
+// Fused attention: per problem blockIdx.y, out = softmax(scale * q k^T) v
+// over [seq_len x d_k] row-major heads `stride` floats apart.
+struct ZnAttnArgs {
+    const float *q;
+    const float *k;
+    const float *v;
+    float *out;
+    int64_t stride;
+    int32_t seq_len, d_k;
+    float scale_log2;  // scale * log2(e): scores are exponentiated base 2
 };
 
 // im2col (Backend.im2col layout): col[(b*OH*OW + oh*OW + ow)][(kh*KW + kw)*C + ic].
