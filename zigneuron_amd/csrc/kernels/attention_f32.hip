@@ -5,8 +5,8 @@
 //
 // Each wave owns 32 queries and walks the keys in blocks of BKV, keeping a
 // running row maximum and row sum (the online softmax): for every block
-//   S^T = K_blk . Q^T            (v_mfma_f32_32x32x2f32, K-dim = head dim)
-//   m'  = max(m, max_key S^T),  P^T = exp2(S^T*c - m'),  c = scale*log2(e)
+//   S^T = K_blk . (c Q)^T        (v_mfma_f32_32x32x2f32, K-dim = head dim)
+//   m'  = max(m, max_key S^T),  P^T = exp2(S^T - m'),  c = scale*log2(e)
 //   O^T = O^T * exp2(m - m') + V_blk^T . P^T,   l = l * exp2(m - m') + sum P
 // and at the end O = O^T^T / l.
 //
@@ -32,15 +32,85 @@
 
 namespace {
 
-constexpr float kLog2e = 1.44269504088896340736f;
-
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// One key block of the walk: S^T = K_blk . Q^T, the online-softmax update of
+// (m, l, O^T) and O^T += V_blk^T . P^T.  MASK: the block runs past seq_len
+// (only the last one can), its missing keys get score -inf.
+template <int DP, int BKV, bool MASK>
+__device__ __forceinline__ void attention_block(const float *lk, const float *lv, const float (&qf)[DP / 8][4],
+                                                zn_f32x16 (&o)[DP / 32], float &m, float &l, int kv0, int S,
+                                                int lane) {
+    constexpr int FD = DP / 32;   // 32-row blocks of O^T (head dim)
+    constexpr int FS = BKV / 32;  // 32-row blocks of S^T (keys)
+    const int h = lane >> 5;
+    zn_f32x16 s[FS];
+#pragma unroll
+    for (int f = 0; f < FS; ++f)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[f][r] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < DP / 8; ++g) {
+        float kf[FS][4];
+        read_frags_dma<BKV, DP, FS, true>(lk, 0, 8 * g, lane, kf);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int f = 0; f < FS; ++f) s[f] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[f][t], qf[g][t], s[f], 0, 0, 0);
+    }
+
+    // scores are already in the log2 domain (Q was scaled by scale*log2(e))
+    float mb = -INFINITY;
+#pragma unroll
+    for (int f = 0; f < FS; ++f)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            if constexpr (MASK)
+                if (kv0 + 32 * f + 8 * (r / 4) + 4 * h + (r % 4) >= S) s[f][r] = -INFINITY;
+            mb = fmaxf(mb, s[f][r]);
+        }
+    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    const float mn = fmaxf(m, mb);  // finite: every block holds at least one key
+    const float alpha = exp2_fast(m - mn);
+    float rs = 0.0f;
+#pragma unroll
+    for (int f = 0; f < FS; ++f)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float e = exp2_fast(s[f][r] - mn);
+            s[f][r] = e;
+            rs += e;
+        }
+    l = l * alpha + rs;
+    m = mn;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // some query's maximum moved
+#pragma unroll
+        for (int f = 0; f < FD; ++f)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[f][r] *= alpha;
+    }
+
+    // O^T += V_blk^T . P^T; P^T is the S^T accumulator, register 4g + t
+#pragma unroll
+    for (int fs = 0; fs < FS; ++fs)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float vf[FD][4];
+            read_frags_x<DP, BKV, FD>(lv, 0, 32 * fs + 8 * g, lane, vf);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int f = 0; f < FD; ++f)
+                    o[f] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[f][t], s[fs][4 * g + t], o[f], 0, 0, 0);
+        }
+}
+
+// Grid: blockIdx.x = problem, blockIdx.y = block of NW*32 queries, so the
+// query blocks of one problem share an XCD and its L2 copy of K and V.
 template <int DP, int BKV, int NW, int W>
 __device__ __forceinline__ void attention_tile(const ZnAttnArgs &p) {
     constexpr int NT = NW * kWave;
-    constexpr int FD = DP / 32;   // 32-row blocks of O^T (head dim)
-    constexpr int FS = BKV / 32;  // 32-row blocks of S^T (keys)
+    constexpr int FD = DP / 32;
     static_assert(DP % 32 == 0 && BKV % 32 == 0, "whole 32x32 blocks");
     typedef DmaStage<BKV, DP, NT, true, W> SK;   // K block, [key][d]
     typedef DmaStage<DP, BKV, NT, false, W> SV;  // V block, [key][d]
@@ -51,11 +121,11 @@ __device__ __forceinline__ void attention_tile(const ZnAttnArgs &p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int j = lane & 31, h = lane >> 5;
     const int S = p.seq_len, D = p.d_k;
-    const int64_t base = (int64_t)blockIdx.y * p.stride;
+    const int64_t base = (int64_t)blockIdx.x * p.stride;
     const float *gq = p.q + base;
-    const int q = (int)blockIdx.x * (NW * 32) + wave * 32 + j;  // this lane's query
+    const int q = (int)blockIdx.y * (NW * 32) + wave * 32 + j;  // this lane's query
 
-    // Q^T fragments, the B operand of S^T = K . Q^T: qf[g][t] = Q[q][8g + 4h + t].
+    // Q^T fragments, the B operand of S^T = K . Q^T: qf[g][t] = Q[q][8g + 4h + t] * scale*log2(e).
     float qf[DP / 8][4];
 #pragma unroll
     for (int g = 0; g < DP / 8; ++g) {
@@ -64,10 +134,11 @@ __device__ __forceinline__ void attention_tile(const ZnAttnArgs &p) {
             zn_f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
             if (q < S && f0 < D) v = *reinterpret_cast<const zn_f32x4 *>(gq + (int64_t)q * D + f0);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) qf[g][t] = v[t];
+            for (int t = 0; t < 4; ++t) qf[g][t] = v[t] * p.scale_log2;
         } else {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) qf[g][t] = (q < S && f0 + t < D) ? gq[(int64_t)q * D + f0 + t] : 0.0f;
+            for (int t = 0; t < 4; ++t)
+                qf[g][t] = (q < S && f0 + t < D) ? gq[(int64_t)q * D + f0 + t] * p.scale_log2 : 0.0f;
         }
     }
 
@@ -83,6 +154,7 @@ __device__ __forceinline__ void attention_tile(const ZnAttnArgs &p) {
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + base, bytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + base, bytes);
     const int nblk = (S + BKV - 1) / BKV;
+    const int nfull = S / BKV;  // blocks with no missing keys
     SK::issue(rk, lds_k[0], D, 0, 0, S, D, wave, lane);
     SV::issue(rv, lds_v[0], D, 0, 0, D, S, wave, lane);
     for (int b = 0; b < nblk; ++b) {
@@ -93,70 +165,10 @@ __device__ __forceinline__ void attention_tile(const ZnAttnArgs &p) {
             SK::issue(rk, lds_k[cur ^ 1], D, (b + 1) * BKV, 0, S, D, wave, lane);
             SV::issue(rv, lds_v[cur ^ 1], D, 0, (b + 1) * BKV, D, S, wave, lane);
         }
-
-        // S^T = K_blk . Q^T
-        zn_f32x16 s[FS];
-#pragma unroll
-        for (int f = 0; f < FS; ++f)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[f][r] = 0.0f;
-        const float *lk = lds_k[cur];
-#pragma unroll
-        for (int g = 0; g < DP / 8; ++g) {
-            float kf[FS][4];
-            read_frags_dma<BKV, DP, FS, true>(lk, 0, 8 * g, lane, kf);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int f = 0; f < FS; ++f) s[f] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[f][t], qf[g][t], s[f], 0, 0, 0);
-        }
-
-        // online softmax over this block's keys
-        const int kv0 = b * BKV;
-        const bool ragged = kv0 + BKV > S;
-        float mb = -INFINITY;
-#pragma unroll
-        for (int f = 0; f < FS; ++f)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = s[f][r] * p.scale_log2;
-                if (ragged && kv0 + 32 * f + 8 * (r / 4) + 4 * h + (r % 4) >= S) x = -INFINITY;
-                s[f][r] = x;
-                mb = fmaxf(mb, x);
-            }
-        mb = fmaxf(mb, __shfl_xor(mb, 32));
-        const float mn = fmaxf(m, mb);  // finite: every block holds at least one key
-        const float alpha = exp2_fast(m - mn);
-        float rs = 0.0f;
-#pragma unroll
-        for (int f = 0; f < FS; ++f)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = exp2_fast(s[f][r] - mn);
-                s[f][r] = e;
-                rs += e;
-            }
-        l = l * alpha + rs;
-        m = mn;
-#pragma unroll
-        for (int f = 0; f < FD; ++f)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[f][r] *= alpha;
-
-        // O^T += V_blk^T . P^T; P^T is the S^T accumulator, register 4g + t
-        const float *lv = lds_v[cur];
-#pragma unroll
-        for (int fs = 0; fs < FS; ++fs)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float vf[FD][4];
-                read_frags_x<DP, BKV, FD>(lv, 0, 32 * fs + 8 * g, lane, vf);
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-#pragma unroll
-                    for (int f = 0; f < FD; ++f)
-                        o[f] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[f][t], s[fs][4 * g + t], o[f], 0, 0, 0);
-            }
+        if (b < nfull)
+            attention_block<DP, BKV, false>(lds_k[cur], lds_v[cur], qf, o, m, l, b * BKV, S, lane);
+        else
+            attention_block<DP, BKV, true>(lds_k[cur], lds_v[cur], qf, o, m, l, b * BKV, S, lane);
     }
 
     // O[q][d] = O^T[d][q] / l.  Register r of block f holds d = FD*(8(r/4) + 4h + r%4) + f:
@@ -190,7 +202,7 @@ __device__ __forceinline__ void attention_tile(const ZnAttnArgs &p) {
 }  // namespace
 
 // zn_attention_d<DP>[_v]: head dims up to DP (zero-padded), 4 waves = 128
-// queries per workgroup, blockIdx.y = problem.  _v: 16-byte loads and stores
+// queries per workgroup, blockIdx.x = problem, blockIdx.y = query block.  _v: 16-byte loads and stores
 // (d_k % 4 == 0, 16-byte aligned Q, K, V and O).
 #define ZN_ATTN_KERNEL(DP, BKV, W, SUFFIX)                                                   \
     extern "C" __global__ __launch_bounds__(256, 2) void zn_attention_d##DP##SUFFIX(ZnAttnArgs p) { \

@@ -886,7 +886,7 @@ int zn_hip_attention_forward(zn_ctx *ctx, const float *q, const float *k, const 
     int rc = select_device(ctx);
     if (rc) return rc;
     const int64_t sd = seq_len * d_k, ss = seq_len * seq_len;
-    if (d_k <= kAttnDims[2] && sd <= (int64_t)INT_MAX / 4) {
+    if (d_k <= kAttnDims[2] && sd <= (int64_t)INT_MAX / 4 && cdiv(seq_len, kAttnQueries) <= 65535) {
         const int dim = d_k <= kAttnDims[0] ? 0 : d_k <= kAttnDims[1] ? 1 : 2;
         const int vec = d_k % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
         ZnAttnArgs a;
@@ -898,16 +898,17 @@ int zn_hip_attention_forward(zn_ctx *ctx, const float *q, const float *k, const 
         a.seq_len = (int32_t)seq_len;
         a.d_k = (int32_t)d_k;
         a.scale_log2 = scale * 1.44269504088896340736f;
-        const int64_t gx = cdiv(seq_len, kAttnQueries);
-        constexpr int64_t kMaxGridY = 65535;
-        for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
-            const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
+        // grid.x = problem (so one problem's query blocks share an XCD), grid.y = query block
+        const int64_t gy = cdiv(seq_len, kAttnQueries);
+        constexpr int64_t kMaxGridX = (int64_t)1 << 30;
+        for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridX) {
+            const int64_t nb = batch - b0 < kMaxGridX ? batch - b0 : kMaxGridX;
             ZnAttnArgs c = a;
             c.q = q + b0 * sd;
             c.k = k + b0 * sd;
             c.v = v + b0 * sd;
             c.out = out + b0 * sd;
-            if ((rc = launch(ctx, ctx->attn[dim][vec], (unsigned)gx, (unsigned)nb, 256, &c))) return rc;
+            if ((rc = launch(ctx, ctx->attn[dim][vec], (unsigned)nb, (unsigned)gy, 256, &c))) return rc;
         }
         return ZN_OK;
     }
