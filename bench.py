@@ -133,7 +133,16 @@ def bench_conv_attention(ctx, rng, reps, warmup):
     e = config_entry("C5 conv end-to-end (implicit GEMM)", "nn", OC, H * W, 9 * C, B, ms, {"bias": True})
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
     res.append(e)
-    for buf in (x, w, bias, o):
+    go = ctx.to_device(uniform(rng, (B, OC, H, W)))
+    gi, gw, gb = ctx.alloc(B * C * H * W), ctx.alloc(OC * 9 * C), ctx.alloc(OC)
+    ms = time_launches(ctx, lambda: ctx.conv2d_backward_im2col(x, w, go, gi, gw, gb, B, C, OC, 3, 3, H, W, H, W,
+                                                               1, 1, 1, 1), reps, warmup)
+    flops = 2 * 2.0 * B * H * W * OC * 9 * C  # the weight- and input-gradient GEMMs
+    e = {"name": "C5 conv backward (im2col + 2 GEMMs + col2im + bias)", "kernel_ms": round(ms, 5),
+         "tflops": round(flops / (ms * 1e-3) / 1e12, 3)}
+    log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
+    res.append(e)
+    for buf in (x, w, bias, o, go, gi, gw, gb):
         buf.close()
     BH, S, D = 128, 1024, 64
     q, k, v = (ctx.to_device(uniform(rng, (BH, S, D))) for _ in range(3))

@@ -207,6 +207,31 @@ int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *w
                                  float *output, int64_t batch, int64_t in_channels, int64_t out_channels, int64_t k_h,
                                  int64_t k_w, int64_t in_h, int64_t in_w, int64_t out_h, int64_t out_w,
                                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w);
+/* Backend.col2im (src/backend.zig:3833-3877) on device: NCHW output = the sum
+ * of the col entries [(b*OH*OW + oh*OW + ow)][(kh*kW + kw)*C + ic] landing on
+ * each pixel, added in the reference's order (bit-identical); output is
+ * overwritten. */
+int zn_hip_col2im(zn_ctx *ctx, const float *col, float *output, int64_t batch, int64_t channels, int64_t in_h,
+                  int64_t in_w, int64_t k_h, int64_t k_w, int64_t out_h, int64_t out_w, int64_t stride_h,
+                  int64_t stride_w, int64_t pad_h, int64_t pad_w);
+/* cpuConv2dBackwardIm2col (src/backend.zig:3954-4065) on device.  Like the
+ * reference, grad_output is read as [batch*OH*OW][OC] by the weight and input
+ * gradients (grad_weights = go^T . im2col(input), grad_input =
+ * col2im(go . W), W and grad_weights in the col K order) and as NCHW by
+ * grad_bias (the per-channel sum).  All three outputs are overwritten. */
+int zn_hip_conv2d_backward_im2col(zn_ctx *ctx, const float *input, const float *weights, const float *grad_output,
+                                  float *grad_input, float *grad_weights, float *grad_bias, int64_t batch,
+                                  int64_t in_channels, int64_t out_channels, int64_t k_h, int64_t k_w, int64_t in_h,
+                                  int64_t in_w, int64_t out_h, int64_t out_w, int64_t stride_h, int64_t stride_w,
+                                  int64_t pad_h, int64_t pad_w);
+/* The direct branch of cpuConv2dBackward (src/backend.zig:3064-3094) on
+ * device: NCHW grad_output, weights and grad_weights as [OC][C][kH][kW]
+ * (the gradients of zn_hip_conv2d_forward_direct).  Outputs overwritten. */
+int zn_hip_conv2d_backward_direct(zn_ctx *ctx, const float *input, const float *weights, const float *grad_output,
+                                  float *grad_input, float *grad_weights, float *grad_bias, int64_t batch,
+                                  int64_t in_channels, int64_t out_channels, int64_t k_h, int64_t k_w, int64_t in_h,
+                                  int64_t in_w, int64_t out_h, int64_t out_w, int64_t stride_h, int64_t stride_w,
+                                  int64_t pad_h, int64_t pad_w);
 /* Row softmax of scaled scores (out may equal in): out[r,:] = exp(s - max) /
  * sum(exp(s - max)), s = in[r,:] * scale, the softmax of cpuAttentionForward
  * (src/backend.zig:3201-3214). */
@@ -276,6 +301,15 @@ int zn_hip_conv2d_forward_host(zn_ctx *ctx, const float *input, size_t input_len
                                size_t output_len, size_t in_channels, size_t out_channels, size_t k_h, size_t k_w,
                                size_t in_h, size_t in_w, size_t out_h, size_t out_w, size_t stride_h, size_t stride_w,
                                size_t pad_h, size_t pad_w);
+/* Backend.conv2dBackward (src/backend.zig:520, CPU arm :3049-3095): batch =
+ * input_len / (C*H*W); the im2col branch (zn_hip_conv2d_backward_im2col) when
+ * batch*OC*OH*OW >= 1024 and kH*kW >= 9, the direct branch otherwise. */
+int zn_hip_conv2d_backward_host(zn_ctx *ctx, const float *input, size_t input_len, const float *weights,
+                                size_t weights_len, const float *grad_output, size_t grad_output_len,
+                                float *grad_input, size_t grad_input_len, float *grad_weights, size_t grad_weights_len,
+                                float *grad_bias, size_t grad_bias_len, size_t in_channels, size_t out_channels,
+                                size_t k_h, size_t k_w, size_t in_h, size_t in_w, size_t out_h, size_t out_w,
+                                size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w);
 /* Backend.attentionForward (src/backend.zig:631-638): one head [seq_len x
  * d_k]; `scores` (length >= seq_len, as the reference requires) is not
  * written: the device keeps its scores in HBM. */

@@ -328,6 +328,118 @@ void zno_conv2d_forward(const float *input, size_t input_len, const float *weigh
                 }
 }
 
+void zno_col2im(const float *col, float *output, size_t batch, size_t channels, size_t in_h, size_t in_w,
+                size_t k_h, size_t k_w, size_t out_h, size_t out_w, size_t stride_h, size_t stride_w,
+                size_t pad_h, size_t pad_w) {
+    const size_t col_h = out_h * out_w, col_w = k_h * k_w * channels;
+    memset(output, 0, batch * channels * in_h * in_w * sizeof(float));
+    for (size_t bi = 0; bi < batch; ++bi)
+        for (size_t oh = 0; oh < out_h; ++oh)
+            for (size_t ow = 0; ow < out_w; ++ow) {
+                const float *src = col + (bi * col_h + oh * out_w + ow) * col_w;
+                const long h0 = (long)(oh * stride_h) - (long)pad_h;
+                const long w0 = (long)(ow * stride_w) - (long)pad_w;
+                for (size_t ic = 0; ic < channels; ++ic)
+                    for (size_t kh = 0; kh < k_h; ++kh)
+                        for (size_t kw = 0; kw < k_w; ++kw) {
+                            const long ih = h0 + (long)kh, iw = w0 + (long)kw;
+                            if (ih < 0 || iw < 0 || ih >= (long)in_h || iw >= (long)in_w) continue;
+                            float *dst = output + ((bi * channels + ic) * in_h + (size_t)ih) * in_w + (size_t)iw;
+                            *dst = *dst + src[(kh * k_w + kw) * channels + ic];
+                        }
+            }
+}
+
+void zno_conv2d_backward_direct(const float *input, const float *weights, const float *grad_output, float *grad_input,
+                                float *grad_weights, float *grad_bias, size_t batch, size_t channels,
+                                size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w, size_t out_h,
+                                size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w) {
+    memset(grad_input, 0, batch * channels * in_h * in_w * sizeof(float));
+    memset(grad_weights, 0, out_channels * channels * k_h * k_w * sizeof(float));
+    memset(grad_bias, 0, out_channels * sizeof(float));
+    for (size_t bi = 0; bi < batch; ++bi)
+        for (size_t oc = 0; oc < out_channels; ++oc)
+            for (size_t oh = 0; oh < out_h; ++oh)
+                for (size_t ow = 0; ow < out_w; ++ow) {
+                    const float go = grad_output[((bi * out_channels + oc) * out_h + oh) * out_w + ow];
+                    grad_bias[oc] = grad_bias[oc] + go;
+                    const long h0 = (long)(oh * stride_h) - (long)pad_h;
+                    const long w0 = (long)(ow * stride_w) - (long)pad_w;
+                    for (size_t ic = 0; ic < channels; ++ic)
+                        for (size_t kh = 0; kh < k_h; ++kh)
+                            for (size_t kw = 0; kw < k_w; ++kw) {
+                                const long ih = h0 + (long)kh, iw = w0 + (long)kw;
+                                if (ih < 0 || iw < 0 || ih >= (long)in_h || iw >= (long)in_w) continue;
+                                const size_t in_idx = ((bi * channels + ic) * in_h + (size_t)ih) * in_w + (size_t)iw;
+                                const size_t w_idx = ((oc * channels + ic) * k_h + kh) * k_w + kw;
+                                const float pw = input[in_idx] * go;
+                                grad_weights[w_idx] = grad_weights[w_idx] + pw;
+                                const float pi = weights[w_idx] * go;
+                                grad_input[in_idx] = grad_input[in_idx] + pi;
+                            }
+                }
+}
+
+void zno_conv2d_backward_im2col(const float *input, const float *weights, const float *grad_output, float *grad_input,
+                                float *grad_weights, float *grad_bias, size_t batch, size_t channels,
+                                size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w, size_t out_h,
+                                size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w) {
+    const size_t col_h = out_h * out_w, col_w = k_h * k_w * channels, rows = batch * col_h;
+    float *col = (float *)malloc(rows * col_w * sizeof(float));
+    float *grad_col = (float *)malloc(rows * col_w * sizeof(float));
+    if (!col || !grad_col) {
+        free(col);
+        free(grad_col);
+        return;
+    }
+    memset(grad_weights, 0, out_channels * col_w * sizeof(float));
+    memset(grad_bias, 0, out_channels * sizeof(float));
+    zno_im2col(input, col, batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w);
+    for (size_t bi = 0; bi < batch; ++bi)
+        for (size_t oc = 0; oc < out_channels; ++oc)
+            for (size_t hw = 0; hw < col_h; ++hw)
+                grad_bias[oc] = grad_bias[oc] + grad_output[(bi * out_channels + oc) * col_h + hw];
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t oc = 0; oc < out_channels; ++oc) {
+            const float go = grad_output[r * out_channels + oc];
+            float *gw = grad_weights + oc * col_w;
+            const float *cr = col + r * col_w;
+            for (size_t i = 0; i < col_w; ++i) {
+                const float prod = cr[i] * go;
+                gw[i] = gw[i] + prod;
+            }
+        }
+    memset(grad_col, 0, rows * col_w * sizeof(float));
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t oc = 0; oc < out_channels; ++oc) {
+            const float go = grad_output[r * out_channels + oc];
+            const float *w = weights + oc * col_w;
+            float *gc = grad_col + r * col_w;
+            for (size_t i = 0; i < col_w; ++i) {
+                const float prod = w[i] * go;
+                gc[i] = gc[i] + prod;
+            }
+        }
+    zno_col2im(grad_col, grad_input, batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h, stride_w, pad_h,
+               pad_w);
+    free(col);
+    free(grad_col);
+}
+
+void zno_conv2d_backward(const float *input, size_t input_len, const float *weights, const float *grad_output,
+                         float *grad_input, float *grad_weights, float *grad_bias, size_t channels,
+                         size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w, size_t out_h,
+                         size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w) {
+    const size_t batch = input_len / (channels * in_h * in_w);
+    const size_t total_out = batch * out_channels * out_h * out_w;
+    if (total_out >= 1024 && k_h * k_w >= 9)
+        zno_conv2d_backward_im2col(input, weights, grad_output, grad_input, grad_weights, grad_bias, batch, channels,
+                                   out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w);
+    else
+        zno_conv2d_backward_direct(input, weights, grad_output, grad_input, grad_weights, grad_bias, batch, channels,
+                                   out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w);
+}
+
 void zno_attention(const float *q, const float *k, const float *v, float *out, float *scores, size_t seq_len,
                    size_t d_k, float scale) {
     for (size_t i = 0; i < seq_len; ++i) {

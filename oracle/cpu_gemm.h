@@ -75,6 +75,32 @@ void zno_conv2d_im2col_gemm(const float *col, const float *weights, const float 
 void zno_conv2d_forward(const float *input, size_t input_len, const float *weights, const float *bias, float *out,
                         size_t channels, size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w,
                         size_t out_h, size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w);
+/* Backend.col2im (src/backend.zig:3833-3877): output (NCHW) = 0, then every
+ * in-image col element added at its input position, loops b, oh, ow, ic, kh, kw. */
+void zno_col2im(const float *col, float *output, size_t batch, size_t channels, size_t in_h, size_t in_w,
+                size_t k_h, size_t k_w, size_t out_h, size_t out_w, size_t stride_h, size_t stride_w,
+                size_t pad_h, size_t pad_w);
+/* The direct branch of cpuConv2dBackward (src/backend.zig:3064-3094): NCHW
+ * grad_output, OIHW weights; grad_input, grad_weights, grad_bias overwritten. */
+void zno_conv2d_backward_direct(const float *input, const float *weights, const float *grad_output, float *grad_input,
+                                float *grad_weights, float *grad_bias, size_t batch, size_t channels,
+                                size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w, size_t out_h,
+                                size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w);
+/* cpuConv2dBackwardIm2col (src/backend.zig:3954-4065): grad_bias from the NCHW
+ * grad_output; grad_weights[oc][c] = sum over rows r of col[r][c] *
+ * grad_output[r*OC + oc] and grad_col[r][c] = sum over oc of W[oc][c] *
+ * grad_output[r*OC + oc] (grad_output read as [batch*OH*OW][OC], weights in
+ * the col K order); grad_input = col2im(grad_col). */
+void zno_conv2d_backward_im2col(const float *input, const float *weights, const float *grad_output, float *grad_input,
+                                float *grad_weights, float *grad_bias, size_t batch, size_t channels,
+                                size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w, size_t out_h,
+                                size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w);
+/* cpuConv2dBackward (src/backend.zig:3049-3095): batch = input_len / (C*H*W);
+ * the im2col branch when batch*OC*OH*OW >= 1024 and kH*kW >= 9, else direct. */
+void zno_conv2d_backward(const float *input, size_t input_len, const float *weights, const float *grad_output,
+                         float *grad_input, float *grad_weights, float *grad_bias, size_t channels,
+                         size_t out_channels, size_t k_h, size_t k_w, size_t in_h, size_t in_w, size_t out_h,
+                         size_t out_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w);
 /* cpuAttentionForward (src/backend.zig:3197-3222), single head [S x D]. */
 void zno_attention(const float *q, const float *k, const float *v, float *out, float *scores,
                    size_t seq_len, size_t d_k, float scale);

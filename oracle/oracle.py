@@ -52,6 +52,10 @@ def lib() -> ctypes.CDLL:
             "zno_conv2d_im2col_gemm": [P, P, P, P, S, S, S, S],
             "zno_attention": [P, P, P, P, P, S, S, F],
             "zno_conv2d_forward": [P, S, P, P, P] + [S] * 12,
+            "zno_col2im": [P, P] + [S] * 12,
+            "zno_conv2d_backward_direct": [P, P, P, P, P, P] + [S] * 13,
+            "zno_conv2d_backward_im2col": [P, P, P, P, P, P] + [S] * 13,
+            "zno_conv2d_backward": [P, S, P, P, P, P, P] + [S] * 12,
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -187,6 +191,36 @@ def conv2d_forward(x, weights, bias, channels, out_channels, k_h, k_w, in_h, in_
     lib().zno_conv2d_forward(_p(x), x.size, _p(w), _p(bias), _p(out), channels, out_channels, k_h, k_w, in_h, in_w,
                              out_h, out_w, stride, stride, pad, pad)
     return out
+
+
+def col2im(col, batch, channels, in_h, in_w, k_h, k_w, stride=1, pad=0):
+    """Backend.col2im: col [batch*OH*OW, kH*kW*C] -> NCHW [batch, C, H, W]."""
+    col = _f32(col)
+    out_h = (in_h + 2 * pad - k_h) // stride + 1
+    out_w = (in_w + 2 * pad - k_w) // stride + 1
+    out = np.empty((batch, channels, in_h, in_w), np.float32)
+    lib().zno_col2im(_p(col), _p(out), batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride, stride, pad, pad)
+    return out
+
+
+def conv2d_backward(x, weights, grad_output, channels, out_channels, k_h, k_w, in_h, in_w, stride=1, pad=0,
+                    branch="auto"):
+    """cpuConv2dBackward (branch "auto": the reference's size switch; "direct" or
+    "im2col" force one branch).  Returns (grad_input, grad_weights, grad_bias)."""
+    x, w, go = _f32(x), _f32(weights), _f32(grad_output)
+    out_h = (in_h + 2 * pad - k_h) // stride + 1
+    out_w = (in_w + 2 * pad - k_w) // stride + 1
+    batch = x.size // (channels * in_h * in_w)
+    gi = np.empty((batch, channels, in_h, in_w), np.float32)
+    gw = np.empty(out_channels * channels * k_h * k_w, np.float32)
+    gb = np.empty(out_channels, np.float32)
+    geo = (channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride, stride, pad, pad)
+    if branch == "auto":
+        lib().zno_conv2d_backward(_p(x), x.size, _p(w), _p(go), _p(gi), _p(gw), _p(gb), *geo)
+    else:
+        fn = {"direct": lib().zno_conv2d_backward_direct, "im2col": lib().zno_conv2d_backward_im2col}[branch]
+        fn(_p(x), _p(w), _p(go), _p(gi), _p(gw), _p(gb), batch, *geo)
+    return gi, gw, gb
 
 
 def attention(q, k, v, seq_len, d_k, scale):

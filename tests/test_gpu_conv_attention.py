@@ -295,3 +295,123 @@ def test_c5_conv_end_to_end(ctx):
     conv_check(out[[0, B - 1]], np.ascontiguousarray(x[[0, B - 1]]), w, bias, case, "C5")
     for buf in (dx, dw, db, do):
         buf.close()
+
+
+# ------------------------------------------------------------ conv backward
+BWD_CASES = [  # batch, C, H, W, OC, kH, kW, stride, pad
+    (2, 3, 9, 7, 5, 3, 3, 1, 1),
+    (1, 4, 8, 8, 6, 3, 3, 2, 1),
+    (3, 2, 6, 5, 4, 2, 3, 1, 0),
+    (2, 16, 12, 12, 24, 3, 3, 1, 1),
+    (2, 5, 13, 11, 7, 5, 5, 2, 2),
+    (1, 1, 5, 5, 1, 1, 1, 1, 0),
+]
+
+
+@pytest.mark.parametrize("case", BWD_CASES)
+def test_col2im_bit_exact(ctx, case):
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    col = uniform(np.random.default_rng(12), (B * OH * OW, KH * KW * C))
+    announce(f"col2im {case}")
+    dcol = ctx.to_device(col)
+    dout = ctx.alloc(B * C * H * W).fill(np.nan)
+    ctx.col2im(dcol, dout, B, C, H, W, KH, KW, OH, OW, st, st, pd, pd)
+    np.testing.assert_array_equal(dout.download().reshape(B, C, H, W),
+                                  oracle.col2im(col, B, C, H, W, KH, KW, stride=st, pad=pd))
+    dcol.close()
+    dout.close()
+
+
+def backward_check(got, x, w, go, case, branch, what):
+    """Componentwise against the oracle branch; the denominators are the same
+    algorithm run on |x|, |w|, |go| (every output is a sum of products)."""
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    ref = oracle.conv2d_backward(x, w, go, C, OC, KH, KW, H, W, st, pd, branch=branch)
+    den = oracle.conv2d_backward(np.abs(x), np.abs(w), np.abs(go), C, OC, KH, KW, H, W, st, pd, branch=branch)
+    counts = (OC * KH * KW, B * OH * OW, B * OH * OW)  # terms per grad_input, grad_weights, grad_bias element
+    for name, g, r, d, n in zip(("grad_input", "grad_weights", "grad_bias"), got, ref, den, counts):
+        d = d.astype(np.float64).ravel()
+        err = np.abs(g.astype(np.float64).ravel() - r.astype(np.float64).ravel())
+        ok = err <= tol(n) * d + 1e-30
+        assert ok.all(), f"{what} {name}: worst {np.max(err / np.maximum(d, 1e-30)):.3e} > {tol(n):.3e}"
+
+
+def run_backward(ctx, case, branch, seed=13):
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    rng = np.random.default_rng(seed)
+    x, w = uniform(rng, (B, C, H, W)), uniform(rng, (OC, KH * KW * C))
+    go = uniform(rng, (B, OC, OH, OW))
+    dx, dw, dgo = ctx.to_device(x), ctx.to_device(w), ctx.to_device(go)
+    dgi = ctx.alloc(B * C * H * W).fill(np.nan)
+    dgw = ctx.alloc(OC * KH * KW * C).fill(np.nan)
+    dgb = ctx.alloc(OC).fill(np.nan)
+    fn = ctx.conv2d_backward_im2col if branch == "im2col" else ctx.conv2d_backward_direct
+    fn(dx, dw, dgo, dgi, dgw, dgb, B, C, OC, KH, KW, H, W, OH, OW, st, st, pd, pd)
+    got = (dgi.download(), dgw.download(), dgb.download())
+    for buf in (dx, dw, dgo, dgi, dgw, dgb):
+        buf.close()
+    return got, x, w, go
+
+
+@pytest.mark.parametrize("branch", ["im2col", "direct"])
+@pytest.mark.parametrize("case", BWD_CASES)
+def test_conv2d_backward_device(ctx, case, branch):
+    announce(f"conv2d backward {branch} {case}")
+    got, x, w, go = run_backward(ctx, case, branch)
+    backward_check(got, x, w, go, case, branch, f"{branch} {case}")
+
+
+@pytest.mark.parametrize("case", [(2, 3, 9, 7, 5, 3, 3, 1, 1), (4, 8, 16, 16, 16, 3, 3, 1, 1),
+                                  (2, 4, 10, 10, 6, 2, 2, 1, 0)])
+def test_backend_conv2d_backward_host(backend, case):
+    """Backend.conv2dBackward on host slices: the reference's size switch
+    selects the branch (the last two cases run im2col, then direct on a 2x2)."""
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    rng = np.random.default_rng(14)
+    x, w = uniform(rng, (B, C, H, W)), uniform(rng, (OC, KH * KW * C))
+    go = uniform(rng, (B, OC, OH, OW))
+    gi = np.full(B * C * H * W, np.nan, np.float32)
+    gw = np.full(OC * KH * KW * C, np.nan, np.float32)
+    gb = np.full(OC, np.nan, np.float32)
+    announce(f"Backend.conv2dBackward {case}")
+    backend.conv2dBackward(x.ravel(), w.ravel(), go.ravel(), gi, gw, gb, C, OC, KH, KW, H, W, OH, OW, st, st, pd, pd)
+    backward_check((gi, gw, gb), x, w, go, case, "auto", f"host {case}")
+
+
+def test_c5_conv_backward_properties(ctx):
+    """C5 (batch 32, 64->128, 3x3, 56x56, pad 1) through the im2col branch,
+    checked in fp64: grad_bias = per-channel sums, grad_weights = go2^T . col,
+    grad_input = col2im(go2 . W) for two images (go2 = grad_output as
+    [batch*OH*OW][OC], the reference's reading)."""
+    B, C, H, W, OC = 32, 64, 56, 56, 128
+    rng = np.random.default_rng(15)
+    x, w = uniform(rng, (B, C, H, W)), uniform(rng, (OC, 9 * C))
+    go = uniform(rng, (B, OC, H, W))
+    announce("C5 conv backward")
+    dx, dw, dgo = ctx.to_device(x), ctx.to_device(w), ctx.to_device(go)
+    dgi, dgw, dgb = ctx.alloc(B * C * H * W), ctx.alloc(OC * 9 * C), ctx.alloc(OC)
+    ctx.conv2d_backward_im2col(dx, dw, dgo, dgi, dgw, dgb, B, C, OC, 3, 3, H, W, H, W, 1, 1, 1, 1)
+    gi, gw, gb = dgi.download().reshape(B, C, H, W), dgw.download().reshape(OC, 9 * C), dgb.download()
+    for buf in (dx, dw, dgo, dgi, dgw, dgb):
+        buf.close()
+    go64 = go.astype(np.float64)
+    gb_ref = go64.sum(axis=(0, 2, 3))
+    assert np.all(np.abs(gb - gb_ref) <= tol(B * H * W) * np.abs(go64).sum(axis=(0, 2, 3)))
+    go2 = go.reshape(B * H * W, OC).astype(np.float64)
+    col = oracle.im2col(x, B, C, H, W, 3, 3, stride=1, pad=1).astype(np.float64)
+    gw_ref = go2.T @ col
+    gw_den = np.abs(go2).T @ np.abs(col)
+    assert np.all(np.abs(gw - gw_ref) <= tol(B * H * W) * gw_den)
+    del col
+    rows = H * W
+    for b in (0, B - 1):
+        g2 = go2[b * rows:(b + 1) * rows]
+        gcol = g2 @ w.astype(np.float64)
+        gcol_abs = np.abs(g2) @ np.abs(w.astype(np.float64))
+        ref = oracle.col2im(gcol.astype(np.float32), 1, C, H, W, 3, 3, stride=1, pad=1)[0]
+        den = oracle.col2im(gcol_abs.astype(np.float32), 1, C, H, W, 3, 3, stride=1, pad=1)[0]
+        assert np.all(np.abs(gi[b] - ref) <= tol(9 * OC) * den * 1.01 + 1e-6), f"image {b}"

@@ -233,6 +233,94 @@ def test_im2col_conv_matches_direct_convolution():
     assert np.abs(gemm - nt).max() <= 1e-5
 
 
+def _ints(rng, shape, lo=-3, hi=4):
+    """Small integers as float32: every sum below is exact in fp32."""
+    return rng.integers(lo, hi, size=shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("geo", [(2, 3, 6, 5, 3, 3, 1, 1), (1, 2, 7, 7, 2, 3, 2, 1), (2, 4, 5, 6, 1, 1, 1, 0),
+                                 (1, 1, 9, 8, 4, 2, 3, 2)])
+def test_col2im_is_the_adjoint_of_im2col(geo):
+    """<im2col(x), c> = <x, col2im(c)> exactly (integer data), and
+    col2im(im2col(x)) = x times the number of windows covering each pixel."""
+    B, C, H, W, KH, KW, stride, pad = geo
+    OH, OW = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    rng = np.random.default_rng(sum(geo))
+    x = _ints(rng, (B, C, H, W))
+    c = _ints(rng, (B * OH * OW, KH * KW * C))
+    lhs = int((oracle.im2col(x, B, C, H, W, KH, KW, stride, pad).astype(np.int64) * c.astype(np.int64)).sum())
+    rhs = int((x.astype(np.int64) * oracle.col2im(c, B, C, H, W, KH, KW, stride, pad).astype(np.int64)).sum())
+    assert lhs == rhs
+    cover = np.zeros((H, W), np.int64)
+    for oh in range(OH):
+        for ow in range(OW):
+            for kh in range(KH):
+                for kw in range(KW):
+                    ih, iw = oh * stride - pad + kh, ow * stride - pad + kw
+                    if 0 <= ih < H and 0 <= iw < W:
+                        cover[ih, iw] += 1
+    back = oracle.col2im(oracle.im2col(x, B, C, H, W, KH, KW, stride, pad), B, C, H, W, KH, KW, stride, pad)
+    np.testing.assert_array_equal(back, x * cover[None, None].astype(np.float32))
+
+
+@pytest.mark.parametrize("geo", [(2, 3, 6, 5, 4, 3, 3, 1, 1), (1, 2, 7, 6, 3, 2, 2, 2, 0), (2, 3, 5, 5, 2, 1, 1, 1, 0)])
+def test_conv_backward_direct_is_the_adjoint_of_the_forward(geo):
+    """Direct branch (NCHW, OIHW): with integer data, <conv(x, w), g> equals
+    <x, grad_input> and <w, grad_weights>; grad_bias = the sum of g over b, h, w."""
+    B, C, H, W, OC, KH, KW, stride, pad = geo
+    OH, OW = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    rng = np.random.default_rng(sum(geo) + 1)
+    x, w, g = _ints(rng, (B, C, H, W)), _ints(rng, (OC, C, KH, KW)), _ints(rng, (B, OC, OH, OW))
+    zero = np.zeros(OC, np.float32)
+    # direct forward: force it with a 1-element batch loop when the switch would pick im2col
+    y = np.concatenate([oracle.conv2d_forward(x[b:b + 1], w, zero, C, OC, KH, KW, H, W, stride, pad)
+                        for b in range(B)]) if OC * OH * OW < 1024 or KH * KW < 9 else None
+    gi, gw, gb = oracle.conv2d_backward(x, w, g, C, OC, KH, KW, H, W, stride, pad, branch="direct")
+    ref_y = np.zeros((B, OC, OH, OW), np.int64)
+    xp = np.pad(x.astype(np.int64), ((0, 0), (0, 0), (pad, pad), (pad, pad)))
+    for oh in range(OH):
+        for ow in range(OW):
+            patch = xp[:, :, oh * stride:oh * stride + KH, ow * stride:ow * stride + KW]
+            ref_y[:, :, oh, ow] = np.einsum("bchw,ochw->bo", patch, w.astype(np.int64))
+    if y is not None:
+        np.testing.assert_array_equal(y, ref_y.astype(np.float32))
+    inner = int((ref_y * g.astype(np.int64)).sum())
+    assert inner == int((x.astype(np.int64) * gi.astype(np.int64)).sum())
+    assert inner == int((w.astype(np.int64).ravel() * gw.astype(np.int64)).sum())
+    np.testing.assert_array_equal(gb, g.sum(axis=(0, 2, 3)))
+
+
+def test_conv_backward_im2col_contract():
+    """The im2col branch reads grad_output as [batch*OH*OW][OC] for both GEMMs
+    (NCHW only for grad_bias): grad_weights = go2^T . col, grad_input =
+    col2im(go2 . W), exact on integer data; the branch switch follows the
+    forward's rule (batch*OC*OH*OW >= 1024 and kH*kW >= 9)."""
+    B, C, H, W, OC, KH, KW, stride, pad = 2, 3, 6, 7, 5, 3, 3, 1, 1
+    OH, OW = H, W
+    rng = np.random.default_rng(77)
+    x, w = _ints(rng, (B, C, H, W)), _ints(rng, (OC, KH * KW * C))
+    g = _ints(rng, (B, OC, OH, OW))
+    gi, gw, gb = oracle.conv2d_backward(x, w, g, C, OC, KH, KW, H, W, stride, pad, branch="im2col")
+    col = oracle.im2col(x, B, C, H, W, KH, KW, stride, pad).astype(np.int64)
+    go2 = g.reshape(B * OH * OW, OC).astype(np.int64)
+    np.testing.assert_array_equal(gw, (go2.T @ col).ravel().astype(np.float32))
+    grad_col = (go2 @ w.astype(np.int64)).astype(np.float32)
+    np.testing.assert_array_equal(gi, oracle.col2im(grad_col, B, C, H, W, KH, KW, stride, pad))
+    np.testing.assert_array_equal(gb, g.sum(axis=(0, 2, 3)))
+    # the switch: this size (B*OC*OH*OW = 420 < 1024) runs the direct branch
+    auto = oracle.conv2d_backward(x, w, g, C, OC, KH, KW, H, W, stride, pad)
+    direct = oracle.conv2d_backward(x, w, g, C, OC, KH, KW, H, W, stride, pad, branch="direct")
+    for a, d in zip(auto, direct):
+        np.testing.assert_array_equal(a, d)
+    big = (4, 3, 8, 8, 5)  # 4*5*8*8 = 1280 >= 1024 with a 3x3 kernel: im2col branch
+    xb, gbig = _ints(rng, big[:4]), _ints(rng, (4, 5, 8, 8))
+    wb = _ints(rng, (5, 27))
+    auto = oracle.conv2d_backward(xb, wb, gbig, 3, 5, 3, 3, 8, 8, 1, 1)
+    forced = oracle.conv2d_backward(xb, wb, gbig, 3, 5, 3, 3, 8, 8, 1, 1, branch="im2col")
+    for a, f in zip(auto, forced):
+        np.testing.assert_array_equal(a, f)
+
+
 def test_attention_matches_fp64_softmax():
     rng = np.random.default_rng(8)
     S, D = 33, 16

@@ -138,9 +138,13 @@ SIGNATURES = {
     "zn_hip_im2col": (I, [P, P, P] + [I64] * 12),
     "zn_hip_conv2d_forward_im2col": (I, [P, P, P, P, P] + [I64] * 13),
     "zn_hip_conv2d_forward_direct": (I, [P, P, P, P, P] + [I64] * 13),
+    "zn_hip_col2im": (I, [P, P, P] + [I64] * 12),
+    "zn_hip_conv2d_backward_im2col": (I, [P] + [P] * 6 + [I64] * 13),
+    "zn_hip_conv2d_backward_direct": (I, [P] + [P] * 6 + [I64] * 13),
     "zn_hip_softmax_rows": (I, [P, P, P, I64, I64, F]),
     "zn_hip_attention_forward": (I, [P, P, P, P, P, I64, I64, I64, F]),
     "zn_hip_conv2d_forward_host": (I, [P, P, S, P, S, P, S, P, S] + [S] * 11),
+    "zn_hip_conv2d_backward_host": (I, [P, P, S, P, S, P, S, P, S, P, S, P, S] + [S] * 12),
     "zn_hip_attention_forward_host": (I, [P, P, S, P, S, P, S, P, S, P, S, S, S, F]),
 }
 

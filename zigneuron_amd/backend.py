@@ -218,6 +218,30 @@ class Context:
             self.handle, _dptr(inp), _dptr(weights), _dptr(bias), _dptr(out), batch, in_channels, out_channels, k_h,
             k_w, in_h, in_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w), "zn_hip_conv2d_forward_direct")
 
+    def col2im(self, col, out, batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h=1, stride_w=1,
+               pad_h=0, pad_w=0) -> None:
+        """Backend.col2im on device (bit-identical to the reference); `out` is overwritten."""
+        check(_lib.load().zn_hip_col2im(self.handle, _dptr(col), _dptr(out), batch, channels, in_h, in_w, k_h, k_w,
+                                        out_h, out_w, stride_h, stride_w, pad_h, pad_w), "zn_hip_col2im")
+
+    def conv2d_backward_im2col(self, inp, weights, grad_output, grad_input, grad_weights, grad_bias, batch,
+                               in_channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride_h=1, stride_w=1,
+                               pad_h=0, pad_w=0) -> None:
+        """cpuConv2dBackwardIm2col on device (grad_output read as [batch*OH*OW][OC] by the GEMMs)."""
+        check(_lib.load().zn_hip_conv2d_backward_im2col(
+            self.handle, _dptr(inp), _dptr(weights), _dptr(grad_output), _dptr(grad_input), _dptr(grad_weights),
+            _dptr(grad_bias), batch, in_channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride_h, stride_w,
+            pad_h, pad_w), "zn_hip_conv2d_backward_im2col")
+
+    def conv2d_backward_direct(self, inp, weights, grad_output, grad_input, grad_weights, grad_bias, batch,
+                               in_channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride_h=1, stride_w=1,
+                               pad_h=0, pad_w=0) -> None:
+        """The direct branch of cpuConv2dBackward on device (NCHW, OIHW)."""
+        check(_lib.load().zn_hip_conv2d_backward_direct(
+            self.handle, _dptr(inp), _dptr(weights), _dptr(grad_output), _dptr(grad_input), _dptr(grad_weights),
+            _dptr(grad_bias), batch, in_channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride_h, stride_w,
+            pad_h, pad_w), "zn_hip_conv2d_backward_direct")
+
     def softmax_rows(self, inp, out, rows, n, scale=1.0) -> None:
         check(_lib.load().zn_hip_softmax_rows(self.handle, _dptr(inp), _dptr(out), rows, n, float(scale)),
               "zn_hip_softmax_rows")
@@ -354,6 +378,17 @@ class Backend:
             self._h, _ptr(x), x.size, _ptr(w), w.size, _ptr(b), b.size, _ptr(out), out.size, in_channels,
             out_channels, kernel_h, kernel_w, input_h, input_w, output_h, output_w, stride_h, stride_w, padding_h,
             padding_w), "zn_hip_conv2d_forward_host")
+
+    def conv2dBackward(self, inp, weights, grad_output, grad_input, grad_weights, grad_bias, in_channels,
+                       out_channels, kernel_h, kernel_w, input_h, input_w, output_h, output_w, stride_h, stride_w,
+                       padding_h, padding_w):
+        """Backend.conv2dBackward (src/backend.zig:520, :3049-3095), batch = len(input) / (C*H*W)."""
+        x, w, go = _f32_in(inp), _f32_in(weights), _f32_in(grad_output)
+        gi, gw, gb = _f32_out(grad_input), _f32_out(grad_weights), _f32_out(grad_bias)
+        check(_lib.load().zn_hip_conv2d_backward_host(
+            self._h, _ptr(x), x.size, _ptr(w), w.size, _ptr(go), go.size, _ptr(gi), gi.size, _ptr(gw), gw.size,
+            _ptr(gb), gb.size, in_channels, out_channels, kernel_h, kernel_w, input_h, input_w, output_h, output_w,
+            stride_h, stride_w, padding_h, padding_w), "zn_hip_conv2d_backward_host")
 
     def attentionForward(self, q, k, v, output, scores_buffer, seq_len, d_k, scaling_factor):
         """Backend.attentionForward (src/backend.zig:631-638), one head [seq_len x d_k]."""

@@ -114,18 +114,33 @@ extern "C" __global__ __launch_bounds__(256) void zn_accumulate_bias(ZnEltArgs p
     p.out[col] = s;
 }
 
+// Filter tap index <-> (ic, kh, kw) for the two col K orders.
+__device__ __forceinline__ void zn_tap_decode(const ZnIm2colArgs &p, int tap, int &ic, int &kh, int &kw) {
+    if (p.k_order == 0) {
+        const int kpos = tap / p.channels;
+        ic = tap - kpos * p.channels;
+        kh = kpos / p.k_w;
+        kw = kpos - kh * p.k_w;
+    } else {
+        const int khw = p.k_h * p.k_w;
+        ic = tap / khw;
+        const int kpos = tap - ic * khw;
+        kh = kpos / p.k_w;
+        kw = kpos - kh * p.k_w;
+    }
+}
+
 // Backend.im2col (src/backend.zig:3775-3827): one thread per element of
-// col[(b*OH*OW + oh*OW + ow)][(kh*KW + kw)*C + ic]; zero outside the padded
-// input.  Writes are coalesced along the col row.
+// col[(b*OH*OW + oh*OW + ow)][tap]; zero outside the padded input.  Writes
+// are coalesced along the col row.
 extern "C" __global__ __launch_bounds__(256) void zn_im2col(ZnIm2colArgs p) {
     const int64_t kc = (int64_t)p.k_h * p.k_w * p.channels;
     const int64_t hw = (int64_t)p.out_h * p.out_w;
     const int64_t total = (int64_t)p.batch * hw * kc;
     for (int64_t i = gtid(); i < total; i += gstride()) {
         const int64_t row = i / kc;
-        const int colc = (int)(i - row * kc);
-        const int kpos = colc / p.channels, ic = colc - kpos * p.channels;
-        const int kh = kpos / p.k_w, kw = kpos - kh * p.k_w;
+        int ic, kh, kw;
+        zn_tap_decode(p, (int)(i - row * kc), ic, kh, kw);
         const int64_t b = row / hw;
         const int r = (int)(row - b * hw);
         const int oh = r / p.out_w, ow = r - oh * p.out_w;
@@ -133,8 +148,67 @@ extern "C" __global__ __launch_bounds__(256) void zn_im2col(ZnIm2colArgs p) {
         const int iw = ow * p.stride_w - p.pad_w + kw;
         float v = 0.0f;
         if (ih >= 0 && iw >= 0 && ih < p.in_h && iw < p.in_w)
-            v = p.input[((b * p.channels + ic) * p.in_h + ih) * (int64_t)p.in_w + iw];
+            v = p.image[((b * p.channels + ic) * p.in_h + ih) * (int64_t)p.in_w + iw];
         p.col[i] = v;
+    }
+}
+
+// Backend.col2im (src/backend.zig:3833-3877) as a gather: one thread per
+// NCHW output element, summing, from 0, the col entries that land on it in
+// the reference's order (output rows oh, then ow, ascending; each (oh, ow)
+// reaches a given input pixel through at most one tap), so the result is
+// bit-identical to the reference's scatter.
+extern "C" __global__ __launch_bounds__(256) void zn_col2im(ZnIm2colArgs p) {
+    const int64_t kc = (int64_t)p.k_h * p.k_w * p.channels;
+    const int64_t hw = (int64_t)p.out_h * p.out_w;
+    const int64_t plane = (int64_t)p.in_h * p.in_w;
+    const int64_t total = (int64_t)p.batch * p.channels * plane;
+    for (int64_t i = gtid(); i < total; i += gstride()) {
+        const int64_t bc = i / plane;
+        const int pix = (int)(i - bc * plane);
+        const int64_t b = bc / p.channels;
+        const int ic = (int)(bc - b * p.channels);
+        const int ih = pix / p.in_w, iw = pix - ih * p.in_w;
+        // output rows whose window covers ih: 0 <= ih + pad_h - oh*stride_h < k_h
+        const int hh = ih + p.pad_h, ww = iw + p.pad_w;
+        const int oh_lo = hh >= p.k_h ? (hh - p.k_h) / p.stride_h + 1 : 0;
+        const int oh_hi = min(hh / p.stride_h, p.out_h - 1);
+        const int ow_lo = ww >= p.k_w ? (ww - p.k_w) / p.stride_w + 1 : 0;
+        const int ow_hi = min(ww / p.stride_w, p.out_w - 1);
+        const float *cb = p.col + b * hw * kc;
+        float sum = 0.0f;
+        for (int oh = oh_lo; oh <= oh_hi; ++oh) {
+            const int kh = hh - oh * p.stride_h;
+            for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+                const int kw = ww - ow * p.stride_w;
+                const int tap = p.k_order == 0 ? (kh * p.k_w + kw) * p.channels + ic : (ic * p.k_h + kh) * p.k_w + kw;
+                sum = sum + cb[((int64_t)oh * p.out_w + ow) * kc + tap];
+            }
+        }
+        p.image[i] = sum;
+    }
+}
+
+// out[c] = sum over (b, p) of in[(b*C + c)*hw + p]: one workgroup per
+// channel, each thread a fixed strided subset in ascending order, then a
+// fixed tree, so results do not depend on scheduling (the grad_bias of
+// cpuConv2dBackward, src/backend.zig:3073-3074, 3983-3993).
+extern "C" __global__ __launch_bounds__(256) void zn_channel_sum(ZnChannelSumArgs p) {
+    __shared__ float red[256];
+    for (int64_t c = blockIdx.x; c < p.channels; c += gridDim.x) {
+        float s = 0.0f;
+        for (int64_t b = 0; b < p.batch; ++b) {
+            const float *src = p.in + (b * p.channels + c) * p.hw;
+            for (int64_t i = threadIdx.x; i < p.hw; i += 256) s = s + src[i];
+        }
+        __syncthreads();  // `red` may still be read for the previous channel
+        red[threadIdx.x] = s;
+        __syncthreads();
+        for (int w = 128; w > 0; w >>= 1) {
+            if ((int)threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) p.out[c] = red[0];
     }
 }
 

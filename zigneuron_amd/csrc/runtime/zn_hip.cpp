@@ -21,6 +21,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <map>
 #include <new>
 #include <string>
@@ -44,10 +45,11 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
                                          {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kNumElt };
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kChannelSum, kNumElt };
 constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", "zn_add_bias",
                                            "zn_activation_forward", "zn_activation_backward",
-                                           "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows"};
+                                           "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows",
+                                           "zn_col2im",          "zn_channel_sum"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
@@ -790,7 +792,7 @@ int zn_hip_im2col(zn_ctx *ctx, const float *input, float *col, int64_t batch, in
     if (total == 0) return ZN_OK;
     if (!input || !col) return ZN_ERR_INVALID_ARG;
     ZnIm2colArgs a;
-    a.input = input;
+    a.image = const_cast<float *>(input);  // read only by zn_im2col
     a.col = col;
     a.batch = (int32_t)batch;
     a.channels = (int32_t)channels;
@@ -804,6 +806,7 @@ int zn_hip_im2col(zn_ctx *ctx, const float *input, float *col, int64_t batch, in
     a.stride_w = (int32_t)stride_w;
     a.pad_h = (int32_t)pad_h;
     a.pad_w = (int32_t)pad_w;
+    a.k_order = 0;
     return elt_launch(ctx, kIm2col, total, a);
 }
 
@@ -854,6 +857,151 @@ int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *w
                                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w) {
     return conv2d_device(ctx, input, weights, bias, output, batch, in_channels, out_channels, k_h, k_w, in_h, in_w,
                          out_h, out_w, stride_h, stride_w, pad_h, pad_w, 1);
+}
+
+// ------------------------------------------------------- conv backward
+static ZnIm2colArgs col_args(float *image, float *col, int64_t batch, int64_t c, int64_t kh, int64_t kw, int64_t h,
+                             int64_t w, int64_t oh, int64_t ow, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                             int k_order) {
+    ZnIm2colArgs a;
+    a.image = image;
+    a.col = col;
+    a.batch = (int32_t)batch;
+    a.channels = (int32_t)c;
+    a.in_h = (int32_t)h;
+    a.in_w = (int32_t)w;
+    a.k_h = (int32_t)kh;
+    a.k_w = (int32_t)kw;
+    a.out_h = (int32_t)oh;
+    a.out_w = (int32_t)ow;
+    a.stride_h = (int32_t)sh;
+    a.stride_w = (int32_t)sw;
+    a.pad_h = (int32_t)ph;
+    a.pad_w = (int32_t)pw;
+    a.k_order = k_order;
+    return a;
+}
+
+// Convolution backward on device.  k_order 0 follows cpuConv2dBackwardIm2col
+// (src/backend.zig:3954-4065): grad_output is read as [batch*OH*OW][OC] by
+// both GEMMs (grad_W = go2^T . col as one TN GEMM over all images, grad_col =
+// go2 . W as an NN GEMM), W in the col K order.  k_order 1 is the direct
+// branch (src/backend.zig:3064-3094), NCHW grad_output and OIHW weights:
+// grad_W = sum over images of go_b . col_b (a strided-batched NN GEMM whose
+// per-image products are added in image order), grad_col_b = go_b^T . W
+// (strided-batched TN).  Both finish with col2im into grad_input and the
+// per-channel sum of the NCHW grad_output into grad_bias.  Images are taken
+// in chunks whose col buffer stays under 1 GiB.
+static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *weights, const float *grad_output,
+                                  float *grad_input, float *grad_weights, float *grad_bias, int64_t batch, int64_t c,
+                                  int64_t oc, int64_t kh, int64_t kw, int64_t h, int64_t w, int64_t oh, int64_t ow,
+                                  int64_t sh, int64_t sw, int64_t ph, int64_t pw, int k_order) {
+    if (!ctx || !conv_dims_ok(batch, c, oc, kh, kw, h, w, oh, ow, sh, sw, ph, pw)) return ZN_ERR_INVALID_ARG;
+    if (batch == 0) return ZN_OK;
+    if (!input || !weights || !grad_output || !grad_input || !grad_weights || !grad_bias) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    const int64_t hw = oh * ow, taps = c * kh * kw, plane = c * h * w;
+    if (hw == 0) {  // no output pixels: every gradient is zero
+        if ((rc = zn_hip_fill_f32(ctx, grad_input, 0.0f, batch * plane)) ||
+            (rc = zn_hip_fill_f32(ctx, grad_weights, 0.0f, oc * taps)))
+            return rc;
+        return zn_hip_fill_f32(ctx, grad_bias, 0.0f, oc);
+    }
+    constexpr int64_t kColFloats = (int64_t)1 << 28;  // 1 GiB of col per chunk
+    if (hw * taps > kColFloats) return ZN_ERR_OVERFLOW;
+    const int64_t chunk = std::min<int64_t>(batch, kColFloats / (hw * taps));
+    Lease col(ctx), part(ctx);
+    if ((rc = col.get((size_t)(chunk * hw * taps)))) return rc;
+    if (k_order == 1 && (rc = part.get((size_t)(chunk * oc * taps)))) return rc;
+    for (int64_t b0 = 0; b0 < batch; b0 += chunk) {
+        const int64_t nb = std::min(chunk, batch - b0);
+        const int64_t rows = nb * hw;
+        const float *go = grad_output + b0 * oc * hw;
+        float *gi = grad_input + b0 * plane;
+        ZnIm2colArgs ia = col_args(const_cast<float *>(input) + b0 * plane, col.ptr, nb, c, kh, kw, h, w, oh, ow, sh,
+                                   sw, ph, pw, k_order);
+        if ((rc = elt_launch(ctx, kIm2col, rows * taps, ia))) return rc;
+        if (k_order == 0) {
+            // grad_W (+)= go2^T . col: TN, M = OC, N = taps, K = rows
+            if ((rc = gemm_launch(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, col.ptr, taps, 0, grad_weights, taps, 0,
+                                  1, b0 > 0, nullptr, ZN_ACT_LINEAR)))
+                return rc;
+            // grad_col = go2 . W: NN, M = rows, N = taps, K = OC (into the col buffer)
+            if ((rc = gemm_launch(ctx, ZN_LAYOUT_NN, rows, taps, oc, go, oc, 0, weights, taps, 0, col.ptr, taps, 0, 1,
+                                  0, nullptr, ZN_ACT_LINEAR)))
+                return rc;
+        } else {
+            // per image go_b [OC x HW] . col_b [HW x taps] -> part[b], then summed in image order
+            if ((rc = gemm_launch(ctx, ZN_LAYOUT_NN, oc, taps, hw, go, hw, oc * hw, col.ptr, taps, hw * taps, part.ptr,
+                                  taps, oc * taps, nb, 0, nullptr, ZN_ACT_LINEAR)))
+                return rc;
+            ZnReduceArgs r;
+            std::memset(&r, 0, sizeof(r));
+            r.ws = part.ptr;
+            r.c = grad_weights;
+            r.ldc = taps;
+            r.m = (int32_t)oc;
+            r.n = (int32_t)taps;
+            r.batch = 1;
+            r.splits = (int32_t)nb;
+            r.accumulate = b0 > 0;
+            r.act = ZN_ACT_LINEAR;
+            r.vec = (taps % 4 == 0 && aligned16(grad_weights) && aligned16(part.ptr)) ? 1 : 0;
+            int64_t blocks = cdiv(oc * taps / (r.vec ? 4 : 1), 256);
+            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 8;
+            if (blocks > cap) blocks = cap;
+            if ((rc = launch(ctx, ctx->splitk_reduce, (unsigned)blocks, 1, 256, &r))) return rc;
+            // grad_col_b = go_b^T . W: TN, M = HW, N = taps, K = OC, per image
+            if ((rc = gemm_launch(ctx, ZN_LAYOUT_TN, hw, taps, oc, go, hw, oc * hw, weights, taps, 0, col.ptr, taps,
+                                  hw * taps, nb, 0, nullptr, ZN_ACT_LINEAR)))
+                return rc;
+        }
+        ZnIm2colArgs ca = col_args(gi, col.ptr, nb, c, kh, kw, h, w, oh, ow, sh, sw, ph, pw, k_order);
+        if ((rc = elt_launch(ctx, kCol2im, nb * plane, ca))) return rc;
+    }
+    ZnChannelSumArgs sa;
+    sa.in = grad_output;
+    sa.out = grad_bias;
+    sa.batch = batch;
+    sa.channels = oc;
+    sa.hw = hw;
+    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+    return launch(ctx, ctx->elt[kChannelSum], (unsigned)std::min<int64_t>(oc, cap), 1, 256, &sa);
+}
+
+int zn_hip_col2im(zn_ctx *ctx, const float *col, float *output, int64_t batch, int64_t channels, int64_t in_h,
+                  int64_t in_w, int64_t k_h, int64_t k_w, int64_t out_h, int64_t out_w, int64_t stride_h,
+                  int64_t stride_w, int64_t pad_h, int64_t pad_w) {
+    if (!ctx || !conv_dims_ok(batch, channels, 1, k_h, k_w, in_h, in_w, out_h, out_w, stride_h, stride_w, pad_h,
+                              pad_w))
+        return ZN_ERR_INVALID_ARG;
+    const int64_t total = batch * channels * in_h * in_w;
+    if (total == 0) return ZN_OK;
+    if (!output || (!col && out_h * out_w > 0)) return ZN_ERR_INVALID_ARG;
+    ZnIm2colArgs a = col_args(output, const_cast<float *>(col), batch, channels, k_h, k_w, in_h, in_w, out_h, out_w,
+                              stride_h, stride_w, pad_h, pad_w, 0);
+    return elt_launch(ctx, kCol2im, total, a);
+}
+
+int zn_hip_conv2d_backward_im2col(zn_ctx *ctx, const float *input, const float *weights, const float *grad_output,
+                                  float *grad_input, float *grad_weights, float *grad_bias, int64_t batch,
+                                  int64_t in_channels, int64_t out_channels, int64_t k_h, int64_t k_w, int64_t in_h,
+                                  int64_t in_w, int64_t out_h, int64_t out_w, int64_t stride_h, int64_t stride_w,
+                                  int64_t pad_h, int64_t pad_w) {
+    return conv2d_backward_device(ctx, input, weights, grad_output, grad_input, grad_weights, grad_bias, batch,
+                                  in_channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride_h, stride_w,
+                                  pad_h, pad_w, 0);
+}
+
+int zn_hip_conv2d_backward_direct(zn_ctx *ctx, const float *input, const float *weights, const float *grad_output,
+                                  float *grad_input, float *grad_weights, float *grad_bias, int64_t batch,
+                                  int64_t in_channels, int64_t out_channels, int64_t k_h, int64_t k_w, int64_t in_h,
+                                  int64_t in_w, int64_t out_h, int64_t out_w, int64_t stride_h, int64_t stride_w,
+                                  int64_t pad_h, int64_t pad_w) {
+    return conv2d_backward_device(ctx, input, weights, grad_output, grad_input, grad_weights, grad_bias, batch,
+                                  in_channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride_h, stride_w,
+                                  pad_h, pad_w, 1);
 }
 
 int zn_hip_softmax_rows(zn_ctx *ctx, const float *in, float *out, int64_t rows, int64_t n, float scale) {
@@ -1065,6 +1213,48 @@ int zn_hip_conv2d_forward_host(zn_ctx *ctx, const float *input, size_t input_len
                        use_im2col ? 0 : 1);
     if (rc) return rc;
     return copy_out_and_wait(ctx, output, dout.ptr, out_count);
+}
+
+int zn_hip_conv2d_backward_host(zn_ctx *ctx, const float *input, size_t input_len, const float *weights,
+                                size_t weights_len, const float *grad_output, size_t grad_output_len,
+                                float *grad_input, size_t grad_input_len, float *grad_weights, size_t grad_weights_len,
+                                float *grad_bias, size_t grad_bias_len, size_t in_channels, size_t out_channels,
+                                size_t k_h, size_t k_w, size_t in_h, size_t in_w, size_t out_h, size_t out_w,
+                                size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w) {
+    if (!ctx || in_channels == 0 || in_h == 0 || in_w == 0) return ZN_ERR_INVALID_ARG;
+    const int64_t lim = INT_MAX;
+    if ((int64_t)in_channels > lim || (int64_t)out_channels > lim || (int64_t)k_h > lim || (int64_t)k_w > lim ||
+        (int64_t)in_h > lim || (int64_t)in_w > lim || (int64_t)out_h > lim || (int64_t)out_w > lim)
+        return ZN_ERR_OVERFLOW;
+    const size_t plane = in_channels * in_h * in_w;
+    const size_t batch = input_len / plane;  // batch_size = input.len / (C*H*W) (src/backend.zig:3050)
+    const size_t taps = in_channels * k_h * k_w;
+    const size_t out_count = batch * out_channels * out_h * out_w;
+    if (weights_len < out_channels * taps || grad_output_len < out_count || grad_input_len < batch * plane ||
+        grad_weights_len < out_channels * taps || grad_bias_len < out_channels)
+        return ZN_ERR_INVALID_ARG;
+    if (batch == 0) return ZN_OK;
+    if (!input || !weights || !grad_output || !grad_input || !grad_weights || !grad_bias) return ZN_ERR_INVALID_ARG;
+    // the reference's switch (src/backend.zig:3053-3062)
+    const bool use_im2col = out_count >= 1024 && k_h * k_w >= 9;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    Lease din(ctx), dw(ctx), dgo(ctx), dgi(ctx), dgw(ctx), dgb(ctx);
+    if ((rc = din.get(batch * plane)) || (rc = dw.get(out_channels * taps)) || (rc = dgo.get(out_count)) ||
+        (rc = dgi.get(batch * plane)) || (rc = dgw.get(out_channels * taps)) || (rc = dgb.get(out_channels)))
+        return rc;
+    if ((rc = copy_in(ctx, din.ptr, input, batch * plane)) || (rc = copy_in(ctx, dw.ptr, weights, out_channels * taps)) ||
+        (rc = copy_in(ctx, dgo.ptr, grad_output, out_count)))
+        return rc;
+    rc = conv2d_backward_device(ctx, din.ptr, dw.ptr, dgo.ptr, dgi.ptr, dgw.ptr, dgb.ptr, (int64_t)batch,
+                                (int64_t)in_channels, (int64_t)out_channels, (int64_t)k_h, (int64_t)k_w, (int64_t)in_h,
+                                (int64_t)in_w, (int64_t)out_h, (int64_t)out_w, (int64_t)stride_h, (int64_t)stride_w,
+                                (int64_t)pad_h, (int64_t)pad_w, use_im2col ? 0 : 1);
+    if (rc) return rc;
+    ZN_HIP_TRY(ctx, hipMemcpyAsync(grad_weights, dgw.ptr, out_channels * taps * sizeof(float), hipMemcpyDeviceToHost,
+                                   ctx->stream));
+    ZN_HIP_TRY(ctx, hipMemcpyAsync(grad_bias, dgb.ptr, out_channels * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    return copy_out_and_wait(ctx, grad_input, dgi.ptr, batch * plane);
 }
 
 int zn_hip_attention_forward_host(zn_ctx *ctx, const float *q, size_t q_len, const float *k, size_t k_len,

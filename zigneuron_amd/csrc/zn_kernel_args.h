@@ -81,11 +81,21 @@ struct ZnAttnArgs {
     float scale_log2;  // scale * log2(e): scores are exponentiated base 2
 };
 
-// im2col (Backend.im2col layout): col[(b*OH*OW + oh*OW + ow)][(kh*KW + kw)*C + ic].
+// im2col / col2im: col[(b*OH*OW + oh*OW + ow)][tap], tap = (kh*KW + kw)*C + ic
+// (k_order 0, the Backend.im2col layout) or (ic*KH + kh)*KW + kw (k_order 1,
+// the OIHW weight order).
 struct ZnIm2colArgs {
-    const float *input;  // NCHW
-    float *col;
+    float *image;  // NCHW: read by im2col, written by col2im
+    float *col;    // written by im2col, read by col2im
     int32_t batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w;
+    int32_t k_order;
+};
+
+// Per-channel sum of an NCHW tensor: out[c] = sum over b, p of in[(b*C + c)*hw + p].
+struct ZnChannelSumArgs {
+    const float *in;
+    float *out;
+    int64_t batch, channels, hw;
 };
 
 #endif
