@@ -130,85 +130,129 @@ __device__ __forceinline__ void zn_tap_decode(const ZnIm2colArgs &p, int tap, in
     }
 }
 
-// Backend.im2col (src/backend.zig:3775-3827): one thread per element of
-// col[(b*OH*OW + oh*OW + ow)][tap]; zero outside the padded input.  Writes
-// are coalesced along the col row.
+// Backend.im2col (src/backend.zig:3775-3827): col[(b*OH*OW + oh*OW + ow)][tap],
+// zero outside the padded input.  A workgroup fills a tile of 64 col rows x
+// 64 taps: lanes run along the rows (neighbouring output pixels, so the NCHW
+// reads are contiguous) into LDS, then along the taps for the col stores.
+constexpr int kIm2colTile = 64;
 extern "C" __global__ __launch_bounds__(256) void zn_im2col(ZnIm2colArgs p) {
-    const int64_t kc = (int64_t)p.k_h * p.k_w * p.channels;
-    const int64_t hw = (int64_t)p.out_h * p.out_w;
-    const int64_t total = (int64_t)p.batch * hw * kc;
-    for (int64_t i = gtid(); i < total; i += gstride()) {
-        const int64_t row = i / kc;
-        int ic, kh, kw;
-        zn_tap_decode(p, (int)(i - row * kc), ic, kh, kw);
+    __shared__ float tile[kIm2colTile][kIm2colTile + 1];
+    const int kc = p.k_h * p.k_w * p.channels;
+    const int hw = p.out_h * p.out_w;
+    const int64_t rows = (int64_t)p.batch * hw;
+    const int64_t row_tiles = (rows + kIm2colTile - 1) / kIm2colTile;
+    const int tap_tiles = (kc + kIm2colTile - 1) / kIm2colTile;
+    const int64_t units = row_tiles * tap_tiles;
+    const int lane = threadIdx.x & 63, sub = threadIdx.x >> 6;
+    for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
+        const int64_t row0 = (u / tap_tiles) * kIm2colTile;
+        const int tap0 = (int)(u % tap_tiles) * kIm2colTile;
+        // gather: this lane's row (output pixel) is fixed, its taps step by 4
+        const int64_t row = row0 + lane;
         const int64_t b = row / hw;
         const int r = (int)(row - b * hw);
         const int oh = r / p.out_w, ow = r - oh * p.out_w;
-        const int ih = oh * p.stride_h - p.pad_h + kh;
-        const int iw = ow * p.stride_w - p.pad_w + kw;
-        float v = 0.0f;
-        if (ih >= 0 && iw >= 0 && ih < p.in_h && iw < p.in_w)
-            v = p.image[((b * p.channels + ic) * p.in_h + ih) * (int64_t)p.in_w + iw];
-        p.col[i] = v;
+        const float *img = p.image + b * p.channels * (int64_t)p.in_h * p.in_w;
+        for (int t = sub; t < kIm2colTile; t += 4) {
+            const int tap = tap0 + t;
+            float v = 0.0f;
+            if (row < rows && tap < kc) {
+                int ic, kh, kw;
+                zn_tap_decode(p, tap, ic, kh, kw);
+                const int ih = oh * p.stride_h - p.pad_h + kh;
+                const int iw = ow * p.stride_w - p.pad_w + kw;
+                if (ih >= 0 && iw >= 0 && ih < p.in_h && iw < p.in_w)
+                    v = img[((int64_t)ic * p.in_h + ih) * p.in_w + iw];
+            }
+            tile[t][lane] = v;
+        }
+        __syncthreads();
+        for (int rr = sub; rr < kIm2colTile; rr += 4) {
+            const int64_t orow = row0 + rr;
+            const int tap = tap0 + lane;
+            if (orow < rows && tap < kc) p.col[orow * kc + tap] = tile[lane][rr];
+        }
+        __syncthreads();  // the tile is rewritten by the next unit
     }
 }
 
-// Backend.col2im (src/backend.zig:3833-3877) as a gather: one thread per
-// NCHW output element, summing, from 0, the col entries that land on it in
-// the reference's order (output rows oh, then ow, ascending; each (oh, ow)
+// Backend.col2im (src/backend.zig:3833-3877) as a gather: every NCHW output
+// element is the sum, from 0, of the col entries that land on it in the
+// reference's order (output rows oh, then ow, ascending; each (oh, ow)
 // reaches a given input pixel through at most one tap), so the result is
-// bit-identical to the reference's scatter.
+// bit-identical to the reference's scatter.  A workgroup owns kCol2imW
+// pixels of one input row for 64 channels at a time: lanes run along the
+// channel (contiguous in the im2col-order col rows) while summing, and the
+// sums go through LDS so the NCHW stores run along the row.
+constexpr int kCol2imW = 64;
 extern "C" __global__ __launch_bounds__(256) void zn_col2im(ZnIm2colArgs p) {
-    const int64_t kc = (int64_t)p.k_h * p.k_w * p.channels;
+    __shared__ float tile[64][kCol2imW + 1];
+    const int kc = p.k_h * p.k_w * p.channels;
     const int64_t hw = (int64_t)p.out_h * p.out_w;
-    const int64_t plane = (int64_t)p.in_h * p.in_w;
-    const int64_t total = (int64_t)p.batch * p.channels * plane;
-    for (int64_t i = gtid(); i < total; i += gstride()) {
-        const int64_t bc = i / plane;
-        const int pix = (int)(i - bc * plane);
-        const int64_t b = bc / p.channels;
-        const int ic = (int)(bc - b * p.channels);
-        const int ih = pix / p.in_w, iw = pix - ih * p.in_w;
-        // output rows whose window covers ih: 0 <= ih + pad_h - oh*stride_h < k_h
-        const int hh = ih + p.pad_h, ww = iw + p.pad_w;
+    const int wtiles = (p.in_w + kCol2imW - 1) / kCol2imW;
+    const int64_t units = (int64_t)p.batch * p.in_h * wtiles;
+    const int lane_c = threadIdx.x & 63, sub = threadIdx.x >> 6;  // channel in group, pixel phase (0..3)
+    for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
+        const int wt = (int)(u % wtiles);
+        const int64_t bh = u / wtiles;
+        const int ih = (int)(bh % p.in_h);
+        const int64_t b = bh / p.in_h;
+        const int iw0 = wt * kCol2imW;
+        const int hh = ih + p.pad_h;
         const int oh_lo = hh >= p.k_h ? (hh - p.k_h) / p.stride_h + 1 : 0;
         const int oh_hi = min(hh / p.stride_h, p.out_h - 1);
-        const int ow_lo = ww >= p.k_w ? (ww - p.k_w) / p.stride_w + 1 : 0;
-        const int ow_hi = min(ww / p.stride_w, p.out_w - 1);
         const float *cb = p.col + b * hw * kc;
-        float sum = 0.0f;
-        for (int oh = oh_lo; oh <= oh_hi; ++oh) {
-            const int kh = hh - oh * p.stride_h;
-            for (int ow = ow_lo; ow <= ow_hi; ++ow) {
-                const int kw = ww - ow * p.stride_w;
-                const int tap = p.k_order == 0 ? (kh * p.k_w + kw) * p.channels + ic : (ic * p.k_h + kh) * p.k_w + kw;
-                sum = sum + cb[((int64_t)oh * p.out_w + ow) * kc + tap];
+        for (int c0 = 0; c0 < p.channels; c0 += 64) {
+            const int ic = c0 + lane_c;
+            for (int x = sub; x < kCol2imW; x += 4) {
+                const int iw = iw0 + x;
+                float sum = 0.0f;
+                if (ic < p.channels && iw < p.in_w) {
+                    const int ww = iw + p.pad_w;
+                    const int ow_lo = ww >= p.k_w ? (ww - p.k_w) / p.stride_w + 1 : 0;
+                    const int ow_hi = min(ww / p.stride_w, p.out_w - 1);
+                    for (int oh = oh_lo; oh <= oh_hi; ++oh) {
+                        const int kh = hh - oh * p.stride_h;
+                        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+                            const int kw = ww - ow * p.stride_w;
+                            const int tap =
+                                p.k_order == 0 ? (kh * p.k_w + kw) * p.channels + ic : (ic * p.k_h + kh) * p.k_w + kw;
+                            sum = sum + cb[((int64_t)oh * p.out_w + ow) * kc + tap];
+                        }
+                    }
+                }
+                tile[lane_c][x] = sum;
             }
+            __syncthreads();
+            for (int cc = sub; cc < 64; cc += 4) {
+                const int c = c0 + cc;
+                const int iw = iw0 + lane_c;
+                if (c < p.channels && iw < p.in_w)
+                    p.image[((b * p.channels + c) * p.in_h + ih) * (int64_t)p.in_w + iw] = tile[cc][lane_c];
+            }
+            __syncthreads();  // the tile is rewritten for the next channel group
         }
-        p.image[i] = sum;
     }
 }
 
-// out[c] = sum over (b, p) of in[(b*C + c)*hw + p]: one workgroup per
-// channel, each thread a fixed strided subset in ascending order, then a
-// fixed tree, so results do not depend on scheduling (the grad_bias of
-// cpuConv2dBackward, src/backend.zig:3073-3074, 3983-3993).
-extern "C" __global__ __launch_bounds__(256) void zn_channel_sum(ZnChannelSumArgs p) {
+// Row sums: out[r] = sum of in[r*n .. r*n + n), one workgroup per row, each
+// thread a fixed strided subset in ascending order, then a fixed tree, so
+// results do not depend on scheduling.  The per-(image, channel) stage of
+// the conv grad_bias (src/backend.zig:3073-3074, 3983-3993).
+extern "C" __global__ __launch_bounds__(256) void zn_row_sum(ZnEltArgs p) {
     __shared__ float red[256];
-    for (int64_t c = blockIdx.x; c < p.channels; c += gridDim.x) {
+    for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
+        const float *src = p.in0 + r * p.n;
         float s = 0.0f;
-        for (int64_t b = 0; b < p.batch; ++b) {
-            const float *src = p.in + (b * p.channels + c) * p.hw;
-            for (int64_t i = threadIdx.x; i < p.hw; i += 256) s = s + src[i];
-        }
-        __syncthreads();  // `red` may still be read for the previous channel
+        for (int64_t i = threadIdx.x; i < p.n; i += 256) s = s + src[i];
+        __syncthreads();  // `red` may still be read for the previous row
         red[threadIdx.x] = s;
         __syncthreads();
         for (int w = 128; w > 0; w >>= 1) {
             if ((int)threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
             __syncthreads();
         }
-        if (threadIdx.x == 0) p.out[c] = red[0];
+        if (threadIdx.x == 0) p.out[r] = red[0];
     }
 }
 

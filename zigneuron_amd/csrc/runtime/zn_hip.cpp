@@ -45,11 +45,11 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
                                          {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kChannelSum, kNumElt };
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kNumElt };
 constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", "zn_add_bias",
                                            "zn_activation_forward", "zn_activation_backward",
                                            "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows",
-                                           "zn_col2im",          "zn_channel_sum"};
+                                           "zn_col2im",          "zn_row_sum"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
@@ -219,7 +219,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // A gathered (implicit convolution) operand costs more per staged element, so
 // the larger l tile, which reuses each staged element over 128 rows, pays
 // off from 2 instead of 4 tiles per CU (C5 conv: l 221 us, m 227 us).
-Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t batch, bool gathered = false) {
+Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t batch, bool gathered = false) {
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     auto tiles = [&](Tile t) { return cdiv(m, kTiles[t].bm) * cdiv(n, kTiles[t].bn) * batch; };
     auto useful = [&](Tile t) { return 4 * m * n * batch >= 3 * tiles(t) * kTiles[t].bm * kTiles[t].bn; };
@@ -227,12 +227,16 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t batch, bool ga
     if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
     if (tiles(kTileL) >= (gathered ? 2 : 4) * cus && useful(kTileL)) return kTileL;
     if (tiles(kTileM) >= cus / 2) return kTileM;
+    // deep K (a reduction over a long batch, e.g. a weight gradient): 64x64
+    // tiles with many K splits beat 32x32 tiles (C5 conv dW, K = 100352: s 283 us)
+    if (k >= 4096 && tiles(kTileM) * (k / 512) >= 2 * cus) return kTileM;
     return kTileS;
 }
 
 // Split-K factor: problems that give fewer than ~4 workgroups per CU (the
 // latency-bound regime: few waves to hide each K slice's load round trip)
-// split K across blockIdx.z, keeping at least two BK slices per split.
+// split K across blockIdx.z, keeping at least two BK slices per split; at
+// most 16 splits, 64 when K >= 16384 (each split then still walks >= 256).
 int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k, int64_t batch) {
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     const TileShape &ts = kTiles[tile];
@@ -242,7 +246,8 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
     int64_t splits = target / tiles;
     const int64_t max_by_k = k / (2 * ts.bk);
     if (splits > max_by_k) splits = max_by_k;
-    if (splits > 16) splits = 16;
+    const int64_t cap = k >= 16384 ? 64 : 16;
+    if (splits > cap) splits = cap;
     return splits < 2 ? 1 : (int)splits;
 }
 
@@ -287,7 +292,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || b_extent > kLimit)) return ZN_ERR_OVERFLOW;
     if (conv && layout != ZN_LAYOUT_NN) return ZN_ERR_INVALID_ARG;
 
-    const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, batch, conv != nullptr);
+    const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, k, batch, conv != nullptr);
     const TileShape &ts = kTiles[tile];
     const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
     if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
@@ -782,6 +787,49 @@ static bool conv_dims_ok(int64_t batch, int64_t c, int64_t oc, int64_t kh, int64
     return batch <= lim && c * kh * kw <= lim && h * w <= lim && oh * ow <= lim && oc <= lim;
 }
 
+static ZnIm2colArgs col_args(float *image, float *col, int64_t batch, int64_t c, int64_t kh, int64_t kw, int64_t h,
+                             int64_t w, int64_t oh, int64_t ow, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                             int k_order) {
+    ZnIm2colArgs a;
+    a.image = image;
+    a.col = col;
+    a.batch = (int32_t)batch;
+    a.channels = (int32_t)c;
+    a.in_h = (int32_t)h;
+    a.in_w = (int32_t)w;
+    a.k_h = (int32_t)kh;
+    a.k_w = (int32_t)kw;
+    a.out_h = (int32_t)oh;
+    a.out_w = (int32_t)ow;
+    a.stride_h = (int32_t)sh;
+    a.stride_w = (int32_t)sw;
+    a.pad_h = (int32_t)ph;
+    a.pad_w = (int32_t)pw;
+    a.k_order = k_order;
+    return a;
+}
+
+// zn_im2col: one workgroup per tile of 64 col rows x 64 taps; zn_col2im: one
+// per 64 pixels of an input row (grid-stride loops cover the rest).
+static int im2col_launch(zn_ctx *ctx, const ZnIm2colArgs &a) {
+    const int rc = select_device(ctx);
+    if (rc) return rc;
+    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 32;
+    const int64_t units = cdiv((int64_t)a.batch * a.out_h * a.out_w, 64) * cdiv((int64_t)a.k_h * a.k_w * a.channels, 64);
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(units, cap));
+    ZnIm2colArgs c = a;
+    return launch(ctx, ctx->elt[kIm2col], (unsigned)blocks, 1, 256, &c);
+}
+static int col2im_launch(zn_ctx *ctx, const ZnIm2colArgs &a) {
+    const int rc = select_device(ctx);
+    if (rc) return rc;
+    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 32;
+    const int64_t units = (int64_t)a.batch * a.in_h * cdiv(a.in_w, 64);
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(units, cap));
+    ZnIm2colArgs c = a;
+    return launch(ctx, ctx->elt[kCol2im], (unsigned)blocks, 1, 256, &c);
+}
+
 int zn_hip_im2col(zn_ctx *ctx, const float *input, float *col, int64_t batch, int64_t channels, int64_t in_h,
                   int64_t in_w, int64_t k_h, int64_t k_w, int64_t out_h, int64_t out_w, int64_t stride_h,
                   int64_t stride_w, int64_t pad_h, int64_t pad_w) {
@@ -791,23 +839,9 @@ int zn_hip_im2col(zn_ctx *ctx, const float *input, float *col, int64_t batch, in
     const int64_t total = batch * out_h * out_w * k_h * k_w * channels;
     if (total == 0) return ZN_OK;
     if (!input || !col) return ZN_ERR_INVALID_ARG;
-    ZnIm2colArgs a;
-    a.image = const_cast<float *>(input);  // read only by zn_im2col
-    a.col = col;
-    a.batch = (int32_t)batch;
-    a.channels = (int32_t)channels;
-    a.in_h = (int32_t)in_h;
-    a.in_w = (int32_t)in_w;
-    a.k_h = (int32_t)k_h;
-    a.k_w = (int32_t)k_w;
-    a.out_h = (int32_t)out_h;
-    a.out_w = (int32_t)out_w;
-    a.stride_h = (int32_t)stride_h;
-    a.stride_w = (int32_t)stride_w;
-    a.pad_h = (int32_t)pad_h;
-    a.pad_w = (int32_t)pad_w;
-    a.k_order = 0;
-    return elt_launch(ctx, kIm2col, total, a);
+    ZnIm2colArgs a = col_args(const_cast<float *>(input), col, batch, channels, k_h, k_w, in_h, in_w, out_h, out_w,
+                              stride_h, stride_w, pad_h, pad_w, 0);  // input is only read by zn_im2col
+    return im2col_launch(ctx, a);
 }
 
 // Implicit-GEMM convolution: per image one NN GEMM
@@ -860,28 +894,6 @@ int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *w
 }
 
 // ------------------------------------------------------- conv backward
-static ZnIm2colArgs col_args(float *image, float *col, int64_t batch, int64_t c, int64_t kh, int64_t kw, int64_t h,
-                             int64_t w, int64_t oh, int64_t ow, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
-                             int k_order) {
-    ZnIm2colArgs a;
-    a.image = image;
-    a.col = col;
-    a.batch = (int32_t)batch;
-    a.channels = (int32_t)c;
-    a.in_h = (int32_t)h;
-    a.in_w = (int32_t)w;
-    a.k_h = (int32_t)kh;
-    a.k_w = (int32_t)kw;
-    a.out_h = (int32_t)oh;
-    a.out_w = (int32_t)ow;
-    a.stride_h = (int32_t)sh;
-    a.stride_w = (int32_t)sw;
-    a.pad_h = (int32_t)ph;
-    a.pad_w = (int32_t)pw;
-    a.k_order = k_order;
-    return a;
-}
-
 // Convolution backward on device.  k_order 0 follows cpuConv2dBackwardIm2col
 // (src/backend.zig:3954-4065): grad_output is read as [batch*OH*OW][OC] by
 // both GEMMs (grad_W = go2^T . col as one TN GEMM over all images, grad_col =
@@ -921,7 +933,7 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
         float *gi = grad_input + b0 * plane;
         ZnIm2colArgs ia = col_args(const_cast<float *>(input) + b0 * plane, col.ptr, nb, c, kh, kw, h, w, oh, ow, sh,
                                    sw, ph, pw, k_order);
-        if ((rc = elt_launch(ctx, kIm2col, rows * taps, ia))) return rc;
+        if ((rc = im2col_launch(ctx, ia))) return rc;
         if (k_order == 0) {
             // grad_W (+)= go2^T . col: TN, M = OC, N = taps, K = rows
             if ((rc = gemm_launch(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, col.ptr, taps, 0, grad_weights, taps, 0,
@@ -958,16 +970,31 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
                 return rc;
         }
         ZnIm2colArgs ca = col_args(gi, col.ptr, nb, c, kh, kw, h, w, oh, ow, sh, sw, ph, pw, k_order);
-        if ((rc = elt_launch(ctx, kCol2im, nb * plane, ca))) return rc;
+        if ((rc = col2im_launch(ctx, ca))) return rc;
     }
-    ZnChannelSumArgs sa;
-    sa.in = grad_output;
-    sa.out = grad_bias;
-    sa.batch = batch;
-    sa.channels = oc;
-    sa.hw = hw;
+    // grad_bias[c] = sum over images of the (image, channel) plane sums, added in image order
+    Lease planes(ctx);
+    if ((rc = planes.get((size_t)(batch * oc)))) return rc;
+    ZnEltArgs ra;
+    std::memset(&ra, 0, sizeof(ra));
+    ra.out = planes.ptr;
+    ra.in0 = grad_output;
+    ra.rows = batch * oc;
+    ra.n = hw;
     const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
-    return launch(ctx, ctx->elt[kChannelSum], (unsigned)std::min<int64_t>(oc, cap), 1, 256, &sa);
+    if ((rc = launch(ctx, ctx->elt[kRowSum], (unsigned)std::min<int64_t>(batch * oc, cap), 1, 256, &ra))) return rc;
+    if (batch > INT_MAX) return ZN_ERR_OVERFLOW;
+    ZnReduceArgs r;
+    std::memset(&r, 0, sizeof(r));
+    r.ws = planes.ptr;
+    r.c = grad_bias;
+    r.m = 1;
+    r.n = (int32_t)oc;
+    r.ldc = oc;
+    r.batch = 1;
+    r.splits = (int32_t)batch;
+    r.act = ZN_ACT_LINEAR;
+    return launch(ctx, ctx->splitk_reduce, (unsigned)std::min<int64_t>(cdiv(oc, 256), cap), 1, 256, &r);
 }
 
 int zn_hip_col2im(zn_ctx *ctx, const float *col, float *output, int64_t batch, int64_t channels, int64_t in_h,
@@ -981,7 +1008,7 @@ int zn_hip_col2im(zn_ctx *ctx, const float *col, float *output, int64_t batch, i
     if (!output || (!col && out_h * out_w > 0)) return ZN_ERR_INVALID_ARG;
     ZnIm2colArgs a = col_args(output, const_cast<float *>(col), batch, channels, k_h, k_w, in_h, in_w, out_h, out_w,
                               stride_h, stride_w, pad_h, pad_w, 0);
-    return elt_launch(ctx, kCol2im, total, a);
+    return col2im_launch(ctx, a);
 }
 
 int zn_hip_conv2d_backward_im2col(zn_ctx *ctx, const float *input, const float *weights, const float *grad_output,

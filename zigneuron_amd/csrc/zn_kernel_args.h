@@ -91,11 +91,5 @@ struct ZnIm2colArgs {
     int32_t k_order;
 };
 
-// Per-channel sum of an NCHW tensor: out[c] = sum over b, p of in[(b*C + c)*hw + p].
-struct ZnChannelSumArgs {
-    const float *in;
-    float *out;
-    int64_t batch, channels, hw;
-};
 
 #endif
