@@ -185,6 +185,22 @@ int zn_hip_activation_backward(zn_ctx *ctx, int act, const float *y, const float
  * (Backend.accumulateBias, src/backend.zig:649-655, 706-713). */
 int zn_hip_accumulate_bias(zn_ctx *ctx, float *grad_bias, const float *gaa, int64_t rows, int64_t n);
 
+/* Dense.backward (src/layer.zig:411-475) on device pointers, row-major
+ * input [batch x in], weights [in x out], activated_output / grad_output /
+ * grad_after_act [batch x out]:
+ *   grad_after_act = activationBackward(act, activated_output, grad_output)
+ *   grad_bias     += column sums of grad_after_act          (accumulateBias)
+ *   grad_input     = grad_after_act . weights^T             (matMulTransposeB)
+ *   grad_weights   = input^T . grad_after_act  (overwritten) (matMulTransposeA)
+ * The first two run as one pass; the bias sums are taken over row splits and
+ * added in split order (deterministic, within the GEMM tolerance rather than
+ * bit-identical to the row-by-row sum of zn_hip_accumulate_bias).
+ * grad_input may be null to skip it. */
+int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float *weights,
+                          const float *activated_output, const float *grad_output, float *grad_after_act,
+                          float *grad_input, float *grad_weights, float *grad_bias, int64_t batch, int64_t in_size,
+                          int64_t out_size);
+
 /* ------------------------------------- conv and attention (device pointers) */
 
 /* Backend.im2col (src/backend.zig:3775-3827) on device: NCHW `input` ->

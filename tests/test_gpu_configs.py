@@ -50,22 +50,35 @@ def test_c1_nn_512(ctx):
     assert_close(c, ref_gemm("nn", a, b, m, n, k), "nn", a, b, m, n, k)
 
 
-def test_c2_mlp_training_step(ctx):
+def check_bias(got, gaa, fused, start=None):
+    start = np.zeros(gaa.shape[1], np.float32) if start is None else start
+    ref = oracle.accumulate_bias(start, gaa)
+    if not fused:
+        np.testing.assert_array_equal(got, ref)
+        return
+    den = np.abs(start.astype(np.float64)) + np.abs(gaa.astype(np.float64)).sum(axis=0)
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= tol(gaa.shape[0]) * den)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_c2_mlp_training_step(ctx, fused):
     """X[256x784] U[0,1) -> W1 He + b1(0) + ReLU -> W2 Xavier + b2(0) linear; dY2 U[-1,1).
-    Each of the six GEMMs is checked against the oracle on the GPU's own inputs."""
+    Each of the six GEMMs is checked against the oracle on the GPU's own inputs.
+    The reference's call sequence gives bit-identical bias gradients; the fused
+    backward sums them over row splits (within the GEMM tolerance)."""
     from zigneuron_amd import DenseDevice
     batch, d_in, d_h, d_out = 256, 784, 128, 10
     rng = np.random.default_rng(42)
     x = uniform(rng, (batch, d_in), 0.0, 1.0)
     dy = uniform(rng, (batch, d_out))
-    announce("C2 MLP step")
+    announce(f"C2 MLP step fused={fused}")
     l1 = DenseDevice(ctx, d_in, d_h, "relu", batch, seed=1)
     l2 = DenseDevice(ctx, d_h, d_out, "linear", batch, seed=2)
     dx, ddy = ctx.to_device(x), ctx.to_device(dy)
     h1 = l1.forward(dx)
     logits = l2.forward(h1)
-    g_h1 = l2.backward(h1, ddy)
-    g_x = l1.backward(dx, g_h1)
+    g_h1 = l2.backward(h1, ddy, fused=fused)
+    g_x = l1.backward(dx, g_h1, fused=fused)
     ctx.sync()
     W1 = l1.weights.download().reshape(d_in, d_h)
     W2 = l2.weights.download().reshape(d_h, d_out)
@@ -85,7 +98,7 @@ def test_c2_mlp_training_step(ctx):
     dW2 = l2.grad_weights.download().reshape(d_h, d_out)
     assert_close(dW2, oracle.matmul_tn(H1, gaa2, d_h, d_out, batch), "tn", H1, gaa2, d_h, d_out, batch,
                  what="L2 dW (TN)")
-    np.testing.assert_array_equal(l2.grad_bias.download(), oracle.accumulate_bias(np.zeros(d_out, np.float32), gaa2))
+    check_bias(l2.grad_bias.download(), gaa2, fused)
     # L1 backward: gaa1 = relu'(H1) * GH1, dX1 = gaa1 . W1^T (NT), dW1 = X^T . gaa1 (TN)
     gaa1 = l1.gaa.download().reshape(batch, d_h)
     np.testing.assert_array_equal(gaa1, oracle.activation_backward("relu", H1, GH1).reshape(batch, d_h))
@@ -95,7 +108,7 @@ def test_c2_mlp_training_step(ctx):
     dW1 = l1.grad_weights.download().reshape(d_in, d_h)
     assert_close(dW1, oracle.matmul_tn(x, gaa1, d_in, d_h, batch, threads=THREADS), "tn", x, gaa1, d_in, d_h, batch,
                  what="L1 dW (TN)")
-    np.testing.assert_array_equal(l1.grad_bias.download(), oracle.accumulate_bias(np.zeros(d_h, np.float32), gaa1))
+    check_bias(l1.grad_bias.download(), gaa1, fused)
 
 
 @pytest.mark.parametrize("which", ["dW_TN", "dX_NT"])
@@ -189,3 +202,36 @@ def test_c5_im2col_conv_gemm(ctx):
     assert_close(c[rows], oracle.matmul_nt(col_s, w, len(rows), OC, K, threads=THREADS), "nt", col_s, w, len(rows),
                  OC, K, what="conv sampled rows")
     checksum_property(c, col, w.T, K, "conv")
+
+
+@pytest.mark.parametrize("act", ["linear", "relu", "sigmoid", "tanh"])
+@pytest.mark.parametrize("shape", [(256, 784, 128), (33, 17, 5), (4096, 1024, 1024), (1, 9, 300)])
+def test_dense_backward_fused(ctx, act, shape):
+    """zn_hip_dense_backward against the reference's four steps: the
+    activation derivative bit-exact, grad_bias (+= onto a non-zero start)
+    within the GEMM tolerance, the NT / TN products componentwise."""
+    batch, d_in, d_out = shape
+    rng = np.random.default_rng(batch + d_in + d_out)
+    x, w = uniform(rng, (batch, d_in)), uniform(rng, (d_in, d_out))
+    y = oracle.activation_forward(act, uniform(rng, (batch, d_out)) * 3).reshape(batch, d_out)
+    go = uniform(rng, (batch, d_out))
+    gb0 = uniform(rng, (d_out,))
+    announce(f"dense backward {act} {shape}")
+    dx, dw, dy, dgo = (ctx.to_device(a) for a in (x, w, y, go))
+    dgaa, dgi, dgw = ctx.alloc(batch * d_out), ctx.alloc(batch * d_in), ctx.alloc(d_in * d_out).fill(np.nan)
+    dgb = ctx.to_device(gb0)
+    ctx.dense_backward(act, dx, dw, dy, dgo, dgaa, dgi, dgw, dgb, batch, d_in, d_out)
+    gaa = dgaa.download().reshape(batch, d_out)
+    np.testing.assert_array_equal(gaa, oracle.activation_backward(act, y, go).reshape(batch, d_out))
+    check_bias(dgb.download(), gaa, True, start=gb0)
+    gi = dgi.download().reshape(batch, d_in)
+    assert_close(gi, oracle.matmul_nt(gaa, w, batch, d_in, d_out, threads=THREADS), "nt", gaa, w, batch, d_in, d_out,
+                 what="grad_input")
+    gw = dgw.download().reshape(d_in, d_out)
+    assert_close(gw, oracle.matmul_tn(x, gaa, d_in, d_out, batch, threads=THREADS), "tn", x, gaa, d_in, d_out, batch,
+                 what="grad_weights")
+    # first layer: no grad_input; grad_weights is overwritten (deterministically), not accumulated
+    ctx.dense_backward(act, dx, dw, dy, dgo, dgaa, None, dgw, dgb, batch, d_in, d_out)
+    np.testing.assert_array_equal(dgw.download().reshape(d_in, d_out), gw)
+    for buf in (dx, dw, dy, dgo, dgaa, dgi, dgw, dgb):
+        buf.close()

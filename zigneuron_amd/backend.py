@@ -199,6 +199,15 @@ class Context:
         check(_lib.load().zn_hip_accumulate_bias(self.handle, _dptr(grad_bias), _dptr(gaa), rows, n),
               "zn_hip_accumulate_bias")
 
+    def dense_backward(self, act, inp, weights, activated_output, grad_output, grad_after_act, grad_input,
+                       grad_weights, grad_bias, batch, in_size, out_size) -> None:
+        """Dense.backward in one call: fused activationBackward + bias-gradient pass, NT, TN
+        (grad_input may be None)."""
+        check(_lib.load().zn_hip_dense_backward(
+            self.handle, act_id(act), _dptr(inp), _dptr(weights), _dptr(activated_output), _dptr(grad_output),
+            _dptr(grad_after_act), _dptr(grad_input), _dptr(grad_weights), _dptr(grad_bias), batch, in_size, out_size),
+            "zn_hip_dense_backward")
+
     # --- convolution and attention on device pointers
     def im2col(self, inp, col, batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h=1, stride_w=1,
                pad_h=0, pad_w=0) -> None:

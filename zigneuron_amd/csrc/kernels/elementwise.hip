@@ -114,6 +114,40 @@ extern "C" __global__ __launch_bounds__(256) void zn_accumulate_bias(ZnEltArgs p
     p.out[col] = s;
 }
 
+// Dense.backward's first two steps in one pass (src/layer.zig:429-445,
+// 458-462): gaa = activationBackward(y, grad_out) elementwise (as
+// zn_activation_backward) and, for the bias gradient, column sums of gaa
+// over the rows of split blockIdx.y (rows ascending within the split).  One
+// thread per column, 256 columns per workgroup, so row loads are coalesced.
+extern "C" __global__ __launch_bounds__(256) void zn_dense_grad_prologue(ZnDenseGradArgs p) {
+    const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (col >= p.n) return;
+    const int64_t r0 = (int64_t)blockIdx.y * p.rows_per_split;
+    const int64_t r1 = r0 + p.rows_per_split < p.rows ? r0 + p.rows_per_split : p.rows;
+    float s = 0.0f;
+    int64_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+        float y[4], g[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            y[q] = p.y[(r + q) * p.n + col];
+            g[q] = p.go[(r + q) * p.n + col];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float d = act_backward(y[q], g[q], p.act);
+            p.gaa[(r + q) * p.n + col] = d;
+            s = s + d;
+        }
+    }
+    for (; r < r1; ++r) {
+        const float d = act_backward(p.y[r * p.n + col], p.go[r * p.n + col], p.act);
+        p.gaa[r * p.n + col] = d;
+        s = s + d;
+    }
+    p.partial[(int64_t)blockIdx.y * p.n + col] = s;
+}
+
 // Filter tap index <-> (ic, kh, kw) for the two col K orders.
 __device__ __forceinline__ void zn_tap_decode(const ZnIm2colArgs &p, int tap, int &ic, int &kh, int &kw) {
     if (p.k_order == 0) {

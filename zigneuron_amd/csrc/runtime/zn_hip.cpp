@@ -45,11 +45,11 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
                                          {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kNumElt };
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kNumElt };
 constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", "zn_add_bias",
                                            "zn_activation_forward", "zn_activation_backward",
                                            "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows",
-                                           "zn_col2im",          "zn_row_sum"};
+                                           "zn_col2im",          "zn_row_sum",  "zn_dense_grad_prologue"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
@@ -891,6 +891,70 @@ int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *w
                                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w) {
     return conv2d_device(ctx, input, weights, bias, output, batch, in_channels, out_channels, k_h, k_w, in_h, in_w,
                          out_h, out_w, stride_h, stride_w, pad_h, pad_w, 1);
+}
+
+// ------------------------------------------------------- Dense backward
+// Dense.backward (src/layer.zig:411-475) on device pointers:
+//   gaa = activationBackward(act, y, grad_output)  and  grad_bias += sum_rows gaa
+// in one pass (zn_dense_grad_prologue: per-split column sums, then the
+// split-K reduce adds the splits in ascending order onto grad_bias), then
+// grad_input = gaa . W^T (NT) and grad_weights = input^T . gaa (TN,
+// overwritten like the reference).  grad_input may be null (first layer).
+int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float *weights,
+                          const float *activated_output, const float *grad_output, float *grad_after_act,
+                          float *grad_input, float *grad_weights, float *grad_bias, int64_t batch, int64_t in_size,
+                          int64_t out_size) {
+    if (!ctx || act < ZN_ACT_LINEAR || act > ZN_ACT_TANH || batch < 0 || in_size < 0 || out_size < 0)
+        return ZN_ERR_INVALID_ARG;
+    if (batch > INT_MAX || in_size > INT_MAX || out_size > INT_MAX) return ZN_ERR_OVERFLOW;
+    if (out_size == 0) return ZN_OK;
+    if (batch > 0 && (!activated_output || !grad_output || !grad_after_act || !grad_bias)) return ZN_ERR_INVALID_ARG;
+    if (in_size > 0 && (!grad_weights || (batch > 0 && (!input || !weights)))) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    if (batch > 0) {
+        const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+        const int64_t col_groups = cdiv(out_size, 256);
+        // enough row splits for ~4 workgroups per CU, at least 16 rows each
+        int64_t splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(batch, 16), 4 * cus / col_groups));
+        if (splits > 65535) splits = 65535;
+        const int64_t per = cdiv(batch, splits);
+        splits = cdiv(batch, per);
+        Lease part(ctx);
+        if ((rc = part.get((size_t)(splits * out_size)))) return rc;
+        ZnDenseGradArgs g;
+        g.y = activated_output;
+        g.go = grad_output;
+        g.gaa = grad_after_act;
+        g.partial = part.ptr;
+        g.rows = batch;
+        g.n = out_size;
+        g.act = act;
+        g.rows_per_split = (int32_t)per;
+        if ((rc = launch(ctx, ctx->elt[kDenseGrad], (unsigned)col_groups, (unsigned)splits, 256, &g))) return rc;
+        ZnReduceArgs r;
+        std::memset(&r, 0, sizeof(r));
+        r.ws = part.ptr;
+        r.c = grad_bias;
+        r.m = 1;
+        r.n = (int32_t)out_size;
+        r.ldc = out_size;
+        r.batch = 1;
+        r.splits = (int32_t)splits;
+        r.accumulate = 1;
+        r.act = ZN_ACT_LINEAR;
+        r.vec = (out_size % 4 == 0 && aligned16(grad_bias) && aligned16(part.ptr)) ? 1 : 0;
+        const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(cdiv(out_size / (r.vec ? 4 : 1), 256), 8 * cus));
+        if ((rc = launch(ctx, ctx->splitk_reduce, (unsigned)blocks, 1, 256, &r))) return rc;
+    }
+    if (in_size == 0) return ZN_OK;
+    if (grad_input && batch > 0 &&
+        (rc = gemm_launch(ctx, ZN_LAYOUT_NT, batch, in_size, out_size, grad_after_act, out_size, 0, weights, out_size,
+                          0, grad_input, in_size, 0, 1, 0, nullptr, ZN_ACT_LINEAR)))
+        return rc;
+    if (batch == 0) return zn_hip_fill_f32(ctx, grad_weights, 0.0f, in_size * out_size);
+    return gemm_launch(ctx, ZN_LAYOUT_TN, in_size, out_size, batch, input, in_size, 0, grad_after_act, out_size, 0,
+                       grad_weights, out_size, 0, 1, 0, nullptr, ZN_ACT_LINEAR);
 }
 
 // ------------------------------------------------------- conv backward

@@ -81,6 +81,18 @@ struct ZnAttnArgs {
     float scale_log2;  // scale * log2(e): scores are exponentiated base 2
 };
 
+// Dense backward prologue: gaa = act'(y) * grad_out elementwise and, per
+// split of `rows_per_split` rows (blockIdx.y), the column sums of gaa.
+struct ZnDenseGradArgs {
+    const float *y;        // activated output [rows x n]
+    const float *go;       // grad_output [rows x n]
+    float *gaa;            // grad after activation [rows x n]
+    float *partial;        // [splits x n] column sums
+    int64_t rows, n;
+    int32_t act;
+    int32_t rows_per_split;
+};
+
 // im2col / col2im: col[(b*OH*OW + oh*OW + ow)][tap], tap = (kh*KW + kw)*C + ic
 // (k_order 0, the Backend.im2col layout) or (ic*KH + kh)*KW + kw (k_order 1,
 // the OIHW weight order).

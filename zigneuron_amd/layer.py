@@ -100,8 +100,16 @@ class DenseDevice:
                        self.output_size, self.out, self.output_size, False, self.bias, self.act)
         return self.out
 
-    def backward(self, x: DeviceBuffer, grad_out: DeviceBuffer) -> DeviceBuffer:
-        """activationBackward -> NT (grad_input) -> accumulateBias -> TN (grad_weights)."""
+    def backward(self, x: DeviceBuffer, grad_out: DeviceBuffer, fused: bool = True) -> DeviceBuffer:
+        """activationBackward -> NT (grad_input) -> accumulateBias -> TN (grad_weights).
+
+        fused: one zn_hip_dense_backward call (activation derivative and bias
+        sums in one pass, bias summed over row splits); otherwise the
+        reference's four calls, with the row-by-row bias sum."""
+        if fused:
+            self.ctx.dense_backward(self.act, x, self.weights, self.out, grad_out, self.gaa, self.grad_input,
+                                    self.grad_weights, self.grad_bias, self.batch, self.input_size, self.output_size)
+            return self.grad_input
         n_out = self.batch * self.output_size
         self.ctx.activation_backward(self.act, self.out, grad_out, self.gaa, n_out)
         self.ctx.sgemm("nt", self.batch, self.input_size, self.output_size, self.gaa, self.output_size,
