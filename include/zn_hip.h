@@ -67,6 +67,7 @@ typedef enum zn_act {
 
 typedef struct zn_ctx zn_ctx;
 typedef struct zn_event zn_event;
+typedef struct zn_graph zn_graph;
 
 typedef struct zn_device_info {
     char name[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
@@ -128,6 +129,25 @@ int zn_hip_copy_f32(zn_ctx *ctx, float *dst, const float *src, int64_t count);
 /* Wait for all work on the context's stream. */
 int zn_hip_sync(zn_ctx *ctx);
 
+/* ----------------------------------------------------------------- graphs */
+
+/* Capture the device-pointer calls that follow on the context's stream into a
+ * HIP graph (stream capture, relaxed mode) instead of running them; replay it
+ * with one launch.  No counterpart in the reference: it serves callers whose
+ * steps are bound by launch cost, such as a small-batch MLP training step.
+ *  - Calls that wait for the device (zn_hip_sync, zn_hip_free, blocking
+ *    copies, the *_host drop-ins) return ZN_ERR_INVALID_ARG while capturing.
+ *  - Run the sequence once before capturing it: a GEMM that would have to
+ *    grow the split-K workspace during capture runs unsplit instead.
+ *  - Buffers the runtime leases during capture belong to the graph until
+ *    zn_hip_graph_destroy; graphs still alive are destroyed by zn_hip_destroy.
+ *  - Nothing in a graph clears memory with a memset node (fills are kernels). */
+int zn_hip_graph_begin(zn_ctx *ctx);
+int zn_hip_graph_end(zn_ctx *ctx, zn_graph **out);
+int zn_hip_graph_launch(zn_ctx *ctx, zn_graph *graph);
+/* Waits for the context's stream, then releases the graph and its buffers. */
+int zn_hip_graph_destroy(zn_graph *graph);
+
 /* ----------------------------------------------------------------- events */
 
 /* HIP events on the context's stream, for kernel timing (the role of the
@@ -151,6 +171,11 @@ int zn_hip_event_destroy(zn_event *ev);
 #define ZN_TILE_64x64 3
 #define ZN_TILE_32x32 4
 int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile);
+/* Split-K override: 0 (the default) lets the policy choose, 1..64 forces that
+ * many K slices (at most K / BK) for every following GEMM on this context.
+ * Like the tile override, a tuning and test hook with no reference
+ * counterpart. */
+int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits);
 
 /* C = act((accumulate ? C : 0) + op(A).op(B) + bias) for one problem.
  * `bias` (length N) may be NULL.  Leading dimensions are in elements and must

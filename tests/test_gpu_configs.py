@@ -235,3 +235,55 @@ def test_dense_backward_fused(ctx, act, shape):
     np.testing.assert_array_equal(dgw.download().reshape(d_in, d_out), gw)
     for buf in (dx, dw, dy, dgo, dgaa, dgi, dgw, dgb):
         buf.close()
+
+
+def test_graph_replay_of_mlp_step_matches_eager(ctx):
+    """The C2 training step (bias-gradient reset by a fill kernel, two fused
+    forwards, two fused backwards) captured once and replayed three times,
+    with unrelated eager GEMMs and synchronisations between the replays:
+    every replay reproduces the eager step bit for bit."""
+    from zigneuron_amd import DenseDevice, InvalidArgumentError
+    batch = 256
+    rng = np.random.default_rng(7)
+    x = ctx.to_device(uniform(rng, (batch, 784), 0.0, 1.0))
+    dy = ctx.to_device(uniform(rng, (batch, 10)))
+    l1 = DenseDevice(ctx, 784, 128, "relu", batch, seed=1)
+    l2 = DenseDevice(ctx, 128, 10, "linear", batch, seed=2)
+
+    def step():
+        l1.grad_bias.fill(0.0)
+        l2.grad_bias.fill(0.0)
+        h = l1.forward(x)
+        l2.forward(h)
+        g = l2.backward(h, dy)
+        l1.backward(x, g)
+
+    def outputs():
+        return [b.download() for b in (l1.out, l2.out, l2.grad_input, l1.grad_input, l1.grad_weights,
+                                       l2.grad_weights, l1.grad_bias, l2.grad_bias)]
+
+    announce("graph replay MLP step")
+    step()
+    ctx.sync()
+    eager = outputs()
+    with pytest.raises(InvalidArgumentError):
+        ctx.capture(ctx.sync)  # waiting for the device is refused under capture
+    graph = ctx.capture(step)
+    other_a, other_b = ctx.to_device(uniform(rng, (300, 200))), ctx.to_device(uniform(rng, (200, 100)))
+    other_c = ctx.alloc(300 * 100)
+    for _ in range(3):
+        for b in (l1.out, l2.out, l2.grad_input, l1.grad_input, l1.grad_weights, l2.grad_weights):
+            b.fill(np.nan)
+        graph.launch()
+        ctx.sync()
+        for got, ref in zip(outputs(), eager):
+            np.testing.assert_array_equal(got, ref)
+        ctx.sgemm("nn", 300, 100, 200, other_a, 200, other_b, 100, other_c, 100)
+        ctx.sync()
+    graph.close()
+    step()  # the context keeps working eagerly after the graph is gone
+    ctx.sync()
+    for got, ref in zip(outputs(), eager):
+        np.testing.assert_array_equal(got, ref)
+    for b in (x, dy, other_a, other_b, other_c):
+        b.close()

@@ -112,11 +112,16 @@ SIGNATURES = {
     "zn_hip_fill_f32": (I, [P, P, F, I64]),
     "zn_hip_copy_f32": (I, [P, P, P, I64]),
     "zn_hip_sync": (I, [P]),
+    "zn_hip_graph_begin": (I, [P]),
+    "zn_hip_graph_end": (I, [P, ctypes.POINTER(P)]),
+    "zn_hip_graph_launch": (I, [P, P]),
+    "zn_hip_graph_destroy": (I, [P]),
     "zn_hip_event_create": (I, [P, ctypes.POINTER(P)]),
     "zn_hip_event_record": (I, [P, P]),
     "zn_hip_event_elapsed_ms": (I, [P, P, ctypes.POINTER(F)]),
     "zn_hip_event_destroy": (I, [P]),
     "zn_hip_set_gemm_tile": (I, [P, I]),
+    "zn_hip_set_gemm_splits": (I, [P, I]),
     "zn_hip_sgemm": (I, [P, I, I64, I64, I64, P, I64, P, I64, P, I64, I, P, I]),
     "zn_hip_sgemm_strided_batched": (I, [P, I, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, I64, I, P, I]),
     "zn_hip_add_bias": (I, [P, P, P, I64, I64]),

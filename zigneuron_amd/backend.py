@@ -62,6 +62,21 @@ def _ptr(x: np.ndarray) -> int:
     return x.ctypes.data
 
 
+class Graph:
+    """A captured sequence of device calls, replayed with one launch (zn_hip_graph_*)."""
+
+    def __init__(self, ctx: "Context", handle: ctypes.c_void_p):
+        self._ctx, self.handle = ctx, handle
+
+    def launch(self) -> None:
+        check(_lib.load().zn_hip_graph_launch(self._ctx.handle, self.handle), "zn_hip_graph_launch")
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.load().zn_hip_graph_destroy(self.handle)
+            self.handle = None
+
+
 class Event:
     def __init__(self, ctx: "Context"):
         self._ctx = ctx
@@ -162,6 +177,21 @@ class Context:
     def event(self) -> Event:
         return Event(self)
 
+    def capture(self, fn) -> Graph:
+        """Run fn() under stream capture and return the graph of its device calls.
+        Run fn() once eagerly first (it sizes the split-K workspace)."""
+        L = _lib.load()
+        check(L.zn_hip_graph_begin(self.handle), "zn_hip_graph_begin")
+        h = ctypes.c_void_p()
+        try:
+            fn()
+        except BaseException:
+            if L.zn_hip_graph_end(self.handle, ctypes.byref(h)) == _lib.ZN_OK and h:
+                L.zn_hip_graph_destroy(h)
+            raise
+        check(L.zn_hip_graph_end(self.handle, ctypes.byref(h)), "zn_hip_graph_end")
+        return Graph(self, h)
+
     def copy(self, dst: int, src: int, count: int) -> None:
         check(_lib.load().zn_hip_copy_f32(self.handle, int(dst), int(src), int(count)), "zn_hip_copy_f32")
 
@@ -169,6 +199,10 @@ class Context:
         """Force one macro tile ("256x128", "128x128", "128x64", "64x64", "32x32") or "auto"."""
         check(_lib.load().zn_hip_set_gemm_tile(self.handle, _lib.TILES[tile] if isinstance(tile, str) else tile),
               "zn_hip_set_gemm_tile")
+
+    def set_gemm_splits(self, splits: int = 0) -> None:
+        """Force the number of split-K slices (1..64), or 0 for the policy."""
+        check(_lib.load().zn_hip_set_gemm_splits(self.handle, int(splits)), "zn_hip_set_gemm_splits")
 
     # --- GEMM on device pointers (asynchronous on the context stream)
     def sgemm(self, layout, m, n, k, a, lda, b, ldb, c, ldc, accumulate=False, bias=None, act="linear") -> None:

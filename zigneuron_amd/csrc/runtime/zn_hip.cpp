@@ -75,7 +75,14 @@ struct zn_ctx {
     size_t ws_bytes = 0;
     hipFunction_t elt[kNumElt] = {};
     int last_hip_error = 0;
-    int forced_tile = -1;  // ZN_TILE_AUTO
+    // Graph capture (zn_hip_graph_begin .. _end): leased buffers go to
+    // `captured` instead of back to the pool and become the graph's.
+    bool capturing = false;
+    std::vector<std::pair<void *, size_t>> captured;
+    std::vector<zn_graph *> graphs;   // live graphs, destroyed with the context
+    std::vector<void *> retired_ws;   // workspaces a live graph may still reference
+    int forced_tile = -1;    // ZN_TILE_AUTO
+    int forced_splits = 0;   // 0: the split-K policy decides
     zn_device_info info = {};
     // Cached device buffers for the host-slice entry points, keyed by
     // power-of-two byte size.
@@ -84,6 +91,12 @@ struct zn_ctx {
 
 struct zn_event {
     hipEvent_t ev = nullptr;
+};
+
+struct zn_graph {
+    zn_ctx *ctx = nullptr;
+    hipGraphExec_t exec = nullptr;
+    std::vector<std::pair<void *, size_t>> buffers;  // leased during capture
 };
 
 namespace {
@@ -146,6 +159,7 @@ int pool_get(zn_ctx *ctx, size_t bytes, float **out) {
         // release cached buffers (after the stream drains: queued kernels may
         // still use buffers returned to the cache) and retry once
         (void)hipGetLastError();
+        if (ctx->capturing) return fail_hip(ctx, e, ZN_ERR_OOM);  // no stream sync under capture
         (void)hipStreamSynchronize(ctx->stream);
         for (auto &kv : ctx->pool)
             for (void *q : kv.second) (void)hipFree(q);
@@ -161,17 +175,25 @@ int pool_get(zn_ctx *ctx, size_t bytes, float **out) {
 }
 
 void pool_put(zn_ctx *ctx, float *p, size_t bytes) {
-    if (p) ctx->pool[bucket_of(bytes ? bytes : 4)].push_back(p);
+    if (!p) return;
+    if (ctx->capturing)
+        ctx->captured.emplace_back(p, bucket_of(bytes ? bytes : 4));  // the graph keeps using it
+    else
+        ctx->pool[bucket_of(bytes ? bytes : 4)].push_back(p);
 }
 
 // Make the split-K workspace at least `bytes` long.  Growing waits for the
 // stream first, because queued kernels may still use the old buffer.
 int ensure_workspace(zn_ctx *ctx, size_t bytes) {
     if (ctx->ws_bytes >= bytes) return ZN_OK;
+    if (ctx->capturing) return ZN_ERR_INVALID_ARG;  // no sync under capture: the GEMM runs unsplit
     size_t want = ctx->ws_bytes ? ctx->ws_bytes : ((size_t)1 << 22);
     while (want < bytes) want <<= 1;
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->ws && !ctx->graphs.empty())
+        ctx->retired_ws.push_back(ctx->ws);  // a live graph may reference it
+    else if (ctx->ws)
+        (void)hipFree(ctx->ws);
     ctx->ws = nullptr;
     ctx->ws_bytes = 0;
     void *p = nullptr;
@@ -210,42 +232,46 @@ int launch(zn_ctx *ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned thre
 // ------------------------------------------------------------ GEMM policy
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Tile choice, from measurements on MI355X (256 CUs): the largest tiles win
-// once they give every CU two or more workgroups; below that, latency
-// hiding needs more, smaller workgroups (64x64); N <= 64 uses 128x64 so no
-// MFMA block idles; tiny problems use 32x32 to spread over more CUs.
-// A tile whose padding wastes more than a quarter of its MFMA work (for
-// example 256-row tiles over M = 128) is skipped for the next smaller one.
+// Tile choice, from measurements on MI355X (256 CUs, per-launch times from
+// graph replays): the largest tiles win once they give every CU two or more
+// workgroups; below that, 64x64 tiles (4 waves) are the fastest down to the
+// smallest problems (32x32 single-wave tiles never beat them and are left to
+// explicit selection); N <= 64 uses 128x64 so no MFMA block idles.  A tile
+// whose padding wastes more than a quarter of its MFMA work (for example
+// 256-row tiles over M = 128) is skipped for the next smaller one.
 // A gathered (implicit convolution) operand costs more per staged element, so
 // the larger l tile, which reuses each staged element over 128 rows, pays
 // off from 2 instead of 4 tiles per CU (C5 conv: l 221 us, m 227 us).
 Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t batch, bool gathered = false) {
+    (void)k;
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     auto tiles = [&](Tile t) { return cdiv(m, kTiles[t].bm) * cdiv(n, kTiles[t].bn) * batch; };
     auto useful = [&](Tile t) { return 4 * m * n * batch >= 3 * tiles(t) * kTiles[t].bm * kTiles[t].bn; };
     if (n <= 64 && tiles(kTileN) >= cus) return kTileN;
     if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
     if (tiles(kTileL) >= (gathered ? 2 : 4) * cus && useful(kTileL)) return kTileL;
-    if (tiles(kTileM) >= cus / 2) return kTileM;
-    // deep K (a reduction over a long batch, e.g. a weight gradient): 64x64
-    // tiles with many K splits beat 32x32 tiles (C5 conv dW, K = 100352: s 283 us)
-    if (k >= 4096 && tiles(kTileM) * (k / 512) >= 2 * cus) return kTileM;
-    return kTileS;
+    return kTileM;
 }
 
-// Split-K factor: problems that give fewer than ~4 workgroups per CU (the
-// latency-bound regime: few waves to hide each K slice's load round trip)
-// split K across blockIdx.z, keeping at least two BK slices per split; at
-// most 16 splits, 64 when K >= 16384 (each split then still walks >= 256).
+// Split-K factor, from the same measurements.  Each split costs a pass of
+// the reduce kernel (a few us), so:
+//  * 2*CUs or more (problem, tile) pairs: no split;
+//  * CUs/2 .. 2*CUs pairs: split only deep K, keeping >= 1024 per slice
+//    (1024x1024x4096 TN: 4 slices; 1000^3: none);
+//  * fewer pairs: aim at 2*CUs workgroups with >= 128 of K per slice
+//    (>= 64 when there are at most 8 tiles).
+// At most 16 slices, 64 when K >= 16384 (long reductions such as a conv
+// weight gradient over a whole batch).
 int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k, int64_t batch) {
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     const TileShape &ts = kTiles[tile];
     const int64_t tiles = cdiv(m, ts.bm) * cdiv(n, ts.bn) * batch;
-    const int64_t target = 4 * cus;
-    if (tiles >= target / 2) return 1;
-    int64_t splits = target / tiles;
-    const int64_t max_by_k = k / (2 * ts.bk);
-    if (splits > max_by_k) splits = max_by_k;
+    if (tiles >= 2 * cus) return 1;
+    int64_t splits;
+    if (tiles >= cus / 2)
+        splits = std::min<int64_t>(4 * cus / tiles, k / 1024);
+    else
+        splits = std::min<int64_t>(2 * cus / tiles, k / (tiles <= 8 ? 64 : 128));
     const int64_t cap = k >= 16384 ? 64 : 16;
     if (splits > cap) splits = cap;
     return splits < 2 ? 1 : (int)splits;
@@ -335,7 +361,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     if (rc) return rc;
     constexpr int64_t kMaxGridY = 65535;
     const int64_t chunk_batch = batch < kMaxGridY ? batch : kMaxGridY;
-    int splits = choose_splits(ctx, tile, m, n, k, batch);
+    int splits = ctx->forced_splits > 0 ? (int)std::min<int64_t>(ctx->forced_splits, std::max<int64_t>(1, k / ts.bk))
+                                        : choose_splits(ctx, tile, m, n, k, batch);
     int64_t k_chunk = k;
     if (splits > 1) {
         k_chunk = cdiv(cdiv(k, splits), ts.bk) * ts.bk;
@@ -413,6 +440,7 @@ int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n) {
 }
 
 int copy_out_and_wait(zn_ctx *ctx, float *dst, const float *src, size_t n) {
+    if (ctx->capturing) return ZN_ERR_INVALID_ARG;
     if (n) ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     return ZN_OK;
@@ -561,7 +589,18 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
 int zn_hip_destroy(zn_ctx *ctx) {
     if (!ctx) return ZN_OK;
     if (ctx->device >= 0) (void)hipSetDevice(ctx->device);
+    if (ctx->capturing) {  // abandon an open capture
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(ctx->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        (void)hipGetLastError();
+        ctx->capturing = false;
+        for (auto &b : ctx->captured) ctx->pool[b.second].push_back(b.first);
+        ctx->captured.clear();
+    }
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    while (!ctx->graphs.empty()) (void)zn_hip_graph_destroy(ctx->graphs.back());
+    for (void *w : ctx->retired_ws) (void)hipFree(w);
+    ctx->retired_ws.clear();
     for (auto &kv : ctx->pool)
         for (void *p : kv.second) (void)hipFree(p);
     ctx->pool.clear();
@@ -604,6 +643,7 @@ int zn_hip_alloc(zn_ctx *ctx, size_t bytes, void **out) {
 int zn_hip_free(zn_ctx *ctx, void *ptr) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
     if (!ptr) return ZN_OK;
+    if (ctx->capturing) return ZN_ERR_INVALID_ARG;
     int rc = select_device(ctx);
     if (rc) return rc;
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
@@ -614,7 +654,7 @@ int zn_hip_free(zn_ctx *ctx, void *ptr) {
 static int zn_copy(zn_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind, bool wait) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
     if (bytes == 0) return ZN_OK;
-    if (!dst || !src) return ZN_ERR_INVALID_ARG;
+    if (!dst || !src || (wait && ctx->capturing)) return ZN_ERR_INVALID_ARG;
     int rc = select_device(ctx);
     if (rc) return rc;
     ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
@@ -660,10 +700,84 @@ int zn_hip_copy_f32(zn_ctx *ctx, float *dst, const float *src, int64_t count) {
 }
 
 int zn_hip_sync(zn_ctx *ctx) {
-    if (!ctx) return ZN_ERR_INVALID_ARG;
+    if (!ctx || ctx->capturing) return ZN_ERR_INVALID_ARG;
     int rc = select_device(ctx);
     if (rc) return rc;
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return ZN_OK;
+}
+
+// ----------------------------------------------------------------- graphs
+int zn_hip_graph_begin(zn_ctx *ctx) {
+    if (!ctx || ctx->capturing) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    ZN_HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+    ctx->capturing = true;
+    ctx->captured.clear();
+    return ZN_OK;
+}
+
+int zn_hip_graph_end(zn_ctx *ctx, zn_graph **out) {
+    if (!ctx || !out || !ctx->capturing) return ZN_ERR_INVALID_ARG;
+    *out = nullptr;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    ctx->capturing = false;
+    std::vector<std::pair<void *, size_t>> bufs;
+    bufs.swap(ctx->captured);
+    auto give_back = [&]() {
+        for (auto &b : bufs) ctx->pool[b.second].push_back(b.first);
+    };
+    if (e != hipSuccess || !g) {
+        give_back();
+        return fail_hip(ctx, e != hipSuccess ? e : hipErrorUnknown);
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        give_back();
+        return fail_hip(ctx, e);
+    }
+    zn_graph *graph = new (std::nothrow) zn_graph();
+    if (!graph) {
+        (void)hipGraphExecDestroy(exec);
+        give_back();
+        return ZN_ERR_OOM;
+    }
+    graph->ctx = ctx;
+    graph->exec = exec;
+    graph->buffers.swap(bufs);
+    ctx->graphs.push_back(graph);
+    *out = graph;
+    return ZN_OK;
+}
+
+int zn_hip_graph_launch(zn_ctx *ctx, zn_graph *graph) {
+    if (!ctx || !graph || graph->ctx != ctx || ctx->capturing) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    ZN_HIP_TRY(ctx, hipGraphLaunch(graph->exec, ctx->stream));
+    return ZN_OK;
+}
+
+int zn_hip_graph_destroy(zn_graph *graph) {
+    if (!graph) return ZN_OK;
+    zn_ctx *ctx = graph->ctx;
+    if (ctx->device >= 0) (void)hipSetDevice(ctx->device);
+    if (!ctx->capturing) (void)hipStreamSynchronize(ctx->stream);  // replays may still run
+    (void)hipGraphExecDestroy(graph->exec);
+    for (auto &b : graph->buffers) ctx->pool[b.second].push_back(b.first);
+    auto &gs = ctx->graphs;
+    gs.erase(std::remove(gs.begin(), gs.end(), graph), gs.end());
+    if (gs.empty()) {
+        for (void *w : ctx->retired_ws) (void)hipFree(w);
+        ctx->retired_ws.clear();
+    }
+    delete graph;
     return ZN_OK;
 }
 
@@ -708,6 +822,12 @@ int zn_hip_event_destroy(zn_event *ev) {
 int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile) {
     if (!ctx || tile < ZN_TILE_AUTO || tile >= kNumTiles) return ZN_ERR_INVALID_ARG;
     ctx->forced_tile = tile;
+    return ZN_OK;
+}
+
+int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits) {
+    if (!ctx || splits < 0 || splits > 64) return ZN_ERR_INVALID_ARG;
+    ctx->forced_splits = splits;
     return ZN_OK;
 }
 
