@@ -287,3 +287,32 @@ def test_graph_replay_of_mlp_step_matches_eager(ctx):
         np.testing.assert_array_equal(got, ref)
     for b in (x, dy, other_a, other_b, other_c):
         b.close()
+
+
+def test_znn_model_loads_into_hbm_and_matches_oracle(ctx, tmp_path):
+    """A C2-shaped MLP (784 -> 128 relu -> 10 linear) written as a .znn file,
+    loaded straight into HBM, run forward on the GPU against the oracle's
+    matMulBias path on the same weights, and written back byte for byte."""
+    from zigneuron_amd import serialization as znn
+    from zigneuron_amd.layer import init_weights
+    rng = np.random.default_rng(11)
+    specs = [znn.DenseSpec(784, 128, "relu", init_weights(784, 128, "relu", 3), uniform(rng, (128,))),
+             znn.DenseSpec(128, 10, "linear", init_weights(128, 10, "linear", 4), uniform(rng, (10,)))]
+    path = tmp_path / "mlp.znn"
+    znn.save_model(specs, str(path))
+    batch = 256
+    announce("znn load + forward")
+    layers = znn.load_model(str(path), ctx, batch=batch)
+    x = uniform(rng, (batch, 784), 0.0, 1.0)
+    h = ctx.to_device(x)
+    inp = x
+    for spec, layer in zip(specs, layers):
+        out = layer.forward(h)
+        got = out.download().reshape(batch, spec.output_size)
+        ref = oracle.matmul_bias_act(inp, spec.weights, spec.bias, batch, spec.output_size, spec.input_size, spec.act)
+        assert_close(got, ref, "nn", inp, spec.weights, batch, spec.output_size, spec.input_size, bias=spec.bias,
+                     act=spec.act, what=f"znn layer {spec.input_size}->{spec.output_size}")
+        h, inp = out, got
+    back = tmp_path / "back.znn"
+    znn.save_model(layers, str(back))
+    assert back.read_bytes() == path.read_bytes()
