@@ -93,7 +93,8 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
     """Kernel time of every BASELINE configuration (device-resident inputs)."""
     out = []
 
-    def run(name, layout, m, n, k, batch=1, a_shape=None, b_shape=None, bias=None, act="linear", lo=-1.0):
+    def run(name, layout, m, n, k, batch=1, a_shape=None, b_shape=None, bias=None, act="linear", lo=-1.0,
+            graph=False):
         lda = m if layout == "tn" else k
         ldb = k if layout == "nt" else n
         a_shape = a_shape or ((k, m) if layout == "tn" else (m, k))
@@ -107,16 +108,32 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
         else:
             fn = lambda: ctx.sgemm_strided_batched(layout, m, n, k, a, lda, a_shape[0] * a_shape[1], b, ldb,  # noqa
                                                    b_shape[0] * b_shape[1], c, n, m * n, batch)
-        ms = time_launches(ctx, fn, reps, warmup)
+        if graph:  # tiny GEMMs: device time from a replayed graph of 20 launches (no host launch cost)
+            g = ctx.capture(lambda: [fn() for _ in range(20)])
+            ms = time_launches(ctx, g.launch, reps, warmup) / 20
+            g.close()
+        else:
+            ms = time_launches(ctx, fn, reps, warmup)
         for buf in (a, b, c, db):
             if buf is not None:
                 buf.close()
         e = config_entry(name, layout, m, n, k, batch, ms, {"bias": bias is not None, "act": act})
-        log(f"  {name:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s  {e['pct_f32_peak']:5.1f}% peak")
+        if graph:
+            e["timing"] = "graph replay"
+        log(f"  {name:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s  {e['pct_f32_peak']:5.1f}% peak"
+            f"  {e['hbm_gbs']:7.1f} GB/s")
         out.append(e)
         return ms
 
     run("C1 NN 512^3", "nn", 512, 512, 512)
+    # C2: the six GEMMs of the MLP step one by one (batch 256, 784 -> 128 -> 10)
+    zeros = lambda n: np.zeros(n, np.float32)  # noqa: E731
+    run("C2 L1 fwd NN+bias+relu 256x128x784", "nn", 256, 128, 784, bias=zeros(128), act="relu", lo=0.0, graph=True)
+    run("C2 L2 fwd NN+bias 256x10x128", "nn", 256, 10, 128, bias=zeros(10), graph=True)
+    run("C2 L2 dX NT 256x128x10", "nt", 256, 128, 10, graph=True)
+    run("C2 L2 dW TN 128x10x256", "tn", 128, 10, 256, graph=True)
+    run("C2 L1 dX NT 256x784x128", "nt", 256, 784, 128, graph=True)
+    run("C2 L1 dW TN 784x128x256", "tn", 784, 128, 256, graph=True)
     run("C3 dW TN 1024x1024x4096", "tn", 1024, 1024, 4096)
     run("C3 dX NT 4096x1024x1024", "nt", 4096, 1024, 1024)
     run("C4 NN 1000^3", "nn", 1000, 1000, 1000)
