@@ -235,19 +235,21 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Tile choice, from measurements on MI355X (256 CUs, per-launch times from
 // graph replays): the largest tiles win once they give every CU two or more
 // workgroups; below that, 64x64 tiles (4 waves) are the fastest down to the
-// smallest problems (32x32 single-wave tiles never beat them and are left to
-// explicit selection); N <= 64 uses 128x64 so no MFMA block idles.  A tile
+// smallest problems and for N <= 64 (C5 P.V: 169 us against 184 us for
+// 128x64); 32x32 and 128x64 tiles never beat them and are left to explicit
+// selection.  A tile
 // whose padding wastes more than a quarter of its MFMA work (for example
 // 256-row tiles over M = 128) is skipped for the next smaller one.
 // A gathered (implicit convolution) operand costs more per staged element, so
 // the larger l tile, which reuses each staged element over 128 rows, pays
 // off from 2 instead of 4 tiles per CU (C5 conv: l 221 us, m 227 us).
 Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t batch, bool gathered = false) {
-    (void)k;
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     auto tiles = [&](Tile t) { return cdiv(m, kTiles[t].bm) * cdiv(n, kTiles[t].bn) * batch; };
     auto useful = [&](Tile t) { return 4 * m * n * batch >= 3 * tiles(t) * kTiles[t].bm * kTiles[t].bn; };
-    if (n <= 64 && tiles(kTileN) >= cus) return kTileN;
+    // short K: a tile's epilogue outweighs its K walk, and the smaller l tile
+    // overlaps them better (C5 QK^T, K = 64: l 242 us, x 252 us, round-robin A/B)
+    if (k <= 256 && tiles(kTileL) >= 2 * cus && useful(kTileL)) return kTileL;
     if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
     if (tiles(kTileL) >= (gathered ? 2 : 4) * cus && useful(kTileL)) return kTileL;
     return kTileM;
