@@ -64,7 +64,8 @@ def test_code_objects_hold_every_kernel():
                 assert f"zn_sgemm_{lay}_{t}{v}".encode() in gemm
     for t in ("x", "l", "n", "m", "s"):
         for v in ("", "_v"):
-            assert f"zn_conv_nn_{t}{v}".encode() in gemm
+            for g in ("", "_g"):
+                assert f"zn_conv_nn_{t}{v}{g}".encode() in gemm
     assert b"zn_splitk_reduce" in gemm
     for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",
               "zn_accumulate_bias", "zn_im2col", "zn_softmax_rows", "zn_col2im", "zn_row_sum", "zn_dense_grad_prologue"):

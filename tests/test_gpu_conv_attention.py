@@ -97,7 +97,12 @@ def test_conv2d_forward_im2col_device(ctx, case):
 @pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "32x32"])
 @pytest.mark.parametrize("case", [(3, 5, 11, 9, 7, 3, 3, 2, 1), (2, 8, 10, 12, 40, 3, 2, 1, 1),
                                   (2, 7, 13, 11, 20, 5, 5, 2, 2), (1, 64, 9, 9, 33, 1, 1, 1, 0),
-                                  (2, 4, 17, 19, 8, 7, 7, 3, 3), (1, 1, 70, 70, 3, 4, 4, 1, 2)])
+                                  (2, 4, 17, 19, 8, 7, 7, 3, 3), (1, 1, 70, 70, 3, 4, 4, 1, 2),
+                                  # stride 1 and OW % 4 == 0: the 4-pixel gather, with chunks that
+                                  # straddle the left, right or both paddings
+                                  (2, 5, 9, 12, 7, 3, 3, 1, 1), (1, 3, 7, 16, 9, 5, 5, 1, 2),
+                                  (2, 4, 6, 8, 6, 1, 1, 1, 0), (1, 2, 5, 20, 3, 3, 7, 1, 3),
+                                  (2, 3, 4, 4, 5, 3, 3, 1, 1), (1, 6, 3, 2, 4, 1, 3, 1, 1)])
 def test_conv_implicit_gemm_every_tile(ctx, case, tile):
     """Both weight orders through every forced tile: im2col order against the
     reference's im2col GEMM, OIHW order against the direct convolution."""

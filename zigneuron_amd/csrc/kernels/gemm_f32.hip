@@ -150,6 +150,89 @@ __device__ __forceinline__ void tile_coords(const ZnGemmArgs &p, int &tm, int &t
     tn = in_group / gsize;
 }
 
+// The convolution operand with 16-byte loads, for stride_w == 1 and
+// out_w % 4 == 0: lane L of a wave instruction stages a chunk of 4
+// neighbouring output pixels (one output row, so 4 consecutive input
+// columns) of one filter tap.  A lane's pixel chunk is fixed for the whole
+// tile (Lane); its tap changes with the instruction and is decoded per lane.
+// Chunks wholly inside the image are one DMA.  A chunk that straddles the
+// left or right padding is DMAed as zeros (out-of-range offset), and the lane
+// loads its in-image elements with ordinary guarded loads and writes the
+// chunk into LDS after its own DMA has landed (patch, before the barrier), so
+// no access ever leaves the image.
+template <int BN, int BK, int NT>
+struct ConvGather16Stage {
+    static constexpr int kFloats = BN * BK;
+    static constexpr int kPerInst = 4 * kWave;  // 256 floats per wave instruction
+    static constexpr int kInsts = kFloats / kPerInst;
+    static constexpr int kWaves = NT / kWave;
+    static constexpr int kPerWave = kInsts / kWaves;
+    static_assert(kInsts % kWaves == 0 && kPerWave >= 1, "load blocks must split evenly over waves");
+    static_assert(kPerInst % BN == 0, "a wave instruction covers whole k rows");
+    static constexpr int kRowsPerInst = kPerInst / BN;
+
+    struct Lane {
+        int ih0, iw0;  // top-left input tap of the chunk's first pixel
+        int kl;        // k row of this lane within a wave instruction
+        bool ok;       // the chunk lies inside the problem
+    };
+    struct Patch {
+        zn_f32x4 v[kPerWave];
+        uint32_t mask;  // bit j: instruction j's chunk needs the patch
+    };
+
+    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int lane) {
+        Lane l;
+        const int n = n0 + (4 * lane) % BN;  // first pixel of the chunk (n0 and out_w are multiples of 4)
+        const int oh = n / g.out_w, ow = n - oh * g.out_w;
+        l.ih0 = oh * g.stride_h - g.pad_h;
+        l.iw0 = ow - g.pad_w;  // stride_w == 1
+        l.kl = (4 * lane) / BN;
+        l.ok = n < nmax;
+        return l;
+    }
+
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const float *image, float *lds,
+                                                 const ZnConvGeom &g, const Lane &ln, int k0, int kmax, int wave,
+                                                 int lane, Patch &pt) {
+        pt.mask = 0;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int row = j * kWaves + wave;  // wave-uniform
+            const int p0 = row * kPerInst;
+            const int k = k0 + row * kRowsPerInst + ln.kl;
+            int ic, kh, kw;
+            ConvGatherStage<BN, BK, NT>::decode_k(g, k, ic, kh, kw);
+            const int ih = ln.ih0 + kh, iws = ln.iw0 + kw;
+            const bool row_ok = ln.ok && k < kmax && (unsigned)ih < (unsigned)g.in_h;
+            const bool full = row_ok && iws >= 0 && iws + 3 < g.in_w;
+            const int row_off = (ic * g.in_h + ih) * g.in_w;
+            const uint32_t off = full ? (uint32_t)(row_off + iws) * 4u : kOutOfRange;
+            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                         :
+                         : "s"(lds_addr), "v"(off), "s"(rsrc)
+                         : "memory");
+            pt.v[j] = zn_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (row_ok && !full && iws + 3 >= 0 && iws < g.in_w) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if ((unsigned)(iws + e) < (unsigned)g.in_w) pt.v[j][e] = image[row_off + iws + e];
+                pt.mask |= 1u << j;
+            }
+        }
+    }
+
+    // After this wave's DMA has landed: write the patched chunks.
+    __device__ static __forceinline__ void apply(float *lds, const Patch &pt, int wave, int lane) {
+        if (!pt.mask) return;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j)
+            if (pt.mask & (1u << j))
+                *reinterpret_cast<zn_f32x4 *>(lds + (j * kWaves + wave) * kPerInst + 4 * lane) = pt.v[j];
+    }
+};
+
 // Epilogue of one macro tile: v = acc (+ C) (+ bias) -> act -> store.
 // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
 // holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
@@ -224,7 +307,7 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
 // an NCHW image).  Iteration kt waits
 // for its stage (vmcnt(0) + barrier), refills the other stage with slice
 // kt + 1, then computes slice kt while that load is in flight.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, bool CONV>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, bool CONV, int GW = 4>
 __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -234,6 +317,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     typedef DmaStage<BM, BK, NT, AK, WA> SA;
     typedef DmaStage<BN, BK, NT, BKC, WB> SB;
     typedef ConvGatherStage<BN, BK, NT> SC;
+    typedef ConvGather16Stage<BN, BK, NT> SC16;
     __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
@@ -267,9 +351,15 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
 
     typename SC::Lane cl{};
-    if constexpr (CONV && SC::kFixedN) cl = SC::lane_setup(p.conv, n0, p.n, wave, lane);
+    typename SC16::Lane cl16{};
+    typename SC16::Patch patch;
+    patch.mask = 0;
+    if constexpr (CONV && GW == 4 && SC::kFixedN) cl = SC::lane_setup(p.conv, n0, p.n, wave, lane);
+    if constexpr (CONV && GW == 16) cl16 = SC16::lane_setup(p.conv, n0, p.n, lane);
     auto issue_b = [&](float *lds, int k0) {
-        if constexpr (CONV)
+        if constexpr (CONV && GW == 16)
+            SC16::issue(rb, gb, lds, p.conv, cl16, k0, kend, wave, lane, patch);
+        else if constexpr (CONV)
             SC::issue(rb, lds, p.conv, cl, n0, k0, p.n, kend, wave, lane);
         else
             SB::issue(rb, lds, ldb, n0, k0, p.n, kend, wave, lane);
@@ -280,6 +370,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     }
     for (int kt = 0; kt < ktiles; ++kt) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of slice kt is in LDS
+        if constexpr (CONV && GW == 16) SC16::apply(lds_b[kt & 1], patch, wave, lane);
         __syncthreads();  // every wave's part is; every wave is done reading slice kt - 1
         const int cur = kt & 1;
         if (kt + 1 < ktiles) {
@@ -341,14 +432,17 @@ ZN_GEMM_TILE(s, 32, 32, 32, 1, 1, 1)
 // Implicit-GEMM convolution, per image b = blockIdx.y:
 // out_b[OC][OH*OW] = W[OC][K] . im2col(input_b)^T (+ bias[oc]), an NN GEMM
 // whose B operand is gathered from the NCHW input (ZnConvGeom).  _v: W rows
-// are 16-byte aligned.
-#define ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
+// are 16-byte aligned; _g: the input is gathered in chunks of 4 pixels with
+// 16-byte loads (stride_w == 1, out_w % 4 == 0), otherwise element by element.
+#define ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, GW, SUFFIX)                            \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_conv_nn_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, true, false, WA, 4, true>(p);                          \
+        gemm_tile_dma<BM, BN, BK, WM, WN, true, false, WA, 4, true, GW>(p);                      \
     }
 #define ZN_CONV_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, 4, _v)                                    \
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, 4, )                                       \
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, 16, _v_g)                                 \
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, 16, _g)
 
 ZN_CONV_TILE(x, 256, 128, 16, 4, 2, 1)
 ZN_CONV_TILE(l, 128, 128, 16, 2, 2, 4)

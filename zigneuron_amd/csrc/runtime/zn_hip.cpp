@@ -68,7 +68,7 @@ struct zn_ctx {
     hipModule_t attn_module = nullptr;
     hipFunction_t attn[3][2] = {};             // fused attention [head dim 32/64/128][16-byte I/O]
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
-    hipFunction_t conv[kNumTiles][2] = {};     // implicit-GEMM convolution [tile][16-byte W rows]
+    hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -379,7 +379,9 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     args.splits = splits;
     args.k_chunk = (int32_t)k_chunk;
     args.ws = ctx->ws;
-    hipFunction_t f = conv ? ctx->conv[tile][vec ? 1 : 0] : ctx->gemm[layout][tile][vec ? 1 : 0];
+    // 4-pixel (16-byte) gather: unit column stride, and whole chunks of 4 pixels per output row
+    const int gather4 = conv && conv->stride_w == 1 && conv->out_w % 4 == 0 ? 1 : 0;
+    hipFunction_t f = conv ? ctx->conv[tile][vec ? 1 : 0][gather4] : ctx->gemm[layout][tile][vec ? 1 : 0];
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
         ZnGemmArgs part = args;
@@ -569,11 +571,13 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                     return bail(ZN_ERR_SYMBOL);
             }
     for (int t = 0; t < kNumTiles; ++t)
-        for (int v = 0; v < 2; ++v) {
-            char name[64];
-            std::snprintf(name, sizeof(name), "zn_conv_nn_%s%s", kTiles[t].suffix, v ? "_v" : "");
-            if (hipModuleGetFunction(&ctx->conv[t][v], ctx->gemm_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
-        }
+        for (int v = 0; v < 2; ++v)
+            for (int g = 0; g < 2; ++g) {
+                char name[64];
+                std::snprintf(name, sizeof(name), "zn_conv_nn_%s%s%s", kTiles[t].suffix, v ? "_v" : "", g ? "_g" : "");
+                if (hipModuleGetFunction(&ctx->conv[t][v][g], ctx->gemm_module, name) != hipSuccess)
+                    return bail(ZN_ERR_SYMBOL);
+            }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess)
         return bail(ZN_ERR_SYMBOL);
     for (int i = 0; i < kNumElt; ++i)
