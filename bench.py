@@ -269,6 +269,69 @@ def cpu_baseline(target_s=5.0):
             "single_thread_tflops": round(res["single"]["tflops"], 5), "cpu_model": cpu_model}
 
 
+def cpu_rows():
+    """The oracle (the reference's CPU path restated) on bounded samples of the
+    other configurations, single-threaded, so each GPU number has its CPU
+    counterpart beside it.  Each sample is one unit of the GPU workload (one
+    MLP step, a row block of a GEMM, one image, one attention head)."""
+    from oracle import oracle
+    from zigneuron_amd.layer import init_weights
+    rng = np.random.default_rng(2)
+    out = []
+
+    def rec(name, sample, seconds, flops, unit_count, unit):
+        e = {"name": name, "sample": sample, "seconds": round(seconds, 4), "gflops": round(flops / seconds / 1e9, 3),
+             f"ms_per_{unit}": round(seconds / unit_count * 1e3, 3), "threads": 1}
+        log(f"  cpu {name:34s} {e['gflops']:8.3f} GFLOP/s  ({sample})")
+        out.append(e)
+
+    # C2: one training step of the 784-128-10 MLP at batch 256 (the reference's Dense sequence)
+    x, dy = uniform(rng, (256, 784), 0.0, 1.0), uniform(rng, (256, 10))
+    w1, w2 = init_weights(784, 128, "relu", 1), init_weights(128, 10, "linear", 2)
+    b1, b2 = np.zeros(128, np.float32), np.zeros(10, np.float32)
+    t = time.perf_counter()
+    h = oracle.matmul_bias_act(x, w1, b1, 256, 128, 784, "relu")
+    oracle.matmul_bias_act(h, w2, b2, 256, 10, 128, "linear")
+    g2 = oracle.activation_backward("linear", np.zeros((256, 10), np.float32), dy)
+    gh = oracle.matmul_nt(g2, w2, 256, 128, 10)
+    oracle.accumulate_bias(np.zeros(10, np.float32), g2.reshape(256, 10))
+    oracle.matmul_tn(h, g2, 128, 10, 256)
+    g1 = oracle.activation_backward("relu", h, gh).reshape(256, 128)
+    oracle.matmul_nt(g1, w1, 256, 784, 128)
+    oracle.accumulate_bias(np.zeros(128, np.float32), g1)
+    oracle.matmul_tn(x, g1, 784, 128, 256)
+    dt = time.perf_counter() - t
+    rec("C2 MLP train step", "one full step", dt, 2.0 * 256 * (784 * 128 + 128 * 10) * 3, 1, "step")
+    # C3: 64 of the 1024 output rows of dW (TN) and of 4096 rows of dX (NT)
+    xa, dya, w = uniform(rng, (4096, 64)), uniform(rng, (4096, 1024)), uniform(rng, (1024, 1024))
+    t = time.perf_counter()
+    oracle.matmul_tn(xa, dya, 64, 1024, 4096)
+    dt = time.perf_counter() - t
+    rec("C3 dW TN 1024x1024x4096", "64 of 1024 rows", dt, 2.0 * 64 * 1024 * 4096, 64 / 1024, "full_gemm")
+    t = time.perf_counter()
+    oracle.matmul_nt(dya[:256], w, 256, 1024, 1024)
+    dt = time.perf_counter() - t
+    rec("C3 dX NT 4096x1024x1024", "256 of 4096 rows", dt, 2.0 * 256 * 1024 * 1024, 256 / 4096, "full_gemm")
+    # C5 convolution, forward and backward (the reference's im2col branch), one of 32 images
+    ximg, wc = uniform(rng, (1, 64, 56, 56)), uniform(rng, (128, 576))
+    bc, goc = uniform(rng, (128,)), uniform(rng, (1, 128, 56, 56))
+    t = time.perf_counter()
+    oracle.conv2d_forward(ximg, wc, bc, 64, 128, 3, 3, 56, 56, 1, 1)
+    dt = time.perf_counter() - t
+    rec("C5 conv forward (im2col branch)", "1 of 32 images", dt, 2.0 * 3136 * 128 * 576, 1 / 32, "batch")
+    t = time.perf_counter()
+    oracle.conv2d_backward(ximg, wc, goc, 64, 128, 3, 3, 56, 56, 1, 1, branch="im2col")
+    dt = time.perf_counter() - t
+    rec("C5 conv backward (im2col branch)", "1 of 32 images", dt, 4.0 * 3136 * 128 * 576, 1 / 32, "batch")
+    # C5 attention: one of 128 heads
+    q, kk, v = (uniform(rng, (1024, 64)) for _ in range(3))
+    t = time.perf_counter()
+    oracle.attention(q, kk, v, 1024, 64, 0.125)
+    dt = time.perf_counter() - t
+    rec("C5 attention", "1 of 128 heads", dt, 4.0 * 1024 * 1024 * 64, 1 / 128, "batch")
+    return out
+
+
 def copy_calibration(ctx, steps, warmup) -> int:
     """1 GiB read + 1 GiB write per launch with the plain streaming copy kernel."""
     count = (1 << 30) // 4
@@ -359,6 +422,7 @@ def main() -> int:
     if not args.no_cpu:
         log("CPU baseline (oracle):")
         cpu = cpu_baseline()
+        cpu["configs"] = cpu_rows()
 
     traffic = load_traffic()
     line = {
