@@ -316,3 +316,23 @@ def test_znn_model_loads_into_hbm_and_matches_oracle(ctx, tmp_path):
     back = tmp_path / "back.znn"
     znn.save_model(layers, str(back))
     assert back.read_bytes() == path.read_bytes()
+
+
+def test_graph_and_buffer_outlive_their_context():
+    """Closing a context releases its graphs: a graph or buffer closed later is
+    a no-op, and launching such a graph raises instead of touching freed state."""
+    from zigneuron_amd import Context, InvalidArgumentError
+    c = Context(0)
+    a, b, out = c.to_device(np.ones((64, 64), np.float32)), c.to_device(np.ones((64, 64), np.float32)), c.alloc(4096)
+    c.sgemm("nn", 64, 64, 64, a, 64, b, 64, out, 64)
+    c.sync()
+    g = c.capture(lambda: c.sgemm("nn", 64, 64, 64, a, 64, b, 64, out, 64))
+    g.launch()
+    c.sync()
+    np.testing.assert_array_equal(out.download(), np.full(4096, 64.0, np.float32))
+    c.close()
+    with pytest.raises(InvalidArgumentError):
+        g.launch()
+    g.close()
+    for buf in (a, b, out):
+        buf.close()

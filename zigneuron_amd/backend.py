@@ -13,6 +13,7 @@ keep tensors resident in HBM.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Optional
 
 import numpy as np
@@ -67,14 +68,25 @@ class Graph:
 
     def __init__(self, ctx: "Context", handle: ctypes.c_void_p):
         self._ctx, self.handle = ctx, handle
+        ctx._graphs.add(self)
 
     def launch(self) -> None:
+        if not self.handle or not self._ctx.handle:
+            raise InvalidArgumentError(_lib.ZN_ERR_INVALID_ARG, "zn_hip_graph_launch", "graph or context closed")
         check(_lib.load().zn_hip_graph_launch(self._ctx.handle, self.handle), "zn_hip_graph_launch")
 
     def close(self) -> None:
-        if self.handle:
+        """Release the graph (a no-op once it or its context is closed: the
+        context's destruction releases its graphs)."""
+        if self.handle and self._ctx.handle:
             _lib.load().zn_hip_graph_destroy(self.handle)
-            self.handle = None
+        self.handle = None
+
+    def __del__(self):  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Event:
@@ -136,9 +148,10 @@ class DeviceBuffer:
         return self.ptr + 4 * int(elements)
 
     def close(self) -> None:
-        if self.ptr:
+        """Free the buffer; after its context is closed this only drops the pointer."""
+        if self.ptr and self.ctx.handle:
             check(_lib.load().zn_hip_free(self.ctx.handle, self.ptr), "zn_hip_free")
-            self.ptr = 0
+        self.ptr = 0
 
     def __del__(self):  # pragma: no cover
         try:
@@ -156,6 +169,7 @@ class Context:
         d = code_object_dir.encode() if code_object_dir else None
         check(_lib.load().zn_hip_create(int(device), d, ctypes.byref(h)), "zn_hip_create")
         self.handle = h.value
+        self._graphs = weakref.WeakSet()
         info = _lib.DeviceInfo()
         check(_lib.load().zn_hip_device_info(self.handle, ctypes.byref(info)), "zn_hip_device_info")
         self.arch = info.name.decode()
@@ -295,6 +309,8 @@ class Context:
 
     def close(self) -> None:
         if self.handle:
+            for g in list(self._graphs):  # zn_hip_destroy releases them
+                g.handle = None
             _lib.load().zn_hip_destroy(self.handle)
             self.handle = None
 
