@@ -89,6 +89,9 @@ def config_entry(name, layout, m, n, k, batch, ms, extra=None):
     return e
 
 
+USE_GRAPHS = True  # cleared by --no-graph
+
+
 def bench_configs(ctx, rng, reps=10, warmup=3):
     """Kernel time of every BASELINE configuration (device-resident inputs)."""
     out = []
@@ -108,7 +111,7 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
         else:
             fn = lambda: ctx.sgemm_strided_batched(layout, m, n, k, a, lda, a_shape[0] * a_shape[1], b, ldb,  # noqa
                                                    b_shape[0] * b_shape[1], c, n, m * n, batch)
-        if graph:  # tiny GEMMs: device time from a replayed graph of 20 launches (no host launch cost)
+        if graph and USE_GRAPHS:  # tiny GEMMs: device time from a replayed graph of 20 launches (no host launch cost)
             g = ctx.capture(lambda: [fn() for _ in range(20)])
             ms = time_launches(ctx, g.launch, reps, warmup) / 20
             g.close()
@@ -118,7 +121,7 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
             if buf is not None:
                 buf.close()
         e = config_entry(name, layout, m, n, k, batch, ms, {"bias": bias is not None, "act": act})
-        if graph:
+        if graph and USE_GRAPHS:
             e["timing"] = "graph replay"
         log(f"  {name:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s  {e['pct_f32_peak']:5.1f}% peak"
             f"  {e['hbm_gbs']:7.1f} GB/s")
@@ -223,11 +226,12 @@ def bench_mlp_step(ctx, rng, reps, warmup):
     e = {"name": "C2 MLP train step (6 GEMMs + 4 helpers)", "step_ms": round(ms, 5),
          "gemm_gflop": round(flops / 1e9, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 3)}
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us per step (one host call per kernel)")
-    graph = ctx.capture(step)  # the same step, replayed as one HIP graph
-    gms = time_launches(ctx, graph.launch, reps * 5, warmup)
-    graph.close()
-    e["graph_step_ms"] = round(gms, 5)
-    log(f"  {'C2 MLP train step, HIP graph replay':28s} {gms * 1e3:9.1f} us per step")
+    if USE_GRAPHS:
+        graph = ctx.capture(step)  # the same step, replayed as one HIP graph
+        gms = time_launches(ctx, graph.launch, reps * 5, warmup)
+        graph.close()
+        e["graph_step_ms"] = round(gms, 5)
+        log(f"  {'C2 MLP train step, HIP graph replay':28s} {gms * 1e3:9.1f} us per step")
     return e
 
 
@@ -363,10 +367,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-configs", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time everything eagerly, without HIP graph capture (for rocprofv3 --pmc runs, whose "
+                         "counter collection does not support captured graphs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time only a 1 GiB device-to-device copy (zn_copy_f32): the known-size reference "
                          "for scaling FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    global USE_GRAPHS
+    USE_GRAPHS = not args.no_graph
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is "
               "design-only here.", file=sys.stderr)
