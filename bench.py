@@ -168,7 +168,8 @@ def bench_conv_attention(ctx, rng, reps, warmup):
     ms = time_launches(ctx, lambda: ctx.conv2d_backward_im2col(x, w, go, gi, gw, gb, B, C, OC, 3, 3, H, W, H, W,
                                                                1, 1, 1, 1), reps, warmup)
     flops = 2 * 2.0 * B * H * W * OC * 9 * C  # the weight- and input-gradient GEMMs
-    e = {"name": "C5 conv backward (im2col + 2 GEMMs + col2im + bias)", "kernel_ms": round(ms, 5),
+    # stride 1, OC % 4 == 0: im2col + TN grad_W GEMM, implicit transposed-conv grad_input GEMM, bias sums
+    e = {"name": "C5 conv backward (im2col branch)", "kernel_ms": round(ms, 5),
          "tflops": round(flops / (ms * 1e-3) / 1e12, 3)}
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
     res.append(e)

@@ -48,6 +48,13 @@ CONV_CASES = [  # batch, C, H, W, OC, kH, kW, stride, pad
     (3, 2, 6, 5, 4, 2, 3, 1, 0),
     (2, 16, 12, 12, 24, 3, 3, 1, 1),
     (1, 1, 5, 5, 1, 1, 1, 1, 0),
+    # stride 1 and OC % 4 == 0: grad_input of the im2col branch is one
+    # transposed-convolution GEMM (no grad_col, no col2im)
+    (2, 6, 10, 9, 8, 3, 3, 1, 1),
+    (1, 3, 8, 8, 16, 1, 1, 1, 0),
+    (2, 5, 6, 7, 4, 3, 5, 1, 2),
+    (3, 7, 17, 19, 12, 3, 3, 1, 1),
+    (1, 8, 6, 6, 256, 3, 3, 1, 1),
 ]
 
 
@@ -310,6 +317,13 @@ BWD_CASES = [  # batch, C, H, W, OC, kH, kW, stride, pad
     (2, 16, 12, 12, 24, 3, 3, 1, 1),
     (2, 5, 13, 11, 7, 5, 5, 2, 2),
     (1, 1, 5, 5, 1, 1, 1, 1, 0),
+    # stride 1 and OC % 4 == 0: grad_input of the im2col branch is one
+    # transposed-convolution GEMM (no grad_col, no col2im)
+    (2, 6, 10, 9, 8, 3, 3, 1, 1),
+    (1, 3, 8, 8, 16, 1, 1, 1, 0),
+    (2, 5, 6, 7, 4, 3, 5, 1, 2),
+    (3, 7, 17, 19, 12, 3, 3, 1, 1),
+    (1, 8, 6, 6, 256, 3, 3, 1, 1),
 ]
 
 
@@ -367,6 +381,51 @@ def test_conv2d_backward_device(ctx, case, branch):
     announce(f"conv2d backward {branch} {case}")
     got, x, w, go = run_backward(ctx, case, branch)
     backward_check(got, x, w, go, case, branch, f"{branch} {case}")
+
+
+TRANSPOSED_CASES = [(2, 6, 10, 9, 8, 3, 3, 1, 1), (1, 5, 7, 12, 36, 5, 3, 1, 2), (2, 33, 5, 6, 4, 1, 1, 1, 0),
+                    (1, 2, 4, 4, 20, 3, 3, 1, 2), (2, 70, 9, 9, 8, 3, 3, 1, 1)]
+
+
+@pytest.mark.parametrize("tile", ["256x128", "128x128", "128x64", "64x64", "32x32"])
+@pytest.mark.parametrize("case", TRANSPOSED_CASES)
+def test_conv_backward_transposed_every_tile(ctx, case, tile):
+    """The stride-1 input gradient as an implicit transposed convolution
+    through every forced tile, with the policy's split-K and with 3 forced
+    slices (partial sums reduced in slice order)."""
+    announce(f"conv backward transposed tile {tile} {case}")
+    ctx.set_gemm_tile(tile)
+    try:
+        for splits in (0, 3):
+            ctx.set_gemm_splits(splits)
+            got, x, w, go = run_backward(ctx, case, "im2col", seed=16)
+            backward_check(got, x, w, go, case, "im2col", f"{tile} splits {splits} {case}")
+    finally:
+        ctx.set_gemm_tile("auto")
+        ctx.set_gemm_splits(0)
+
+
+def test_conv_backward_unaligned_grad_output(ctx):
+    """grad_output one float off 16-byte alignment: the transposed GEMM needs
+    whole 16-byte chunks, so the materialized grad_col + col2im path runs."""
+    case = (2, 6, 10, 9, 8, 3, 3, 1, 1)
+    B, C, H, W, OC, KH, KW, st, pd = case
+    OH, OW = out_hw(H, W, KH, KW, st, pd)
+    rng = np.random.default_rng(17)
+    x, w = uniform(rng, (B, C, H, W)), uniform(rng, (OC, KH * KW * C))
+    go = uniform(rng, (B, OC, OH, OW))
+    dx, dw = ctx.to_device(x), ctx.to_device(w)
+    dgo = ctx.alloc(go.size + 1)
+    dgo.upload(np.concatenate([np.zeros(1, np.float32), go.ravel()]))
+    dgi = ctx.alloc(B * C * H * W).fill(np.nan)
+    dgw = ctx.alloc(OC * KH * KW * C).fill(np.nan)
+    dgb = ctx.alloc(OC).fill(np.nan)
+    announce("conv backward unaligned grad_output")
+    ctx.conv2d_backward_im2col(dx, dw, dgo.offset(1), dgi, dgw, dgb, B, C, OC, KH, KW, H, W, OH, OW, st, st, pd, pd)
+    got = (dgi.download(), dgw.download(), dgb.download())
+    for buf in (dx, dw, dgo, dgi, dgw, dgb):
+        buf.close()
+    backward_check(got, x, w, go, case, "im2col", "unaligned grad_output")
 
 
 @pytest.mark.parametrize("case", [(2, 3, 9, 7, 5, 3, 3, 1, 1), (4, 8, 16, 16, 16, 3, 3, 1, 1),

@@ -290,6 +290,21 @@ extern "C" __global__ __launch_bounds__(256) void zn_row_sum(ZnEltArgs p) {
     }
 }
 
+// W' for the stride-1 transposed-convolution GEMM of the input gradient
+// (cpuConv2dBackwardIm2col's grad_col = go2 . W followed by col2im, src/
+// backend.zig:3995-4060, as one GEMM): the [OC][kH*kW][C] weights regrouped
+// to [C][kH*kW][OC].  A pure permutation (bit-exact); weights are small, so
+// one thread per output element with coalesced writes is enough.
+extern "C" __global__ __launch_bounds__(256) void zn_weight_regroup(ZnRegroupArgs p) {
+    const int64_t per_ic = (int64_t)p.taps_per_channel * p.out_channels;
+    const int64_t total = per_ic * p.channels;
+    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < total; o += (int64_t)gridDim.x * 256) {
+        const int64_t ic = o / per_ic, r = o - ic * per_ic;
+        const int64_t t = r / p.out_channels, oc = r - t * p.out_channels;
+        p.out[o] = p.in[(oc * p.taps_per_channel + t) * p.channels + ic];
+    }
+}
+
 namespace {
 
 constexpr int kSoftmaxThreads = 256;

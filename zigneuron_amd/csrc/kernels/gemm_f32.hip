@@ -233,6 +233,47 @@ struct ConvGather16Stage {
     }
 };
 
+// The transposed-convolution operand (the input gradient of a stride-1
+// convolution as an implicit GEMM): B[n][k] with n = input pixel (ih, iw)
+// and k = (kh*k_w + kw)*OC + oc is grad_output[(ih + pad_h - kh, iw + pad_w -
+// kw)][oc], grad_output read as [OH*OW][OC] rows (the reading of
+// cpuConv2dBackwardIm2col).  The operand is K-contiguous (stored [BN][BK],
+// swizzled like DmaStage), and a 16-byte chunk is 4 consecutive oc of one
+// grad_output row (OC % 4 == 0), so each chunk is either wholly inside the
+// output image or wholly outside (zeros): no patching.  ZnConvGeom fields as
+// used here: channels = OC, in_h x in_w = OH x OW (the gathered image),
+// out_w = W (decodes n), div1 = OC, k_w, pad as in the forward.
+template <int BN, int BK, int NT>
+struct ConvTGatherStage {
+    typedef DmaStage<BN, BK, NT, true, 16> Layout;
+    static constexpr int kPerWave = Layout::kPerWave;
+    static constexpr int kWaves = NT / kWave;
+
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
+                                                 int n0, int k0, int nmax, int kmax, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int p0 = (j * kWaves + wave) * Layout::kPerInst;
+            const int pos = p0 + 4 * lane;
+            const int row = pos / BK;
+            const int c = ((pos % BK) / 4) ^ Layout::swz(row);
+            const int n = n0 + row, k = k0 + 4 * c;
+            const int ih = zn_udiv(n, g.ow_mul, g.ow_shift), iw = n - ih * g.out_w;
+            const int khw = zn_udiv(k, g.div1_mul, g.div1_shift);
+            const int oc = k - khw * g.div1;
+            const int kh = zn_udiv(khw, g.kw_mul, g.kw_shift), kw = khw - kh * g.k_w;
+            const int oh = ih + g.pad_h - kh, ow = iw + g.pad_w - kw;
+            const bool ok = n < nmax && k < kmax && (unsigned)oh < (unsigned)g.in_h && (unsigned)ow < (unsigned)g.in_w;
+            const uint32_t off = ok ? (uint32_t)((oh * g.in_w + ow) * g.channels + oc) * 4u : kOutOfRange;
+            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                         :
+                         : "s"(lds_addr), "v"(off), "s"(rsrc)
+                         : "memory");
+        }
+    }
+};
+
 // Epilogue of one macro tile: v = acc (+ C) (+ bias) -> act -> store.
 // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
 // holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
@@ -307,17 +348,20 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
 // an NCHW image).  Iteration kt waits
 // for its stage (vmcnt(0) + barrier), refills the other stage with slice
 // kt + 1, then computes slice kt while that load is in flight.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, bool CONV, int GW = 4>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, bool CONV, int GW = 4,
+          bool CONVT = false>
 __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
     static_assert(!CONV || (!BKC && WB == 4), "the convolution operand is X-contiguous and gathered");
+    static_assert(!CONVT || (BKC && WB == 16 && !CONV), "the transposed-convolution operand is K-contiguous");
     typedef DmaStage<BM, BK, NT, AK, WA> SA;
     typedef DmaStage<BN, BK, NT, BKC, WB> SB;
     typedef ConvGatherStage<BN, BK, NT> SC;
     typedef ConvGather16Stage<BN, BK, NT> SC16;
+    typedef ConvTGatherStage<BN, BK, NT> ST;
     __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
@@ -345,7 +389,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
     const uint32_t b_bytes =
-        CONV ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+        (CONV || CONVT) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
              : (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
@@ -357,7 +401,9 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     if constexpr (CONV && GW == 4 && SC::kFixedN) cl = SC::lane_setup(p.conv, n0, p.n, wave, lane);
     if constexpr (CONV && GW == 16) cl16 = SC16::lane_setup(p.conv, n0, p.n, lane);
     auto issue_b = [&](float *lds, int k0) {
-        if constexpr (CONV && GW == 16)
+        if constexpr (CONVT)
+            ST::issue(rb, lds, p.conv, n0, k0, p.n, kend, wave, lane);
+        else if constexpr (CONV && GW == 16)
             SC16::issue(rb, gb, lds, p.conv, cl16, k0, kend, wave, lane, patch);
         else if constexpr (CONV)
             SC::issue(rb, lds, p.conv, cl, n0, k0, p.n, kend, wave, lane);
@@ -449,6 +495,24 @@ ZN_CONV_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_CONV_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_CONV_TILE(m, 64, 64, 32, 2, 2, 1)
 ZN_CONV_TILE(s, 32, 32, 32, 1, 1, 1)
+
+// Input gradient of a stride-1 convolution, per image b = blockIdx.y:
+// grad_input_b[C][H*W] = W'[C][K] . B^T, NT, W' = weights regrouped as
+// [ic][(kh*kW + kw)*OC + oc] and B gathered from grad_output rows
+// (ConvTGatherStage).  _v: W' rows are 16-byte aligned.
+#define ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convt_nt_##TILE##SUFFIX(ZnGemmArgs p) { \
+        gemm_tile_dma<BM, BN, BK, WM, WN, true, true, WA, 16, false, 4, true>(p);                \
+    }
+#define ZN_CONVT_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
+    ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
+    ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+
+ZN_CONVT_TILE(x, 256, 128, 16, 4, 2, 1)
+ZN_CONVT_TILE(l, 128, 128, 16, 2, 2, 4)
+ZN_CONVT_TILE(n, 128, 64, 16, 2, 1, 1)
+ZN_CONVT_TILE(m, 64, 64, 32, 2, 2, 1)
+ZN_CONVT_TILE(s, 32, 32, 32, 1, 1, 1)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not

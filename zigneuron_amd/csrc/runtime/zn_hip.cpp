@@ -45,11 +45,12 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
                                          {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kNumElt };
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kNumElt };
 constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", "zn_add_bias",
                                            "zn_activation_forward", "zn_activation_backward",
                                            "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows",
-                                           "zn_col2im",          "zn_row_sum",  "zn_dense_grad_prologue"};
+                                           "zn_col2im",          "zn_row_sum",  "zn_dense_grad_prologue",
+                                           "zn_weight_regroup"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
@@ -69,6 +70,7 @@ struct zn_ctx {
     hipFunction_t attn[3][2] = {};             // fused attention [head dim 32/64/128][16-byte I/O]
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
+    hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -293,11 +295,14 @@ void udiv_magic(uint32_t d, uint32_t &mul, uint32_t &shift) {
 
 // `conv` (optional) turns B into the implicit im2col operand of an NCHW
 // image batch (B[k][n] gathered per ZnConvGeom, images `stride_b` apart);
-// the problem is then NN with M = out channels, N = out pixels.
+// the problem is then NN with M = out channels, N = out pixels.  With
+// `convt` it is instead the transposed-convolution operand of a stride-1
+// input gradient (B[n][k] gathered from [OH*OW][OC] grad_output rows, K-
+// contiguous 16-byte chunks), NT with M = in channels, N = in pixels.
 int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                    int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
                    int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows,
-                   const ZnConvGeom *conv = nullptr) {
+                   const ZnConvGeom *conv = nullptr, bool convt = false) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
     if (layout < ZN_LAYOUT_NN || layout > ZN_LAYOUT_TN) return ZN_ERR_INVALID_ARG;
     if (act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
@@ -318,7 +323,9 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     const int64_t kLimit = (int64_t)INT_MAX / 4;
     const int64_t b_extent = conv ? (int64_t)conv->channels * conv->in_h * conv->in_w : (b_outer - 1) * ldb + b_row;
     if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || b_extent > kLimit)) return ZN_ERR_OVERFLOW;
-    if (conv && layout != ZN_LAYOUT_NN) return ZN_ERR_INVALID_ARG;
+    if (conv && layout != (convt ? ZN_LAYOUT_NT : ZN_LAYOUT_NN)) return ZN_ERR_INVALID_ARG;
+    if (convt && (!conv || k % 4 != 0 || conv->channels % 4 != 0 || !aligned16(b) || stride_b % 4 != 0))
+        return ZN_ERR_INVALID_ARG;  // whole 16-byte chunks of grad_output rows
 
     const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, k, batch, conv != nullptr);
     const TileShape &ts = kTiles[tile];
@@ -381,7 +388,9 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     args.ws = ctx->ws;
     // 4-pixel (16-byte) gather: unit column stride, and whole chunks of 4 pixels per output row
     const int gather4 = conv && conv->stride_w == 1 && conv->out_w % 4 == 0 ? 1 : 0;
-    hipFunction_t f = conv ? ctx->conv[tile][vec ? 1 : 0][gather4] : ctx->gemm[layout][tile][vec ? 1 : 0];
+    hipFunction_t f = convt  ? ctx->convt[tile][vec ? 1 : 0]
+                      : conv ? ctx->conv[tile][vec ? 1 : 0][gather4]
+                             : ctx->gemm[layout][tile][vec ? 1 : 0];
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
         ZnGemmArgs part = args;
@@ -578,6 +587,13 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                 if (hipModuleGetFunction(&ctx->conv[t][v][g], ctx->gemm_module, name) != hipSuccess)
                     return bail(ZN_ERR_SYMBOL);
             }
+    for (int t = 0; t < kNumTiles; ++t)
+        for (int v = 0; v < 2; ++v) {
+            char name[64];
+            std::snprintf(name, sizeof(name), "zn_convt_nt_%s%s", kTiles[t].suffix, v ? "_v" : "");
+            if (hipModuleGetFunction(&ctx->convt[t][v], ctx->gemm_module, name) != hipSuccess)
+                return bail(ZN_ERR_SYMBOL);
+        }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess)
         return bail(ZN_ERR_SYMBOL);
     for (int i = 0; i < kNumElt; ++i)
@@ -1113,7 +1129,12 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
     constexpr int64_t kColFloats = (int64_t)1 << 28;  // 1 GiB of col per chunk
     if (hw * taps > kColFloats) return ZN_ERR_OVERFLOW;
     const int64_t chunk = std::min<int64_t>(batch, kColFloats / (hw * taps));
-    Lease col(ctx), part(ctx);
+    // Stride 1 in the im2col reading: grad_input is one transposed-convolution
+    // GEMM over all images (no grad_col, no col2im), when grad_output rows
+    // split into whole 16-byte chunks of 4 channels.
+    const bool transposed = k_order == 0 && sh == 1 && sw == 1 && oc % 4 == 0 && aligned16(grad_output) &&
+                            oc * hw <= INT_MAX / 4 && h * w <= INT_MAX && kh * kw * oc <= INT_MAX;
+    Lease col(ctx), part(ctx), wt(ctx);
     if ((rc = col.get((size_t)(chunk * hw * taps)))) return rc;
     if (k_order == 1 && (rc = part.get((size_t)(chunk * oc * taps)))) return rc;
     for (int64_t b0 = 0; b0 < batch; b0 += chunk) {
@@ -1129,6 +1150,7 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
             if ((rc = gemm_launch(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, col.ptr, taps, 0, grad_weights, taps, 0,
                                   1, b0 > 0, nullptr, ZN_ACT_LINEAR)))
                 return rc;
+            if (transposed) continue;  // grad_input after the loop
             // grad_col = go2 . W: NN, M = rows, N = taps, K = OC (into the col buffer)
             if ((rc = gemm_launch(ctx, ZN_LAYOUT_NN, rows, taps, oc, go, oc, 0, weights, taps, 0, col.ptr, taps, 0, 1,
                                   0, nullptr, ZN_ACT_LINEAR)))
@@ -1161,6 +1183,40 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
         }
         ZnIm2colArgs ca = col_args(gi, col.ptr, nb, c, kh, kw, h, w, oh, ow, sh, sw, ph, pw, k_order);
         if ((rc = col2im_launch(ctx, ca))) return rc;
+    }
+    if (transposed) {
+        // grad_input_b[ic][(ih, iw)] = sum over (kh, kw, oc) of W'[ic][(kh*kW + kw)*OC + oc] .
+        // go2[b*OH*OW + (ih + ph - kh)*OW + (iw + pw - kw)][oc]  (terms outside the output image are 0)
+        const int64_t kt = kh * kw * oc;
+        if ((rc = wt.get((size_t)(c * kt)))) return rc;
+        ZnRegroupArgs ra;
+        ra.in = weights;
+        ra.out = wt.ptr;
+        ra.out_channels = (int32_t)oc;
+        ra.channels = (int32_t)c;
+        ra.taps_per_channel = (int32_t)(kh * kw);
+        const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 8;
+        if ((rc = launch(ctx, ctx->elt[kRegroup], (unsigned)std::min<int64_t>(cdiv(c * kt, 256), cap), 1, 256, &ra)))
+            return rc;
+        ZnConvGeom g;
+        std::memset(&g, 0, sizeof(g));
+        g.channels = (int32_t)oc;  // gathered image: OH x OW rows of OC channels
+        g.in_h = (int32_t)oh;
+        g.in_w = (int32_t)ow;
+        g.k_h = (int32_t)kh;
+        g.k_w = (int32_t)kw;
+        g.out_w = (int32_t)w;  // decodes the GEMM column into (ih, iw)
+        g.stride_h = 1;
+        g.stride_w = 1;
+        g.pad_h = (int32_t)ph;
+        g.pad_w = (int32_t)pw;
+        g.div1 = (int32_t)oc;
+        udiv_magic((uint32_t)g.div1, g.div1_mul, g.div1_shift);
+        udiv_magic((uint32_t)g.k_w, g.kw_mul, g.kw_shift);
+        udiv_magic((uint32_t)g.out_w, g.ow_mul, g.ow_shift);
+        if ((rc = gemm_launch_ex(ctx, ZN_LAYOUT_NT, c, h * w, kt, wt.ptr, kt, 0, grad_output, kt, oc * hw, grad_input,
+                                 h * w, plane, batch, 0, nullptr, ZN_ACT_LINEAR, 0, &g, true)))
+            return rc;
     }
     // grad_bias[c] = sum over images of the (image, channel) plane sums, added in image order
     Lease planes(ctx);

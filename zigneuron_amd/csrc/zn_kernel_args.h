@@ -103,5 +103,12 @@ struct ZnIm2colArgs {
     int32_t k_order;
 };
 
+// Weight regroup for the transposed-convolution input gradient:
+// out[ic][t*OC + oc] = in[oc][t*C + ic] for t < taps_per_channel (kH*kW).
+struct ZnRegroupArgs {
+    const float *in;
+    float *out;
+    int32_t out_channels, channels, taps_per_channel;
+};
 
 #endif
