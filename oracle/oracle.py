@@ -163,13 +163,18 @@ def accumulate_bias(grad_bias, gaa):
     return gb
 
 
+def _geometry(in_h, in_w, k_h, k_w, stride, pad):
+    """stride and pad as one int or an (h, w) pair -> (out_h, out_w, sh, sw, ph, pw)."""
+    sh, sw = (stride, stride) if np.isscalar(stride) else tuple(stride)
+    ph, pw = (pad, pad) if np.isscalar(pad) else tuple(pad)
+    return (in_h + 2 * ph - k_h) // sh + 1, (in_w + 2 * pw - k_w) // sw + 1, sh, sw, ph, pw
+
+
 def im2col(x, batch, channels, in_h, in_w, k_h, k_w, stride=1, pad=0):
     x = _f32(x)
-    out_h = (in_h + 2 * pad - k_h) // stride + 1
-    out_w = (in_w + 2 * pad - k_w) // stride + 1
+    out_h, out_w, sh, sw, ph, pw = _geometry(in_h, in_w, k_h, k_w, stride, pad)
     col = np.empty((batch * out_h * out_w, k_h * k_w * channels), np.float32)
-    lib().zno_im2col(_p(x), _p(col), batch, channels, in_h, in_w, k_h, k_w, out_h, out_w,
-                     stride, stride, pad, pad)
+    lib().zno_im2col(_p(x), _p(col), batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, sh, sw, ph, pw)
     return col
 
 
@@ -184,37 +189,35 @@ def conv2d_im2col_gemm(col, weights, bias, batch, out_channels, col_height, col_
 def conv2d_forward(x, weights, bias, channels, out_channels, k_h, k_w, in_h, in_w, stride=1, pad=0):
     """cpuConv2dForward with its naive / im2col switch; returns [batch, OC, OH, OW]."""
     x, w, bias = _f32(x), _f32(weights), _f32(bias)
-    out_h = (in_h + 2 * pad - k_h) // stride + 1
-    out_w = (in_w + 2 * pad - k_w) // stride + 1
+    out_h, out_w, sh, sw, ph, pw = _geometry(in_h, in_w, k_h, k_w, stride, pad)
     batch = x.size // (channels * in_h * in_w)
     out = np.empty((batch, out_channels, out_h, out_w), np.float32)
     lib().zno_conv2d_forward(_p(x), x.size, _p(w), _p(bias), _p(out), channels, out_channels, k_h, k_w, in_h, in_w,
-                             out_h, out_w, stride, stride, pad, pad)
+                             out_h, out_w, sh, sw, ph, pw)
     return out
 
 
 def col2im(col, batch, channels, in_h, in_w, k_h, k_w, stride=1, pad=0):
     """Backend.col2im: col [batch*OH*OW, kH*kW*C] -> NCHW [batch, C, H, W]."""
     col = _f32(col)
-    out_h = (in_h + 2 * pad - k_h) // stride + 1
-    out_w = (in_w + 2 * pad - k_w) // stride + 1
+    out_h, out_w, sh, sw, ph, pw = _geometry(in_h, in_w, k_h, k_w, stride, pad)
     out = np.empty((batch, channels, in_h, in_w), np.float32)
-    lib().zno_col2im(_p(col), _p(out), batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride, stride, pad, pad)
+    lib().zno_col2im(_p(col), _p(out), batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, sh, sw, ph, pw)
     return out
 
 
 def conv2d_backward(x, weights, grad_output, channels, out_channels, k_h, k_w, in_h, in_w, stride=1, pad=0,
                     branch="auto"):
     """cpuConv2dBackward (branch "auto": the reference's size switch; "direct" or
-    "im2col" force one branch).  Returns (grad_input, grad_weights, grad_bias)."""
+    "im2col" force one branch).  stride and pad: an int or an (h, w) pair.
+    Returns (grad_input, grad_weights, grad_bias)."""
     x, w, go = _f32(x), _f32(weights), _f32(grad_output)
-    out_h = (in_h + 2 * pad - k_h) // stride + 1
-    out_w = (in_w + 2 * pad - k_w) // stride + 1
+    out_h, out_w, sh, sw, ph, pw = _geometry(in_h, in_w, k_h, k_w, stride, pad)
     batch = x.size // (channels * in_h * in_w)
     gi = np.empty((batch, channels, in_h, in_w), np.float32)
     gw = np.empty(out_channels * channels * k_h * k_w, np.float32)
     gb = np.empty(out_channels, np.float32)
-    geo = (channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, stride, stride, pad, pad)
+    geo = (channels, out_channels, k_h, k_w, in_h, in_w, out_h, out_w, sh, sw, ph, pw)
     if branch == "auto":
         lib().zno_conv2d_backward(_p(x), x.size, _p(w), _p(go), _p(gi), _p(gw), _p(gb), *geo)
     else:

@@ -38,8 +38,13 @@ def backend(ctx):
     return Backend(ctx)
 
 
+def pair(v):
+    return (v, v) if np.isscalar(v) else tuple(v)
+
+
 def out_hw(h, w, k_h, k_w, stride, pad):
-    return (h + 2 * pad - k_h) // stride + 1, (w + 2 * pad - k_w) // stride + 1
+    (sh, sw), (ph, pw) = pair(stride), pair(pad)
+    return (h + 2 * ph - k_h) // sh + 1, (w + 2 * pw - k_w) // sw + 1
 
 
 CONV_CASES = [  # batch, C, H, W, OC, kH, kW, stride, pad
@@ -368,7 +373,8 @@ def run_backward(ctx, case, branch, seed=13):
     dgw = ctx.alloc(OC * KH * KW * C).fill(np.nan)
     dgb = ctx.alloc(OC).fill(np.nan)
     fn = ctx.conv2d_backward_im2col if branch == "im2col" else ctx.conv2d_backward_direct
-    fn(dx, dw, dgo, dgi, dgw, dgb, B, C, OC, KH, KW, H, W, OH, OW, st, st, pd, pd)
+    (sh, sw), (ph, pw) = pair(st), pair(pd)
+    fn(dx, dw, dgo, dgi, dgw, dgb, B, C, OC, KH, KW, H, W, OH, OW, sh, sw, ph, pw)
     got = (dgi.download(), dgw.download(), dgb.download())
     for buf in (dx, dw, dgo, dgi, dgw, dgb):
         buf.close()
@@ -381,6 +387,33 @@ def test_conv2d_backward_device(ctx, case, branch):
     announce(f"conv2d backward {branch} {case}")
     got, x, w, go = run_backward(ctx, case, branch)
     backward_check(got, x, w, go, case, branch, f"{branch} {case}")
+
+
+# stride_w 1 and OW % 4 == 0: the weight gradient gathers col from the input
+# (no im2col); with stride 1 and OC % 4 == 0 as well, no col buffer at all.
+# Chunks straddle the left, right or both paddings; stride_h 2 and 3 keep only
+# the weight gradient implicit.
+IMPLICIT_W_CASES = [(2, 16, 12, 12, 24, 3, 3, 1, 1), (2, 5, 9, 12, 7, 3, 3, 1, 1), (1, 3, 7, 16, 8, 5, 5, 1, 2),
+                    (3, 4, 6, 8, 12, 1, 1, 1, 0), (1, 2, 5, 20, 4, 3, 7, 1, 3), (2, 3, 4, 4, 8, 3, 3, 1, 1),
+                    (2, 6, 11, 8, 8, 3, 3, (2, 1), (1, 1)), (1, 5, 13, 12, 6, 3, 3, (3, 1), (0, 1)),
+                    (1, 70, 9, 8, 4, 3, 3, 1, 1)]
+
+
+@pytest.mark.parametrize("tile", ["auto", "256x128", "128x128", "128x64", "64x64", "32x32"])
+@pytest.mark.parametrize("case", IMPLICIT_W_CASES)
+def test_conv_backward_implicit_weight_grad_every_tile(ctx, case, tile):
+    """The weight gradient as an implicit GEMM (col gathered in 4-pixel chunks)
+    through every forced tile, with the policy's split-K and 5 forced slices."""
+    announce(f"conv backward implicit grad_W tile {tile} {case}")
+    ctx.set_gemm_tile(tile)
+    try:
+        for splits in (0, 5):
+            ctx.set_gemm_splits(splits)
+            got, x, w, go = run_backward(ctx, case, "im2col", seed=18)
+            backward_check(got, x, w, go, case, "im2col", f"{tile} splits {splits} {case}")
+    finally:
+        ctx.set_gemm_tile("auto")
+        ctx.set_gemm_splits(0)
 
 
 TRANSPOSED_CASES = [(2, 6, 10, 9, 8, 3, 3, 1, 1), (1, 5, 7, 12, 36, 5, 3, 1, 2), (2, 33, 5, 6, 4, 1, 1, 1, 0),

@@ -290,6 +290,42 @@ def test_conv_backward_direct_is_the_adjoint_of_the_forward(geo):
     np.testing.assert_array_equal(gb, g.sum(axis=(0, 2, 3)))
 
 
+def _im2col_brute(x, KH, KW, sh, sw, ph, pw):
+    """im2col by its definition, col[(b, oh, ow)][(kh, kw, ic)] = x[b, ic, oh*sh - ph + kh, ow*sw - pw + kw]
+    (0 outside the image), written independently of the oracle's loops."""
+    B, C, H, W = x.shape
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    xp = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)))
+    col = np.empty((B, OH, OW, KH, KW, C), x.dtype)
+    for kh in range(KH):
+        for kw in range(KW):
+            col[:, :, :, kh, kw, :] = xp[:, :, kh:kh + sh * (OH - 1) + 1:sh, kw:kw + sw * (OW - 1) + 1:sw].transpose(0, 2, 3, 1)
+    return col.reshape(B * OH * OW, KH * KW * C)
+
+
+@pytest.mark.parametrize("geo", [(2, 3, 7, 9, 4, 3, 3, (2, 1), (1, 1)), (1, 2, 6, 8, 8, 3, 5, (1, 1), (0, 2)),
+                                 (2, 4, 9, 8, 4, 2, 3, (3, 1), (1, 0))])
+def test_conv_backward_im2col_contract_unequal_strides(geo):
+    """Separate stride_h / stride_w and pad_h / pad_w (the reference takes both
+    pairs): im2col equals its definition, and the im2col branch's gradients
+    follow its contract exactly on integer data."""
+    B, C, H, W, OC, KH, KW, (sh, sw), (ph, pw) = geo
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    rng = np.random.default_rng(sum(geo[:7]) + 5)
+    x, w = _ints(rng, (B, C, H, W)), _ints(rng, (OC, KH * KW * C))
+    g = _ints(rng, (B, OC, OH, OW))
+    col = oracle.im2col(x, B, C, H, W, KH, KW, (sh, sw), (ph, pw))
+    np.testing.assert_array_equal(col, _im2col_brute(x, KH, KW, sh, sw, ph, pw))
+    gi, gw, gb = oracle.conv2d_backward(x, w, g, C, OC, KH, KW, H, W, (sh, sw), (ph, pw), branch="im2col")
+    go2 = g.reshape(B * OH * OW, OC).astype(np.int64)
+    np.testing.assert_array_equal(gw, (go2.T @ col.astype(np.int64)).ravel().astype(np.float32))
+    grad_col = (go2 @ w.astype(np.int64)).astype(np.float32)
+    lhs = int((grad_col.astype(np.int64) * col.astype(np.int64)).sum())  # <grad_col, im2col(x)> = <col2im(grad_col), x>
+    assert lhs == int((gi.astype(np.int64) * x.astype(np.int64)).sum())
+    np.testing.assert_array_equal(gi, oracle.col2im(grad_col, B, C, H, W, KH, KW, (sh, sw), (ph, pw)))
+    np.testing.assert_array_equal(gb, g.sum(axis=(0, 2, 3)))
+
+
 def test_conv_backward_im2col_contract():
     """The im2col branch reads grad_output as [batch*OH*OW][OC] for both GEMMs
     (NCHW only for grad_bias): grad_weights = go2^T . col, grad_input =

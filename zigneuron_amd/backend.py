@@ -215,7 +215,7 @@ class Context:
               "zn_hip_set_gemm_tile")
 
     def set_gemm_splits(self, splits: int = 0) -> None:
-        """Force the number of split-K slices (1..64), or 0 for the policy."""
+        """Force the number of split-K slices (1..256), or 0 for the policy."""
         check(_lib.load().zn_hip_set_gemm_splits(self.handle, int(splits)), "zn_hip_set_gemm_splits")
 
     # --- GEMM on device pointers (asynchronous on the context stream)

@@ -136,12 +136,26 @@ struct ConvGatherStage {
     }
 };
 
-// Tile coordinates of this workgroup: optional XCD-contiguous remap, then
-// groups of `group_m` tile rows (group_m = 1 is plain row-major order).
-__device__ __forceinline__ void tile_coords(const ZnGemmArgs &p, int &tm, int &tn) {
+// Tile coordinates and split-K slice of this workgroup: optional XCD-
+// contiguous remap, then groups of `group_m` tile rows (group_m = 1 is plain
+// row-major order).  Workgroups go to the 8 XCDs round-robin by linear id,
+// and each XCD has its own L2.  xcd_remap 2 (split-K, one problem): the
+// (slice, tile) pairs are numbered slice-major and each XCD takes a
+// contiguous run of them, so the tiles of one K slice, which read the same
+// rows of A and B, share one L2 instead of fetching them once per XCD.
+__device__ __forceinline__ void tile_coords(const ZnGemmArgs &p, int &tm, int &tn, int &slice) {
     int pid = blockIdx.x;
+    slice = blockIdx.z;
     const int ntiles = p.tiles_m * p.tiles_n;
-    if (p.xcd_remap) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+    if (p.xcd_remap == 1) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+    if (p.xcd_remap == 2) {
+        const int lin = blockIdx.x + ntiles * blockIdx.z;  // gridDim.y == 1
+        const int total = ntiles * p.splits, per = total >> 3, extra = total & 7;
+        const int xcd = lin & 7;
+        const int seq = xcd * per + min(xcd, extra) + (lin >> 3);
+        slice = seq / ntiles;
+        pid = seq - slice * ntiles;
+    }
     const int group_span = p.group_m * p.tiles_n;
     const int first_m = (pid / group_span) * p.group_m;
     const int gsize = min(p.tiles_m - first_m, p.group_m);
@@ -274,18 +288,105 @@ struct ConvTGatherStage {
     }
 };
 
+// The weight-gradient operand of a convolution with stride_w == 1 and
+// out_w % 4 == 0, without the col buffer: B[k][n] = col[k][n], k = output
+// pixel over `images` images (b*OH*OW + oh*OW + ow), n = im2col tap
+// (kh*k_w + kw)*C + ic, i.e. input[b][ic][oh*stride_h - pad_h + kh][ow -
+// pad_w + kw].  The operand is K-contiguous (stored [BN][BK], swizzled like
+// DmaStage): a 16-byte chunk is 4 consecutive k, i.e. 4 neighbouring output
+// pixels of one output row, which read 4 consecutive input columns of one
+// tap.  A lane's tap and chunk column are fixed for the whole tile (Lane);
+// its pixels move with k0.  Chunks that straddle the left or right padding
+// are DMAed as zeros and patched like ConvGather16Stage's.
+template <int BN, int BK, int NT>
+struct ConvWGatherStage {
+    typedef DmaStage<BN, BK, NT, true, 16> Layout;
+    static constexpr int kNoRow = -(1 << 30);  // plus any oh*stride_h stays negative
+    static constexpr int kPerWave = Layout::kPerWave;
+    static constexpr int kWaves = NT / kWave;
+
+    struct Lane {
+        int tap_off[kPerWave];  // ic*H*W + (kh - pad_h)*W + (kw - pad_w), relative to the pixel's (oh*sh, ow)
+        int dh[kPerWave];       // kh - pad_h; kNoRow for a tap past the problem (never in the image)
+        int dw[kPerWave];       // kw - pad_w
+        int kc[kPerWave];       // first k of the chunk, relative to k0
+    };
+    struct Patch {
+        zn_f32x4 v[kPerWave];
+        uint32_t mask;
+    };
+
+    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int wave, int lane) {
+        Lane l;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int pos = (j * kWaves + wave) * Layout::kPerInst + 4 * lane;
+            const int row = pos / BK;
+            const int n = n0 + row;
+            int ic, kh, kw;
+            ConvGatherStage<BN, BK, NT>::decode_k(g, n, ic, kh, kw);
+            l.dh[j] = n < nmax ? kh - g.pad_h : kNoRow;
+            l.dw[j] = kw - g.pad_w;
+            l.tap_off[j] = (ic * g.in_h + kh - g.pad_h) * g.in_w + kw - g.pad_w;
+            l.kc[j] = 4 * (((pos % BK) / 4) ^ Layout::swz(row));
+        }
+        return l;
+    }
+
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const float *image, float *lds,
+                                                 const ZnConvGeom &g, const Lane &ln, int k0, int kmax, int wave,
+                                                 int lane, Patch &pt) {
+        pt.mask = 0;
+        const int plane = g.channels * g.in_h * g.in_w;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int p0 = (j * kWaves + wave) * Layout::kPerInst;
+            const int k = k0 + ln.kc[j];
+            const int q = zn_udiv(k, g.ow_mul, g.ow_shift), ow = k - q * g.out_w;
+            const int b = zn_udiv(q, g.oh_mul, g.oh_shift), oh = q - b * g.out_h;
+            const int ohs = oh * g.stride_h;
+            const int ih = ohs + ln.dh[j], iws = ow + ln.dw[j];
+            const bool row_ok = k < kmax && (unsigned)ih < (unsigned)g.in_h;
+            const bool full = row_ok && iws >= 0 && iws + 3 < g.in_w;
+            const int src = b * plane + ln.tap_off[j] + ohs * g.in_w + ow;  // = b*plane + (ic*H + ih)*W + iws
+            const uint32_t off = full ? (uint32_t)src * 4u : kOutOfRange;
+            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                         :
+                         : "s"(lds_addr), "v"(off), "s"(rsrc)
+                         : "memory");
+            pt.v[j] = zn_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (row_ok && !full && iws + 3 >= 0 && iws < g.in_w) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if ((unsigned)(iws + e) < (unsigned)g.in_w) pt.v[j][e] = image[src + e];
+                pt.mask |= 1u << j;
+            }
+        }
+    }
+
+    // After this wave's DMA has landed: write the patched chunks.
+    __device__ static __forceinline__ void apply(float *lds, const Patch &pt, int wave, int lane) {
+        if (!pt.mask) return;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j)
+            if (pt.mask & (1u << j))
+                *reinterpret_cast<zn_f32x4 *>(lds + (j * kWaves + wave) * Layout::kPerInst + 4 * lane) = pt.v[j];
+    }
+};
+
 // Epilogue of one macro tile: v = acc (+ C) (+ bias) -> act -> store.
 // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
 // holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
 // stores its raw partial sums to the workspace instead.
 template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
 __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
-                                           int m0, int n0, int wm0, int wn0, int lane) {
+                                           int m0, int n0, int wm0, int wn0, int lane, int slice) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
     const int64_t bz = blockIdx.y;
     float *gc = p.c + bz * p.stride_c;
     const bool split = p.splits > 1;
-    if (split) gc = p.ws + ((int64_t)bz * p.splits + blockIdx.z) * (int64_t)p.m * p.n;
+    if (split) gc = p.ws + ((int64_t)bz * p.splits + slice) * (int64_t)p.m * p.n;
     const int64_t ldc = split ? (int64_t)p.n : p.ldc;
     const bool accumulate = !split && p.accumulate;
     const int act = split ? 0 : p.act;
@@ -349,7 +450,7 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
 // for its stage (vmcnt(0) + barrier), refills the other stage with slice
 // kt + 1, then computes slice kt while that load is in flight.
 template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, bool CONV, int GW = 4,
-          bool CONVT = false>
+          bool CONVT = false, bool CONVW = false>
 __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -357,19 +458,21 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
     static_assert(!CONV || (!BKC && WB == 4), "the convolution operand is X-contiguous and gathered");
     static_assert(!CONVT || (BKC && WB == 16 && !CONV), "the transposed-convolution operand is K-contiguous");
+    static_assert(!CONVW || (BKC && WB == 16 && !CONV && !CONVT), "the weight-gradient operand is K-contiguous");
     typedef DmaStage<BM, BK, NT, AK, WA> SA;
     typedef DmaStage<BN, BK, NT, BKC, WB> SB;
     typedef ConvGatherStage<BN, BK, NT> SC;
     typedef ConvGather16Stage<BN, BK, NT> SC16;
     typedef ConvTGatherStage<BN, BK, NT> ST;
+    typedef ConvWGatherStage<BN, BK, NT> SW;
     __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
-    int tm, tn;
-    tile_coords(p, tm, tn);
+    int tm, tn, slice;
+    tile_coords(p, tm, tn, slice);
     const int m0 = tm * BM, n0 = tn * BN;
     const int64_t bz = blockIdx.y;
     const float *ga = p.a + bz * p.stride_a;
@@ -383,13 +486,14 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
 
-    const int kbeg = (int)blockIdx.z * p.k_chunk;
+    const int kbeg = slice * p.k_chunk;
     const int kend = min(p.k, kbeg + p.k_chunk);
     const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
     const uint32_t b_bytes =
-        (CONV || CONVT) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+        CONVW ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+        : (CONV || CONVT) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
              : (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
@@ -400,8 +504,14 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     patch.mask = 0;
     if constexpr (CONV && GW == 4 && SC::kFixedN) cl = SC::lane_setup(p.conv, n0, p.n, wave, lane);
     if constexpr (CONV && GW == 16) cl16 = SC16::lane_setup(p.conv, n0, p.n, lane);
+    typename SW::Lane clw{};
+    typename SW::Patch wpatch;
+    wpatch.mask = 0;
+    if constexpr (CONVW) clw = SW::lane_setup(p.conv, n0, p.n, wave, lane);
     auto issue_b = [&](float *lds, int k0) {
-        if constexpr (CONVT)
+        if constexpr (CONVW)
+            SW::issue(rb, gb, lds, p.conv, clw, k0, kend, wave, lane, wpatch);
+        else if constexpr (CONVT)
             ST::issue(rb, lds, p.conv, n0, k0, p.n, kend, wave, lane);
         else if constexpr (CONV && GW == 16)
             SC16::issue(rb, gb, lds, p.conv, cl16, k0, kend, wave, lane, patch);
@@ -417,6 +527,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     for (int kt = 0; kt < ktiles; ++kt) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of slice kt is in LDS
         if constexpr (CONV && GW == 16) SC16::apply(lds_b[kt & 1], patch, wave, lane);
+        if constexpr (CONVW) SW::apply(lds_b[kt & 1], wpatch, wave, lane);
         __syncthreads();  // every wave's part is; every wave is done reading slice kt - 1
         const int cur = kt & 1;
         if (kt + 1 < ktiles) {
@@ -439,7 +550,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
                         acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
         }
     }
-    store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, m0, n0, wm0, wn0, lane);
+    store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, m0, n0, wm0, wn0, lane, slice);
 }
 
 }  // namespace
@@ -513,6 +624,25 @@ ZN_CONVT_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_CONVT_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_CONVT_TILE(m, 64, 64, 32, 2, 2, 1)
 ZN_CONVT_TILE(s, 32, 32, 32, 1, 1, 1)
+
+// Weight gradient of a convolution with stride_w == 1 and out_w % 4 == 0:
+// grad_W[OC][taps] = go2^T . col with K = the output pixels of all images,
+// A = grad_output read as [pixels][OC] rows (X-contiguous, like TN) and
+// B = col gathered from the NCHW input (ConvWGatherStage).  _v: OC % 4 == 0
+// and grad_output 16-byte aligned.
+#define ZN_CONVW_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convw_tn_##TILE##SUFFIX(ZnGemmArgs p) { \
+        gemm_tile_dma<BM, BN, BK, WM, WN, false, true, WA, 16, false, 4, false, true>(p);        \
+    }
+#define ZN_CONVW_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
+    ZN_CONVW_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
+    ZN_CONVW_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+
+ZN_CONVW_TILE(x, 256, 128, 16, 4, 2, 1)
+ZN_CONVW_TILE(l, 128, 128, 16, 2, 2, 4)
+ZN_CONVW_TILE(n, 128, 64, 16, 2, 1, 1)
+ZN_CONVW_TILE(m, 64, 64, 32, 2, 2, 1)
+ZN_CONVW_TILE(s, 32, 32, 32, 1, 1, 1)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not

@@ -71,6 +71,7 @@ struct zn_ctx {
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
+    hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -293,16 +294,23 @@ void udiv_magic(uint32_t d, uint32_t &mul, uint32_t &shift) {
     shift = l;
 }
 
-// `conv` (optional) turns B into the implicit im2col operand of an NCHW
-// image batch (B[k][n] gathered per ZnConvGeom, images `stride_b` apart);
-// the problem is then NN with M = out channels, N = out pixels.  With
-// `convt` it is instead the transposed-convolution operand of a stride-1
-// input gradient (B[n][k] gathered from [OH*OW][OC] grad_output rows, K-
-// contiguous 16-byte chunks), NT with M = in channels, N = in pixels.
+// Gathered B operands (ZnConvGeom), selected by `conv` + `mode`:
+//  kGatherIm2col:     the implicit im2col operand of an NCHW image batch
+//                     (images `stride_b` apart), NN with M = out channels,
+//                     N = out pixels;
+//  kGatherTransposed: the transposed-convolution operand of a stride-1 input
+//                     gradient (B[n][k] from [OH*OW][OC] grad_output rows,
+//                     K-contiguous 16-byte chunks), NT with M = in channels,
+//                     N = in pixels;
+//  kGatherWeightGrad: the col operand of a weight gradient (B[k][n] =
+//                     col[pixel][tap] over conv->images images, K-contiguous
+//                     4-pixel chunks), TN with M = out channels, N = taps.
+enum GatherMode { kGatherIm2col, kGatherTransposed, kGatherWeightGrad };
+
 int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                    int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
                    int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows,
-                   const ZnConvGeom *conv = nullptr, bool convt = false) {
+                   const ZnConvGeom *conv = nullptr, GatherMode mode = kGatherIm2col) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
     if (layout < ZN_LAYOUT_NN || layout > ZN_LAYOUT_TN) return ZN_ERR_INVALID_ARG;
     if (act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
@@ -321,11 +329,19 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     const int64_t a_outer = layout == ZN_LAYOUT_TN ? k : m;
     const int64_t b_outer = layout == ZN_LAYOUT_NT ? n : k;
     const int64_t kLimit = (int64_t)INT_MAX / 4;
-    const int64_t b_extent = conv ? (int64_t)conv->channels * conv->in_h * conv->in_w : (b_outer - 1) * ldb + b_row;
+    const int64_t images = conv && mode == kGatherWeightGrad ? conv->images : 1;
+    const int64_t b_extent =
+        conv ? images * conv->channels * conv->in_h * conv->in_w : (b_outer - 1) * ldb + b_row;
     if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || b_extent > kLimit)) return ZN_ERR_OVERFLOW;
-    if (conv && layout != (convt ? ZN_LAYOUT_NT : ZN_LAYOUT_NN)) return ZN_ERR_INVALID_ARG;
-    if (convt && (!conv || k % 4 != 0 || conv->channels % 4 != 0 || !aligned16(b) || stride_b % 4 != 0))
+    constexpr int kGatherLayout[3] = {ZN_LAYOUT_NN, ZN_LAYOUT_NT, ZN_LAYOUT_TN};
+    if (conv && layout != kGatherLayout[mode]) return ZN_ERR_INVALID_ARG;
+    if (conv && mode == kGatherTransposed &&
+        (k % 4 != 0 || conv->channels % 4 != 0 || !aligned16(b) || stride_b % 4 != 0))
         return ZN_ERR_INVALID_ARG;  // whole 16-byte chunks of grad_output rows
+    if (conv && mode == kGatherWeightGrad &&
+        (conv->stride_w != 1 || conv->out_w % 4 != 0 || conv->k_order != 0 || batch != 1 ||
+         k != images * conv->out_h * conv->out_w))
+        return ZN_ERR_INVALID_ARG;  // whole 4-pixel chunks of one output row, over all images
 
     const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, k, batch, conv != nullptr);
     const TileShape &ts = kTiles[tile];
@@ -388,12 +404,14 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     args.ws = ctx->ws;
     // 4-pixel (16-byte) gather: unit column stride, and whole chunks of 4 pixels per output row
     const int gather4 = conv && conv->stride_w == 1 && conv->out_w % 4 == 0 ? 1 : 0;
-    hipFunction_t f = convt  ? ctx->convt[tile][vec ? 1 : 0]
-                      : conv ? ctx->conv[tile][vec ? 1 : 0][gather4]
-                             : ctx->gemm[layout][tile][vec ? 1 : 0];
+    hipFunction_t f = !conv                     ? ctx->gemm[layout][tile][vec ? 1 : 0]
+                      : mode == kGatherTransposed ? ctx->convt[tile][vec ? 1 : 0]
+                      : mode == kGatherWeightGrad ? ctx->convw[tile][vec ? 1 : 0]
+                                                  : ctx->conv[tile][vec ? 1 : 0][gather4];
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
         ZnGemmArgs part = args;
+        if (splits > 1 && nb == 1) part.xcd_remap = 2;  // the tiles of one K slice share an XCD's L2
         part.a = a ? a + b0 * stride_a : nullptr;
         part.b = b ? b + b0 * stride_b : nullptr;
         part.c = c + b0 * stride_c;
@@ -592,6 +610,9 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             char name[64];
             std::snprintf(name, sizeof(name), "zn_convt_nt_%s%s", kTiles[t].suffix, v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->convt[t][v], ctx->gemm_module, name) != hipSuccess)
+                return bail(ZN_ERR_SYMBOL);
+            std::snprintf(name, sizeof(name), "zn_convw_tn_%s%s", kTiles[t].suffix, v ? "_v" : "");
+            if (hipModuleGetFunction(&ctx->convw[t][v], ctx->gemm_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
         }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess)
@@ -848,7 +869,7 @@ int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile) {
 }
 
 int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits) {
-    if (!ctx || splits < 0 || splits > 64) return ZN_ERR_INVALID_ARG;
+    if (!ctx || splits < 0 || splits > 256) return ZN_ERR_INVALID_ARG;
     ctx->forced_splits = splits;
     return ZN_OK;
 }
@@ -999,7 +1020,7 @@ static int conv2d_device(zn_ctx *ctx, const float *input, const float *weights, 
     if (batch == 0 || hw == 0) return ZN_OK;
     if (!input || !weights || !bias || !output) return ZN_ERR_INVALID_ARG;
     if (h * w > INT_MAX || c * h * w > INT_MAX / 4) return ZN_ERR_OVERFLOW;
-    ZnConvGeom g;
+    ZnConvGeom g = {};
     g.channels = (int32_t)c;
     g.in_h = (int32_t)h;
     g.in_w = (int32_t)w;
@@ -1110,6 +1131,12 @@ int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float 
 // (strided-batched TN).  Both finish with col2im into grad_input and the
 // per-channel sum of the NCHW grad_output into grad_bias.  Images are taken
 // in chunks whose col buffer stays under 1 GiB.
+//
+// In the k_order 0 reading two of those steps become implicit GEMMs:
+//  * stride_w 1, OW % 4 == 0: grad_W gathers col from the input (no im2col);
+//  * stride 1, OC % 4 == 0, 16-byte-aligned grad_output: grad_input is one
+//    transposed-convolution GEMM over all images (no grad_col, no col2im).
+// With both, no col buffer is allocated.
 static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *weights, const float *grad_output,
                                   float *grad_input, float *grad_weights, float *grad_bias, int64_t batch, int64_t c,
                                   int64_t oc, int64_t kh, int64_t kw, int64_t h, int64_t w, int64_t oh, int64_t ow,
@@ -1126,29 +1153,62 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
             return rc;
         return zn_hip_fill_f32(ctx, grad_bias, 0.0f, oc);
     }
-    constexpr int64_t kColFloats = (int64_t)1 << 28;  // 1 GiB of col per chunk
-    if (hw * taps > kColFloats) return ZN_ERR_OVERFLOW;
-    const int64_t chunk = std::min<int64_t>(batch, kColFloats / (hw * taps));
-    // Stride 1 in the im2col reading: grad_input is one transposed-convolution
-    // GEMM over all images (no grad_col, no col2im), when grad_output rows
-    // split into whole 16-byte chunks of 4 channels.
+    const int64_t kOffsetFloats = INT_MAX / 4;  // 32-bit byte offsets per operand
+    const bool implicit_w = k_order == 0 && sw == 1 && ow % 4 == 0 && plane <= kOffsetFloats && hw * oc <= kOffsetFloats;
     const bool transposed = k_order == 0 && sh == 1 && sw == 1 && oc % 4 == 0 && aligned16(grad_output) &&
-                            oc * hw <= INT_MAX / 4 && h * w <= INT_MAX && kh * kw * oc <= INT_MAX;
+                            oc * hw <= kOffsetFloats && h * w <= INT_MAX && kh * kw * oc <= INT_MAX;
+    const bool need_col = !(implicit_w && transposed);
+    constexpr int64_t kColFloats = (int64_t)1 << 28;  // 1 GiB of col per chunk
+    int64_t chunk = batch;
+    if (need_col) {
+        if (hw * taps > kColFloats) return ZN_ERR_OVERFLOW;
+        chunk = std::min<int64_t>(chunk, kColFloats / (hw * taps));
+    }
+    if (implicit_w) chunk = std::min<int64_t>(chunk, std::min(kOffsetFloats / plane, kOffsetFloats / (hw * oc)));
     Lease col(ctx), part(ctx), wt(ctx);
-    if ((rc = col.get((size_t)(chunk * hw * taps)))) return rc;
+    if (need_col && (rc = col.get((size_t)(chunk * hw * taps)))) return rc;
     if (k_order == 1 && (rc = part.get((size_t)(chunk * oc * taps)))) return rc;
+    ZnConvGeom gw = {};  // the implicit weight gradient's gather
+    if (implicit_w) {
+        gw.channels = (int32_t)c;
+        gw.in_h = (int32_t)h;
+        gw.in_w = (int32_t)w;
+        gw.k_h = (int32_t)kh;
+        gw.k_w = (int32_t)kw;
+        gw.out_w = (int32_t)ow;
+        gw.out_h = (int32_t)oh;
+        gw.stride_h = (int32_t)sh;
+        gw.stride_w = 1;
+        gw.pad_h = (int32_t)ph;
+        gw.pad_w = (int32_t)pw;
+        gw.k_order = 0;
+        gw.div1 = (int32_t)c;
+        udiv_magic((uint32_t)gw.div1, gw.div1_mul, gw.div1_shift);
+        udiv_magic((uint32_t)gw.k_w, gw.kw_mul, gw.kw_shift);
+        udiv_magic((uint32_t)gw.out_w, gw.ow_mul, gw.ow_shift);
+        udiv_magic((uint32_t)gw.out_h, gw.oh_mul, gw.oh_shift);
+    }
     for (int64_t b0 = 0; b0 < batch; b0 += chunk) {
         const int64_t nb = std::min(chunk, batch - b0);
         const int64_t rows = nb * hw;
         const float *go = grad_output + b0 * oc * hw;
         float *gi = grad_input + b0 * plane;
-        ZnIm2colArgs ia = col_args(const_cast<float *>(input) + b0 * plane, col.ptr, nb, c, kh, kw, h, w, oh, ow, sh,
-                                   sw, ph, pw, k_order);
-        if ((rc = im2col_launch(ctx, ia))) return rc;
+        if (implicit_w) {
+            // grad_W (+)= go2^T . col with col gathered from this chunk's images: TN, M = OC, N = taps, K = rows
+            gw.images = (int32_t)nb;
+            if ((rc = gemm_launch_ex(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, input + b0 * plane, taps, 0,
+                                     grad_weights, taps, 0, 1, b0 > 0, nullptr, ZN_ACT_LINEAR, 0, &gw,
+                                     kGatherWeightGrad)))
+                return rc;
+        } else {
+            ZnIm2colArgs ia = col_args(const_cast<float *>(input) + b0 * plane, col.ptr, nb, c, kh, kw, h, w, oh, ow,
+                                       sh, sw, ph, pw, k_order);
+            if ((rc = im2col_launch(ctx, ia))) return rc;
+        }
         if (k_order == 0) {
             // grad_W (+)= go2^T . col: TN, M = OC, N = taps, K = rows
-            if ((rc = gemm_launch(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, col.ptr, taps, 0, grad_weights, taps, 0,
-                                  1, b0 > 0, nullptr, ZN_ACT_LINEAR)))
+            if (!implicit_w && (rc = gemm_launch(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, col.ptr, taps, 0,
+                                                 grad_weights, taps, 0, 1, b0 > 0, nullptr, ZN_ACT_LINEAR)))
                 return rc;
             if (transposed) continue;  // grad_input after the loop
             // grad_col = go2 . W: NN, M = rows, N = taps, K = OC (into the col buffer)
@@ -1215,7 +1275,7 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
         udiv_magic((uint32_t)g.k_w, g.kw_mul, g.kw_shift);
         udiv_magic((uint32_t)g.out_w, g.ow_mul, g.ow_shift);
         if ((rc = gemm_launch_ex(ctx, ZN_LAYOUT_NT, c, h * w, kt, wt.ptr, kt, 0, grad_output, kt, oc * hw, grad_input,
-                                 h * w, plane, batch, 0, nullptr, ZN_ACT_LINEAR, 0, &g, true)))
+                                 h * w, plane, batch, 0, nullptr, ZN_ACT_LINEAR, 0, &g, kGatherTransposed)))
             return rc;
     }
     // grad_bias[c] = sum over images of the (image, channel) plane sums, added in image order

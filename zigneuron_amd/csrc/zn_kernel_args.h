@@ -20,6 +20,10 @@ struct ZnConvGeom {
     // k_h*k_w for 1); the other divisors are k_w and out_w.
     int32_t div1;
     uint32_t div1_mul, div1_shift, kw_mul, kw_shift, ow_mul, ow_shift;
+    // Weight gradient only (K runs over the pixels of `images` images):
+    // out_h and its divisor.
+    int32_t out_h, images;
+    uint32_t oh_mul, oh_shift;
 };
 
 // One (possibly batched) fp32 GEMM: C = act((acc ? C : 0) + op(A) op(B) + bias).
@@ -36,7 +40,8 @@ struct ZnGemmArgs {
     int32_t act;               // zn_act
     int32_t vec_c;             // 1: ldc and C allow vector stores
     int32_t group_m;           // tile rows per raster group
-    int32_t xcd_remap;         // 1: gridDim.x % 8 == 0, give each XCD a contiguous tile range
+    int32_t xcd_remap;         // 1: gridDim.x % 8 == 0, give each XCD a contiguous tile range;
+                               // 2: split-K with gridDim.y == 1, each XCD a contiguous (slice, tile) range
     // split-K: blockIdx.z = slice of K; splits > 1 writes raw partial sums to
     // ws[(problem * splits + slice)][m][n] and a reduce kernel finishes C.
     int32_t splits;
