@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle
-from _parity import uniform, normal, tol
+from _parity import as_kn, as_mk, normal, tol, uniform
 from gpu_common import announce, assert_close, ref_gemm, run_gemm, stored_shapes
 
 pytestmark = pytest.mark.gpu
@@ -274,6 +274,41 @@ def test_padded_and_unaligned_operands(ctx, layout):
     assert_close(c_full[:, :n], ref_gemm(layout, a, b, m, n, k), layout, a, b, m, n, k)
     assert np.all(c_full[:, n:] == -7.0), "wrote outside the n columns of a padded C row"
     for buf in (da, db, dc):
+        buf.close()
+
+
+@pytest.mark.parametrize("layout,m,n,k", [("nn", 4097, 1023, 777), ("nt", 1501, 1003, 999), ("tn", 999, 1502, 1001)])
+def test_large_unaligned_operands_are_packed(ctx, layout, m, n, k):
+    """Large problems whose rows are not 16-byte aligned whole float4s are
+    first copied into zero-padded aligned rows, then staged with 16-byte
+    loads.  Bit-identical to the problem with every dimension padded to a
+    multiple of 4 with zeros (16-byte staging, no copy), and within tolerance
+    of fp64.  The base pointer of A is also one float off alignment."""
+    rng = np.random.default_rng(6)
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    announce(f"packed operands {layout} {m}x{n}x{k}")
+    da = ctx.to_device(np.concatenate([[0.0], a.ravel()]).astype(np.float32))
+    db = ctx.to_device(b)
+    dc = ctx.alloc(m * n).fill(np.nan)
+    ctx.sgemm(layout, m, n, k, da.offset(1), a_shape[1], db, b_shape[1], dc, n)
+    c = dc.download().reshape(m, n)
+    mp, np_, kp = (-(-d // 4) * 4 for d in (m, n, k))
+    pa_shape, pb_shape = stored_shapes(layout, mp, np_, kp)
+    pa = np.zeros(pa_shape, np.float32)
+    pa[:a_shape[0], :a_shape[1]] = a
+    pb = np.zeros(pb_shape, np.float32)
+    pb[:b_shape[0], :b_shape[1]] = b
+    dpa, dpb = ctx.to_device(pa), ctx.to_device(pb)
+    dc2 = ctx.alloc(mp * np_).fill(np.nan)
+    ctx.sgemm(layout, mp, np_, kp, dpa, pa_shape[1], dpb, pb_shape[1], dc2, np_)
+    np.testing.assert_array_equal(c, dc2.download().reshape(mp, np_)[:m, :n])
+    rows = np.random.default_rng(7).choice(m, 48, replace=False)
+    a_mk, b_kn = as_mk(a, layout, m, k), as_kn(b, layout, k, n)
+    ref = a_mk[rows].astype(np.float64) @ b_kn.astype(np.float64)
+    den = np.abs(a_mk[rows]).astype(np.float64) @ np.abs(b_kn).astype(np.float64)
+    assert np.all(np.abs(c[rows] - ref) <= tol(k) * den), "packed GEMM outside 1e-5*sqrt(K) of fp64"
+    for buf in (da, db, dc, dpa, dpb, dc2):
         buf.close()
 
 

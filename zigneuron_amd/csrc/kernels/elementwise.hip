@@ -290,6 +290,23 @@ extern "C" __global__ __launch_bounds__(256) void zn_row_sum(ZnEltArgs p) {
     }
 }
 
+// A GEMM operand whose rows are not 16-byte aligned (or not whole float4s)
+// copied into rows of ld_dst floats with a zero tail, so the GEMM can stage
+// it with 16-byte loads.  A copy (bit-exact); one float4 of dst per thread
+// and step.
+extern "C" __global__ __launch_bounds__(256) void zn_pack_rows(ZnPackArgs p) {
+    const int64_t per_row = p.ld_dst >> 2;
+    const int64_t total = p.rows * per_row;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / per_row, c = (i - r * per_row) * 4;
+        const float *src = p.src + r * p.ld_src;
+        zn_f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = c + e < p.cols ? src[c + e] : 0.0f;
+        reinterpret_cast<zn_f32x4 *>(p.dst)[i] = v;
+    }
+}
+
 // W' for the stride-1 transposed-convolution GEMM of the input gradient
 // (cpuConv2dBackwardIm2col's grad_col = go2 . W followed by col2im, src/
 // backend.zig:3995-4060, as one GEMM): the [OC][kH*kW][C] weights regrouped

@@ -490,11 +490,14 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     const int kend = min(p.k, kbeg + p.k_chunk);
     const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
-    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + p.k : (p.k - 1) * lda + p.m) * 4u;
+    // 16-byte staging reads whole float4s: the last row's extent is rounded
+    // up to 4 floats (rows that are whole float4s, or packed with a zero tail)
+    constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
     const uint32_t b_bytes =
         CONVW ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
         : (CONV || CONVT) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
-             : (uint32_t)(BKC ? (p.n - 1) * ldb + p.k : (p.k - 1) * ldb + p.n) * 4u;
+             : (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
 

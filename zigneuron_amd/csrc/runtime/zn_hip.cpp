@@ -45,12 +45,12 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
                                          {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kNumElt };
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kPack, kNumElt };
 constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", "zn_add_bias",
                                            "zn_activation_forward", "zn_activation_backward",
                                            "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows",
                                            "zn_col2im",          "zn_row_sum",  "zn_dense_grad_prologue",
-                                           "zn_weight_regroup"};
+                                           "zn_weight_regroup", "zn_pack_rows"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
@@ -307,6 +307,8 @@ void udiv_magic(uint32_t d, uint32_t &mul, uint32_t &shift) {
 //                     4-pixel chunks), TN with M = out channels, N = taps.
 enum GatherMode { kGatherIm2col, kGatherTransposed, kGatherWeightGrad };
 
+constexpr double kPackMinMacs = 536870912.0;  // 2^29 multiply-adds: the copy costs a few us
+
 int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                    int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
                    int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows,
@@ -348,6 +350,44 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
     if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
 
+    // Operands whose rows are not 16-byte aligned whole float4s would be
+    // staged with 4-byte loads (4x the load instructions).  For large single
+    // problems they are first copied into zero-padded aligned rows (C4
+    // 4097x1023x777: 95 us with 4-byte staging, the GEMM alone 75 us with
+    // 16-byte staging); the padding adds exact zeros past K, which the 4-byte
+    // path stages as well, so the result is the same.
+    Lease pack_a(ctx), pack_b(ctx);
+    bool a_packed = false, b_packed = false;  // rows padded with zeros to whole float4s
+    if (!conv && batch == 1 && k > 0 && (double)m * n * k >= kPackMinMacs) {
+        const bool a_vec = aligned16(a) && lda % 4 == 0 && a_row % 4 == 0;
+        const bool b_vec = aligned16(b) && ldb % 4 == 0 && b_row % 4 == 0;
+        auto pack = [&](Lease &l, const float *&src, int64_t &ld, int64_t rows, int64_t cols, bool &packed) -> int {
+            const int64_t ld_dst = (cols + 3) & ~(int64_t)3;
+            if ((rows - 1) * ld_dst + ld_dst > kLimit) return ZN_OK;  // stays on the 4-byte path
+            int rc2 = l.get((size_t)(rows * ld_dst));
+            if (rc2) return rc2;
+            ZnPackArgs pa;
+            pa.src = src;
+            pa.dst = l.ptr;
+            pa.rows = rows;
+            pa.cols = cols;
+            pa.ld_src = ld;
+            pa.ld_dst = ld_dst;
+            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+            if ((rc2 = select_device(ctx)) ||
+                (rc2 = launch(ctx, ctx->elt[kPack], (unsigned)std::min<int64_t>(cdiv(rows * ld_dst / 4, 256), cap), 1,
+                              256, &pa)))
+                return rc2;
+            src = l.ptr;
+            ld = ld_dst;
+            packed = true;
+            return ZN_OK;
+        };
+        int rcp;
+        if (!a_vec && (rcp = pack(pack_a, a, lda, a_outer, a_row, a_packed))) return rcp;
+        if (!b_vec && (rcp = pack(pack_b, b, ldb, b_outer, b_row, b_packed))) return rcp;
+    }
+
     ZnGemmArgs args;
     std::memset(&args, 0, sizeof(args));
     args.a = a;
@@ -372,7 +412,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // 16-byte staging: aligned rows and contiguous extents that are whole float4s
     const bool vec = conv ? (aligned16(a) && lda % 4 == 0 && stride_a % 4 == 0 && a_row % 4 == 0)
                           : (aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0 && stride_a % 4 == 0 &&
-                             stride_b % 4 == 0 && a_row % 4 == 0 && b_row % 4 == 0);
+                             stride_b % 4 == 0 && (a_row % 4 == 0 || a_packed) && (b_row % 4 == 0 || b_packed));
     args.vec_c = aligned16(c) && ldc % 4 == 0 && stride_c % 4 == 0;
     // Plain row-major tile order: on MI355X it gave the lowest L2-miss traffic
     // for multi-round problems (8192^3 NN: 5.6 GB fetched per launch against

@@ -108,6 +108,14 @@ struct ZnIm2colArgs {
     int32_t k_order;
 };
 
+// Row packing: dst[r][c] = c < cols ? src[r * ld_src + c] : 0 for
+// c < ld_dst (a multiple of 4, dst 16-byte aligned).
+struct ZnPackArgs {
+    const float *src;
+    float *dst;
+    int64_t rows, cols, ld_src, ld_dst;
+};
+
 // Weight regroup for the transposed-convolution input gradient:
 // out[ic][t*OC + oc] = in[oc][t*C + ic] for t < taps_per_channel (kH*kW).
 struct ZnRegroupArgs {
