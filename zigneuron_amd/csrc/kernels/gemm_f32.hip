@@ -379,9 +379,13 @@ struct ConvWGatherStage {
 // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
 // holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
 // stores its raw partial sums to the workspace instead.
-template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
-__device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
-                                           int m0, int n0, int wm0, int wn0, int lane, int slice) {
+// The activation is a template argument: one copy of the element loop per
+// activation, entered once, keeps the executed code of a launch short (the
+// instruction cache is cold for most small launches: alternating two small
+// GEMM kernels cost 1.6 us per launch more than repeating one).
+template <int BM, int BN, int WM, int WN, bool AK, bool BKC, int ACT>
+__device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+                                               int m0, int n0, int wm0, int wn0, int lane, int slice) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
     const int64_t bz = blockIdx.y;
     float *gc = p.c + bz * p.stride_c;
@@ -389,7 +393,6 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
     if (split) gc = p.ws + ((int64_t)bz * p.splits + slice) * (int64_t)p.m * p.n;
     const int64_t ldc = split ? (int64_t)p.n : p.ldc;
     const bool accumulate = !split && p.accumulate;
-    const int act = split ? 0 : p.act;
     const int j = lane & 31;
     const int h = lane >> 5;
     const bool has_bias = !split && p.bias != nullptr;
@@ -423,7 +426,7 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
                         float x = acc[fm][fn][r];
                         if (accumulate) x = v[fn] + x;
                         if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
-                        v[fn] = zn_activate(x, act);
+                        v[fn] = zn_activate(x, ACT);
                     }
                     *dst = v;
                     continue;
@@ -437,10 +440,21 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
                     float x = acc[fm][fn][r];
                     if (accumulate) x = crow[col] + x;
                     if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
-                    crow[col] = zn_activate(x, act);
+                    crow[col] = zn_activate(x, ACT);
                 }
             }
         }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
+__device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+                                           int m0, int n0, int wm0, int wn0, int lane, int slice) {
+    switch (p.splits > 1 ? 0 : p.act) {  // split-K slices store raw partial sums
+    case 1: store_tile_act<BM, BN, WM, WN, AK, BKC, 1>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
+    case 2: store_tile_act<BM, BN, WM, WN, AK, BKC, 2>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
+    case 3: store_tile_act<BM, BN, WM, WN, AK, BKC, 3>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
+    default: store_tile_act<BM, BN, WM, WN, AK, BKC, 0>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
     }
 }
 
