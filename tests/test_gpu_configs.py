@@ -205,7 +205,8 @@ def test_c5_im2col_conv_gemm(ctx):
 
 
 @pytest.mark.parametrize("act", ["linear", "relu", "sigmoid", "tanh"])
-@pytest.mark.parametrize("shape", [(256, 784, 128), (33, 17, 5), (4096, 1024, 1024), (1, 9, 300)])
+@pytest.mark.parametrize("shape", [(256, 784, 128), (33, 17, 5), (4096, 1024, 1024), (1, 9, 300), (96, 200, 2048),
+                                   (2048, 64, 12)])
 def test_dense_backward_fused(ctx, act, shape):
     """zn_hip_dense_backward against the reference's four steps: the
     activation derivative bit-exact, grad_bias (+= onto a non-zero start)

@@ -143,9 +143,11 @@ struct ConvGatherStage {
 // (slice, tile) pairs are numbered slice-major and each XCD takes a
 // contiguous run of them, so the tiles of one K slice, which read the same
 // rows of A and B, share one L2 instead of fetching them once per XCD.
-__device__ __forceinline__ void tile_coords(const ZnGemmArgs &p, int &tm, int &tn, int &slice) {
-    int pid = blockIdx.x;
-    slice = blockIdx.z;
+// `wg` >= 0 (a grouped launch) is this workgroup's index within its problem,
+// which is unsplit.
+__device__ __forceinline__ void tile_coords(const ZnGemmArgs &p, int &tm, int &tn, int &slice, int wg = -1) {
+    int pid = wg >= 0 ? wg : (int)blockIdx.x;
+    slice = wg >= 0 ? 0 : (int)blockIdx.z;
     const int ntiles = p.tiles_m * p.tiles_n;
     if (p.xcd_remap == 1) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
     if (p.xcd_remap == 2) {
@@ -379,10 +381,13 @@ struct ConvWGatherStage {
 // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
 // holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
 // stores its raw partial sums to the workspace instead.
-// The activation is a template argument: one copy of the element loop per
-// activation, entered once, keeps the executed code of a launch short (the
-// instruction cache is cold for most small launches: alternating two small
-// GEMM kernels cost 1.6 us per launch more than repeating one).
+// ACT >= 0: the activation is a template argument, one copy of the element
+// loop per activation, entered once.  That keeps the executed code of a
+// launch short for the small tiles (the instruction cache is cold for most
+// small launches: alternating two small GEMM kernels cost 1.6 us per launch
+// more than repeating one).  ACT = -1 reads it at run time; the 128x128 and
+// 256x128 tiles keep that form (the specialised copies made the 8192^3 main
+// loop 0.9-1.3% slower in NN and NT).
 template <int BM, int BN, int WM, int WN, bool AK, bool BKC, int ACT>
 __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
                                                int m0, int n0, int wm0, int wn0, int lane, int slice) {
@@ -393,6 +398,7 @@ __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32
     if (split) gc = p.ws + ((int64_t)bz * p.splits + slice) * (int64_t)p.m * p.n;
     const int64_t ldc = split ? (int64_t)p.n : p.ldc;
     const bool accumulate = !split && p.accumulate;
+    const int act = ACT >= 0 ? ACT : (split ? 0 : p.act);
     const int j = lane & 31;
     const int h = lane >> 5;
     const bool has_bias = !split && p.bias != nullptr;
@@ -426,7 +432,7 @@ __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32
                         float x = acc[fm][fn][r];
                         if (accumulate) x = v[fn] + x;
                         if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
-                        v[fn] = zn_activate(x, ACT);
+                        v[fn] = zn_activate(x, act);
                     }
                     *dst = v;
                     continue;
@@ -440,7 +446,7 @@ __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32
                     float x = acc[fm][fn][r];
                     if (accumulate) x = crow[col] + x;
                     if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
-                    crow[col] = zn_activate(x, ACT);
+                    crow[col] = zn_activate(x, act);
                 }
             }
         }
@@ -450,6 +456,10 @@ __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32
 template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
 __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
                                            int m0, int n0, int wm0, int wn0, int lane, int slice) {
+    if constexpr (BM * BN >= 128 * 128) {
+        store_tile_act<BM, BN, WM, WN, AK, BKC, -1>(p, acc, m0, n0, wm0, wn0, lane, slice);
+        return;
+    }
     switch (p.splits > 1 ? 0 : p.act) {  // split-K slices store raw partial sums
     case 1: store_tile_act<BM, BN, WM, WN, AK, BKC, 1>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
     case 2: store_tile_act<BM, BN, WM, WN, AK, BKC, 2>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
@@ -465,7 +475,7 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
 // kt + 1, then computes slice kt while that load is in flight.
 template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, bool CONV, int GW = 4,
           bool CONVT = false, bool CONVW = false>
-__device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
+__device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -486,9 +496,9 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
     int tm, tn, slice;
-    tile_coords(p, tm, tn, slice);
+    tile_coords(p, tm, tn, slice, wg);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int64_t bz = blockIdx.y;
+    const int64_t bz = blockIdx.y;  // 0 in grouped launches
     const float *ga = p.a + bz * p.stride_a;
     const float *gb = p.b + bz * p.stride_b;
 
@@ -665,13 +675,12 @@ ZN_CONVW_TILE(s, 32, 32, 32, 1, 1, 1)
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not
 // depend on scheduling.  Grid-stride over batch * m * n (float4 along n when
 // n, ldc and C allow it).
-extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs p) {
+__device__ __forceinline__ void splitk_reduce_body(const ZnReduceArgs &p, int64_t block, int64_t blocks) {
     const int64_t mn = (int64_t)p.m * p.n;
     const int vw = p.vec ? 4 : 1;
     const int64_t per_problem = mn / vw;
     const int64_t total = per_problem * p.batch;
-    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
-         t += (int64_t)gridDim.x * blockDim.x) {
+    for (int64_t t = block * 256 + threadIdx.x; t < total; t += blocks * 256) {
         const int64_t b = t / per_problem;
         const int64_t e = (t - b * per_problem) * vw;  // element index within the problem
         const int64_t row = e / p.n, col = e - row * p.n;
@@ -698,3 +707,23 @@ extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs 
         }
     }
 }
+
+extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs p) {
+    splitk_reduce_body(p, blockIdx.x, gridDim.x);
+}
+
+// Dense backward GEMMs in one launch (ZnDenseBwdArgs): grad_input = gaa . W^T
+// (NT), grad_weights = input^T . gaa (TN), and the bias reduce.  _v: both
+// GEMMs stage with 16-byte loads.
+#define ZN_DENSE_BWD_KERNEL(SUFFIX, W)                                                              \
+    extern "C" __global__ __launch_bounds__(256, 1) void zn_dense_bwd_m##SUFFIX(ZnDenseBwdArgs p) { \
+        const int b = blockIdx.x;                                                                    \
+        if (b < p.wg_nt)                                                                             \
+            gemm_tile_dma<64, 64, 32, 2, 2, true, true, W, W, false>(p.nt, b);                      \
+        else if (b < p.wg_nt + p.wg_tn)                                                              \
+            gemm_tile_dma<64, 64, 32, 2, 2, false, false, W, W, false>(p.tn, b - p.wg_nt);          \
+        else                                                                                         \
+            splitk_reduce_body(p.bias, b - p.wg_nt - p.wg_tn, p.wg_bias);                           \
+    }
+ZN_DENSE_BWD_KERNEL(_v, 16)
+ZN_DENSE_BWD_KERNEL(, 4)

@@ -72,6 +72,7 @@ struct zn_ctx {
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
+    hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -655,7 +656,9 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             if (hipModuleGetFunction(&ctx->convw[t][v], ctx->gemm_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
         }
-    if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess)
+    if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess ||
+        hipModuleGetFunction(&ctx->dense_bwd[0], ctx->gemm_module, "zn_dense_bwd_m") != hipSuccess ||
+        hipModuleGetFunction(&ctx->dense_bwd[1], ctx->gemm_module, "zn_dense_bwd_m_v") != hipSuccess)
         return bail(ZN_ERR_SYMBOL);
     for (int i = 0; i < kNumElt; ++i)
         if (hipModuleGetFunction(&ctx->elt[i], ctx->elt_module, kEltName[i]) != hipSuccess) return bail(ZN_ERR_SYMBOL);
@@ -1097,6 +1100,50 @@ int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *w
 }
 
 // ------------------------------------------------------- Dense backward
+// One unsplit 64x64-tile GEMM of a grouped launch.
+static ZnGemmArgs grouped_gemm_args(const float *a, int64_t lda, const float *b, int64_t ldb, float *c, int64_t ldc,
+                                    int64_t m, int64_t n, int64_t k) {
+    ZnGemmArgs g;
+    std::memset(&g, 0, sizeof(g));
+    g.a = a;
+    g.b = b;
+    g.c = c;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc = ldc;
+    g.m = (int32_t)m;
+    g.n = (int32_t)n;
+    g.k = (int32_t)k;
+    g.tiles_m = (int32_t)cdiv(m, 64);
+    g.tiles_n = (int32_t)cdiv(n, 64);
+    g.act = ZN_ACT_LINEAR;
+    g.vec_c = aligned16(c) && ldc % 4 == 0;
+    g.group_m = 1;
+    g.splits = 1;
+    g.k_chunk = (int32_t)k;
+    return g;
+}
+
+// zn_dense_bwd_m[_v]: grad_input = gaa . W^T (NT, skipped when null),
+// grad_weights = input^T . gaa (TN) and grad_bias += the ordered sum of the
+// prologue's partials (r), in one launch.
+static int dense_backward_grouped(zn_ctx *ctx, const float *input, const float *weights, const float *gaa,
+                                  float *grad_input, float *grad_weights, const ZnReduceArgs &r, int bias_blocks,
+                                  int64_t batch, int64_t in_size, int64_t out_size, int wg_nt, int wg_tn) {
+    ZnDenseBwdArgs d;
+    std::memset(&d, 0, sizeof(d));
+    if (grad_input) d.nt = grouped_gemm_args(gaa, out_size, weights, out_size, grad_input, in_size, batch, in_size, out_size);
+    d.tn = grouped_gemm_args(input, in_size, gaa, out_size, grad_weights, out_size, in_size, out_size, batch);
+    d.bias = r;
+    d.wg_nt = wg_nt;
+    d.wg_tn = wg_tn;
+    d.wg_bias = bias_blocks;
+    // 16-byte staging when every staged row is a whole number of aligned float4s
+    const bool vec_tn = aligned16(input) && aligned16(gaa) && in_size % 4 == 0 && out_size % 4 == 0;
+    const bool vec_nt = !grad_input || (aligned16(weights) && out_size % 4 == 0);
+    return launch(ctx, ctx->dense_bwd[vec_tn && vec_nt ? 1 : 0], (unsigned)(wg_nt + wg_tn + bias_blocks), 1, 256, &d);
+}
+
 // Dense.backward (src/layer.zig:411-475) on device pointers:
 //   gaa = activationBackward(act, y, grad_output)  and  grad_bias += sum_rows gaa
 // in one pass (zn_dense_grad_prologue: per-split column sums, then the
@@ -1148,6 +1195,14 @@ int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float 
         r.act = ZN_ACT_LINEAR;
         r.vec = (out_size % 4 == 0 && aligned16(grad_bias) && aligned16(part.ptr)) ? 1 : 0;
         const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(cdiv(out_size / (r.vec ? 4 : 1), 256), 8 * cus));
+        // Small layers: grad_input, grad_weights and the bias reduce in one
+        // launch (64x64 tiles, unsplit; C2's layers: 5 launches -> 2).
+        const int64_t wg_nt = grad_input ? cdiv(batch, 64) * cdiv(in_size, 64) : 0;
+        const int64_t wg_tn = cdiv(in_size, 64) * cdiv(out_size, 64);
+        if (in_size > 0 && wg_nt + wg_tn <= 2 * cus && batch <= 2048 && out_size <= 2048 && ctx->forced_tile < 0 &&
+            ctx->forced_splits == 0 && in_size <= INT_MAX / 4 / std::max<int64_t>(batch, out_size))
+            return dense_backward_grouped(ctx, input, weights, grad_after_act, grad_input, grad_weights, r,
+                                          (int)blocks, batch, in_size, out_size, (int)wg_nt, (int)wg_tn);
         if ((rc = launch(ctx, ctx->splitk_reduce, (unsigned)blocks, 1, 256, &r))) return rc;
     }
     if (in_size == 0) return ZN_OK;

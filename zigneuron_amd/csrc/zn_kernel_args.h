@@ -63,6 +63,17 @@ struct ZnReduceArgs {
     int32_t bias_rows;
 };
 
+// The GEMMs of one Dense backward in one launch (after the prologue that
+// wrote grad_after_act and the bias partial sums): workgroups [0, wg_nt)
+// compute grad_input (NT), the next wg_tn grad_weights (TN), the last wg_bias
+// reduce the bias partial sums.  Both GEMMs use the 64x64 tile, unsplit.
+struct ZnDenseBwdArgs {
+    ZnGemmArgs nt;
+    ZnGemmArgs tn;
+    ZnReduceArgs bias;
+    int32_t wg_nt, wg_tn, wg_bias;
+};
+
 // Elementwise helpers (fill, copy, bias, activations, bias gradient, row
 // softmax).
 struct ZnEltArgs {
