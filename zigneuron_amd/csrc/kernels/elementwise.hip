@@ -307,6 +307,34 @@ extern "C" __global__ __launch_bounds__(256) void zn_pack_rows(ZnPackArgs p) {
     }
 }
 
+// NCHW -> NHWC for the convolution forward's 4-channel gather: 32x32 tiles
+// through LDS, read along pixels and written along channels (both
+// coalesced).  A permutation (bit-exact).  Grid-stride over (image, tile).
+extern "C" __global__ __launch_bounds__(256) void zn_nchw_to_nhwc(ZnTransposeArgs p) {
+    __shared__ float tile[32][33];
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    const int64_t tc = (p.channels + 31) / 32, tp = (p.pixels + 31) / 32;
+    const int64_t per_image = tc * tp, total = per_image * p.batch;
+    for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+        const int64_t b = t / per_image, r = t - b * per_image;
+        const int64_t c0 = (r / tp) * 32, p0 = (r % tp) * 32;
+        const float *src = p.src + b * p.channels * p.pixels;
+        float *dst = p.dst + b * p.channels * p.pixels;
+        __syncthreads();  // the previous tile's reads of `tile` are done
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t c = c0 + ty + 8 * i, q = p0 + tx;
+            if (c < p.channels && q < p.pixels) tile[ty + 8 * i][tx] = src[c * p.pixels + q];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t q = p0 + ty + 8 * i, c = c0 + tx;
+            if (c < p.channels && q < p.pixels) dst[q * p.channels + c] = tile[tx][ty + 8 * i];
+        }
+    }
+}
+
 // W' for the stride-1 transposed-convolution GEMM of the input gradient
 // (cpuConv2dBackwardIm2col's grad_col = go2 . W followed by col2im, src/
 // backend.zig:3995-4060, as one GEMM): the [OC][kH*kW][C] weights regrouped

@@ -35,6 +35,16 @@
 
 namespace {
 
+// Where the B operand of a GEMM comes from (gemm_tile_dma's G):
+enum ZnGather {
+    kGNone = 0,        // a plain matrix
+    kGIm2col = 1,      // implicit im2col of an NCHW batch, element gather (ConvGatherStage)
+    kGIm2col4 = 2,     // the same, 4-pixel 16-byte gather (ConvGather16Stage)
+    kGTransposed = 3,  // transposed convolution of grad_output rows (ConvTGatherStage)
+    kGWeight = 4,      // col of a weight gradient (ConvWGatherStage)
+    kGNhwc = 5,        // implicit im2col of an NHWC batch, 4-channel 16-byte gather (ConvNhwcGatherStage)
+};
+
 __device__ __forceinline__ float zn_activate(float v, int act) {
     switch (act) {
     case 1: return v > 0.0f ? v : 0.0f;               // relu   (src/backend.zig:239-240)
@@ -377,6 +387,82 @@ struct ConvWGatherStage {
     }
 };
 
+// The implicit im2col operand of an NHWC image batch: B[n][k] with n = output
+// pixel (oh, ow) and k = (kh*k_w + kw)*C + ic (the im2col K order) is
+// image[(oh*stride_h - pad_h + kh, ow*stride_w - pad_w + kw)][ic].  The
+// operand is K-contiguous (stored [BN][BK], swizzled like DmaStage): a 16-byte
+// chunk is 4 consecutive channels of one pixel (C % 4 == 0), so it is either
+// wholly inside the image or wholly padding (zeros), at any stride.
+// ZnConvGeom as in the forward: channels = C, in_h x in_w, out_w decodes n,
+// div1 = C, k_w.
+template <int BN, int BK, int NT>
+struct ConvNhwcGatherStage {
+    typedef DmaStage<BN, BK, NT, true, 16> Layout;
+    static constexpr int kPerWave = Layout::kPerWave;
+    static constexpr int kWaves = NT / kWave;
+
+    // A lane's output pixel and chunk column are fixed for the whole tile:
+    // decoded once.  ih0/iw0: the pixel's top-left input tap (ih0 = kNoRow
+    // for a pixel past the problem, so no tap is ever inside the image).
+    struct Lane {
+        int ih0[kPerWave], iw0[kPerWave];
+        int kc[kPerWave];  // first k of the chunk, relative to k0
+    };
+    static constexpr int kNoRow = -(1 << 30);
+
+    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int wave, int lane) {
+        Lane l;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int pos = (j * kWaves + wave) * Layout::kPerInst + 4 * lane;
+            const int row = pos / BK;
+            const int n = n0 + row;
+            const int oh = zn_udiv(n, g.ow_mul, g.ow_shift), ow = n - oh * g.out_w;
+            l.ih0[j] = n < nmax ? oh * g.stride_h - g.pad_h : kNoRow;
+            l.iw0[j] = ow * g.stride_w - g.pad_w;
+            l.kc[j] = 4 * (((pos % BK) / 4) ^ Layout::swz(row));
+        }
+        return l;
+    }
+
+    // tap_uniform (C % BK == 0): the slice [k0, k0 + BK) lies in one filter
+    // tap, decoded once per slice on the scalar unit.
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
+                                                 const Lane &ln, int k0, int kmax, int wave, int lane) {
+        int kh_u = 0, kw_u = 0, ic_u = 0;
+        if (g.tap_uniform) {
+            const int khw = zn_udiv(k0, g.div1_mul, g.div1_shift);
+            ic_u = k0 - khw * g.div1;
+            kh_u = zn_udiv(khw, g.kw_mul, g.kw_shift);
+            kw_u = khw - kh_u * g.k_w;
+        }
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int p0 = (j * kWaves + wave) * Layout::kPerInst;
+            const int k = k0 + ln.kc[j];
+            int kh, kw, ic;
+            if (g.tap_uniform) {
+                kh = kh_u;
+                kw = kw_u;
+                ic = ic_u + ln.kc[j];
+            } else {
+                const int khw = zn_udiv(k, g.div1_mul, g.div1_shift);
+                ic = k - khw * g.div1;
+                kh = zn_udiv(khw, g.kw_mul, g.kw_shift);
+                kw = khw - kh * g.k_w;
+            }
+            const int ih = ln.ih0[j] + kh, iw = ln.iw0[j] + kw;
+            const bool ok = k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
+            const uint32_t off = ok ? (uint32_t)((ih * g.in_w + iw) * g.channels + ic) * 4u : kOutOfRange;
+            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                         :
+                         : "s"(lds_addr), "v"(off), "s"(rsrc)
+                         : "memory");
+        }
+    }
+};
+
 // Epilogue of one macro tile: v = acc (+ C) (+ bias) -> act -> store.
 // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
 // holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
@@ -469,26 +555,30 @@ __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 
 }
 
 // The GEMM main loop: two LDS stages filled by DMA (WA/WB = 16: 16-byte
-// loads for aligned operands, 4: 4-byte loads otherwise; CONV gathers B from
-// an NCHW image).  Iteration kt waits
+// loads for aligned operands, 4: 4-byte loads otherwise; G != kGNone gathers
+// B, ZnGather).  Iteration kt waits
 // for its stage (vmcnt(0) + barrier), refills the other stage with slice
 // kt + 1, then computes slice kt while that load is in flight.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, bool CONV, int GW = 4,
-          bool CONVT = false, bool CONVW = false>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, int G = kGNone>
 __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) {
+    constexpr bool CONV = G == kGIm2col || G == kGIm2col4;
+    constexpr int GW = G == kGIm2col4 ? 16 : 4;
+    constexpr bool CONVT = G == kGTransposed, CONVW = G == kGWeight, NHWC = G == kGNhwc;
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
     static_assert(!CONV || (!BKC && WB == 4), "the convolution operand is X-contiguous and gathered");
-    static_assert(!CONVT || (BKC && WB == 16 && !CONV), "the transposed-convolution operand is K-contiguous");
-    static_assert(!CONVW || (BKC && WB == 16 && !CONV && !CONVT), "the weight-gradient operand is K-contiguous");
+    static_assert(!CONVT || (BKC && WB == 16), "the transposed-convolution operand is K-contiguous");
+    static_assert(!CONVW || (BKC && WB == 16), "the weight-gradient operand is K-contiguous");
+    static_assert(!NHWC || (BKC && WB == 16), "the NHWC im2col operand is K-contiguous");
     typedef DmaStage<BM, BK, NT, AK, WA> SA;
     typedef DmaStage<BN, BK, NT, BKC, WB> SB;
     typedef ConvGatherStage<BN, BK, NT> SC;
     typedef ConvGather16Stage<BN, BK, NT> SC16;
     typedef ConvTGatherStage<BN, BK, NT> ST;
     typedef ConvWGatherStage<BN, BK, NT> SW;
+    typedef ConvNhwcGatherStage<BN, BK, NT> SN;
     __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
@@ -520,7 +610,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
     const uint32_t b_bytes =
         CONVW ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
-        : (CONV || CONVT) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+        : (CONV || CONVT || NHWC) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
              : (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
@@ -535,8 +625,12 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
     typename SW::Patch wpatch;
     wpatch.mask = 0;
     if constexpr (CONVW) clw = SW::lane_setup(p.conv, n0, p.n, wave, lane);
+    typename SN::Lane cln{};
+    if constexpr (NHWC) cln = SN::lane_setup(p.conv, n0, p.n, wave, lane);
     auto issue_b = [&](float *lds, int k0) {
-        if constexpr (CONVW)
+        if constexpr (NHWC)
+            SN::issue(rb, lds, p.conv, cln, k0, kend, wave, lane);
+        else if constexpr (CONVW)
             SW::issue(rb, gb, lds, p.conv, clw, k0, kend, wave, lane, wpatch);
         else if constexpr (CONVT)
             ST::issue(rb, lds, p.conv, n0, k0, p.n, kend, wave, lane);
@@ -595,7 +689,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
 // 4-byte loads straight into LDS.
 #define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                            \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void NAME(ZnGemmArgs p) {        \
-        gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC, (VEC) ? 16 : 4, (VEC) ? 16 : 4, false>(p);    \
+        gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC, (VEC) ? 16 : 4, (VEC) ? 16 : 4>(p);           \
     }
 
 #define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, VEC, SUFFIX)                            \
@@ -618,15 +712,15 @@ ZN_GEMM_TILE(s, 32, 32, 32, 1, 1, 1)
 // whose B operand is gathered from the NCHW input (ZnConvGeom).  _v: W rows
 // are 16-byte aligned; _g: the input is gathered in chunks of 4 pixels with
 // 16-byte loads (stride_w == 1, out_w % 4 == 0), otherwise element by element.
-#define ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, GW, SUFFIX)                            \
+#define ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, G, SUFFIX)                             \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_conv_nn_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, true, false, WA, 4, true, GW>(p);                      \
+        gemm_tile_dma<BM, BN, BK, WM, WN, true, false, WA, 4, G>(p);                              \
     }
 #define ZN_CONV_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, 4, _v)                                    \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, 4, )                                       \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, 16, _v_g)                                 \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, 16, _g)
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, kGIm2col, _v)                             \
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, kGIm2col, )                                \
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, kGIm2col4, _v_g)                          \
+    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, kGIm2col4, _g)
 
 ZN_CONV_TILE(x, 256, 128, 16, 4, 2, 1)
 ZN_CONV_TILE(l, 128, 128, 16, 2, 2, 4)
@@ -640,7 +734,7 @@ ZN_CONV_TILE(s, 32, 32, 32, 1, 1, 1)
 // (ConvTGatherStage).  _v: W' rows are 16-byte aligned.
 #define ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convt_nt_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, true, true, WA, 16, false, 4, true>(p);                \
+        gemm_tile_dma<BM, BN, BK, WM, WN, true, true, WA, 16, kGTransposed>(p);                  \
     }
 #define ZN_CONVT_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
     ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
@@ -659,7 +753,7 @@ ZN_CONVT_TILE(s, 32, 32, 32, 1, 1, 1)
 // and grad_output 16-byte aligned.
 #define ZN_CONVW_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convw_tn_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, false, true, WA, 16, false, 4, false, true>(p);        \
+        gemm_tile_dma<BM, BN, BK, WM, WN, false, true, WA, 16, kGWeight>(p);                     \
     }
 #define ZN_CONVW_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
     ZN_CONVW_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
@@ -670,6 +764,24 @@ ZN_CONVW_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_CONVW_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_CONVW_TILE(m, 64, 64, 32, 2, 2, 1)
 ZN_CONVW_TILE(s, 32, 32, 32, 1, 1, 1)
+
+// Convolution forward on an NHWC copy of the input, per image b = blockIdx.y:
+// out_b[OC][OH*OW] = W[OC][K] . B^T (+ bias[oc]), NT, W in the im2col K order
+// and B gathered 4 channels at a time (ConvNhwcGatherStage, C % 4 == 0, any
+// stride).  _v: W rows are 16-byte aligned.
+#define ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convf_nt_##TILE##SUFFIX(ZnGemmArgs p) { \
+        gemm_tile_dma<BM, BN, BK, WM, WN, true, true, WA, 16, kGNhwc>(p);                        \
+    }
+#define ZN_CONVF_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
+    ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
+    ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+
+ZN_CONVF_TILE(x, 256, 128, 16, 4, 2, 1)
+ZN_CONVF_TILE(l, 128, 128, 16, 2, 2, 4)
+ZN_CONVF_TILE(n, 128, 64, 16, 2, 1, 1)
+ZN_CONVF_TILE(m, 64, 64, 32, 2, 2, 1)
+ZN_CONVF_TILE(s, 32, 32, 32, 1, 1, 1)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not
@@ -719,9 +831,9 @@ extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs 
     extern "C" __global__ __launch_bounds__(256, 1) void zn_dense_bwd_m##SUFFIX(ZnDenseBwdArgs p) { \
         const int b = blockIdx.x;                                                                    \
         if (b < p.wg_nt)                                                                             \
-            gemm_tile_dma<64, 64, 32, 2, 2, true, true, W, W, false>(p.nt, b);                      \
+            gemm_tile_dma<64, 64, 32, 2, 2, true, true, W, W>(p.nt, b);                             \
         else if (b < p.wg_nt + p.wg_tn)                                                              \
-            gemm_tile_dma<64, 64, 32, 2, 2, false, false, W, W, false>(p.tn, b - p.wg_nt);          \
+            gemm_tile_dma<64, 64, 32, 2, 2, false, false, W, W>(p.tn, b - p.wg_nt);                 \
         else                                                                                         \
             splitk_reduce_body(p.bias, b - p.wg_nt - p.wg_tn, p.wg_bias);                           \
     }

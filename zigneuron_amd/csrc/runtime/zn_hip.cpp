@@ -45,12 +45,12 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
                                          {32, 32, 32, 64, "s"}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kPack, kNumElt };
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kPack, kToNhwc, kNumElt };
 constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", "zn_add_bias",
                                            "zn_activation_forward", "zn_activation_backward",
                                            "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows",
                                            "zn_col2im",          "zn_row_sum",  "zn_dense_grad_prologue",
-                                           "zn_weight_regroup", "zn_pack_rows"};
+                                           "zn_weight_regroup", "zn_pack_rows", "zn_nchw_to_nhwc"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
@@ -73,6 +73,7 @@ struct zn_ctx {
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
     hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
+    hipFunction_t convf[kNumTiles][2] = {};    // convolution forward on NHWC [tile][16-byte W rows]
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -305,8 +306,11 @@ void udiv_magic(uint32_t d, uint32_t &mul, uint32_t &shift) {
 //                     N = in pixels;
 //  kGatherWeightGrad: the col operand of a weight gradient (B[k][n] =
 //                     col[pixel][tap] over conv->images images, K-contiguous
-//                     4-pixel chunks), TN with M = out channels, N = taps.
-enum GatherMode { kGatherIm2col, kGatherTransposed, kGatherWeightGrad };
+//                     4-pixel chunks), TN with M = out channels, N = taps;
+//  kGatherNhwc:       the implicit im2col operand of an NHWC image batch
+//                     (B[n][k], K-contiguous 4-channel chunks), NT with
+//                     M = out channels, N = out pixels.
+enum GatherMode { kGatherIm2col, kGatherTransposed, kGatherWeightGrad, kGatherNhwc };
 
 constexpr double kPackMinMacs = 536870912.0;  // 2^29 multiply-adds: the copy costs a few us
 
@@ -336,17 +340,21 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     const int64_t b_extent =
         conv ? images * conv->channels * conv->in_h * conv->in_w : (b_outer - 1) * ldb + b_row;
     if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || b_extent > kLimit)) return ZN_ERR_OVERFLOW;
-    constexpr int kGatherLayout[3] = {ZN_LAYOUT_NN, ZN_LAYOUT_NT, ZN_LAYOUT_TN};
+    constexpr int kGatherLayout[4] = {ZN_LAYOUT_NN, ZN_LAYOUT_NT, ZN_LAYOUT_TN, ZN_LAYOUT_NT};
     if (conv && layout != kGatherLayout[mode]) return ZN_ERR_INVALID_ARG;
-    if (conv && mode == kGatherTransposed &&
+    if (conv && (mode == kGatherTransposed || mode == kGatherNhwc) &&
         (k % 4 != 0 || conv->channels % 4 != 0 || !aligned16(b) || stride_b % 4 != 0))
-        return ZN_ERR_INVALID_ARG;  // whole 16-byte chunks of grad_output rows
+        return ZN_ERR_INVALID_ARG;  // whole 16-byte chunks of 4 channels
     if (conv && mode == kGatherWeightGrad &&
         (conv->stride_w != 1 || conv->out_w % 4 != 0 || conv->k_order != 0 || batch != 1 ||
          k != images * conv->out_h * conv->out_w))
         return ZN_ERR_INVALID_ARG;  // whole 4-pixel chunks of one output row, over all images
 
-    const Tile tile = ctx->forced_tile >= 0 ? (Tile)ctx->forced_tile : choose_tile(ctx, m, n, k, batch, conv != nullptr);
+    // The NHWC forward gather runs best on 64x64 tiles (C5 forward, rocprofv3 trace: 156 us against 172 us for
+    // 128x128 and 314 us for 256x128).
+    const Tile tile = ctx->forced_tile >= 0                       ? (Tile)ctx->forced_tile
+                      : conv && mode == kGatherNhwc ? kTileM
+                                                                  : choose_tile(ctx, m, n, k, batch, conv != nullptr);
     const TileShape &ts = kTiles[tile];
     const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
     if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
@@ -410,6 +418,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     args.act = act;
     args.bias_rows = bias_rows ? 1 : 0;
     if (conv) args.conv = *conv;
+    // NHWC forward: each BK slice of K lies in one filter tap when the channels are whole slices
+    if (conv && mode == kGatherNhwc) args.conv.tap_uniform = conv->channels % ts.bk == 0 ? 1 : 0;
     // 16-byte staging: aligned rows and contiguous extents that are whole float4s
     const bool vec = conv ? (aligned16(a) && lda % 4 == 0 && stride_a % 4 == 0 && a_row % 4 == 0)
                           : (aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0 && stride_a % 4 == 0 &&
@@ -448,6 +458,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     hipFunction_t f = !conv                     ? ctx->gemm[layout][tile][vec ? 1 : 0]
                       : mode == kGatherTransposed ? ctx->convt[tile][vec ? 1 : 0]
                       : mode == kGatherWeightGrad ? ctx->convw[tile][vec ? 1 : 0]
+                      : mode == kGatherNhwc       ? ctx->convf[tile][vec ? 1 : 0]
                                                   : ctx->conv[tile][vec ? 1 : 0][gather4];
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
@@ -654,6 +665,9 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                 return bail(ZN_ERR_SYMBOL);
             std::snprintf(name, sizeof(name), "zn_convw_tn_%s%s", kTiles[t].suffix, v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->convw[t][v], ctx->gemm_module, name) != hipSuccess)
+                return bail(ZN_ERR_SYMBOL);
+            std::snprintf(name, sizeof(name), "zn_convf_nt_%s%s", kTiles[t].suffix, v ? "_v" : "");
+            if (hipModuleGetFunction(&ctx->convf[t][v], ctx->gemm_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
         }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess ||
@@ -1079,7 +1093,35 @@ static int conv2d_device(zn_ctx *ctx, const float *input, const float *weights, 
     udiv_magic((uint32_t)g.div1, g.div1_mul, g.div1_shift);
     udiv_magic((uint32_t)g.k_w, g.kw_mul, g.kw_shift);
     udiv_magic((uint32_t)g.out_w, g.ow_mul, g.ow_shift);
-    return gemm_launch_ex(ctx, ZN_LAYOUT_NN, oc, hw, kdim, weights, kdim, 0, input, hw, c * h * w, output, hw,
+    const int64_t plane = c * h * w;
+    if (k_order == 0 && c % 4 == 0 && kdim % 4 == 0) {
+        // NHWC copy of the images (in chunks of at most 2^28 floats), then an
+        // NT GEMM gathering 4 channels per 16-byte load: no partial chunks
+        // at the padding, at any stride.
+        const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(batch, ((int64_t)1 << 28) / plane));
+        Lease nhwc(ctx);
+        int rc = nhwc.get((size_t)(chunk * plane));
+        if (rc) return rc;
+        for (int64_t b0 = 0; b0 < batch; b0 += chunk) {
+            const int64_t nb = std::min(chunk, batch - b0);
+            ZnTransposeArgs t;
+            t.src = input + b0 * plane;
+            t.dst = nhwc.ptr;
+            t.batch = nb;
+            t.channels = c;
+            t.pixels = h * w;
+            const int64_t tiles = nb * cdiv(c, 32) * cdiv(h * w, 32);
+            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+            if ((rc = select_device(ctx)) ||
+                (rc = launch(ctx, ctx->elt[kToNhwc], (unsigned)std::min<int64_t>(tiles, cap), 1, 256, &t)) ||
+                (rc = gemm_launch_ex(ctx, ZN_LAYOUT_NT, oc, hw, kdim, weights, kdim, 0, nhwc.ptr, kdim, plane,
+                                     output + b0 * oc * hw, hw, oc * hw, nb, 0, bias, ZN_ACT_LINEAR, 1, &g,
+                                     kGatherNhwc)))
+                return rc;
+        }
+        return ZN_OK;
+    }
+    return gemm_launch_ex(ctx, ZN_LAYOUT_NN, oc, hw, kdim, weights, kdim, 0, input, hw, plane, output, hw,
                           oc * hw, batch, 0, bias, ZN_ACT_LINEAR, 1, &g);
 }
 

@@ -24,6 +24,9 @@ struct ZnConvGeom {
     // out_h and its divisor.
     int32_t out_h, images;
     uint32_t oh_mul, oh_shift;
+    // NHWC forward only: 1 when every K slice lies in one filter tap
+    // (channels a multiple of the tile's BK).
+    int32_t tap_uniform;
 };
 
 // One (possibly batched) fp32 GEMM: C = act((acc ? C : 0) + op(A) op(B) + bias).
@@ -125,6 +128,14 @@ struct ZnPackArgs {
     const float *src;
     float *dst;
     int64_t rows, cols, ld_src, ld_dst;
+};
+
+// Per image b < batch: dst_b[p][c] = src_b[c][p] for c < channels, p < pixels
+// (NCHW -> NHWC).
+struct ZnTransposeArgs {
+    const float *src;
+    float *dst;
+    int64_t batch, channels, pixels;
 };
 
 // Weight regroup for the transposed-convolution input gradient:
