@@ -43,6 +43,7 @@ enum ZnGather {
     kGTransposed = 3,  // transposed convolution of grad_output rows (ConvTGatherStage)
     kGWeight = 4,      // col of a weight gradient (ConvWGatherStage)
     kGNhwc = 5,        // implicit im2col of an NHWC batch, 4-channel 16-byte gather (ConvNhwcGatherStage)
+    kGNhwcW = 6,       // col of a weight gradient from an NHWC batch, X-contiguous (ConvNhwcWGatherStage)
 };
 
 __device__ __forceinline__ float zn_activate(float v, int act) {
@@ -463,6 +464,65 @@ struct ConvNhwcGatherStage {
     }
 };
 
+// The col operand of a weight gradient from an NHWC image batch: B[k][n] =
+// col[k][n] with k = output pixel over `images` images (b*OH*OW + oh*OW +
+// ow) and n = im2col tap (kh*k_w + kw)*C + ic, i.e. image_b[(oh*stride_h -
+// pad_h + kh, ow*stride_w - pad_w + kw)][ic].  X-contiguous (stored
+// [BK][BN] like DmaStage): a 16-byte chunk is 4 consecutive channels of one
+// tap at one pixel (C % 4 == 0), wholly inside the image or wholly padding,
+// at any stride.  A lane's tap is fixed for the tile; its pixel moves with k0.
+template <int BN, int BK, int NT>
+struct ConvNhwcWGatherStage {
+    typedef DmaStage<BN, BK, NT, false, 16> Layout;
+    static constexpr int kPerWave = Layout::kPerWave;
+    static constexpr int kWaves = NT / kWave;
+    static_assert(Layout::kPerInst % BN == 0, "a wave instruction covers whole k rows");
+    static constexpr int kRowsPerInst = Layout::kPerInst / BN;
+    static constexpr int kNoRow = -(1 << 30);
+
+    struct Lane {
+        int dh, dw;   // kh - pad_h (kNoRow past the problem), kw - pad_w
+        int tap_off;  // (kh - pad_h) * W * C + (kw - pad_w) * C + ic
+        int kl;       // k row of this lane within a wave instruction
+    };
+
+    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int lane) {
+        Lane l;
+        const int n = n0 + (4 * lane) % BN;
+        const int khw = zn_udiv(n, g.div1_mul, g.div1_shift);
+        const int ic = n - khw * g.div1;
+        const int kh = zn_udiv(khw, g.kw_mul, g.kw_shift), kw = khw - kh * g.k_w;
+        l.dh = n < nmax ? kh - g.pad_h : kNoRow;
+        l.dw = kw - g.pad_w;
+        l.tap_off = ((kh - g.pad_h) * g.in_w + (kw - g.pad_w)) * g.channels + ic;
+        l.kl = (4 * lane) / BN;
+        return l;
+    }
+
+    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
+                                                 const Lane &ln, int k0, int kmax, int wave) {
+        const int plane = g.channels * g.in_h * g.in_w;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int row = j * kWaves + wave;  // wave-uniform
+            const int p0 = row * Layout::kPerInst;
+            const int k = k0 + row * kRowsPerInst + ln.kl;
+            const int q = zn_udiv(k, g.ow_mul, g.ow_shift), ow = k - q * g.out_w;
+            const int b = zn_udiv(q, g.oh_mul, g.oh_shift), oh = q - b * g.out_h;
+            const int ohs = oh * g.stride_h, ows = ow * g.stride_w;
+            const int ih = ohs + ln.dh, iw = ows + ln.dw;
+            const bool ok = k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
+            const int src = b * plane + (ohs * g.in_w + ows) * g.channels + ln.tap_off;
+            const uint32_t off = ok ? (uint32_t)src * 4u : kOutOfRange;
+            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                         :
+                         : "s"(lds_addr), "v"(off), "s"(rsrc)
+                         : "memory");
+        }
+    }
+};
+
 // Epilogue of one macro tile: v = acc (+ C) (+ bias) -> act -> store.
 // 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
 // holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
@@ -563,7 +623,7 @@ template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int
 __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) {
     constexpr bool CONV = G == kGIm2col || G == kGIm2col4;
     constexpr int GW = G == kGIm2col4 ? 16 : 4;
-    constexpr bool CONVT = G == kGTransposed, CONVW = G == kGWeight, NHWC = G == kGNhwc;
+    constexpr bool CONVT = G == kGTransposed, CONVW = G == kGWeight, NHWC = G == kGNhwc, NHWCW = G == kGNhwcW;
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -572,6 +632,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
     static_assert(!CONVT || (BKC && WB == 16), "the transposed-convolution operand is K-contiguous");
     static_assert(!CONVW || (BKC && WB == 16), "the weight-gradient operand is K-contiguous");
     static_assert(!NHWC || (BKC && WB == 16), "the NHWC im2col operand is K-contiguous");
+    static_assert(!NHWCW || (!BKC && WB == 16), "the NHWC weight-gradient operand is X-contiguous");
     typedef DmaStage<BM, BK, NT, AK, WA> SA;
     typedef DmaStage<BN, BK, NT, BKC, WB> SB;
     typedef ConvGatherStage<BN, BK, NT> SC;
@@ -579,6 +640,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
     typedef ConvTGatherStage<BN, BK, NT> ST;
     typedef ConvWGatherStage<BN, BK, NT> SW;
     typedef ConvNhwcGatherStage<BN, BK, NT> SN;
+    typedef ConvNhwcWGatherStage<BN, BK, NT> SNW;
     __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
@@ -609,7 +671,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
     constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
     const uint32_t b_bytes =
-        CONVW ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+        (CONVW || NHWCW) ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
         : (CONV || CONVT || NHWC) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
              : (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
@@ -627,9 +689,13 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
     if constexpr (CONVW) clw = SW::lane_setup(p.conv, n0, p.n, wave, lane);
     typename SN::Lane cln{};
     if constexpr (NHWC) cln = SN::lane_setup(p.conv, n0, p.n, wave, lane);
+    typename SNW::Lane clnw{};
+    if constexpr (NHWCW) clnw = SNW::lane_setup(p.conv, n0, p.n, lane);
     auto issue_b = [&](float *lds, int k0) {
         if constexpr (NHWC)
             SN::issue(rb, lds, p.conv, cln, k0, kend, wave, lane);
+        else if constexpr (NHWCW)
+            SNW::issue(rb, lds, p.conv, clnw, k0, kend, wave);
         else if constexpr (CONVW)
             SW::issue(rb, gb, lds, p.conv, clw, k0, kend, wave, lane, wpatch);
         else if constexpr (CONVT)
@@ -782,6 +848,24 @@ ZN_CONVF_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_CONVF_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_CONVF_TILE(m, 64, 64, 32, 2, 2, 1)
 ZN_CONVF_TILE(s, 32, 32, 32, 1, 1, 1)
+
+// Weight gradient from an NHWC copy of the input: grad_W[OC][taps] =
+// go2^T . col, TN, K = the output pixels of all images, B gathered 4 channels
+// at a time (ConvNhwcWGatherStage, C % 4 == 0, any stride).  _v: OC % 4 == 0
+// and grad_output 16-byte aligned.
+#define ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                               \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convwn_tn_##TILE##SUFFIX(ZnGemmArgs p) { \
+        gemm_tile_dma<BM, BN, BK, WM, WN, false, false, WA, 16, kGNhwcW>(p);                     \
+    }
+#define ZN_CONVWN_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                             \
+    ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                      \
+    ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+
+ZN_CONVWN_TILE(x, 256, 128, 16, 4, 2, 1)
+ZN_CONVWN_TILE(l, 128, 128, 16, 2, 2, 4)
+ZN_CONVWN_TILE(n, 128, 64, 16, 2, 1, 1)
+ZN_CONVWN_TILE(m, 64, 64, 32, 2, 2, 1)
+ZN_CONVWN_TILE(s, 32, 32, 32, 1, 1, 1)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not

@@ -74,6 +74,7 @@ struct zn_ctx {
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
     hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
     hipFunction_t convf[kNumTiles][2] = {};    // convolution forward on NHWC [tile][16-byte W rows]
+    hipFunction_t convwn[kNumTiles][2] = {};   // weight gradient on NHWC [tile][16-byte grad_output rows]
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -309,8 +310,11 @@ void udiv_magic(uint32_t d, uint32_t &mul, uint32_t &shift) {
 //                     4-pixel chunks), TN with M = out channels, N = taps;
 //  kGatherNhwc:       the implicit im2col operand of an NHWC image batch
 //                     (B[n][k], K-contiguous 4-channel chunks), NT with
-//                     M = out channels, N = out pixels.
-enum GatherMode { kGatherIm2col, kGatherTransposed, kGatherWeightGrad, kGatherNhwc };
+//                     M = out channels, N = out pixels;
+//  kGatherWeightNhwc: the col operand of a weight gradient from an NHWC
+//                     batch (B[k][n], X-contiguous 4-channel chunks), TN like
+//                     kGatherWeightGrad.
+enum GatherMode { kGatherIm2col, kGatherTransposed, kGatherWeightGrad, kGatherNhwc, kGatherWeightNhwc };
 
 constexpr double kPackMinMacs = 536870912.0;  // 2^29 multiply-adds: the copy costs a few us
 
@@ -336,11 +340,12 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     const int64_t a_outer = layout == ZN_LAYOUT_TN ? k : m;
     const int64_t b_outer = layout == ZN_LAYOUT_NT ? n : k;
     const int64_t kLimit = (int64_t)INT_MAX / 4;
-    const int64_t images = conv && mode == kGatherWeightGrad ? conv->images : 1;
+    const bool weight_mode = mode == kGatherWeightGrad || mode == kGatherWeightNhwc;
+    const int64_t images = conv && weight_mode ? conv->images : 1;
     const int64_t b_extent =
         conv ? images * conv->channels * conv->in_h * conv->in_w : (b_outer - 1) * ldb + b_row;
     if (k > 0 && ((a_outer - 1) * lda + a_row > kLimit || b_extent > kLimit)) return ZN_ERR_OVERFLOW;
-    constexpr int kGatherLayout[4] = {ZN_LAYOUT_NN, ZN_LAYOUT_NT, ZN_LAYOUT_TN, ZN_LAYOUT_NT};
+    constexpr int kGatherLayout[5] = {ZN_LAYOUT_NN, ZN_LAYOUT_NT, ZN_LAYOUT_TN, ZN_LAYOUT_NT, ZN_LAYOUT_TN};
     if (conv && layout != kGatherLayout[mode]) return ZN_ERR_INVALID_ARG;
     if (conv && (mode == kGatherTransposed || mode == kGatherNhwc) &&
         (k % 4 != 0 || conv->channels % 4 != 0 || !aligned16(b) || stride_b % 4 != 0))
@@ -349,6 +354,10 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         (conv->stride_w != 1 || conv->out_w % 4 != 0 || conv->k_order != 0 || batch != 1 ||
          k != images * conv->out_h * conv->out_w))
         return ZN_ERR_INVALID_ARG;  // whole 4-pixel chunks of one output row, over all images
+    if (conv && mode == kGatherWeightNhwc &&
+        (conv->channels % 4 != 0 || conv->k_order != 0 || batch != 1 || !aligned16(b) ||
+         k != images * conv->out_h * conv->out_w))
+        return ZN_ERR_INVALID_ARG;  // whole 4-channel chunks, over all images
 
     // The NHWC forward gather runs best on 64x64 tiles (C5 forward, rocprofv3 trace: 156 us against 172 us for
     // 128x128 and 314 us for 256x128).
@@ -459,6 +468,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
                       : mode == kGatherTransposed ? ctx->convt[tile][vec ? 1 : 0]
                       : mode == kGatherWeightGrad ? ctx->convw[tile][vec ? 1 : 0]
                       : mode == kGatherNhwc       ? ctx->convf[tile][vec ? 1 : 0]
+                      : mode == kGatherWeightNhwc ? ctx->convwn[tile][vec ? 1 : 0]
                                                   : ctx->conv[tile][vec ? 1 : 0][gather4];
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
@@ -668,6 +678,9 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                 return bail(ZN_ERR_SYMBOL);
             std::snprintf(name, sizeof(name), "zn_convf_nt_%s%s", kTiles[t].suffix, v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->convf[t][v], ctx->gemm_module, name) != hipSuccess)
+                return bail(ZN_ERR_SYMBOL);
+            std::snprintf(name, sizeof(name), "zn_convwn_tn_%s%s", kTiles[t].suffix, v ? "_v" : "");
+            if (hipModuleGetFunction(&ctx->convwn[t][v], ctx->gemm_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
         }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess ||
@@ -1291,7 +1304,12 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
         return zn_hip_fill_f32(ctx, grad_bias, 0.0f, oc);
     }
     const int64_t kOffsetFloats = INT_MAX / 4;  // 32-bit byte offsets per operand
-    const bool implicit_w = k_order == 0 && sw == 1 && ow % 4 == 0 && plane <= kOffsetFloats && hw * oc <= kOffsetFloats;
+    // grad_W without im2col: from an NHWC copy of the input (C % 4 == 0, any
+    // stride), else by the 4-pixel gather of the NCHW input (stride_w 1,
+    // OW % 4 == 0)
+    const bool nhwc_w = k_order == 0 && c % 4 == 0 && plane <= kOffsetFloats && hw * oc <= kOffsetFloats;
+    const bool implicit_w = k_order == 0 && (nhwc_w || (sw == 1 && ow % 4 == 0)) && plane <= kOffsetFloats &&
+                            hw * oc <= kOffsetFloats;
     const bool transposed = k_order == 0 && sh == 1 && sw == 1 && oc % 4 == 0 && aligned16(grad_output) &&
                             oc * hw <= kOffsetFloats && h * w <= INT_MAX && kh * kw * oc <= INT_MAX;
     const bool need_col = !(implicit_w && transposed);
@@ -1302,8 +1320,9 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
         chunk = std::min<int64_t>(chunk, kColFloats / (hw * taps));
     }
     if (implicit_w) chunk = std::min<int64_t>(chunk, std::min(kOffsetFloats / plane, kOffsetFloats / (hw * oc)));
-    Lease col(ctx), part(ctx), wt(ctx);
+    Lease col(ctx), part(ctx), wt(ctx), nhwc(ctx);
     if (need_col && (rc = col.get((size_t)(chunk * hw * taps)))) return rc;
+    if (nhwc_w && (rc = nhwc.get((size_t)(chunk * plane)))) return rc;
     if (k_order == 1 && (rc = part.get((size_t)(chunk * oc * taps)))) return rc;
     ZnConvGeom gw = {};  // the implicit weight gradient's gather
     if (implicit_w) {
@@ -1315,7 +1334,7 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
         gw.out_w = (int32_t)ow;
         gw.out_h = (int32_t)oh;
         gw.stride_h = (int32_t)sh;
-        gw.stride_w = 1;
+        gw.stride_w = (int32_t)sw;
         gw.pad_h = (int32_t)ph;
         gw.pad_w = (int32_t)pw;
         gw.k_order = 0;
@@ -1330,7 +1349,22 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
         const int64_t rows = nb * hw;
         const float *go = grad_output + b0 * oc * hw;
         float *gi = grad_input + b0 * plane;
-        if (implicit_w) {
+        if (nhwc_w) {
+            // grad_W (+)= go2^T . col with col gathered from an NHWC copy of this chunk's images
+            gw.images = (int32_t)nb;
+            ZnTransposeArgs t;
+            t.src = input + b0 * plane;
+            t.dst = nhwc.ptr;
+            t.batch = nb;
+            t.channels = c;
+            t.pixels = h * w;
+            const int64_t tiles = nb * cdiv(c, 32) * cdiv(h * w, 32);
+            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+            if ((rc = launch(ctx, ctx->elt[kToNhwc], (unsigned)std::min<int64_t>(tiles, cap), 1, 256, &t)) ||
+                (rc = gemm_launch_ex(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, nhwc.ptr, taps, 0, grad_weights,
+                                     taps, 0, 1, b0 > 0, nullptr, ZN_ACT_LINEAR, 0, &gw, kGatherWeightNhwc)))
+                return rc;
+        } else if (implicit_w) {
             // grad_W (+)= go2^T . col with col gathered from this chunk's images: TN, M = OC, N = taps, K = rows
             gw.images = (int32_t)nb;
             if ((rc = gemm_launch_ex(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, input + b0 * plane, taps, 0,
