@@ -22,9 +22,13 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <condition_variable>
 #include <map>
+#include <memory>
+#include <mutex>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../../include/zn_hip.h"
@@ -61,6 +65,69 @@ constexpr int kAttnQueries = 128;  // queries per workgroup (4 waves x 32)
 
 }  // namespace
 
+// Host memcpy split over a few persistent threads (the caller takes one
+// part).  One host thread drives a context, so one copy runs at a time.
+struct HostCopier {
+    std::vector<std::thread> workers;
+    std::mutex mu;
+    std::condition_variable job_cv, done_cv;
+    char *dst = nullptr;
+    const char *src = nullptr;
+    size_t bytes = 0;
+    uint64_t generation = 0;
+    int pending = 0;
+    bool stop = false;
+
+    explicit HostCopier(int threads) {
+        for (int i = 0; i < threads; ++i) workers.emplace_back([this, i] { run(i + 1); });
+    }
+    ~HostCopier() {
+        {
+            std::lock_guard<std::mutex> g(mu);
+            stop = true;
+        }
+        job_cv.notify_all();
+        for (auto &t : workers) t.join();
+    }
+    // Part `part` of `parts` equal 64-byte-aligned slices of the current job.
+    void slice(int part, int parts) const {
+        const size_t per = ((bytes + parts - 1) / parts + 63) & ~(size_t)63;
+        const size_t begin = std::min(bytes, per * part), end = std::min(bytes, begin + per);
+        if (end > begin) std::memcpy(dst + begin, src + begin, end - begin);
+    }
+    void run(int part) {
+        uint64_t seen = 0;
+        for (;;) {
+            std::unique_lock<std::mutex> lk(mu);
+            job_cv.wait(lk, [&] { return stop || generation != seen; });
+            if (stop) return;
+            seen = generation;
+            lk.unlock();
+            slice(part, (int)workers.size() + 1);
+            lk.lock();
+            if (--pending == 0) done_cv.notify_one();
+        }
+    }
+    void copy(void *d, const void *s, size_t n) {
+        if (workers.empty() || n < ((size_t)1 << 20)) {
+            std::memcpy(d, s, n);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> g(mu);
+            dst = (char *)d;
+            src = (const char *)s;
+            bytes = n;
+            pending = (int)workers.size();
+            ++generation;
+        }
+        job_cv.notify_all();
+        slice(0, (int)workers.size() + 1);
+        std::unique_lock<std::mutex> lk(mu);
+        done_cv.wait(lk, [&] { return pending == 0; });
+    }
+};
+
 struct zn_ctx {
     int device = -1;
     hipStream_t stream = nullptr;
@@ -93,6 +160,13 @@ struct zn_ctx {
     // Cached device buffers for the host-slice entry points, keyed by
     // power-of-two byte size.
     std::map<size_t, std::vector<void *>> pool;
+    // Host-slice copies of 4 MiB and more go through two pinned staging
+    // buffers (hipHostMalloc, created on first use): a threaded host memcpy
+    // fills or drains one while the DMA engine moves the other.  Pageable
+    // copies ran at 21 GB/s H2D and 15 GB/s D2H on MI355X, pinned ones at 57.
+    float *pinned[2] = {};
+    hipEvent_t pinned_done[2] = {};
+    std::unique_ptr<HostCopier> copier;
 };
 
 struct zn_event {
@@ -526,15 +600,76 @@ int elt_launch(zn_ctx *ctx, EltKernel kernel, int64_t work_items, const Args &ar
     return launch(ctx, ctx->elt[kernel], (unsigned)blocks, 1, (unsigned)threads, &a);
 }
 
-int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n) {
-    if (n == 0) return ZN_OK;
-    ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+constexpr size_t kStageBytes = (size_t)32 << 20;  // per pinned staging buffer
+constexpr size_t kStageMin = (size_t)4 << 20;      // smaller copies stay pageable
+
+int ensure_staging(zn_ctx *ctx) {
+    if (ctx->pinned[0]) return ZN_OK;
+    for (int i = 0; i < 2; ++i) {
+        ZN_HIP_TRY(ctx, hipHostMalloc((void **)&ctx->pinned[i], kStageBytes, hipHostMallocDefault));
+        ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->pinned_done[i], hipEventDisableTiming));
+    }
+    const unsigned hw = std::thread::hardware_concurrency();
+    ctx->copier.reset(new HostCopier((int)std::min(15u, hw > 1 ? hw - 1 : 0u)));
     return ZN_OK;
 }
 
+// Host -> device on the context stream.  Large copies: chunk i is copied into
+// pinned buffer i % 2 once that buffer's previous DMA has finished, then
+// DMAed; host copies and DMAs of consecutive chunks overlap.  Host-slice
+// calls are not capturable (they read and write host memory synchronously).
+int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n) {
+    if (ctx->capturing) return ZN_ERR_INVALID_ARG;
+    if (n == 0) return ZN_OK;
+    const size_t bytes = n * sizeof(float);
+    if (bytes < kStageMin) {
+        ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+        return ZN_OK;
+    }
+    int rc = ensure_staging(ctx);
+    if (rc) return rc;
+    for (size_t off = 0, i = 0; off < bytes; off += kStageBytes, ++i) {
+        const size_t len = std::min(kStageBytes, bytes - off);
+        const int s = (int)(i & 1);
+        ZN_HIP_TRY(ctx, hipEventSynchronize(ctx->pinned_done[s]));  // its previous DMA has read it
+        ctx->copier->copy(ctx->pinned[s], (const char *)src + off, len);
+        ZN_HIP_TRY(ctx, hipMemcpyAsync((char *)dst + off, ctx->pinned[s], len, hipMemcpyHostToDevice, ctx->stream));
+        ZN_HIP_TRY(ctx, hipEventRecord(ctx->pinned_done[s], ctx->stream));
+    }
+    return ZN_OK;
+}
+
+// Device -> host after the work queued on the stream, then wait.  Large
+// copies: the DMA of chunk i + 1 runs while chunk i is copied out of its
+// pinned buffer.
 int copy_out_and_wait(zn_ctx *ctx, float *dst, const float *src, size_t n) {
     if (ctx->capturing) return ZN_ERR_INVALID_ARG;
-    if (n) ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+    const size_t bytes = n * sizeof(float);
+    if (bytes < kStageMin) {
+        if (n) ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+        ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        return ZN_OK;
+    }
+    int rc = ensure_staging(ctx);
+    if (rc) return rc;
+    const size_t chunks = (bytes + kStageBytes - 1) / kStageBytes;
+    auto issue = [&](size_t i) -> int {
+        const size_t off = i * kStageBytes, len = std::min(kStageBytes, bytes - off);
+        const int s = (int)(i & 1);
+        ZN_HIP_TRY(ctx, hipMemcpyAsync(ctx->pinned[s], (const char *)src + off, len, hipMemcpyDeviceToHost,
+                                       ctx->stream));
+        ZN_HIP_TRY(ctx, hipEventRecord(ctx->pinned_done[s], ctx->stream));
+        return ZN_OK;
+    };
+    if ((rc = issue(0))) return rc;
+    for (size_t i = 0; i < chunks; ++i) {
+        // buffer (i + 1) % 2 was drained by this host thread in step i - 1
+        if (i + 1 < chunks && (rc = issue(i + 1))) return rc;
+        const int s = (int)(i & 1);
+        ZN_HIP_TRY(ctx, hipEventSynchronize(ctx->pinned_done[s]));
+        const size_t off = i * kStageBytes, len = std::min(kStageBytes, bytes - off);
+        ctx->copier->copy((char *)dst + off, ctx->pinned[s], len);
+    }
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     return ZN_OK;
 }
@@ -711,6 +846,13 @@ int zn_hip_destroy(zn_ctx *ctx) {
         ctx->captured.clear();
     }
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    ctx->copier.reset();
+    for (int i = 0; i < 2; ++i) {
+        if (ctx->pinned_done[i]) (void)hipEventDestroy(ctx->pinned_done[i]);
+        if (ctx->pinned[i]) (void)hipHostFree(ctx->pinned[i]);
+        ctx->pinned_done[i] = nullptr;
+        ctx->pinned[i] = nullptr;
+    }
     while (!ctx->graphs.empty()) (void)zn_hip_graph_destroy(ctx->graphs.back());
     for (void *w : ctx->retired_ws) (void)hipFree(w);
     ctx->retired_ws.clear();
