@@ -176,6 +176,12 @@ int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile);
  * Like the tile override, a tuning and test hook with no reference
  * counterpart. */
 int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits);
+/* Persistent-kernel override: -1 (the default) lets the policy choose, 0
+ * never uses the persistent GEMM kernels, 1 uses them for every eligible
+ * GEMM (unsplit, 16-byte staging, K > 0, a tile other than 32x32).  Results
+ * are bit-identical either way.  A tuning and test hook with no reference
+ * counterpart. */
+int zn_hip_set_gemm_persistent(zn_ctx *ctx, int mode);
 
 /* C = act((accumulate ? C : 0) + op(A).op(B) + bias) for one problem.
  * `bias` (length N) may be NULL.  Leading dimensions are in elements and must

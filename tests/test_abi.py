@@ -62,6 +62,8 @@ def test_code_objects_hold_every_kernel():
         for t in ("x", "l", "n", "m", "s"):
             for v in ("", "_v"):
                 assert f"zn_sgemm_{lay}_{t}{v}".encode() in gemm
+        for t in ("x", "l", "n", "m"):
+            assert f"zn_sgemmp_{lay}_{t}_v".encode() in gemm
     for t in ("x", "l", "n", "m", "s"):
         for v in ("", "_v"):
             for g in ("", "_g"):

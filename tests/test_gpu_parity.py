@@ -87,6 +87,41 @@ def test_kat_integer_matmuls_bit_exact(backend, kats, tag):
     np.testing.assert_array_equal(c, want)
 
 
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+def test_host_slice_chunked_pipeline(ctx, backend, layout):
+    """Host-slice NN/NT calls with A of 16 MiB or more run as row chunks whose
+    uploads, GEMMs and downloads overlap on three streams.  Every chunk is an
+    unsplit GEMM like the whole problem, so the result is bit-identical to the
+    device-pointer call; ragged rows, accumulate and the fused epilogue are
+    checked against the oracle."""
+    rng = np.random.default_rng(91)
+    m, n, k = 4096, 1000, 1024  # two chunks of 2048 rows
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    announce(f"host-slice chunked {layout} {m}x{n}x{k}")
+    c = np.full(m * n, np.nan, np.float32)
+    fn = backend.matMul if layout == "nn" else backend.matMulTransposeB
+    fn(a, b, c, m, n, k, False)
+    np.testing.assert_array_equal(c.reshape(m, n), run_gemm(ctx, layout, a, b, m, n, k))
+    # ragged rows (three balanced chunks), accumulating
+    m = 4100
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    c0 = uniform(rng, (m, n))
+    c = c0.ravel().copy()
+    announce(f"host-slice chunked {layout} {m}x{n}x{k} accumulate")
+    fn(a, b, c, m, n, k, True)
+    ref = ref_gemm(layout, a, b, m, n, k, c0=c0, accumulate=True)
+    assert_close(c.reshape(m, n), ref, layout, a, b, m, n, k, c0=c0, accumulate=True, what="chunked host")
+    if layout == "nn":
+        bias = uniform(rng, (n,))
+        announce(f"host-slice chunked nn {m}x{n}x{k} bias relu")
+        c = np.full(m * n, np.nan, np.float32)
+        backend.matMulBiasRelu(a, b, bias, c, m, n, k)
+        ref = ref_gemm("nn", a, b, m, n, k, bias=bias, act="relu")
+        assert_close(c.reshape(m, n), ref, "nn", a, b, m, n, k, bias=bias, act="relu", what="chunked host")
+
+
 def test_kat_dense_layer(backend, kats):
     """src/test/unit/layer.zig:16-55,169-241 through the Dense mirror."""
     from zigneuron_amd import Dense

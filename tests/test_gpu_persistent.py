@@ -1,0 +1,97 @@
+"""GPU: the persistent GEMM kernels (zn_sgemmp_*) against the plain ones.
+
+A persistent workgroup walks several (problem, tile) items and keeps its LDS
+pipeline running across tile boundaries; each output element still sums K in
+the same order, so results must be bit-identical to the plain kernels for
+every layout, tile, epilogue, accumulation and batch.  The plain kernels are
+checked against the oracle elsewhere; one case here is also checked against
+the oracle directly.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _parity import uniform
+from gpu_common import announce, assert_close, ref_gemm, stored_shapes
+
+pytestmark = pytest.mark.gpu
+
+TILES = {"256x128": 0, "128x128": 1, "128x64": 2, "64x64": 3}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from zigneuron_amd import Context
+    c = Context(0)
+    yield c
+    c.set_gemm_tile("auto")
+    c.set_gemm_persistent(-1)
+    c.close()
+
+
+def _both(ctx, layout, m, n, k, batch, tile, acc=False, bias=False, act="linear", seed=0):
+    rng = np.random.default_rng(seed)
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a = uniform(rng, (batch,) + a_shape)
+    b = uniform(rng, (batch,) + b_shape)
+    c0 = uniform(rng, (batch, m, n))
+    bv = uniform(rng, (n,)) if bias else None
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    dbias = ctx.to_device(bv) if bias else None
+    outs = []
+    ctx.set_gemm_tile(TILES[tile])
+    for mode in (0, 1):
+        ctx.set_gemm_persistent(mode)
+        dc = ctx.to_device(c0)
+        if batch == 1:
+            ctx.sgemm(layout, m, n, k, da, lda, db, ldb, dc, n, acc, dbias, act)
+        else:
+            ctx.sgemm_strided_batched(layout, m, n, k, da, lda, a_shape[0] * a_shape[1], db, ldb,
+                                      b_shape[0] * b_shape[1], dc, n, m * n, batch)
+        outs.append(dc.download().reshape(batch, m, n))
+        dc.close()
+    ctx.set_gemm_tile("auto")
+    ctx.set_gemm_persistent(-1)
+    for x in (da, db, dbias):
+        if x is not None:
+            x.close()
+    return outs, a, b, c0, bv
+
+
+CASES = [
+    # layout, m, n, k, batch, tile
+    ("nt", 1024, 1024, 64, 16, "128x128"),   # the C5 QK^T shape, 16 heads
+    ("nn", 1024, 64, 1024, 8, "64x64"),
+    ("tn", 780, 516, 96, 3, "128x64"),        # ragged edges in every tile row and column
+    ("nn", 1000, 1000, 40, 1, "256x128"),
+    ("nt", 4097, 300, 128, 1, "64x64"),
+    ("tn", 2048, 2048, 256, 1, "256x128"),
+    ("nn", 96, 80, 8, 40, "64x64"),           # K shorter than one slice
+]
+
+
+@pytest.mark.parametrize("layout,m,n,k,batch,tile", CASES)
+def test_persistent_bit_identical(ctx, layout, m, n, k, batch, tile):
+    announce(f"persistent {layout} {m}x{n}x{k} batch {batch} tile {tile}")
+    (plain, pers), *_ = _both(ctx, layout, m, n, k, batch, tile, seed=m + n + k)
+    assert np.isfinite(plain).all()
+    np.testing.assert_array_equal(pers.view(np.uint32), plain.view(np.uint32))
+
+
+@pytest.mark.parametrize("act", ["linear", "relu", "sigmoid", "tanh"])
+def test_persistent_epilogues_and_accumulate(ctx, act):
+    for tile in ("128x128", "64x64"):
+        announce(f"persistent epilogue {act} tile {tile}")
+        (plain, pers), *_ = _both(ctx, "nn", 700, 900, 72, 1, tile, acc=True, bias=True, act=act, seed=7)
+        np.testing.assert_array_equal(pers.view(np.uint32), plain.view(np.uint32))
+
+
+def test_persistent_against_oracle(ctx):
+    m, n, k = 1500, 700, 100
+    announce(f"persistent vs oracle nt {m}x{n}x{k}")
+    (plain, pers), a, b, c0, _ = _both(ctx, "nt", m, n, k, 1, "128x128", acc=True, seed=3)
+    ref = ref_gemm("nt", a[0], b[0], m, n, k, c0=c0[0], accumulate=True)
+    assert_close(pers[0], ref, "nt", a[0], b[0], m, n, k, c0=c0[0], accumulate=True, what="persistent")

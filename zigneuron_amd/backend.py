@@ -218,6 +218,10 @@ class Context:
         """Force the number of split-K slices (1..256), or 0 for the policy."""
         check(_lib.load().zn_hip_set_gemm_splits(self.handle, int(splits)), "zn_hip_set_gemm_splits")
 
+    def set_gemm_persistent(self, mode: int = -1) -> None:
+        """-1: the policy decides; 0: never; 1: every eligible GEMM runs on the persistent kernels."""
+        check(_lib.load().zn_hip_set_gemm_persistent(self.handle, int(mode)), "zn_hip_set_gemm_persistent")
+
     # --- GEMM on device pointers (asynchronous on the context stream)
     def sgemm(self, layout, m, n, k, a, lda, b, ldb, c, ldc, accumulate=False, bias=None, act="linear") -> None:
         check(_lib.load().zn_hip_sgemm(self.handle, layout_id(layout), m, n, k, _dptr(a), lda, _dptr(b), ldb,

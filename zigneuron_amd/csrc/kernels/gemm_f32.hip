@@ -536,9 +536,8 @@ struct ConvNhwcWGatherStage {
 // loop 0.9-1.3% slower in NN and NT).
 template <int BM, int BN, int WM, int WN, bool AK, bool BKC, int ACT>
 __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
-                                               int m0, int n0, int wm0, int wn0, int lane, int slice) {
+                                               int64_t bz, int m0, int n0, int wm0, int wn0, int lane, int slice) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
-    const int64_t bz = blockIdx.y;
     float *gc = p.c + bz * p.stride_c;
     const bool split = p.splits > 1;
     if (split) gc = p.ws + ((int64_t)bz * p.splits + slice) * (int64_t)p.m * p.n;
@@ -601,16 +600,16 @@ __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32
 
 template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
 __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
-                                           int m0, int n0, int wm0, int wn0, int lane, int slice) {
+                                           int64_t bz, int m0, int n0, int wm0, int wn0, int lane, int slice) {
     if constexpr (BM * BN >= 128 * 128) {
-        store_tile_act<BM, BN, WM, WN, AK, BKC, -1>(p, acc, m0, n0, wm0, wn0, lane, slice);
+        store_tile_act<BM, BN, WM, WN, AK, BKC, -1>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
         return;
     }
     switch (p.splits > 1 ? 0 : p.act) {  // split-K slices store raw partial sums
-    case 1: store_tile_act<BM, BN, WM, WN, AK, BKC, 1>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
-    case 2: store_tile_act<BM, BN, WM, WN, AK, BKC, 2>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
-    case 3: store_tile_act<BM, BN, WM, WN, AK, BKC, 3>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
-    default: store_tile_act<BM, BN, WM, WN, AK, BKC, 0>(p, acc, m0, n0, wm0, wn0, lane, slice); break;
+    case 1: store_tile_act<BM, BN, WM, WN, AK, BKC, 1>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
+    case 2: store_tile_act<BM, BN, WM, WN, AK, BKC, 2>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
+    case 3: store_tile_act<BM, BN, WM, WN, AK, BKC, 3>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
+    default: store_tile_act<BM, BN, WM, WN, AK, BKC, 0>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
     }
 }
 
@@ -737,7 +736,128 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
                         acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
         }
     }
-    store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, m0, n0, wm0, wn0, lane, slice);
+    store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
+}
+
+// Store instructions a wave issues for a tile that lies wholly inside C:
+// one per (row block, accumulator register) on the vector-store path of an
+// X-contiguous B, one per element column otherwise (fewest of the two, since
+// vec_c decides at run time).  Capped at the 6-bit vmcnt field.
+template <int FM, int FN, bool BKC>
+constexpr int interior_stores() {
+    return (!BKC && FN > 1 ? FM * 16 : FM * 16 * FN) < 63 ? (!BKC && FN > 1 ? FM * 16 : FM * 16 * FN) : 63;
+}
+
+// Persistent plain GEMM (unsplit, one or more problems): workgroup g takes
+// the work items g, g + G, g + 2G, ... (G = gridDim.x) of the problem-major,
+// row-major (problem, tile) order, and the two-stage LDS pipeline runs on
+// across tile boundaries: the first slice of the next tile is in flight
+// while the last slice of the current one is multiplied and its results are
+// stored, so no tile waits for its first load or a fresh dispatch.  The
+// activation is a template argument (the kernel dispatches once at entry).
+//
+// The first wait of a tile must cover that prefetch but not the stores
+// issued after it.  Vector memory operations of a wave retire in issue order
+// (the compiler's own waits rely on it: a load followed by two stores is
+// awaited with vmcnt(2)), so after a tile that lay wholly inside C, whose
+// epilogue issued at least S = interior_stores() stores after the prefetch,
+// vmcnt(S) leaves only those stores in flight; after an edge tile (fewer
+// stores) it waits for everything.
+// `lds` holds the two A stages, then the two B stages (2 * (BM + BN) * BK
+// floats, 1 KB aligned), declared by the kernel once for all activations.
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, int ACT>
+__device__ __forceinline__ void gemm_persistent(const ZnGemmArgs &p, float *lds) {
+    constexpr int NT = WM * WN * kWave;
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int FM = WTM / 32, FN = WTN / 32;
+    constexpr int S = interior_stores<FM, FN, BKC>();
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+    typedef DmaStage<BM, BK, NT, AK, WA> SA;
+    typedef DmaStage<BN, BK, NT, BKC, WB> SB;
+    float(*lds_a)[SA::kFloats] = reinterpret_cast<float(*)[SA::kFloats]>(lds);
+    float(*lds_b)[SB::kFloats] = reinterpret_cast<float(*)[SB::kFloats]>(lds + 2 * SA::kFloats);
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+    const int ntiles = p.tiles_m * p.tiles_n;
+    const int total = ntiles * p.batch;
+    const int step = gridDim.x;
+    int w = blockIdx.x;
+    if (w >= total) return;  // the host launches at most `total` workgroups
+
+    const int ktiles = (p.k + BK - 1) / BK;  // >= 1: the host sends K = 0 to the plain kernels
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
+    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
+
+    // work item -> problem and tile origin (wave-uniform)
+    auto decode = [&](int wi, int &bz, int &m0, int &n0) {
+        bz = wi / ntiles;
+        const int pid = wi - bz * ntiles;
+        const int tm = pid / p.tiles_n;
+        m0 = tm * BM;
+        n0 = (pid - tm * p.tiles_n) * BN;
+    };
+    auto issue = [&](int bz, int m0, int n0, int k0, int st) {
+        SA::issue(make_rsrc(p.a + (int64_t)bz * p.stride_a, a_bytes), lds_a[st], lda, m0, k0, p.m, p.k, wave, lane);
+        SB::issue(make_rsrc(p.b + (int64_t)bz * p.stride_b, b_bytes), lds_b[st], ldb, n0, k0, p.n, p.k, wave, lane);
+    };
+
+    zn_f32x16 acc[FM][FN];
+    {
+        int bz, m0, n0;
+        decode(w, bz, m0, n0);
+        issue(bz, m0, n0, 0, 0);
+    }
+    int stage = 0;
+    bool after_interior = false;  // the previous tile's epilogue issued >= S stores after the prefetch
+    for (;;) {
+        int bz, m0, n0;
+        decode(w, bz, m0, n0);
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+        const bool has_next = w + step < total;
+        for (int kt = 0; kt < ktiles; ++kt) {
+            if (kt == 0 && after_interior)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S) : "memory");  // the prefetch has landed
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();  // every wave's part of this stage is in LDS; the other stage is free
+            if (kt + 1 < ktiles) {
+                issue(bz, m0, n0, (kt + 1) * BK, stage ^ 1);
+            } else if (has_next) {  // the next tile's first slice
+                int bz2, m2, n2;
+                decode(w + step, bz2, m2, n2);
+                issue(bz2, m2, n2, 0, stage ^ 1);
+            }
+            const float *la = lds_a[stage];
+            const float *lb = lds_b[stage];
+#pragma unroll
+            for (int kg = 0; kg < BK; kg += 8) {
+                float fa[FM][4], fb[FN][4];
+                read_frags_dma<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
+                read_frags_dma<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn)
+                            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
+            }
+            stage ^= 1;
+        }
+        store_tile_act<BM, BN, WM, WN, AK, BKC, ACT>(p, acc, bz, m0, n0, wm0, wn0, lane, 0);
+        if (!has_next) break;
+        after_interior = m0 + BM <= p.m && n0 + BN <= p.n;
+        w += step;
+    }
 }
 
 }  // namespace
@@ -772,6 +892,28 @@ ZN_GEMM_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_GEMM_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_GEMM_TILE(m, 64, 64, 32, 2, 2, 1)
 ZN_GEMM_TILE(s, 32, 32, 32, 1, 1, 1)
+
+// Persistent plain GEMMs (gemm_persistent), 16-byte staging only:
+// zn_sgemmp_<layout>_<tile>_v, for problems of several rounds of tiles.
+#define ZN_GEMMP_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, MINB)                                 \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void NAME(ZnGemmArgs p) {        \
+        __shared__ __attribute__((aligned(1024))) float lds[2 * (BM + BN) * BK];                 \
+        switch (p.act) {                                                                         \
+        case 1: gemm_persistent<BM, BN, BK, WM, WN, AK, BKC, 16, 16, 1>(p, lds); break;          \
+        case 2: gemm_persistent<BM, BN, BK, WM, WN, AK, BKC, 16, 16, 2>(p, lds); break;          \
+        case 3: gemm_persistent<BM, BN, BK, WM, WN, AK, BKC, 16, 16, 3>(p, lds); break;          \
+        default: gemm_persistent<BM, BN, BK, WM, WN, AK, BKC, 16, 16, 0>(p, lds); break;         \
+        }                                                                                        \
+    }
+#define ZN_GEMMP_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                           \
+    ZN_GEMMP_KERNEL(zn_sgemmp_nn_##TILE##_v, BM, BN, BK, WM, WN, true, false, MINB)             \
+    ZN_GEMMP_KERNEL(zn_sgemmp_nt_##TILE##_v, BM, BN, BK, WM, WN, true, true, MINB)              \
+    ZN_GEMMP_KERNEL(zn_sgemmp_tn_##TILE##_v, BM, BN, BK, WM, WN, false, false, MINB)
+
+ZN_GEMMP_TILE(x, 256, 128, 16, 4, 2, 1)
+ZN_GEMMP_TILE(l, 128, 128, 16, 2, 2, 4)
+ZN_GEMMP_TILE(n, 128, 64, 16, 2, 1, 1)
+ZN_GEMMP_TILE(m, 64, 64, 32, 2, 2, 1)
 
 // Implicit-GEMM convolution, per image b = blockIdx.y:
 // out_b[OC][OH*OW] = W[OC][K] . im2col(input_b)^T (+ bias[oc]), an NN GEMM

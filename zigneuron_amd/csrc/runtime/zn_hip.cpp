@@ -142,6 +142,8 @@ struct zn_ctx {
     hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
     hipFunction_t convf[kNumTiles][2] = {};    // convolution forward on NHWC [tile][16-byte W rows]
     hipFunction_t convwn[kNumTiles][2] = {};   // weight gradient on NHWC [tile][16-byte grad_output rows]
+    hipFunction_t gemmp[3][kNumTiles] = {};    // persistent plain GEMM, 16-byte staging [layout][tile] (not s)
+    int gemmp_occ[3][kNumTiles] = {};          // its resident workgroups per CU
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -156,6 +158,7 @@ struct zn_ctx {
     std::vector<void *> retired_ws;   // workspaces a live graph may still reference
     int forced_tile = -1;    // ZN_TILE_AUTO
     int forced_splits = 0;   // 0: the split-K policy decides
+    int forced_persistent = -1;  // -1: the policy decides; 0: never; 1: whenever eligible
     zn_device_info info = {};
     // Cached device buffers for the host-slice entry points, keyed by
     // power-of-two byte size.
@@ -167,6 +170,14 @@ struct zn_ctx {
     float *pinned[2] = {};
     hipEvent_t pinned_done[2] = {};
     std::unique_ptr<HostCopier> copier;
+    // Pipelined host-slice GEMMs (created on first use): an upload and a
+    // download stream, a second pinned ring for downloads, and per-chunk
+    // events (A chunk uploaded, C chunk computed; by chunk parity).
+    hipStream_t up = nullptr, down = nullptr;
+    float *pinned_out[2] = {};
+    hipEvent_t pinned_out_done[2] = {};
+    hipEvent_t chunk_in[2] = {}, chunk_out[2] = {};
+    hipEvent_t entry = nullptr;
 };
 
 struct zn_event {
@@ -544,9 +555,30 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
                       : mode == kGatherNhwc       ? ctx->convf[tile][vec ? 1 : 0]
                       : mode == kGatherWeightNhwc ? ctx->convwn[tile][vec ? 1 : 0]
                                                   : ctx->conv[tile][vec ? 1 : 0][gather4];
+    // Plain unsplit GEMMs with short K (at most 8 slices per tile) and more
+    // than one round of tiles run on the persistent kernels: as many
+    // workgroups as can be resident, each walking its share of the (problem,
+    // tile) items with the LDS pipeline running on across tiles, so no tile
+    // waits for a fresh dispatch and its first load (C5 QK^T, K = 64:
+    // 232 -> 215 us).  Longer tiles keep the hardware's dynamic assignment,
+    // which balances the CUs better (C5 convolution GEMM, K = 576: 132 us
+    // plain, 150 us persistent; 8192^3 0.6% slower persistent).
+    if (!conv && splits == 1 && vec && k > 0 && tile != kTileS && ctx->forced_persistent != 0) {
+        const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+        const int64_t resident = cus * ctx->gemmp_occ[layout][tile];
+        const int64_t total = ntiles * batch;
+        if (total <= INT_MAX &&
+            (ctx->forced_persistent == 1 || (total > resident && k <= 8 * (int64_t)ts.bk))) {
+            ZnGemmArgs part = args;
+            part.batch = (int32_t)batch;
+            return launch(ctx, ctx->gemmp[layout][tile], (unsigned)std::min(total, resident), 1,
+                          (unsigned)ts.threads, &part);
+        }
+    }
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
         ZnGemmArgs part = args;
+        part.batch = (int32_t)nb;
         if (splits > 1 && nb == 1) part.xcd_remap = 2;  // the tiles of one K slice share an XCD's L2
         part.a = a ? a + b0 * stride_a : nullptr;
         part.b = b ? b + b0 * stride_b : nullptr;
@@ -614,16 +646,18 @@ int ensure_staging(zn_ctx *ctx) {
     return ZN_OK;
 }
 
-// Host -> device on the context stream.  Large copies: chunk i is copied into
-// pinned buffer i % 2 once that buffer's previous DMA has finished, then
-// DMAed; host copies and DMAs of consecutive chunks overlap.  Host-slice
-// calls are not capturable (they read and write host memory synchronously).
-int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n) {
+// Host -> device on `stream` (the context stream by default).  Large copies:
+// chunk i is copied into pinned buffer i % 2 once that buffer's previous DMA
+// has finished, then DMAed; host copies and DMAs of consecutive chunks
+// overlap.  Host-slice calls are not capturable (they read and write host
+// memory synchronously).
+int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n, hipStream_t stream = nullptr) {
     if (ctx->capturing) return ZN_ERR_INVALID_ARG;
     if (n == 0) return ZN_OK;
+    if (!stream) stream = ctx->stream;
     const size_t bytes = n * sizeof(float);
     if (bytes < kStageMin) {
-        ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+        ZN_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream));
         return ZN_OK;
     }
     int rc = ensure_staging(ctx);
@@ -633,8 +667,8 @@ int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n) {
         const int s = (int)(i & 1);
         ZN_HIP_TRY(ctx, hipEventSynchronize(ctx->pinned_done[s]));  // its previous DMA has read it
         ctx->copier->copy(ctx->pinned[s], (const char *)src + off, len);
-        ZN_HIP_TRY(ctx, hipMemcpyAsync((char *)dst + off, ctx->pinned[s], len, hipMemcpyHostToDevice, ctx->stream));
-        ZN_HIP_TRY(ctx, hipEventRecord(ctx->pinned_done[s], ctx->stream));
+        ZN_HIP_TRY(ctx, hipMemcpyAsync((char *)dst + off, ctx->pinned[s], len, hipMemcpyHostToDevice, stream));
+        ZN_HIP_TRY(ctx, hipEventRecord(ctx->pinned_done[s], stream));
     }
     return ZN_OK;
 }
@@ -674,7 +708,101 @@ int copy_out_and_wait(zn_ctx *ctx, float *dst, const float *src, size_t n) {
     return ZN_OK;
 }
 
+int ensure_pipeline(zn_ctx *ctx) {
+    int rc = ensure_staging(ctx);
+    if (rc) return rc;
+    if (ctx->up) return ZN_OK;
+    for (int i = 0; i < 2; ++i) {
+        ZN_HIP_TRY(ctx, hipHostMalloc((void **)&ctx->pinned_out[i], kStageBytes, hipHostMallocDefault));
+        ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->pinned_out_done[i], hipEventDisableTiming));
+        ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->chunk_in[i], hipEventDisableTiming));
+        ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->chunk_out[i], hipEventDisableTiming));
+    }
+    ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->entry, hipEventDisableTiming));
+    ZN_HIP_TRY(ctx, hipStreamCreateWithFlags(&ctx->down, hipStreamNonBlocking));
+    ZN_HIP_TRY(ctx, hipStreamCreateWithFlags(&ctx->up, hipStreamNonBlocking));
+    return ZN_OK;
+}
+
+// Device -> host of `bytes` on the download stream through the download
+// ring: the DMA of piece p + 1 runs while piece p is copied out.  Returns
+// when every piece is in host memory.
+int drain_out(zn_ctx *ctx, char *dst, const char *src, size_t bytes) {
+    const size_t pieces = (bytes + kStageBytes - 1) / kStageBytes;
+    auto issue = [&](size_t p) -> int {
+        const size_t off = p * kStageBytes, len = std::min(kStageBytes, bytes - off);
+        const int s = (int)(p & 1);
+        ZN_HIP_TRY(ctx, hipMemcpyAsync(ctx->pinned_out[s], src + off, len, hipMemcpyDeviceToHost, ctx->down));
+        ZN_HIP_TRY(ctx, hipEventRecord(ctx->pinned_out_done[s], ctx->down));
+        return ZN_OK;
+    };
+    int rc;
+    if (pieces && (rc = issue(0))) return rc;
+    for (size_t p = 0; p < pieces; ++p) {
+        if (p + 1 < pieces && (rc = issue(p + 1))) return rc;  // its buffer was drained in step p - 1
+        const int s = (int)(p & 1);
+        ZN_HIP_TRY(ctx, hipEventSynchronize(ctx->pinned_out_done[s]));
+        const size_t off = p * kStageBytes, len = std::min(kStageBytes, bytes - off);
+        ctx->copier->copy(dst + off, ctx->pinned_out[s], len);
+    }
+    return ZN_OK;
+}
+
+// Host-slice GEMM in row chunks of A and C (NN and NT, whose A chunks are
+// contiguous rows), so that PCIe transfers overlap the GEMM: B (and the
+// bias) go up first on the upload stream; then A chunk i + 1 (and C chunk
+// i + 1 when accumulating) is staged while the context stream multiplies
+// chunk i, and C chunk i - 1 comes down on the download stream (PCIe is full
+// duplex).  Each chunk is an ordinary GEMM of `rows` rows on the device
+// buffers, so the row results are those of the unchunked call whenever both
+// run unsplit (split-K changes only the order of K partial sums).
+int host_gemm_chunked(zn_ctx *ctx, int layout, const float *a, const float *b, const float *bias, float *c, size_t m,
+                      size_t n, size_t k, int accumulate, int act, float *da, float *db, float *dc, float *dbias,
+                      size_t rows) {
+    int rc = ensure_pipeline(ctx);
+    if (rc) return rc;
+    // device buffers from the pool may still be read by work queued on the
+    // context stream: the side streams start after it
+    ZN_HIP_TRY(ctx, hipEventRecord(ctx->entry, ctx->stream));
+    ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->up, ctx->entry, 0));
+    ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->down, ctx->entry, 0));
+    if ((rc = copy_in(ctx, db, b, k * n, ctx->up))) return rc;
+    if (bias && (rc = copy_in(ctx, dbias, bias, n, ctx->up))) return rc;
+    const size_t chunks = (m + rows - 1) / rows;
+    auto stage = [&](size_t i) -> int {
+        const size_t r0 = i * rows, nr = std::min(rows, m - r0);
+        int rc2 = copy_in(ctx, da + r0 * k, a + r0 * k, nr * k, ctx->up);
+        if (!rc2 && accumulate) rc2 = copy_in(ctx, dc + r0 * n, c + r0 * n, nr * n, ctx->up);
+        if (rc2) return rc2;
+        ZN_HIP_TRY(ctx, hipEventRecord(ctx->chunk_in[i & 1], ctx->up));
+        return ZN_OK;
+    };
+    auto drain = [&](size_t i) -> int {
+        const size_t r0 = i * rows, nr = std::min(rows, m - r0);
+        ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->down, ctx->chunk_out[i & 1], 0));
+        return drain_out(ctx, (char *)(c + r0 * n), (const char *)(dc + r0 * n), nr * n * sizeof(float));
+    };
+    const int64_t ldb = layout == ZN_LAYOUT_NT ? (int64_t)k : (int64_t)n;
+    if ((rc = stage(0))) return rc;
+    for (size_t i = 0; i < chunks; ++i) {
+        const size_t r0 = i * rows, nr = std::min(rows, m - r0);
+        ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->stream, ctx->chunk_in[i & 1], 0));
+        rc = gemm_launch(ctx, layout, (int64_t)nr, (int64_t)n, (int64_t)k, da + r0 * k, (int64_t)k, 0, db, ldb, 0,
+                         dc + r0 * n, (int64_t)n, 0, 1, accumulate, bias ? dbias : nullptr, act);
+        if (rc) return rc;
+        ZN_HIP_TRY(ctx, hipEventRecord(ctx->chunk_out[i & 1], ctx->stream));
+        if (i + 1 < chunks && (rc = stage(i + 1))) return rc;
+        if (i >= 1 && (rc = drain(i - 1))) return rc;
+    }
+    if ((rc = drain(chunks - 1))) return rc;
+    ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->down));
+    ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->up));
+    ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return ZN_OK;
+}
+
 // Host-slice GEMM: stage A, B (and C when accumulating), run, download C.
+// Large NN/NT problems go through host_gemm_chunked.
 int host_gemm(zn_ctx *ctx, int layout, const float *a, size_t a_len, const float *b, size_t b_len, const float *bias,
               size_t bias_len, float *c, size_t c_len, size_t m, size_t n, size_t k, int accumulate, int act) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
@@ -690,6 +818,26 @@ int host_gemm(zn_ctx *ctx, int layout, const float *a, size_t a_len, const float
     Lease da(ctx), db(ctx), dc(ctx), dbias(ctx);
     if ((rc = da.get(mk)) || (rc = db.get(kn)) || (rc = dc.get(mn))) return rc;
     if (bias && (rc = dbias.get(n))) return rc;
+    // Row chunks of about a quarter of A, 8 to 64 MiB, whole multiples of 256 rows, at least two,
+    // of nearly equal size
+    constexpr size_t kChunkMin = (size_t)8 << 20, kChunkMax = (size_t)64 << 20;
+    const size_t a_bytes = mk * sizeof(float);
+    if ((layout == ZN_LAYOUT_NN || layout == ZN_LAYOUT_NT) && k > 0 && a_bytes >= 2 * kChunkMin && m >= 512) {
+        const size_t target = std::min(kChunkMax, std::max(kChunkMin, a_bytes / 4));
+        size_t rows = std::max<size_t>(256, target / (k * sizeof(float)) / 256 * 256);
+        const size_t chunks = (m + rows - 1) / rows;
+        rows = ((m + chunks - 1) / chunks + 255) / 256 * 256;  // balanced: no small last chunk
+        if (rows < m) {
+            rc = host_gemm_chunked(ctx, layout, a, b, bias, c, m, n, k, accumulate, act, da.ptr, db.ptr, dc.ptr,
+                                   bias ? dbias.ptr : nullptr, rows);
+            if (rc && ctx->up) {  // nothing may still use the leased buffers when they go back to the pool
+                (void)hipStreamSynchronize(ctx->up);
+                (void)hipStreamSynchronize(ctx->down);
+                (void)hipStreamSynchronize(ctx->stream);
+            }
+            return rc;
+        }
+    }
     if ((rc = copy_in(ctx, da.ptr, a, mk)) || (rc = copy_in(ctx, db.ptr, b, kn))) return rc;
     if (accumulate && (rc = copy_in(ctx, dc.ptr, c, mn))) return rc;
     if (bias && (rc = copy_in(ctx, dbias.ptr, bias, n))) return rc;
@@ -818,6 +966,20 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             if (hipModuleGetFunction(&ctx->convwn[t][v], ctx->gemm_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
         }
+    for (int l = 0; l < 3; ++l)
+        for (int t = 0; t < kNumTiles; ++t) {
+            if (t == kTileS) continue;
+            char name[64];
+            std::snprintf(name, sizeof(name), "zn_sgemmp_%s_%s_v", kLayoutName[l], kTiles[t].suffix);
+            if (hipModuleGetFunction(&ctx->gemmp[l][t], ctx->gemm_module, name) != hipSuccess)
+                return bail(ZN_ERR_SYMBOL);
+            int occ = 0;
+            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, ctx->gemmp[l][t], kTiles[t].threads, 0) !=
+                    hipSuccess ||
+                occ < 1)
+                occ = 1;
+            ctx->gemmp_occ[l][t] = occ;
+        }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess ||
         hipModuleGetFunction(&ctx->dense_bwd[0], ctx->gemm_module, "zn_dense_bwd_m") != hipSuccess ||
         hipModuleGetFunction(&ctx->dense_bwd[1], ctx->gemm_module, "zn_dense_bwd_m_v") != hipSuccess)
@@ -846,7 +1008,22 @@ int zn_hip_destroy(zn_ctx *ctx) {
         ctx->captured.clear();
     }
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->up) (void)hipStreamSynchronize(ctx->up);
+    if (ctx->down) (void)hipStreamSynchronize(ctx->down);
     ctx->copier.reset();
+    for (int i = 0; i < 2; ++i) {
+        if (ctx->pinned_out_done[i]) (void)hipEventDestroy(ctx->pinned_out_done[i]);
+        if (ctx->pinned_out[i]) (void)hipHostFree(ctx->pinned_out[i]);
+        if (ctx->chunk_in[i]) (void)hipEventDestroy(ctx->chunk_in[i]);
+        if (ctx->chunk_out[i]) (void)hipEventDestroy(ctx->chunk_out[i]);
+        ctx->pinned_out_done[i] = ctx->chunk_in[i] = ctx->chunk_out[i] = nullptr;
+        ctx->pinned_out[i] = nullptr;
+    }
+    if (ctx->entry) (void)hipEventDestroy(ctx->entry);
+    ctx->entry = nullptr;
+    if (ctx->up) (void)hipStreamDestroy(ctx->up);
+    if (ctx->down) (void)hipStreamDestroy(ctx->down);
+    ctx->up = ctx->down = nullptr;
     for (int i = 0; i < 2; ++i) {
         if (ctx->pinned_done[i]) (void)hipEventDestroy(ctx->pinned_done[i]);
         if (ctx->pinned[i]) (void)hipHostFree(ctx->pinned[i]);
@@ -1083,6 +1260,12 @@ int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile) {
 int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits) {
     if (!ctx || splits < 0 || splits > 256) return ZN_ERR_INVALID_ARG;
     ctx->forced_splits = splits;
+    return ZN_OK;
+}
+
+int zn_hip_set_gemm_persistent(zn_ctx *ctx, int mode) {
+    if (!ctx || mode < -1 || mode > 1) return ZN_ERR_INVALID_ARG;
+    ctx->forced_persistent = mode;
     return ZN_OK;
 }
 

@@ -51,6 +51,7 @@ struct ZnGemmArgs {
     int32_t k_chunk;           // K per slice, a multiple of the tile's BK
     float *ws;
     int32_t bias_rows;         // 1: bias is indexed by row (length m), else by column (length n)
+    int32_t batch;             // problems; the persistent kernels walk batch * tiles_m * tiles_n work items
     ZnConvGeom conv;           // the zn_conv_* kernels only
 };
 
