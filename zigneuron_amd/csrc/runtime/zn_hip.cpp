@@ -724,26 +724,78 @@ int ensure_pipeline(zn_ctx *ctx) {
     return ZN_OK;
 }
 
-// Device -> host of `bytes` on the download stream through the download
-// ring: the DMA of piece p + 1 runs while piece p is copied out.  Returns
-// when every piece is in host memory.
-int drain_out(zn_ctx *ctx, char *dst, const char *src, size_t bytes) {
-    const size_t pieces = (bytes + kStageBytes - 1) / kStageBytes;
-    auto issue = [&](size_t p) -> int {
-        const size_t off = p * kStageBytes, len = std::min(kStageBytes, bytes - off);
-        const int s = (int)(p & 1);
-        ZN_HIP_TRY(ctx, hipMemcpyAsync(ctx->pinned_out[s], src + off, len, hipMemcpyDeviceToHost, ctx->down));
+// One step of the chunked host GEMM's transfers: `ups` (host -> device, on
+// the upload stream through the staging ring) and `downs` (device -> host,
+// on the download stream through the download ring, after the download
+// stream's pending waits) are cut into ring-sized pieces and interleaved, so
+// both DMA directions run at once while this thread copies host memory in
+// and out of the pinned rings.  Returns when every download piece is in host
+// memory; uploads are only queued.
+struct Span {
+    char *dst;
+    const char *src;
+    size_t bytes;
+};
+
+int transfer_step(zn_ctx *ctx, const std::vector<Span> &ups, const std::vector<Span> &downs) {
+    struct Piece {
+        char *dst;
+        const char *src;
+        size_t len;
+    };
+    auto cut = [](const std::vector<Span> &spans) {
+        std::vector<Piece> out;
+        for (const Span &sp : spans)
+            for (size_t off = 0; off < sp.bytes; off += kStageBytes)
+                out.push_back({sp.dst + off, sp.src + off, std::min(kStageBytes, sp.bytes - off)});
+        return out;
+    };
+    const std::vector<Piece> up = cut(ups), down = cut(downs);
+    auto issue_down = [&](size_t d) -> int {
+        const int s = (int)(d & 1);
+        ZN_HIP_TRY(ctx, hipMemcpyAsync(ctx->pinned_out[s], down[d].src, down[d].len, hipMemcpyDeviceToHost, ctx->down));
         ZN_HIP_TRY(ctx, hipEventRecord(ctx->pinned_out_done[s], ctx->down));
         return ZN_OK;
     };
     int rc;
-    if (pieces && (rc = issue(0))) return rc;
-    for (size_t p = 0; p < pieces; ++p) {
-        if (p + 1 < pieces && (rc = issue(p + 1))) return rc;  // its buffer was drained in step p - 1
-        const int s = (int)(p & 1);
-        ZN_HIP_TRY(ctx, hipEventSynchronize(ctx->pinned_out_done[s]));
-        const size_t off = p * kStageBytes, len = std::min(kStageBytes, bytes - off);
-        ctx->copier->copy(dst + off, ctx->pinned_out[s], len);
+    for (size_t d = 0; d < std::min<size_t>(2, down.size()); ++d)
+        if ((rc = issue_down(d))) return rc;
+    // Whichever side is ready goes next (non-blocking event queries), so a
+    // download that waits for its GEMM does not hold up the uploads; when
+    // neither is ready, block on the upload buffer (uploads gate the next
+    // GEMM) or else on the download.
+    auto ready = [&](hipEvent_t e, bool &yes) -> int {
+        const hipError_t q = hipEventQuery(e);
+        if (q != hipSuccess && q != hipErrorNotReady) return fail_hip(ctx, q);
+        yes = q == hipSuccess;
+        return ZN_OK;
+    };
+    for (size_t u = 0, d = 0; u < up.size() || d < down.size();) {
+        bool up_ready = false, down_ready = false;
+        if (u < up.size() && (rc = ready(ctx->pinned_done[u & 1], up_ready))) return rc;
+        if (d < down.size() && (rc = ready(ctx->pinned_out_done[d & 1], down_ready))) return rc;
+        if (!up_ready && !down_ready) {
+            if (u < up.size()) {
+                ZN_HIP_TRY(ctx, hipEventSynchronize(ctx->pinned_done[u & 1]));  // its previous DMA has read it
+                up_ready = true;
+            } else {
+                ZN_HIP_TRY(ctx, hipEventSynchronize(ctx->pinned_out_done[d & 1]));
+                down_ready = true;
+            }
+        }
+        if (up_ready) {
+            const int s = (int)(u & 1);
+            ctx->copier->copy(ctx->pinned[s], up[u].src, up[u].len);
+            ZN_HIP_TRY(ctx, hipMemcpyAsync(up[u].dst, ctx->pinned[s], up[u].len, hipMemcpyHostToDevice, ctx->up));
+            ZN_HIP_TRY(ctx, hipEventRecord(ctx->pinned_done[s], ctx->up));
+            ++u;
+        }
+        if (down_ready) {
+            const int s = (int)(d & 1);
+            ctx->copier->copy(down[d].dst, ctx->pinned_out[s], down[d].len);
+            if (d + 2 < down.size() && (rc = issue_down(d + 2))) return rc;  // into the buffer just drained
+            ++d;
+        }
     }
     return ZN_OK;
 }
@@ -751,11 +803,12 @@ int drain_out(zn_ctx *ctx, char *dst, const char *src, size_t bytes) {
 // Host-slice GEMM in row chunks of A and C (NN and NT, whose A chunks are
 // contiguous rows), so that PCIe transfers overlap the GEMM: B (and the
 // bias) go up first on the upload stream; then A chunk i + 1 (and C chunk
-// i + 1 when accumulating) is staged while the context stream multiplies
-// chunk i, and C chunk i - 1 comes down on the download stream (PCIe is full
-// duplex).  Each chunk is an ordinary GEMM of `rows` rows on the device
-// buffers, so the row results are those of the unchunked call whenever both
-// run unsplit (split-K changes only the order of K partial sums).
+// i + 1 when accumulating) goes up while the context stream multiplies
+// chunk i and C chunk i - 1 comes down on the download stream (PCIe is full
+// duplex; transfer_step interleaves the two directions).  Each chunk is an
+// ordinary GEMM of `rows` rows on the device buffers, so the row results are
+// those of the unchunked call whenever both run unsplit (split-K changes only
+// the order of K partial sums).
 int host_gemm_chunked(zn_ctx *ctx, int layout, const float *a, const float *b, const float *bias, float *c, size_t m,
                       size_t n, size_t k, int accumulate, int act, float *da, float *db, float *dc, float *dbias,
                       size_t rows) {
@@ -769,32 +822,35 @@ int host_gemm_chunked(zn_ctx *ctx, int layout, const float *a, const float *b, c
     if ((rc = copy_in(ctx, db, b, k * n, ctx->up))) return rc;
     if (bias && (rc = copy_in(ctx, dbias, bias, n, ctx->up))) return rc;
     const size_t chunks = (m + rows - 1) / rows;
-    auto stage = [&](size_t i) -> int {
-        const size_t r0 = i * rows, nr = std::min(rows, m - r0);
-        int rc2 = copy_in(ctx, da + r0 * k, a + r0 * k, nr * k, ctx->up);
-        if (!rc2 && accumulate) rc2 = copy_in(ctx, dc + r0 * n, c + r0 * n, nr * n, ctx->up);
-        if (rc2) return rc2;
-        ZN_HIP_TRY(ctx, hipEventRecord(ctx->chunk_in[i & 1], ctx->up));
-        return ZN_OK;
+    auto first = [&](size_t i) { return i * rows; };
+    auto count = [&](size_t i) { return std::min(rows, m - i * rows); };
+    auto ups = [&](size_t i) {
+        std::vector<Span> v{{(char *)(da + first(i) * k), (const char *)(a + first(i) * k), count(i) * k * sizeof(float)}};
+        if (accumulate)
+            v.push_back({(char *)(dc + first(i) * n), (const char *)(c + first(i) * n), count(i) * n * sizeof(float)});
+        return v;
     };
-    auto drain = [&](size_t i) -> int {
-        const size_t r0 = i * rows, nr = std::min(rows, m - r0);
-        ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->down, ctx->chunk_out[i & 1], 0));
-        return drain_out(ctx, (char *)(c + r0 * n), (const char *)(dc + r0 * n), nr * n * sizeof(float));
+    auto downs = [&](size_t i) {
+        return std::vector<Span>{
+            {(char *)(c + first(i) * n), (const char *)(dc + first(i) * n), count(i) * n * sizeof(float)}};
     };
     const int64_t ldb = layout == ZN_LAYOUT_NT ? (int64_t)k : (int64_t)n;
-    if ((rc = stage(0))) return rc;
+    if ((rc = transfer_step(ctx, ups(0), {}))) return rc;
+    ZN_HIP_TRY(ctx, hipEventRecord(ctx->chunk_in[0], ctx->up));
     for (size_t i = 0; i < chunks; ++i) {
-        const size_t r0 = i * rows, nr = std::min(rows, m - r0);
         ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->stream, ctx->chunk_in[i & 1], 0));
-        rc = gemm_launch(ctx, layout, (int64_t)nr, (int64_t)n, (int64_t)k, da + r0 * k, (int64_t)k, 0, db, ldb, 0,
-                         dc + r0 * n, (int64_t)n, 0, 1, accumulate, bias ? dbias : nullptr, act);
+        rc = gemm_launch(ctx, layout, (int64_t)count(i), (int64_t)n, (int64_t)k, da + first(i) * k, (int64_t)k, 0,
+                         db, ldb, 0, dc + first(i) * n, (int64_t)n, 0, 1, accumulate, bias ? dbias : nullptr, act);
         if (rc) return rc;
         ZN_HIP_TRY(ctx, hipEventRecord(ctx->chunk_out[i & 1], ctx->stream));
-        if (i + 1 < chunks && (rc = stage(i + 1))) return rc;
-        if (i >= 1 && (rc = drain(i - 1))) return rc;
+        if (i >= 1) ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->down, ctx->chunk_out[(i - 1) & 1], 0));
+        if ((rc = transfer_step(ctx, i + 1 < chunks ? ups(i + 1) : std::vector<Span>{},
+                                i >= 1 ? downs(i - 1) : std::vector<Span>{})))
+            return rc;
+        if (i + 1 < chunks) ZN_HIP_TRY(ctx, hipEventRecord(ctx->chunk_in[(i + 1) & 1], ctx->up));
     }
-    if ((rc = drain(chunks - 1))) return rc;
+    ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->down, ctx->chunk_out[(chunks - 1) & 1], 0));
+    if ((rc = transfer_step(ctx, {}, downs(chunks - 1)))) return rc;
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->down));
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->up));
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
