@@ -90,6 +90,35 @@ def config_entry(name, layout, m, n, k, batch, ms, extra=None):
 
 
 USE_GRAPHS = True  # cleared by --no-graph
+CHECK = True  # cleared by --no-cpu: the sampled parity check runs the oracle
+
+
+def sampled_error(layout, a, b, c, m, n, k, bias=None, act="linear", rows=32):
+    """Max componentwise relative error max|C - C_ref| / (|A|.|B| + |bias|) on
+    `rows` evenly spaced rows of one problem (the last of a batch), against the
+    oracle on the same inputs, in fp64; the tolerance is 1e-5 * sqrt(K).  For
+    sigmoid/tanh the bound applies to the pre-activation and the functions are
+    1-Lipschitz."""
+    from oracle import oracle
+    idx = np.unique(np.linspace(0, m - 1, min(rows, m)).astype(np.int64))
+    r = len(idx)
+    if layout == "nn":
+        ar = np.ascontiguousarray(a[idx])
+        ref = (oracle.matmul_bias_act(ar, b, bias, r, n, k, act) if bias is not None
+               else oracle.matmul(ar, b, r, n, k))
+        den = np.abs(ar.astype(np.float64)) @ np.abs(b.astype(np.float64))
+    elif layout == "nt":
+        ar = np.ascontiguousarray(a[idx])
+        ref = oracle.matmul_nt(ar, b, r, n, k)
+        den = np.abs(ar.astype(np.float64)) @ np.abs(b.astype(np.float64)).T
+    else:
+        ar = np.ascontiguousarray(a[:, idx])
+        ref = oracle.matmul_tn(ar, b, r, n, k)
+        den = np.abs(ar.astype(np.float64)).T @ np.abs(b.astype(np.float64))
+    if bias is not None:
+        den = den + np.abs(bias.astype(np.float64))
+    diff = np.abs(c[idx].astype(np.float64) - ref.reshape(r, n).astype(np.float64))
+    return float(np.max(diff / np.maximum(den, np.finfo(np.float64).tiny)))
 
 
 def bench_configs(ctx, rng, reps=10, warmup=3):
@@ -102,8 +131,8 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
         ldb = k if layout == "nt" else n
         a_shape = a_shape or ((k, m) if layout == "tn" else (m, k))
         b_shape = b_shape or ((n, k) if layout == "nt" else (k, n))
-        a = ctx.to_device(uniform(rng, (batch,) + a_shape, lo=lo))
-        b = ctx.to_device(uniform(rng, (batch,) + b_shape))
+        a_h, b_h = uniform(rng, (batch,) + a_shape, lo=lo), uniform(rng, (batch,) + b_shape)
+        a, b = ctx.to_device(a_h), ctx.to_device(b_h)
         c = ctx.alloc(batch * m * n)
         db = ctx.to_device(bias) if bias is not None else None
         if batch == 1:
@@ -117,10 +146,17 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
             g.close()
         else:
             ms = time_launches(ctx, fn, reps, warmup)
+        c_h = c.download().reshape(batch, m, n)
         for buf in (a, b, c, db):
             if buf is not None:
                 buf.close()
+        err = sampled_error(layout, a_h[-1], b_h[-1], c_h[-1], m, n, k, bias, act) if CHECK else None
         e = config_entry(name, layout, m, n, k, batch, ms, {"bias": bias is not None, "act": act})
+        if err is not None:
+            e["max_rel_err"] = float(f"{err:.3e}")
+            e["tol"] = float(f"{1e-5 * np.sqrt(k):.3e}")
+            if not err <= 1e-5 * np.sqrt(k):
+                log(f"  !! {name}: sampled componentwise error {err:.3e} above 1e-5*sqrt(K)")
         if graph and USE_GRAPHS:
             e["timing"] = "graph replay"
         log(f"  {name:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s  {e['pct_f32_peak']:5.1f}% peak"
@@ -275,20 +311,49 @@ def cpu_baseline(target_s=5.0):
 
 
 def cpu_rows():
-    """The oracle (the reference's CPU path restated) on bounded samples of the
-    other configurations, single-threaded, so each GPU number has its CPU
-    counterpart beside it.  Each sample is one unit of the GPU workload (one
-    MLP step, a row block of a GEMM, one image, one attention head)."""
+    """The oracle (the reference's CPU path restated) on the other
+    configurations, so each GPU number has its CPU counterpart beside it:
+    single-threaded on bounded samples (a row block of a GEMM, one MLP step,
+    one image, one attention head), and the plain GEMMs whole on all host
+    cores."""
     from oracle import oracle
     from zigneuron_amd.layer import init_weights
     rng = np.random.default_rng(2)
     out = []
 
-    def rec(name, sample, seconds, flops, unit_count, unit):
+    def rec(name, sample, seconds, flops, unit_count, unit, threads=1):
         e = {"name": name, "sample": sample, "seconds": round(seconds, 4), "gflops": round(flops / seconds / 1e9, 3),
-             f"ms_per_{unit}": round(seconds / unit_count * 1e3, 3), "threads": 1}
-        log(f"  cpu {name:34s} {e['gflops']:8.3f} GFLOP/s  ({sample})")
+             f"ms_per_{unit}": round(seconds / unit_count * 1e3, 3), "threads": threads}
+        log(f"  cpu {name:34s} {e['gflops']:8.3f} GFLOP/s  ({sample}, {threads} thread{'s' if threads > 1 else ''})")
         out.append(e)
+
+    # The GEMM configurations: one thread on a row block of C (rows of A, or columns of A for TN), and
+    # the whole GEMM on all host cores (OpenMP over row blocks, bit-identical to one thread).
+    threads = max(1, min(16, oracle.cpu_count()))
+
+    def gemm(layout, a, b, m, n, k, th):
+        if layout == "nn":
+            return oracle.matmul(a, b, m, n, k, branch="blocked", threads=th)
+        if layout == "tn":
+            return oracle.matmul_tn(a, b, m, n, k, threads=th)
+        return oracle.matmul_nt(a, b, m, n, k, threads=th)
+
+    for name, layout, m, n, k, rows in (("C1 NN 512^3", "nn", 512, 512, 512, 512),
+                                        ("C3 dW TN 1024x1024x4096", "tn", 1024, 1024, 4096, 64),
+                                        ("C3 dX NT 4096x1024x1024", "nt", 4096, 1024, 1024, 256),
+                                        ("C4 NN 1000^3", "nn", 1000, 1000, 1000, 1000),
+                                        ("C4 NN 4097x1023x777", "nn", 4097, 1023, 777, 1024),
+                                        ("C5 conv NT 100352x128x576", "nt", 100352, 128, 576, 12544)):
+        a = uniform(rng, (k, m) if layout == "tn" else (m, k))
+        b = uniform(rng, (n, k) if layout == "nt" else (k, n))
+        part = np.ascontiguousarray(a[:, :rows] if layout == "tn" else a[:rows])
+        t = time.perf_counter()
+        gemm(layout, part, b, rows, n, k, 1)
+        rec(name, "whole GEMM" if rows == m else f"{rows} of {m} rows", time.perf_counter() - t,
+            2.0 * rows * n * k, rows / m, "full_gemm")
+        t = time.perf_counter()
+        gemm(layout, a, b, m, n, k, threads)
+        rec(name, "whole GEMM", time.perf_counter() - t, 2.0 * m * n * k, 1, "full_gemm", threads)
 
     # C2: one training step of the 784-128-10 MLP at batch 256 (the reference's Dense sequence)
     x, dy = uniform(rng, (256, 784), 0.0, 1.0), uniform(rng, (256, 10))
@@ -307,16 +372,6 @@ def cpu_rows():
     oracle.matmul_tn(x, g1, 784, 128, 256)
     dt = time.perf_counter() - t
     rec("C2 MLP train step", "one full step", dt, 2.0 * 256 * (784 * 128 + 128 * 10) * 3, 1, "step")
-    # C3: 64 of the 1024 output rows of dW (TN) and of 4096 rows of dX (NT)
-    xa, dya, w = uniform(rng, (4096, 64)), uniform(rng, (4096, 1024)), uniform(rng, (1024, 1024))
-    t = time.perf_counter()
-    oracle.matmul_tn(xa, dya, 64, 1024, 4096)
-    dt = time.perf_counter() - t
-    rec("C3 dW TN 1024x1024x4096", "64 of 1024 rows", dt, 2.0 * 64 * 1024 * 4096, 64 / 1024, "full_gemm")
-    t = time.perf_counter()
-    oracle.matmul_nt(dya[:256], w, 256, 1024, 1024)
-    dt = time.perf_counter() - t
-    rec("C3 dX NT 4096x1024x1024", "256 of 4096 rows", dt, 2.0 * 256 * 1024 * 1024, 256 / 4096, "full_gemm")
     # C5 convolution, forward and backward (the reference's im2col branch), one of 32 images
     ximg, wc = uniform(rng, (1, 64, 56, 56)), uniform(rng, (128, 576))
     bc, goc = uniform(rng, (128,)), uniform(rng, (1, 128, 56, 56))
@@ -375,8 +430,9 @@ def main() -> int:
                     help="time only a 1 GiB device-to-device copy (zn_copy_f32): the known-size reference "
                          "for scaling FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
-    global USE_GRAPHS
+    global USE_GRAPHS, CHECK
     USE_GRAPHS = not args.no_graph
+    CHECK = not args.no_cpu
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is "
               "design-only here.", file=sys.stderr)
