@@ -1,0 +1,106 @@
+"""GPU: the intra-workgroup split-K kernels (zn_sgemmk<4|8>_*).
+
+The waves of a workgroup each multiply one 32x32 tile over their own slice of
+K and sum the partial tiles in wave order, then apply C_old, the bias and the
+activation.  That is the arithmetic of the 32x32 tile split into as many K
+slices by separate workgroups and finished by the ordered reduce, so the two
+paths must agree bit for bit whenever every wave has a non-empty slice; the
+automatic policy is checked against the oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from _parity import uniform
+from gpu_common import announce, assert_close, ref_gemm, stored_shapes
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from zigneuron_amd import Context
+    c = Context(0)
+    yield c
+    c.set_gemm_tile("auto")
+    c.set_gemm_splits(0)
+    c.set_gemm_wave_split(-1)
+    c.close()
+
+
+def _run(ctx, layout, m, n, k, batch, a, b, c0, bias, act, acc, lda, ldb):
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    dbias = ctx.to_device(bias) if bias is not None else None
+    dc = ctx.to_device(c0)
+    if batch == 1:
+        ctx.sgemm(layout, m, n, k, da, lda, db, ldb, dc, n, acc, dbias, act)
+    else:
+        ctx.sgemm_strided_batched(layout, m, n, k, da, lda, a_shape[0] * a_shape[1], db, ldb,
+                                  b_shape[0] * b_shape[1], dc, n, m * n, batch)
+    out = dc.download().reshape(batch, m, n)
+    for x in (da, db, dc, dbias):
+        if x is not None:
+            x.close()
+    return out
+
+
+CASES = [
+    # layout, m, n, k, batch, waves, bias, act, acc
+    ("nn", 512, 512, 512, 1, 8, False, "linear", False),
+    ("nn", 256, 128, 784, 1, 4, True, "relu", False),   # the C2 first layer
+    ("nn", 256, 10, 128, 1, 4, True, "linear", False),  # the C2 second layer (unaligned rows)
+    ("tn", 784, 128, 256, 1, 4, False, "linear", False),
+    ("nt", 256, 784, 128, 1, 4, False, "linear", True),
+    ("nt", 100, 70, 1000, 1, 8, True, "sigmoid", True),  # ragged everywhere
+    ("tn", 64, 96, 300, 3, 4, False, "tanh", False),
+    ("nn", 33, 65, 200, 5, 4, False, "linear", False),
+]
+
+
+@pytest.mark.parametrize("layout,m,n,k,batch,waves,bias,act,acc", CASES)
+def test_wave_split_matches_split_k(ctx, layout, m, n, k, batch, waves, bias, act, acc):
+    rng = np.random.default_rng(m * 7 + n + k)
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a = uniform(rng, (batch,) + a_shape)
+    b = uniform(rng, (batch,) + b_shape)
+    c0 = uniform(rng, (batch, m, n))
+    bv = uniform(rng, (n,)) if bias else None
+    if batch > 1:
+        bv, act, acc = None, "linear", False  # the strided-batched entry point has no epilogue
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    chunk = -(-(-(-k // waves)) // 32) * 32
+    assert (waves - 1) * chunk < k, "every wave has a slice"
+    announce(f"wave split {waves} {layout} {m}x{n}x{k} batch {batch} act {act} acc {acc}")
+    ctx.set_gemm_wave_split(waves)
+    got = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
+    ctx.set_gemm_wave_split(0)
+    ctx.set_gemm_tile("32x32")
+    ctx.set_gemm_splits(waves)
+    want = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
+    ctx.set_gemm_tile("auto")
+    ctx.set_gemm_splits(0)
+    ctx.set_gemm_wave_split(-1)
+    assert np.isfinite(got).all()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    if batch == 1:
+        ref = ref_gemm(layout, a[0], b[0], m, n, k, c0=c0[0] if acc else None, accumulate=acc, bias=bv, act=act) \
+            if (bv is None or layout == "nn") and not (bv is not None and acc) else None
+        if ref is not None:
+            assert_close(got[0], ref, layout, a[0], b[0], m, n, k, c0=c0[0] if acc else None, accumulate=acc,
+                         bias=bv, act=act, what="wave split")
+
+
+def test_policy_small_problems_against_oracle(ctx):
+    """The automatic choice for problems of at most one 32x32 tile per CU."""
+    rng = np.random.default_rng(5)
+    for layout, m, n, k in (("nn", 512, 512, 512), ("nt", 256, 784, 128), ("tn", 784, 128, 256),
+                            ("nn", 256, 128, 784), ("nn", 300, 200, 3000)):
+        a_shape, b_shape = stored_shapes(layout, m, n, k)
+        a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+        announce(f"wave split policy {layout} {m}x{n}x{k}")
+        got = _run(ctx, layout, m, n, k, 1, a[None], b[None], np.full((1, m, n), np.nan, np.float32), None, "linear",
+                   False, m if layout == "tn" else k, k if layout == "nt" else n)[0]
+        assert_close(got, ref_gemm(layout, a, b, m, n, k), layout, a, b, m, n, k, what="wave split policy")

@@ -123,6 +123,7 @@ SIGNATURES = {
     "zn_hip_set_gemm_tile": (I, [P, I]),
     "zn_hip_set_gemm_splits": (I, [P, I]),
     "zn_hip_set_gemm_persistent": (I, [P, I]),
+    "zn_hip_set_gemm_wave_split": (I, [P, I]),
     "zn_hip_sgemm": (I, [P, I, I64, I64, I64, P, I64, P, I64, P, I64, I, P, I]),
     "zn_hip_sgemm_strided_batched": (I, [P, I, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, I64, I, P, I]),
     "zn_hip_add_bias": (I, [P, P, P, I64, I64]),

@@ -218,6 +218,10 @@ class Context:
         """Force the number of split-K slices (1..256), or 0 for the policy."""
         check(_lib.load().zn_hip_set_gemm_splits(self.handle, int(splits)), "zn_hip_set_gemm_splits")
 
+    def set_gemm_wave_split(self, waves: int = -1) -> None:
+        """-1: the policy decides; 0: never; 4 or 8: every eligible GEMM splits K over that many waves of a workgroup."""
+        check(_lib.load().zn_hip_set_gemm_wave_split(self.handle, int(waves)), "zn_hip_set_gemm_wave_split")
+
     def set_gemm_persistent(self, mode: int = -1) -> None:
         """-1: the policy decides; 0: never; 1: every eligible GEMM runs on the persistent kernels."""
         check(_lib.load().zn_hip_set_gemm_persistent(self.handle, int(mode)), "zn_hip_set_gemm_persistent")

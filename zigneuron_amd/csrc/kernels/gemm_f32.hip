@@ -739,6 +739,141 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
     store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
 }
 
+// Intra-workgroup split-K, for problems of few tiles and long K: each of the
+// KS waves of a workgroup multiplies the whole BM x BN tile over its own
+// contiguous range of K (the ranges of a K split into KS slices of whole BK
+// multiples), staging its operands by DMA into two private LDS stages, so
+// the main loop has no barrier: a wave waits only for its own loads.  The
+// partial tiles then meet in LDS and are summed in wave order, 0 to KS - 1,
+// as the split-K reduce sums its slices (deterministic), and the epilogue
+// (C_old, bias, activation) runs on the sums; wave w finishes the (row
+// block, register) items w, w + KS, ...  No workspace, no second launch.
+//
+// `lds` holds KS private regions of two A and two B stages each
+// (KS * 2 * (BM + BN) * BK floats); the partial tiles reuse it.
+template <int BM, int BN, int BK, int KS, bool AK, bool BKC, int WA, int WB, int ACT>
+__device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds) {
+    constexpr int FM = BM / 32, FN = BN / 32;
+    typedef DmaStage<BM, BK, kWave, AK, WA> SA;
+    typedef DmaStage<BN, BK, kWave, BKC, WB> SB;
+    constexpr int kRegion = 2 * (SA::kFloats + SB::kFloats);
+    static_assert(FM * FN * 16 * kWave <= kRegion, "a wave's partial tile fits in its staging region");
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+    float *region = lds + wave * kRegion;
+    float *lds_a[2] = {region, region + SA::kFloats};
+    float *lds_b[2] = {region + 2 * SA::kFloats, region + 2 * SA::kFloats + SB::kFloats};
+
+    const int tm = (int)blockIdx.x / p.tiles_n, tn = (int)blockIdx.x - tm * p.tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int64_t bz = blockIdx.y;
+    const int chunk = ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
+    const int kbeg = min(p.k, wave * chunk);
+    const int kend = min(p.k, kbeg + chunk);
+    const int ktiles = (kend - kbeg + BK - 1) / BK;
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
+    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + bz * p.stride_a, a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + bz * p.stride_b, b_bytes);
+
+    zn_f32x16 acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+    if (ktiles > 0) {
+        SA::issue(ra, lds_a[0], lda, m0, kbeg, p.m, kend, 0, lane);
+        SB::issue(rb, lds_b[0], ldb, n0, kbeg, p.n, kend, 0, lane);
+    }
+    for (int kt = 0; kt < ktiles; ++kt) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // slice kt is in this wave's stage
+        const int cur = kt & 1;
+        if (kt + 1 < ktiles) {  // the other stage was last read by slice kt - 1, whose MFMAs consumed those reads
+            SA::issue(ra, lds_a[cur ^ 1], lda, m0, kbeg + (kt + 1) * BK, p.m, kend, 0, lane);
+            SB::issue(rb, lds_b[cur ^ 1], ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, 0, lane);
+        }
+#pragma unroll
+        for (int kg = 0; kg < BK; kg += 8) {
+            float fa[FM][4], fb[FN][4];
+            read_frags_dma<BM, BK, FM, AK>(lds_a[cur], 0, kg, lane, fa);
+            read_frags_dma<BN, BK, FN, BKC>(lds_b[cur], 0, kg, lane, fb);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
+        }
+    }
+
+    // partial tiles to LDS: part[wave][fm][fn][r][lane], lanes contiguous
+    __syncthreads();  // every wave is done with every staging region
+    float *part = lds + wave * (FM * FN * 16 * kWave);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[((fm * FN + fn) * 16 + r) * kWave + lane] = acc[fm][fn][r];
+    __syncthreads();
+
+    float *gc = p.c + bz * p.stride_c;
+    const int64_t ldc = p.ldc;
+    const int j = lane & 31, h = lane >> 5;
+    const bool has_bias = p.bias != nullptr;
+    const bool vec = !BKC && FN > 1 && p.vec_c != 0;
+    constexpr int kPart = FM * FN * 16 * kWave;
+    for (int item = wave; item < FM * 16; item += KS) {
+        const int fm = item >> 4, r = item & 15;
+        const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
+        const int row = m0 + (AK ? 32 * fm + bi : FM * bi + fm);
+        if (row >= p.m) continue;
+        float *crow = gc + (int64_t)row * ldc;
+        const float rbias = has_bias && p.bias_rows ? p.bias[row] : 0.0f;
+        float v[FN];
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const int off = ((fm * FN + fn) * 16 + r) * kWave + lane;
+            float x = lds[off];
+#pragma unroll
+            for (int w = 1; w < KS; ++w) x = x + lds[w * kPart + off];
+            v[fn] = x;
+        }
+        if constexpr (!BKC && FN > 1) {
+            const int col0 = n0 + FN * j;
+            if (vec && col0 + FN <= p.n) {
+                typedef typename FVec<FN>::type VT;
+                VT *dst = reinterpret_cast<VT *>(crow + col0);
+                VT o;
+                if (p.accumulate) o = *dst;
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    float x = v[fn];
+                    if (p.accumulate) x = o[fn] + x;
+                    if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col0 + fn]);
+                    o[fn] = zn_activate(x, ACT);
+                }
+                *dst = o;
+                continue;
+            }
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const int col = n0 + (BKC ? 32 * fn + j : FN * j + fn);
+            if (col >= p.n) continue;
+            float x = v[fn];
+            if (p.accumulate) x = crow[col] + x;
+            if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col]);
+            crow[col] = zn_activate(x, ACT);
+        }
+    }
+}
+
 // Store instructions a wave issues for a tile that lies wholly inside C:
 // one per (row block, accumulator register) on the vector-store path of an
 // X-contiguous B, one per element column otherwise (fewest of the two, since
@@ -892,6 +1027,29 @@ ZN_GEMM_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_GEMM_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_GEMM_TILE(m, 64, 64, 32, 2, 2, 1)
 ZN_GEMM_TILE(s, 32, 32, 32, 1, 1, 1)
+
+// Intra-workgroup split-K GEMMs (gemm_ksplit) on 32x32 tiles, BK 32, with
+// KS = 4 or 8 waves: zn_sgemmk<KS>_<layout>[_v], for problems of at most one
+// workgroup per CU whose tiles would otherwise need a split-K reduce launch.
+#define ZN_GEMMK_KERNEL(NAME, KS, AK, BKC, W)                                                    \
+    extern "C" __global__ __launch_bounds__(KS * 64, 1) void NAME(ZnGemmArgs p) {               \
+        __shared__ __attribute__((aligned(1024))) float lds[KS * 2 * (32 + 32) * 32];            \
+        switch (p.act) {                                                                         \
+        case 1: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 1>(p, lds); break;                    \
+        case 2: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 2>(p, lds); break;                    \
+        case 3: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 3>(p, lds); break;                    \
+        default: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 0>(p, lds); break;                   \
+        }                                                                                        \
+    }
+#define ZN_GEMMK_LAYOUTS(KS, W, SUFFIX)                                                         \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##_nn##SUFFIX, KS, true, false, W)                              \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##_nt##SUFFIX, KS, true, true, W)                               \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##_tn##SUFFIX, KS, false, false, W)
+
+ZN_GEMMK_LAYOUTS(4, 16, _v)
+ZN_GEMMK_LAYOUTS(4, 4, )
+ZN_GEMMK_LAYOUTS(8, 16, _v)
+ZN_GEMMK_LAYOUTS(8, 4, )
 
 // Persistent plain GEMMs (gemm_persistent), 16-byte staging only:
 // zn_sgemmp_<layout>_<tile>_v, for problems of several rounds of tiles.

@@ -143,6 +143,7 @@ struct zn_ctx {
     hipFunction_t convf[kNumTiles][2] = {};    // convolution forward on NHWC [tile][16-byte W rows]
     hipFunction_t convwn[kNumTiles][2] = {};   // weight gradient on NHWC [tile][16-byte grad_output rows]
     hipFunction_t gemmp[3][kNumTiles] = {};    // persistent plain GEMM, 16-byte staging [layout][tile] (not s)
+    hipFunction_t gemmk[3][2][2] = {};         // intra-workgroup split-K, 32x32 tiles [layout][4 or 8 waves][16-byte]
     int gemmp_occ[3][kNumTiles] = {};          // its resident workgroups per CU
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
@@ -159,6 +160,7 @@ struct zn_ctx {
     int forced_tile = -1;    // ZN_TILE_AUTO
     int forced_splits = 0;   // 0: the split-K policy decides
     int forced_persistent = -1;  // -1: the policy decides; 0: never; 1: whenever eligible
+    int forced_wave_split = -1;  // -1: the policy decides; 0: never; 4 or 8: that many waves whenever eligible
     zn_device_info info = {};
     // Cached device buffers for the host-slice entry points, keyed by
     // power-of-two byte size.
@@ -555,6 +557,42 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
                       : mode == kGatherNhwc       ? ctx->convf[tile][vec ? 1 : 0]
                       : mode == kGatherWeightNhwc ? ctx->convwn[tile][vec ? 1 : 0]
                                                   : ctx->conv[tile][vec ? 1 : 0][gather4];
+    // Problems of at most one 32x32 tile per CU: one launch in which the
+    // waves of each workgroup split K among themselves and sum their partial
+    // tiles in LDS in wave order (gemm_ksplit), instead of split-K slices in
+    // separate workgroups plus a reduce launch.  On MI355X: C1 512^3 12.6 ->
+    // 6.3 us, the C2 GEMMs 7.7-12.2 -> 4.1-9.3 us; with 1024 tiles (1000^3)
+    // or more the tiled kernels win.  Four waves below K = 512, eight above.
+    {
+        const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+        const int64_t tiles32 = cdiv(m, 32) * cdiv(n, 32) * batch;
+        int waves = 0;
+        if (!conv && k > 0 && ctx->forced_wave_split > 0)
+            waves = ctx->forced_wave_split;
+        else if (!conv && ctx->forced_wave_split < 0 && ctx->forced_tile < 0 && ctx->forced_splits == 0 &&
+                 tiles32 <= cus && k >= 64 && k <= 4096)
+            waves = k >= 512 ? 8 : 4;
+        if (waves) {
+            ZnGemmArgs kargs = args;
+            kargs.tiles_m = (int32_t)cdiv(m, 32);
+            kargs.tiles_n = (int32_t)cdiv(n, 32);
+            kargs.splits = 1;
+            kargs.k_chunk = (int32_t)k;
+            hipFunction_t fk = ctx->gemmk[layout][waves == 8 ? 1 : 0][vec ? 1 : 0];
+            for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
+                const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
+                ZnGemmArgs part = kargs;
+                part.batch = (int32_t)nb;
+                part.a = a + b0 * stride_a;
+                part.b = b + b0 * stride_b;
+                part.c = c + b0 * stride_c;
+                rc = launch(ctx, fk, (unsigned)(kargs.tiles_m * kargs.tiles_n), (unsigned)nb, (unsigned)(waves * 64),
+                            &part);
+                if (rc) return rc;
+            }
+            return ZN_OK;
+        }
+    }
     // Plain unsplit GEMMs with short K (at most 8 slices per tile) and more
     // than one round of tiles run on the persistent kernels: as many
     // workgroups as can be resident, each walking its share of the (problem,
@@ -1023,6 +1061,14 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                 return bail(ZN_ERR_SYMBOL);
         }
     for (int l = 0; l < 3; ++l)
+        for (int w = 0; w < 2; ++w)
+            for (int v = 0; v < 2; ++v) {
+                char name[64];
+                std::snprintf(name, sizeof(name), "zn_sgemmk%d_%s%s", w ? 8 : 4, kLayoutName[l], v ? "_v" : "");
+                if (hipModuleGetFunction(&ctx->gemmk[l][w][v], ctx->gemm_module, name) != hipSuccess)
+                    return bail(ZN_ERR_SYMBOL);
+            }
+    for (int l = 0; l < 3; ++l)
         for (int t = 0; t < kNumTiles; ++t) {
             if (t == kTileS) continue;
             char name[64];
@@ -1316,6 +1362,12 @@ int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile) {
 int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits) {
     if (!ctx || splits < 0 || splits > 256) return ZN_ERR_INVALID_ARG;
     ctx->forced_splits = splits;
+    return ZN_OK;
+}
+
+int zn_hip_set_gemm_wave_split(zn_ctx *ctx, int waves) {
+    if (!ctx || (waves != -1 && waves != 0 && waves != 4 && waves != 8)) return ZN_ERR_INVALID_ARG;
+    ctx->forced_wave_split = waves;
     return ZN_OK;
 }
 
