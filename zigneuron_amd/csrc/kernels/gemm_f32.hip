@@ -752,7 +752,7 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
 // `lds` holds KS private regions of two A and two B stages each
 // (KS * 2 * (BM + BN) * BK floats); the partial tiles reuse it.
 template <int BM, int BN, int BK, int KS, bool AK, bool BKC, int WA, int WB, int ACT>
-__device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds) {
+__device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int wg = -1) {
     constexpr int FM = BM / 32, FN = BN / 32;
     typedef DmaStage<BM, BK, kWave, AK, WA> SA;
     typedef DmaStage<BN, BK, kWave, BKC, WB> SB;
@@ -764,9 +764,10 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds) {
     float *lds_a[2] = {region, region + SA::kFloats};
     float *lds_b[2] = {region + 2 * SA::kFloats, region + 2 * SA::kFloats + SB::kFloats};
 
-    const int tm = (int)blockIdx.x / p.tiles_n, tn = (int)blockIdx.x - tm * p.tiles_n;
+    const int pid = wg >= 0 ? wg : (int)blockIdx.x;  // wg >= 0: this workgroup's tile in a grouped launch
+    const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
     const int m0 = tm * BM, n0 = tn * BN;
-    const int64_t bz = blockIdx.y;
+    const int64_t bz = wg >= 0 ? 0 : blockIdx.y;
     const int chunk = ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
     const int kbeg = min(p.k, wave * chunk);
     const int kend = min(p.k, kbeg + chunk);
@@ -1223,3 +1224,19 @@ extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs 
     }
 ZN_DENSE_BWD_KERNEL(_v, 16)
 ZN_DENSE_BWD_KERNEL(, 4)
+
+// The same grouping on 32x32 tiles whose four waves split K (gemm_ksplit):
+// more, shorter workgroups for the small layers of an MLP.
+#define ZN_DENSE_BWDK_KERNEL(SUFFIX, W)                                                             \
+    extern "C" __global__ __launch_bounds__(256, 1) void zn_dense_bwd_k##SUFFIX(ZnDenseBwdArgs p) { \
+        __shared__ __attribute__((aligned(1024))) float lds[4 * 2 * (32 + 32) * 32];                 \
+        const int b = blockIdx.x;                                                                    \
+        if (b < p.wg_nt)                                                                             \
+            gemm_ksplit<32, 32, 32, 4, true, true, W, W, 0>(p.nt, lds, b);                           \
+        else if (b < p.wg_nt + p.wg_tn)                                                              \
+            gemm_ksplit<32, 32, 32, 4, false, false, W, W, 0>(p.tn, lds, b - p.wg_nt);               \
+        else                                                                                         \
+            splitk_reduce_body(p.bias, b - p.wg_nt - p.wg_tn, p.wg_bias);                           \
+    }
+ZN_DENSE_BWDK_KERNEL(_v, 16)
+ZN_DENSE_BWDK_KERNEL(, 4)

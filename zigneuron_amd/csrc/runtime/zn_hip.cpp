@@ -140,6 +140,7 @@ struct zn_ctx {
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
     hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
+    hipFunction_t dense_bwd_k[2] = {};         // the same on 32x32 tiles with K split over 4 waves [16-byte]
     hipFunction_t convf[kNumTiles][2] = {};    // convolution forward on NHWC [tile][16-byte W rows]
     hipFunction_t convwn[kNumTiles][2] = {};   // weight gradient on NHWC [tile][16-byte grad_output rows]
     hipFunction_t gemmp[3][kNumTiles] = {};    // persistent plain GEMM, 16-byte staging [layout][tile] (not s)
@@ -1084,7 +1085,9 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
         }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess ||
         hipModuleGetFunction(&ctx->dense_bwd[0], ctx->gemm_module, "zn_dense_bwd_m") != hipSuccess ||
-        hipModuleGetFunction(&ctx->dense_bwd[1], ctx->gemm_module, "zn_dense_bwd_m_v") != hipSuccess)
+        hipModuleGetFunction(&ctx->dense_bwd[1], ctx->gemm_module, "zn_dense_bwd_m_v") != hipSuccess ||
+        hipModuleGetFunction(&ctx->dense_bwd_k[0], ctx->gemm_module, "zn_dense_bwd_k") != hipSuccess ||
+        hipModuleGetFunction(&ctx->dense_bwd_k[1], ctx->gemm_module, "zn_dense_bwd_k_v") != hipSuccess)
         return bail(ZN_ERR_SYMBOL);
     for (int i = 0; i < kNumElt; ++i)
         if (hipModuleGetFunction(&ctx->elt[i], ctx->elt_module, kEltName[i]) != hipSuccess) return bail(ZN_ERR_SYMBOL);
@@ -1590,7 +1593,7 @@ int zn_hip_conv2d_forward_direct(zn_ctx *ctx, const float *input, const float *w
 // ------------------------------------------------------- Dense backward
 // One unsplit 64x64-tile GEMM of a grouped launch.
 static ZnGemmArgs grouped_gemm_args(const float *a, int64_t lda, const float *b, int64_t ldb, float *c, int64_t ldc,
-                                    int64_t m, int64_t n, int64_t k) {
+                                    int64_t m, int64_t n, int64_t k, int tile = 64) {
     ZnGemmArgs g;
     std::memset(&g, 0, sizeof(g));
     g.a = a;
@@ -1602,8 +1605,8 @@ static ZnGemmArgs grouped_gemm_args(const float *a, int64_t lda, const float *b,
     g.m = (int32_t)m;
     g.n = (int32_t)n;
     g.k = (int32_t)k;
-    g.tiles_m = (int32_t)cdiv(m, 64);
-    g.tiles_n = (int32_t)cdiv(n, 64);
+    g.tiles_m = (int32_t)cdiv(m, tile);
+    g.tiles_n = (int32_t)cdiv(n, tile);
     g.act = ZN_ACT_LINEAR;
     g.vec_c = aligned16(c) && ldc % 4 == 0;
     g.group_m = 1;
@@ -1615,13 +1618,15 @@ static ZnGemmArgs grouped_gemm_args(const float *a, int64_t lda, const float *b,
 // zn_dense_bwd_m[_v]: grad_input = gaa . W^T (NT, skipped when null),
 // grad_weights = input^T . gaa (TN) and grad_bias += the ordered sum of the
 // prologue's partials (r), in one launch.
+// tile 32: zn_dense_bwd_k[_v], the same on 32x32 tiles whose four waves split K.
 static int dense_backward_grouped(zn_ctx *ctx, const float *input, const float *weights, const float *gaa,
                                   float *grad_input, float *grad_weights, const ZnReduceArgs &r, int bias_blocks,
-                                  int64_t batch, int64_t in_size, int64_t out_size, int wg_nt, int wg_tn) {
+                                  int64_t batch, int64_t in_size, int64_t out_size, int wg_nt, int wg_tn, int tile) {
     ZnDenseBwdArgs d;
     std::memset(&d, 0, sizeof(d));
-    if (grad_input) d.nt = grouped_gemm_args(gaa, out_size, weights, out_size, grad_input, in_size, batch, in_size, out_size);
-    d.tn = grouped_gemm_args(input, in_size, gaa, out_size, grad_weights, out_size, in_size, out_size, batch);
+    if (grad_input)
+        d.nt = grouped_gemm_args(gaa, out_size, weights, out_size, grad_input, in_size, batch, in_size, out_size, tile);
+    d.tn = grouped_gemm_args(input, in_size, gaa, out_size, grad_weights, out_size, in_size, out_size, batch, tile);
     d.bias = r;
     d.wg_nt = wg_nt;
     d.wg_tn = wg_tn;
@@ -1629,7 +1634,8 @@ static int dense_backward_grouped(zn_ctx *ctx, const float *input, const float *
     // 16-byte staging when every staged row is a whole number of aligned float4s
     const bool vec_tn = aligned16(input) && aligned16(gaa) && in_size % 4 == 0 && out_size % 4 == 0;
     const bool vec_nt = !grad_input || (aligned16(weights) && out_size % 4 == 0);
-    return launch(ctx, ctx->dense_bwd[vec_tn && vec_nt ? 1 : 0], (unsigned)(wg_nt + wg_tn + bias_blocks), 1, 256, &d);
+    hipFunction_t f = (tile == 32 ? ctx->dense_bwd_k : ctx->dense_bwd)[vec_tn && vec_nt ? 1 : 0];
+    return launch(ctx, f, (unsigned)(wg_nt + wg_tn + bias_blocks), 1, 256, &d);
 }
 
 // Dense.backward (src/layer.zig:411-475) on device pointers:
@@ -1684,13 +1690,19 @@ int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float 
         r.vec = (out_size % 4 == 0 && aligned16(grad_bias) && aligned16(part.ptr)) ? 1 : 0;
         const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(cdiv(out_size / (r.vec ? 4 : 1), 256), 8 * cus));
         // Small layers: grad_input, grad_weights and the bias reduce in one
-        // launch (64x64 tiles, unsplit; C2's layers: 5 launches -> 2).
-        const int64_t wg_nt = grad_input ? cdiv(batch, 64) * cdiv(in_size, 64) : 0;
-        const int64_t wg_tn = cdiv(in_size, 64) * cdiv(out_size, 64);
-        if (in_size > 0 && wg_nt + wg_tn <= 2 * cus && batch <= 2048 && out_size <= 2048 && ctx->forced_tile < 0 &&
-            ctx->forced_splits == 0 && in_size <= INT_MAX / 4 / std::max<int64_t>(batch, out_size))
-            return dense_backward_grouped(ctx, input, weights, grad_after_act, grad_input, grad_weights, r,
-                                          (int)blocks, batch, in_size, out_size, (int)wg_nt, (int)wg_tn);
+        // launch (C2's layers: 5 launches -> 2).  Up to 2 workgroups per CU
+        // of 32x32 tiles whose four waves split K (C2 step 44 -> 33 us), else
+        // up to 2 per CU of unsplit 64x64 tiles.
+        const bool small = in_size > 0 && batch <= 2048 && out_size <= 2048 && ctx->forced_tile < 0 &&
+                           ctx->forced_splits == 0 && in_size <= INT_MAX / 4 / std::max<int64_t>(batch, out_size);
+        for (int tile : {32, 64}) {
+            const int64_t wg_nt = grad_input ? cdiv(batch, tile) * cdiv(in_size, tile) : 0;
+            const int64_t wg_tn = cdiv(in_size, tile) * cdiv(out_size, tile);
+            if (tile == 32 && ctx->forced_wave_split == 0) continue;
+            if (small && wg_nt + wg_tn <= 2 * cus)
+                return dense_backward_grouped(ctx, input, weights, grad_after_act, grad_input, grad_weights, r,
+                                              (int)blocks, batch, in_size, out_size, (int)wg_nt, (int)wg_tn, tile);
+        }
         if ((rc = launch(ctx, ctx->splitk_reduce, (unsigned)blocks, 1, 256, &r))) return rc;
     }
     if (in_size == 0) return ZN_OK;
