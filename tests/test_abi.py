@@ -54,9 +54,10 @@ def test_ctypes_table_matches_header():
 def test_code_objects_hold_every_kernel():
     from zigneuron_amd import _lib
     gemm = open(os.path.join(_lib.LIB_DIR, "zn_gemm_gfx950.hsaco"), "rb").read()
+    conv = open(os.path.join(_lib.LIB_DIR, "zn_conv_gfx950.hsaco"), "rb").read()
     elt = open(os.path.join(_lib.LIB_DIR, "zn_elementwise_gfx950.hsaco"), "rb").read()
     attn = open(os.path.join(_lib.LIB_DIR, "zn_attention_gfx950.hsaco"), "rb").read()
-    for blob in (gemm, elt, attn):  # an offload bundle (hipcc --genco) or a bare ELF code object
+    for blob in (gemm, conv, elt, attn):  # an offload bundle (hipcc --genco) or a bare ELF code object
         assert blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or blob[:4] == b"\x7fELF"
     for lay in ("nn", "nt", "tn"):
         for t in ("x", "l", "n", "m", "s"):
@@ -70,15 +71,18 @@ def test_code_objects_hold_every_kernel():
     for t in ("x", "l", "n", "m", "s"):
         for v in ("", "_v"):
             for g in ("", "_g"):
-                assert f"zn_conv_nn_{t}{v}{g}".encode() in gemm
-    assert b"zn_splitk_reduce" in gemm
+                assert f"zn_conv_nn_{t}{v}{g}".encode() in conv
+            for fam in ("zn_convt_nt", "zn_convw_tn", "zn_convf_nt", "zn_convwn_tn"):
+                assert f"{fam}_{t}{v}".encode() in conv
+    for k in ("zn_splitk_reduce", "zn_dense_bwd_m", "zn_dense_bwd_m_v", "zn_dense_bwd_k", "zn_dense_bwd_k_v"):
+        assert k.encode() in gemm
     for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",
               "zn_accumulate_bias", "zn_im2col", "zn_softmax_rows", "zn_col2im", "zn_row_sum", "zn_dense_grad_prologue"):
         assert k.encode() in elt
     for d in (32, 64, 128):
         for v in ("", "_v"):
             assert f"zn_attention_d{d}{v}".encode() in attn
-    assert b"gfx950" in gemm and b"gfx950" in attn
+    assert b"gfx950" in gemm and b"gfx950" in conv and b"gfx950" in attn
 
 
 def test_abi_version_and_status_strings(lib):
@@ -131,7 +135,7 @@ def test_dense_init_scales_match_reference():
     assert np.abs(w).max() <= (2 / 784) ** 0.5
 
 
-@pytest.mark.parametrize("obj", ["zn_gemm_gfx950.s", "zn_attention_gfx950.s"])
+@pytest.mark.parametrize("obj", ["zn_gemm_gfx950.s", "zn_conv_gfx950.s", "zn_attention_gfx950.s"])
 def test_lds_dma_m0_use_is_confined(obj):
     """The LDS-DMA staging sets M0 right before each buffer_load ... lds; no other
     instruction in the code objects that use it may read or write M0."""

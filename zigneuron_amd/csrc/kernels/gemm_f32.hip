@@ -1,1002 +1,7 @@
-// fp32 GEMM for gfx950 (CDNA4) on the fp32 matrix cores.
-//
-// One MFMA core serves the three layouts of ZigNeuron's Backend.matMul family
-// (NN: src/backend.zig:169, TN: :298, NT: :310), the fused bias+activation
-// epilogues (:200-295) and a strided-batched grid (blockIdx.y = problem).
-//
-// Structure of one workgroup (BM x BN macro tile, WM x WN waves):
-//  * Two LDS stages, one barrier per BK slice: slice kt + 1 is loaded while
-//    slice kt is multiplied.  Operands go straight from HBM into LDS with
-//    buffer_load ... lds (no staging registers, no LDS stores): 16-byte
-//    loads for aligned operands (the _v kernels), 4-byte loads otherwise.
-//  * Each operand keeps its global layout in LDS: a K-contiguous operand (A
-//    of NN/NT, B of NT) is stored by rows of x, an X-contiguous one (A of TN,
-//    B of NN/TN) by rows of k.  NN, NT and TN differ only in how lanes read
-//    fragments, so no transposing LDS writes are needed.
-//  * v_mfma_f32_32x32x2f32: a 32x32 fp32 block per instruction, K = 2 split
-//    over the two lane halves.  The K order inside a group of 8 is permuted
-//    so that lane half h, step t covers k = 8g + 4h + t; a K-contiguous
-//    fragment is then one 16-byte LDS read per block.
-//  * For an X-contiguous operand the 32 lanes of a block own FX consecutive
-//    tile rows/cols (row = FX*i + f), so their fragment is one FX-wide LDS
-//    read and, for B, their output columns are FX-wide vector stores.
-//  * Edges (ragged M, N, K) are zero-filled in LDS: masked lanes carry an
-//    out-of-range buffer offset and read (or DMA) zeros, so the load path has
-//    no branches; zero products leave the sums unchanged, and stores are
-//    predicated.
-//  * Split-K: blockIdx.z selects a K range; partial sums go to a workspace
-//    and zn_splitk_reduce adds them in slice order (deterministic).
-#include <hip/hip_runtime.h>
-#include <stdint.h>
-
-#include "../zn_kernel_args.h"
-
-#include "zn_mfma_stage.h"
-
-namespace {
-
-// Where the B operand of a GEMM comes from (gemm_tile_dma's G):
-enum ZnGather {
-    kGNone = 0,        // a plain matrix
-    kGIm2col = 1,      // implicit im2col of an NCHW batch, element gather (ConvGatherStage)
-    kGIm2col4 = 2,     // the same, 4-pixel 16-byte gather (ConvGather16Stage)
-    kGTransposed = 3,  // transposed convolution of grad_output rows (ConvTGatherStage)
-    kGWeight = 4,      // col of a weight gradient (ConvWGatherStage)
-    kGNhwc = 5,        // implicit im2col of an NHWC batch, 4-channel 16-byte gather (ConvNhwcGatherStage)
-    kGNhwcW = 6,       // col of a weight gradient from an NHWC batch, X-contiguous (ConvNhwcWGatherStage)
-};
-
-__device__ __forceinline__ float zn_activate(float v, int act) {
-    switch (act) {
-    case 1: return v > 0.0f ? v : 0.0f;               // relu   (src/backend.zig:239-240)
-    case 2: return 1.0f / (1.0f + expf(-v));          // sigmoid (src/backend.zig:264-265)
-    case 3: return tanhf(v);                          // tanh   (src/backend.zig:289-290)
-    default: return v;
-    }
-}
-
-// x / d for 0 <= x < 2^31 with (mul, shift) as stored in ZnConvGeom
-// (Granlund & Montgomery 1994, Theorem 4.2, with 31-bit dividends).
-__device__ __forceinline__ int zn_udiv(int x, uint32_t mul, uint32_t shift) {
-    return (int)(((uint64_t)(uint32_t)x * mul) >> (31 + shift));
-}
-
-// Implicit-GEMM convolution operand: the X-contiguous tile [BK][BN] of the
-// virtual im2col matrix, element (k, n) gathered with 4-byte loads from the
-// NCHW input (out-of-image taps and out-of-problem elements read zero).
-//
-// When BN is a whole number of waves wide and every wave keeps the same BN
-// columns for all of its loads (kFixedN), a lane's output pixel n is fixed
-// for the whole tile: its (oh, ow) decode is done once (Lane), and the filter
-// tap of each load is uniform across the wave, decoded on the scalar unit.
-// Otherwise (BN = 32) every element is decoded per lane.
-template <int BN, int BK, int NT>
-struct ConvGatherStage {
-    static constexpr int kFloats = BN * BK;
-    static constexpr int kInsts = kFloats / kWave;
-    static constexpr int kWaves = NT / kWave;
-    static constexpr int kPerWave = kInsts / kWaves;
-    static_assert(kInsts % kWaves == 0 && kPerWave >= 1, "load blocks must split evenly over waves");
-    static constexpr int kRowWaves = BN / kWave;  // wave loads per k row
-    static constexpr bool kFixedN = BN % kWave == 0 && kWaves % kRowWaves == 0;
-
-    struct Lane {
-        int ih0, iw0;  // top-left input tap of this lane's output pixel
-        int base;      // ih0 * in_w + iw0
-        bool ok;       // the pixel lies inside the problem
-    };
-
-    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int wave, int lane) {
-        Lane l;
-        const int n = n0 + (kFixedN ? (wave % kRowWaves) * kWave : 0) + lane;
-        const int oh = n / g.out_w, ow = n - oh * g.out_w;
-        l.ih0 = oh * g.stride_h - g.pad_h;
-        l.iw0 = ow * g.stride_w - g.pad_w;
-        l.base = l.ih0 * g.in_w + l.iw0;
-        l.ok = n < nmax;
-        return l;
-    }
-
-    __device__ static __forceinline__ void load(__amdgpu_buffer_rsrc_t rsrc, float *lds, int p0, uint32_t off) {
-        const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-                     :
-                     : "s"(lds_addr), "v"(off), "s"(rsrc)
-                     : "memory");
-    }
-
-    // Filter tap of im2col column k: input channel, kernel row and column.
-    __device__ static __forceinline__ void decode_k(const ZnConvGeom &g, int k, int &ic, int &kh, int &kw) {
-        const int q = zn_udiv(k, g.div1_mul, g.div1_shift);
-        const int r = k - q * g.div1;
-        const int kpos = g.k_order == 0 ? q : r;
-        ic = g.k_order == 0 ? r : q;
-        kh = zn_udiv(kpos, g.kw_mul, g.kw_shift);
-        kw = kpos - kh * g.k_w;
-    }
-
-    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
-                                                 const Lane &ln, int n0, int k0, int nmax, int kmax, int wave,
-                                                 int lane) {
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int row = j * kWaves + wave;  // wave-uniform
-            const int p0 = row * kWave;
-            uint32_t off;
-            if constexpr (kFixedN) {
-                const int k = k0 + row / kRowWaves;  // wave-uniform
-                int ic, kh, kw;
-                decode_k(g, k, ic, kh, kw);
-                const int ih = ln.ih0 + kh, iw = ln.iw0 + kw;
-                const bool ok = ln.ok && k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
-                off = ok ? (uint32_t)(ln.base + (ic * g.in_h + kh) * g.in_w + kw) * 4u : kOutOfRange;
-            } else {
-                const int pos = p0 + lane;
-                const int k = k0 + pos / BN;
-                const int n = n0 + pos % BN;
-                int ic, kh, kw;
-                decode_k(g, k, ic, kh, kw);
-                const int oh = zn_udiv(n, g.ow_mul, g.ow_shift), ow = n - oh * g.out_w;
-                const int ih = oh * g.stride_h - g.pad_h + kh;
-                const int iw = ow * g.stride_w - g.pad_w + kw;
-                const bool ok = n < nmax && k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
-                off = ok ? (uint32_t)((ic * g.in_h + ih) * g.in_w + iw) * 4u : kOutOfRange;
-            }
-            load(rsrc, lds, p0, off);
-        }
-    }
-};
-
-// Tile coordinates and split-K slice of this workgroup: optional XCD-
-// contiguous remap, then groups of `group_m` tile rows (group_m = 1 is plain
-// row-major order).  Workgroups go to the 8 XCDs round-robin by linear id,
-// and each XCD has its own L2.  xcd_remap 2 (split-K, one problem): the
-// (slice, tile) pairs are numbered slice-major and each XCD takes a
-// contiguous run of them, so the tiles of one K slice, which read the same
-// rows of A and B, share one L2 instead of fetching them once per XCD.
-// `wg` >= 0 (a grouped launch) is this workgroup's index within its problem,
-// which is unsplit.
-__device__ __forceinline__ void tile_coords(const ZnGemmArgs &p, int &tm, int &tn, int &slice, int wg = -1) {
-    int pid = wg >= 0 ? wg : (int)blockIdx.x;
-    slice = wg >= 0 ? 0 : (int)blockIdx.z;
-    const int ntiles = p.tiles_m * p.tiles_n;
-    if (p.xcd_remap == 1) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
-    if (p.xcd_remap == 2) {
-        const int lin = blockIdx.x + ntiles * blockIdx.z;  // gridDim.y == 1
-        const int total = ntiles * p.splits, per = total >> 3, extra = total & 7;
-        const int xcd = lin & 7;
-        const int seq = xcd * per + min(xcd, extra) + (lin >> 3);
-        slice = seq / ntiles;
-        pid = seq - slice * ntiles;
-    }
-    const int group_span = p.group_m * p.tiles_n;
-    const int first_m = (pid / group_span) * p.group_m;
-    const int gsize = min(p.tiles_m - first_m, p.group_m);
-    const int in_group = pid % group_span;
-    tm = first_m + in_group % gsize;
-    tn = in_group / gsize;
-}
-
-// The convolution operand with 16-byte loads, for stride_w == 1 and
-// out_w % 4 == 0: lane L of a wave instruction stages a chunk of 4
-// neighbouring output pixels (one output row, so 4 consecutive input
-// columns) of one filter tap.  A lane's pixel chunk is fixed for the whole
-// tile (Lane); its tap changes with the instruction and is decoded per lane.
-// Chunks wholly inside the image are one DMA.  A chunk that straddles the
-// left or right padding is DMAed as zeros (out-of-range offset), and the lane
-// loads its in-image elements with ordinary guarded loads and writes the
-// chunk into LDS after its own DMA has landed (patch, before the barrier), so
-// no access ever leaves the image.
-template <int BN, int BK, int NT>
-struct ConvGather16Stage {
-    static constexpr int kFloats = BN * BK;
-    static constexpr int kPerInst = 4 * kWave;  // 256 floats per wave instruction
-    static constexpr int kInsts = kFloats / kPerInst;
-    static constexpr int kWaves = NT / kWave;
-    static constexpr int kPerWave = kInsts / kWaves;
-    static_assert(kInsts % kWaves == 0 && kPerWave >= 1, "load blocks must split evenly over waves");
-    static_assert(kPerInst % BN == 0, "a wave instruction covers whole k rows");
-    static constexpr int kRowsPerInst = kPerInst / BN;
-
-    struct Lane {
-        int ih0, iw0;  // top-left input tap of the chunk's first pixel
-        int kl;        // k row of this lane within a wave instruction
-        bool ok;       // the chunk lies inside the problem
-    };
-    struct Patch {
-        zn_f32x4 v[kPerWave];
-        uint32_t mask;  // bit j: instruction j's chunk needs the patch
-    };
-
-    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int lane) {
-        Lane l;
-        const int n = n0 + (4 * lane) % BN;  // first pixel of the chunk (n0 and out_w are multiples of 4)
-        const int oh = n / g.out_w, ow = n - oh * g.out_w;
-        l.ih0 = oh * g.stride_h - g.pad_h;
-        l.iw0 = ow - g.pad_w;  // stride_w == 1
-        l.kl = (4 * lane) / BN;
-        l.ok = n < nmax;
-        return l;
-    }
-
-    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const float *image, float *lds,
-                                                 const ZnConvGeom &g, const Lane &ln, int k0, int kmax, int wave,
-                                                 int lane, Patch &pt) {
-        pt.mask = 0;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int row = j * kWaves + wave;  // wave-uniform
-            const int p0 = row * kPerInst;
-            const int k = k0 + row * kRowsPerInst + ln.kl;
-            int ic, kh, kw;
-            ConvGatherStage<BN, BK, NT>::decode_k(g, k, ic, kh, kw);
-            const int ih = ln.ih0 + kh, iws = ln.iw0 + kw;
-            const bool row_ok = ln.ok && k < kmax && (unsigned)ih < (unsigned)g.in_h;
-            const bool full = row_ok && iws >= 0 && iws + 3 < g.in_w;
-            const int row_off = (ic * g.in_h + ih) * g.in_w;
-            const uint32_t off = full ? (uint32_t)(row_off + iws) * 4u : kOutOfRange;
-            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(lds_addr), "v"(off), "s"(rsrc)
-                         : "memory");
-            pt.v[j] = zn_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (row_ok && !full && iws + 3 >= 0 && iws < g.in_w) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if ((unsigned)(iws + e) < (unsigned)g.in_w) pt.v[j][e] = image[row_off + iws + e];
-                pt.mask |= 1u << j;
-            }
-        }
-    }
-
-    // After this wave's DMA has landed: write the patched chunks.
-    __device__ static __forceinline__ void apply(float *lds, const Patch &pt, int wave, int lane) {
-        if (!pt.mask) return;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j)
-            if (pt.mask & (1u << j))
-                *reinterpret_cast<zn_f32x4 *>(lds + (j * kWaves + wave) * kPerInst + 4 * lane) = pt.v[j];
-    }
-};
-
-// The transposed-convolution operand (the input gradient of a stride-1
-// convolution as an implicit GEMM): B[n][k] with n = input pixel (ih, iw)
-// and k = (kh*k_w + kw)*OC + oc is grad_output[(ih + pad_h - kh, iw + pad_w -
-// kw)][oc], grad_output read as [OH*OW][OC] rows (the reading of
-// cpuConv2dBackwardIm2col).  The operand is K-contiguous (stored [BN][BK],
-// swizzled like DmaStage), and a 16-byte chunk is 4 consecutive oc of one
-// grad_output row (OC % 4 == 0), so each chunk is either wholly inside the
-// output image or wholly outside (zeros): no patching.  ZnConvGeom fields as
-// used here: channels = OC, in_h x in_w = OH x OW (the gathered image),
-// out_w = W (decodes n), div1 = OC, k_w, pad as in the forward.
-template <int BN, int BK, int NT>
-struct ConvTGatherStage {
-    typedef DmaStage<BN, BK, NT, true, 16> Layout;
-    static constexpr int kPerWave = Layout::kPerWave;
-    static constexpr int kWaves = NT / kWave;
-
-    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
-                                                 int n0, int k0, int nmax, int kmax, int wave, int lane) {
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int p0 = (j * kWaves + wave) * Layout::kPerInst;
-            const int pos = p0 + 4 * lane;
-            const int row = pos / BK;
-            const int c = ((pos % BK) / 4) ^ Layout::swz(row);
-            const int n = n0 + row, k = k0 + 4 * c;
-            const int ih = zn_udiv(n, g.ow_mul, g.ow_shift), iw = n - ih * g.out_w;
-            const int khw = zn_udiv(k, g.div1_mul, g.div1_shift);
-            const int oc = k - khw * g.div1;
-            const int kh = zn_udiv(khw, g.kw_mul, g.kw_shift), kw = khw - kh * g.k_w;
-            const int oh = ih + g.pad_h - kh, ow = iw + g.pad_w - kw;
-            const bool ok = n < nmax && k < kmax && (unsigned)oh < (unsigned)g.in_h && (unsigned)ow < (unsigned)g.in_w;
-            const uint32_t off = ok ? (uint32_t)((oh * g.in_w + ow) * g.channels + oc) * 4u : kOutOfRange;
-            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(lds_addr), "v"(off), "s"(rsrc)
-                         : "memory");
-        }
-    }
-};
-
-// The weight-gradient operand of a convolution with stride_w == 1 and
-// out_w % 4 == 0, without the col buffer: B[k][n] = col[k][n], k = output
-// pixel over `images` images (b*OH*OW + oh*OW + ow), n = im2col tap
-// (kh*k_w + kw)*C + ic, i.e. input[b][ic][oh*stride_h - pad_h + kh][ow -
-// pad_w + kw].  The operand is K-contiguous (stored [BN][BK], swizzled like
-// DmaStage): a 16-byte chunk is 4 consecutive k, i.e. 4 neighbouring output
-// pixels of one output row, which read 4 consecutive input columns of one
-// tap.  A lane's tap and chunk column are fixed for the whole tile (Lane);
-// its pixels move with k0.  Chunks that straddle the left or right padding
-// are DMAed as zeros and patched like ConvGather16Stage's.
-template <int BN, int BK, int NT>
-struct ConvWGatherStage {
-    typedef DmaStage<BN, BK, NT, true, 16> Layout;
-    static constexpr int kNoRow = -(1 << 30);  // plus any oh*stride_h stays negative
-    static constexpr int kPerWave = Layout::kPerWave;
-    static constexpr int kWaves = NT / kWave;
-
-    struct Lane {
-        int tap_off[kPerWave];  // ic*H*W + (kh - pad_h)*W + (kw - pad_w), relative to the pixel's (oh*sh, ow)
-        int dh[kPerWave];       // kh - pad_h; kNoRow for a tap past the problem (never in the image)
-        int dw[kPerWave];       // kw - pad_w
-        int kc[kPerWave];       // first k of the chunk, relative to k0
-    };
-    struct Patch {
-        zn_f32x4 v[kPerWave];
-        uint32_t mask;
-    };
-
-    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int wave, int lane) {
-        Lane l;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int pos = (j * kWaves + wave) * Layout::kPerInst + 4 * lane;
-            const int row = pos / BK;
-            const int n = n0 + row;
-            int ic, kh, kw;
-            ConvGatherStage<BN, BK, NT>::decode_k(g, n, ic, kh, kw);
-            l.dh[j] = n < nmax ? kh - g.pad_h : kNoRow;
-            l.dw[j] = kw - g.pad_w;
-            l.tap_off[j] = (ic * g.in_h + kh - g.pad_h) * g.in_w + kw - g.pad_w;
-            l.kc[j] = 4 * (((pos % BK) / 4) ^ Layout::swz(row));
-        }
-        return l;
-    }
-
-    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const float *image, float *lds,
-                                                 const ZnConvGeom &g, const Lane &ln, int k0, int kmax, int wave,
-                                                 int lane, Patch &pt) {
-        pt.mask = 0;
-        const int plane = g.channels * g.in_h * g.in_w;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int p0 = (j * kWaves + wave) * Layout::kPerInst;
-            const int k = k0 + ln.kc[j];
-            const int q = zn_udiv(k, g.ow_mul, g.ow_shift), ow = k - q * g.out_w;
-            const int b = zn_udiv(q, g.oh_mul, g.oh_shift), oh = q - b * g.out_h;
-            const int ohs = oh * g.stride_h;
-            const int ih = ohs + ln.dh[j], iws = ow + ln.dw[j];
-            const bool row_ok = k < kmax && (unsigned)ih < (unsigned)g.in_h;
-            const bool full = row_ok && iws >= 0 && iws + 3 < g.in_w;
-            const int src = b * plane + ln.tap_off[j] + ohs * g.in_w + ow;  // = b*plane + (ic*H + ih)*W + iws
-            const uint32_t off = full ? (uint32_t)src * 4u : kOutOfRange;
-            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(lds_addr), "v"(off), "s"(rsrc)
-                         : "memory");
-            pt.v[j] = zn_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (row_ok && !full && iws + 3 >= 0 && iws < g.in_w) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if ((unsigned)(iws + e) < (unsigned)g.in_w) pt.v[j][e] = image[src + e];
-                pt.mask |= 1u << j;
-            }
-        }
-    }
-
-    // After this wave's DMA has landed: write the patched chunks.
-    __device__ static __forceinline__ void apply(float *lds, const Patch &pt, int wave, int lane) {
-        if (!pt.mask) return;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j)
-            if (pt.mask & (1u << j))
-                *reinterpret_cast<zn_f32x4 *>(lds + (j * kWaves + wave) * Layout::kPerInst + 4 * lane) = pt.v[j];
-    }
-};
-
-// The implicit im2col operand of an NHWC image batch: B[n][k] with n = output
-// pixel (oh, ow) and k = (kh*k_w + kw)*C + ic (the im2col K order) is
-// image[(oh*stride_h - pad_h + kh, ow*stride_w - pad_w + kw)][ic].  The
-// operand is K-contiguous (stored [BN][BK], swizzled like DmaStage): a 16-byte
-// chunk is 4 consecutive channels of one pixel (C % 4 == 0), so it is either
-// wholly inside the image or wholly padding (zeros), at any stride.
-// ZnConvGeom as in the forward: channels = C, in_h x in_w, out_w decodes n,
-// div1 = C, k_w.
-template <int BN, int BK, int NT>
-struct ConvNhwcGatherStage {
-    typedef DmaStage<BN, BK, NT, true, 16> Layout;
-    static constexpr int kPerWave = Layout::kPerWave;
-    static constexpr int kWaves = NT / kWave;
-
-    // A lane's output pixel and chunk column are fixed for the whole tile:
-    // decoded once.  ih0/iw0: the pixel's top-left input tap (ih0 = kNoRow
-    // for a pixel past the problem, so no tap is ever inside the image).
-    struct Lane {
-        int ih0[kPerWave], iw0[kPerWave];
-        int kc[kPerWave];  // first k of the chunk, relative to k0
-    };
-    static constexpr int kNoRow = -(1 << 30);
-
-    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int wave, int lane) {
-        Lane l;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int pos = (j * kWaves + wave) * Layout::kPerInst + 4 * lane;
-            const int row = pos / BK;
-            const int n = n0 + row;
-            const int oh = zn_udiv(n, g.ow_mul, g.ow_shift), ow = n - oh * g.out_w;
-            l.ih0[j] = n < nmax ? oh * g.stride_h - g.pad_h : kNoRow;
-            l.iw0[j] = ow * g.stride_w - g.pad_w;
-            l.kc[j] = 4 * (((pos % BK) / 4) ^ Layout::swz(row));
-        }
-        return l;
-    }
-
-    // tap_uniform (C % BK == 0): the slice [k0, k0 + BK) lies in one filter
-    // tap, decoded once per slice on the scalar unit.
-    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
-                                                 const Lane &ln, int k0, int kmax, int wave, int lane) {
-        int kh_u = 0, kw_u = 0, ic_u = 0;
-        if (g.tap_uniform) {
-            const int khw = zn_udiv(k0, g.div1_mul, g.div1_shift);
-            ic_u = k0 - khw * g.div1;
-            kh_u = zn_udiv(khw, g.kw_mul, g.kw_shift);
-            kw_u = khw - kh_u * g.k_w;
-        }
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int p0 = (j * kWaves + wave) * Layout::kPerInst;
-            const int k = k0 + ln.kc[j];
-            int kh, kw, ic;
-            if (g.tap_uniform) {
-                kh = kh_u;
-                kw = kw_u;
-                ic = ic_u + ln.kc[j];
-            } else {
-                const int khw = zn_udiv(k, g.div1_mul, g.div1_shift);
-                ic = k - khw * g.div1;
-                kh = zn_udiv(khw, g.kw_mul, g.kw_shift);
-                kw = khw - kh * g.k_w;
-            }
-            const int ih = ln.ih0[j] + kh, iw = ln.iw0[j] + kw;
-            const bool ok = k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
-            const uint32_t off = ok ? (uint32_t)((ih * g.in_w + iw) * g.channels + ic) * 4u : kOutOfRange;
-            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(lds_addr), "v"(off), "s"(rsrc)
-                         : "memory");
-        }
-    }
-};
-
-// The col operand of a weight gradient from an NHWC image batch: B[k][n] =
-// col[k][n] with k = output pixel over `images` images (b*OH*OW + oh*OW +
-// ow) and n = im2col tap (kh*k_w + kw)*C + ic, i.e. image_b[(oh*stride_h -
-// pad_h + kh, ow*stride_w - pad_w + kw)][ic].  X-contiguous (stored
-// [BK][BN] like DmaStage): a 16-byte chunk is 4 consecutive channels of one
-// tap at one pixel (C % 4 == 0), wholly inside the image or wholly padding,
-// at any stride.  A lane's tap is fixed for the tile; its pixel moves with k0.
-template <int BN, int BK, int NT>
-struct ConvNhwcWGatherStage {
-    typedef DmaStage<BN, BK, NT, false, 16> Layout;
-    static constexpr int kPerWave = Layout::kPerWave;
-    static constexpr int kWaves = NT / kWave;
-    static_assert(Layout::kPerInst % BN == 0, "a wave instruction covers whole k rows");
-    static constexpr int kRowsPerInst = Layout::kPerInst / BN;
-    static constexpr int kNoRow = -(1 << 30);
-
-    struct Lane {
-        int dh, dw;   // kh - pad_h (kNoRow past the problem), kw - pad_w
-        int tap_off;  // (kh - pad_h) * W * C + (kw - pad_w) * C + ic
-        int kl;       // k row of this lane within a wave instruction
-    };
-
-    __device__ static __forceinline__ Lane lane_setup(const ZnConvGeom &g, int n0, int nmax, int lane) {
-        Lane l;
-        const int n = n0 + (4 * lane) % BN;
-        const int khw = zn_udiv(n, g.div1_mul, g.div1_shift);
-        const int ic = n - khw * g.div1;
-        const int kh = zn_udiv(khw, g.kw_mul, g.kw_shift), kw = khw - kh * g.k_w;
-        l.dh = n < nmax ? kh - g.pad_h : kNoRow;
-        l.dw = kw - g.pad_w;
-        l.tap_off = ((kh - g.pad_h) * g.in_w + (kw - g.pad_w)) * g.channels + ic;
-        l.kl = (4 * lane) / BN;
-        return l;
-    }
-
-    __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
-                                                 const Lane &ln, int k0, int kmax, int wave) {
-        const int plane = g.channels * g.in_h * g.in_w;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int row = j * kWaves + wave;  // wave-uniform
-            const int p0 = row * Layout::kPerInst;
-            const int k = k0 + row * kRowsPerInst + ln.kl;
-            const int q = zn_udiv(k, g.ow_mul, g.ow_shift), ow = k - q * g.out_w;
-            const int b = zn_udiv(q, g.oh_mul, g.oh_shift), oh = q - b * g.out_h;
-            const int ohs = oh * g.stride_h, ows = ow * g.stride_w;
-            const int ih = ohs + ln.dh, iw = ows + ln.dw;
-            const bool ok = k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
-            const int src = b * plane + (ohs * g.in_w + ows) * g.channels + ln.tap_off;
-            const uint32_t off = ok ? (uint32_t)src * 4u : kOutOfRange;
-            const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(lds_addr), "v"(off), "s"(rsrc)
-                         : "memory");
-        }
-    }
-};
-
-// Epilogue of one macro tile: v = acc (+ C) (+ bias) -> act -> store.
-// 32x32 accumulator layout: register r of lane (j = lane % 32, h = lane / 32)
-// holds block row 8*(r/4) + 4*h + r%4, block column j.  A split-K slice
-// stores its raw partial sums to the workspace instead.
-// ACT >= 0: the activation is a template argument, one copy of the element
-// loop per activation, entered once.  That keeps the executed code of a
-// launch short for the small tiles (the instruction cache is cold for most
-// small launches: alternating two small GEMM kernels cost 1.6 us per launch
-// more than repeating one).  ACT = -1 reads it at run time; the 128x128 and
-// 256x128 tiles keep that form (the specialised copies made the 8192^3 main
-// loop 0.9-1.3% slower in NN and NT).
-template <int BM, int BN, int WM, int WN, bool AK, bool BKC, int ACT>
-__device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
-                                               int64_t bz, int m0, int n0, int wm0, int wn0, int lane, int slice) {
-    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
-    float *gc = p.c + bz * p.stride_c;
-    const bool split = p.splits > 1;
-    if (split) gc = p.ws + ((int64_t)bz * p.splits + slice) * (int64_t)p.m * p.n;
-    const int64_t ldc = split ? (int64_t)p.n : p.ldc;
-    const bool accumulate = !split && p.accumulate;
-    const int act = ACT >= 0 ? ACT : (split ? 0 : p.act);
-    const int j = lane & 31;
-    const int h = lane >> 5;
-    const bool has_bias = !split && p.bias != nullptr;
-    const bool col_bias = has_bias && !p.bias_rows;
-    const bool row_bias = has_bias && p.bias_rows;
-    float bias_v[FN];
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-        const int col = n0 + wn0 + (BKC ? 32 * fn + j : FN * j + fn);
-        bias_v[fn] = (col_bias && col < p.n) ? p.bias[col] : 0.0f;
-    }
-    const bool vec_c = split ? (p.n % 4 == 0) : (p.vec_c != 0);
-    const bool vec_store = !BKC && FN > 1 && vec_c && (n0 + wn0 + FN * j + FN <= p.n);
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
-            const int row = m0 + wm0 + (AK ? 32 * fm + bi : FM * bi + fm);
-            if (row >= p.m) continue;
-            float *crow = gc + (int64_t)row * ldc;
-            const float rb = row_bias ? p.bias[row] : 0.0f;
-            if constexpr (!BKC && FN > 1) {
-                if (vec_store) {
-                    typedef typename FVec<FN>::type VT;
-                    VT *dst = reinterpret_cast<VT *>(crow + n0 + wn0 + FN * j);
-                    VT v;
-                    if (accumulate) v = *dst;
-#pragma unroll
-                    for (int fn = 0; fn < FN; ++fn) {
-                        float x = acc[fm][fn][r];
-                        if (accumulate) x = v[fn] + x;
-                        if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
-                        v[fn] = zn_activate(x, act);
-                    }
-                    *dst = v;
-                    continue;
-                }
-            }
-            {
-#pragma unroll
-                for (int fn = 0; fn < FN; ++fn) {
-                    const int col = n0 + wn0 + (BKC ? 32 * fn + j : FN * j + fn);
-                    if (col >= p.n) continue;
-                    float x = acc[fm][fn][r];
-                    if (accumulate) x = crow[col] + x;
-                    if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
-                    crow[col] = zn_activate(x, act);
-                }
-            }
-        }
-    }
-}
-
-template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
-__device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
-                                           int64_t bz, int m0, int n0, int wm0, int wn0, int lane, int slice) {
-    if constexpr (BM * BN >= 128 * 128) {
-        store_tile_act<BM, BN, WM, WN, AK, BKC, -1>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
-        return;
-    }
-    switch (p.splits > 1 ? 0 : p.act) {  // split-K slices store raw partial sums
-    case 1: store_tile_act<BM, BN, WM, WN, AK, BKC, 1>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
-    case 2: store_tile_act<BM, BN, WM, WN, AK, BKC, 2>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
-    case 3: store_tile_act<BM, BN, WM, WN, AK, BKC, 3>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
-    default: store_tile_act<BM, BN, WM, WN, AK, BKC, 0>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
-    }
-}
-
-// The GEMM main loop: two LDS stages filled by DMA (WA/WB = 16: 16-byte
-// loads for aligned operands, 4: 4-byte loads otherwise; G != kGNone gathers
-// B, ZnGather).  Iteration kt waits
-// for its stage (vmcnt(0) + barrier), refills the other stage with slice
-// kt + 1, then computes slice kt while that load is in flight.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, int G = kGNone>
-__device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) {
-    constexpr bool CONV = G == kGIm2col || G == kGIm2col4;
-    constexpr int GW = G == kGIm2col4 ? 16 : 4;
-    constexpr bool CONVT = G == kGTransposed, CONVW = G == kGWeight, NHWC = G == kGNhwc, NHWCW = G == kGNhwcW;
-    constexpr int NT = WM * WN * kWave;
-    constexpr int WTM = BM / WM, WTN = BN / WN;
-    constexpr int FM = WTM / 32, FN = WTN / 32;
-    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    static_assert(!CONV || (!BKC && WB == 4), "the convolution operand is X-contiguous and gathered");
-    static_assert(!CONVT || (BKC && WB == 16), "the transposed-convolution operand is K-contiguous");
-    static_assert(!CONVW || (BKC && WB == 16), "the weight-gradient operand is K-contiguous");
-    static_assert(!NHWC || (BKC && WB == 16), "the NHWC im2col operand is K-contiguous");
-    static_assert(!NHWCW || (!BKC && WB == 16), "the NHWC weight-gradient operand is X-contiguous");
-    typedef DmaStage<BM, BK, NT, AK, WA> SA;
-    typedef DmaStage<BN, BK, NT, BKC, WB> SB;
-    typedef ConvGatherStage<BN, BK, NT> SC;
-    typedef ConvGather16Stage<BN, BK, NT> SC16;
-    typedef ConvTGatherStage<BN, BK, NT> ST;
-    typedef ConvWGatherStage<BN, BK, NT> SW;
-    typedef ConvNhwcGatherStage<BN, BK, NT> SN;
-    typedef ConvNhwcWGatherStage<BN, BK, NT> SNW;
-    __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
-    __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
-
-    const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
-    int tm, tn, slice;
-    tile_coords(p, tm, tn, slice, wg);
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int64_t bz = blockIdx.y;  // 0 in grouped launches
-    const float *ga = p.a + bz * p.stride_a;
-    const float *gb = p.b + bz * p.stride_b;
-
-    zn_f32x16 acc[FM][FN];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-
-    const int kbeg = slice * p.k_chunk;
-    const int kend = min(p.k, kbeg + p.k_chunk);
-    const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-    const int lda = (int)p.lda, ldb = (int)p.ldb;
-    // 16-byte staging reads whole float4s: the last row's extent is rounded
-    // up to 4 floats (rows that are whole float4s, or packed with a zero tail)
-    constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
-    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
-    const uint32_t b_bytes =
-        (CONVW || NHWCW) ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
-        : (CONV || CONVT || NHWC) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
-             : (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(ga, a_bytes);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(gb, b_bytes);
-
-    typename SC::Lane cl{};
-    typename SC16::Lane cl16{};
-    typename SC16::Patch patch;
-    patch.mask = 0;
-    if constexpr (CONV && GW == 4 && SC::kFixedN) cl = SC::lane_setup(p.conv, n0, p.n, wave, lane);
-    if constexpr (CONV && GW == 16) cl16 = SC16::lane_setup(p.conv, n0, p.n, lane);
-    typename SW::Lane clw{};
-    typename SW::Patch wpatch;
-    wpatch.mask = 0;
-    if constexpr (CONVW) clw = SW::lane_setup(p.conv, n0, p.n, wave, lane);
-    typename SN::Lane cln{};
-    if constexpr (NHWC) cln = SN::lane_setup(p.conv, n0, p.n, wave, lane);
-    typename SNW::Lane clnw{};
-    if constexpr (NHWCW) clnw = SNW::lane_setup(p.conv, n0, p.n, lane);
-    auto issue_b = [&](float *lds, int k0) {
-        if constexpr (NHWC)
-            SN::issue(rb, lds, p.conv, cln, k0, kend, wave, lane);
-        else if constexpr (NHWCW)
-            SNW::issue(rb, lds, p.conv, clnw, k0, kend, wave);
-        else if constexpr (CONVW)
-            SW::issue(rb, gb, lds, p.conv, clw, k0, kend, wave, lane, wpatch);
-        else if constexpr (CONVT)
-            ST::issue(rb, lds, p.conv, n0, k0, p.n, kend, wave, lane);
-        else if constexpr (CONV && GW == 16)
-            SC16::issue(rb, gb, lds, p.conv, cl16, k0, kend, wave, lane, patch);
-        else if constexpr (CONV)
-            SC::issue(rb, lds, p.conv, cl, n0, k0, p.n, kend, wave, lane);
-        else
-            SB::issue(rb, lds, ldb, n0, k0, p.n, kend, wave, lane);
-    };
-    if (ktiles > 0) {
-        SA::issue(ra, lds_a[0], lda, m0, kbeg, p.m, kend, wave, lane);
-        issue_b(lds_b[0], kbeg);
-    }
-    for (int kt = 0; kt < ktiles; ++kt) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of slice kt is in LDS
-        if constexpr (CONV && GW == 16) SC16::apply(lds_b[kt & 1], patch, wave, lane);
-        if constexpr (CONVW) SW::apply(lds_b[kt & 1], wpatch, wave, lane);
-        __syncthreads();  // every wave's part is; every wave is done reading slice kt - 1
-        const int cur = kt & 1;
-        if (kt + 1 < ktiles) {
-            SA::issue(ra, lds_a[cur ^ 1], lda, m0, kbeg + (kt + 1) * BK, p.m, kend, wave, lane);
-            issue_b(lds_b[cur ^ 1], kbeg + (kt + 1) * BK);
-        }
-        const float *la = lds_a[cur];
-        const float *lb = lds_b[cur];
-#pragma unroll
-        for (int kg = 0; kg < BK; kg += 8) {
-            float fa[FM][4], fb[FN][4];
-            read_frags_dma<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
-            read_frags_dma<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-                    for (int fn = 0; fn < FN; ++fn)
-                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
-        }
-    }
-    store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
-}
-
-// Intra-workgroup split-K, for problems of few tiles and long K: each of the
-// KS waves of a workgroup multiplies the whole BM x BN tile over its own
-// contiguous range of K (the ranges of a K split into KS slices of whole BK
-// multiples), staging its operands by DMA into two private LDS stages, so
-// the main loop has no barrier: a wave waits only for its own loads.  The
-// partial tiles then meet in LDS and are summed in wave order, 0 to KS - 1,
-// as the split-K reduce sums its slices (deterministic), and the epilogue
-// (C_old, bias, activation) runs on the sums; wave w finishes the (row
-// block, register) items w, w + KS, ...  No workspace, no second launch.
-//
-// `lds` holds KS private regions of two A and two B stages each
-// (KS * 2 * (BM + BN) * BK floats); the partial tiles reuse it.
-template <int BM, int BN, int BK, int KS, bool AK, bool BKC, int WA, int WB, int ACT>
-__device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int wg = -1) {
-    constexpr int FM = BM / 32, FN = BN / 32;
-    typedef DmaStage<BM, BK, kWave, AK, WA> SA;
-    typedef DmaStage<BN, BK, kWave, BKC, WB> SB;
-    constexpr int kRegion = 2 * (SA::kFloats + SB::kFloats);
-    static_assert(FM * FN * 16 * kWave <= kRegion, "a wave's partial tile fits in its staging region");
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
-    float *region = lds + wave * kRegion;
-    float *lds_a[2] = {region, region + SA::kFloats};
-    float *lds_b[2] = {region + 2 * SA::kFloats, region + 2 * SA::kFloats + SB::kFloats};
-
-    const int pid = wg >= 0 ? wg : (int)blockIdx.x;  // wg >= 0: this workgroup's tile in a grouped launch
-    const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int64_t bz = wg >= 0 ? 0 : blockIdx.y;
-    const int chunk = ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
-    const int kbeg = min(p.k, wave * chunk);
-    const int kend = min(p.k, kbeg + chunk);
-    const int ktiles = (kend - kbeg + BK - 1) / BK;
-    const int lda = (int)p.lda, ldb = (int)p.ldb;
-    constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
-    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
-    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + bz * p.stride_a, a_bytes);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + bz * p.stride_b, b_bytes);
-
-    zn_f32x16 acc[FM][FN];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-    if (ktiles > 0) {
-        SA::issue(ra, lds_a[0], lda, m0, kbeg, p.m, kend, 0, lane);
-        SB::issue(rb, lds_b[0], ldb, n0, kbeg, p.n, kend, 0, lane);
-    }
-    for (int kt = 0; kt < ktiles; ++kt) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // slice kt is in this wave's stage
-        const int cur = kt & 1;
-        if (kt + 1 < ktiles) {  // the other stage was last read by slice kt - 1, whose MFMAs consumed those reads
-            SA::issue(ra, lds_a[cur ^ 1], lda, m0, kbeg + (kt + 1) * BK, p.m, kend, 0, lane);
-            SB::issue(rb, lds_b[cur ^ 1], ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, 0, lane);
-        }
-#pragma unroll
-        for (int kg = 0; kg < BK; kg += 8) {
-            float fa[FM][4], fb[FN][4];
-            read_frags_dma<BM, BK, FM, AK>(lds_a[cur], 0, kg, lane, fa);
-            read_frags_dma<BN, BK, FN, BKC>(lds_b[cur], 0, kg, lane, fb);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-                    for (int fn = 0; fn < FN; ++fn)
-                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
-        }
-    }
-
-    // partial tiles to LDS: part[wave][fm][fn][r][lane], lanes contiguous
-    __syncthreads();  // every wave is done with every staging region
-    float *part = lds + wave * (FM * FN * 16 * kWave);
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) part[((fm * FN + fn) * 16 + r) * kWave + lane] = acc[fm][fn][r];
-    __syncthreads();
-
-    float *gc = p.c + bz * p.stride_c;
-    const int64_t ldc = p.ldc;
-    const int j = lane & 31, h = lane >> 5;
-    const bool has_bias = p.bias != nullptr;
-    const bool vec = !BKC && FN > 1 && p.vec_c != 0;
-    constexpr int kPart = FM * FN * 16 * kWave;
-    for (int item = wave; item < FM * 16; item += KS) {
-        const int fm = item >> 4, r = item & 15;
-        const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
-        const int row = m0 + (AK ? 32 * fm + bi : FM * bi + fm);
-        if (row >= p.m) continue;
-        float *crow = gc + (int64_t)row * ldc;
-        const float rbias = has_bias && p.bias_rows ? p.bias[row] : 0.0f;
-        float v[FN];
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            const int off = ((fm * FN + fn) * 16 + r) * kWave + lane;
-            float x = lds[off];
-#pragma unroll
-            for (int w = 1; w < KS; ++w) x = x + lds[w * kPart + off];
-            v[fn] = x;
-        }
-        if constexpr (!BKC && FN > 1) {
-            const int col0 = n0 + FN * j;
-            if (vec && col0 + FN <= p.n) {
-                typedef typename FVec<FN>::type VT;
-                VT *dst = reinterpret_cast<VT *>(crow + col0);
-                VT o;
-                if (p.accumulate) o = *dst;
-#pragma unroll
-                for (int fn = 0; fn < FN; ++fn) {
-                    float x = v[fn];
-                    if (p.accumulate) x = o[fn] + x;
-                    if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col0 + fn]);
-                    o[fn] = zn_activate(x, ACT);
-                }
-                *dst = o;
-                continue;
-            }
-        }
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            const int col = n0 + (BKC ? 32 * fn + j : FN * j + fn);
-            if (col >= p.n) continue;
-            float x = v[fn];
-            if (p.accumulate) x = crow[col] + x;
-            if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col]);
-            crow[col] = zn_activate(x, ACT);
-        }
-    }
-}
-
-// Store instructions a wave issues for a tile that lies wholly inside C:
-// one per (row block, accumulator register) on the vector-store path of an
-// X-contiguous B, one per element column otherwise (fewest of the two, since
-// vec_c decides at run time).  Capped at the 6-bit vmcnt field.
-template <int FM, int FN, bool BKC>
-constexpr int interior_stores() {
-    return (!BKC && FN > 1 ? FM * 16 : FM * 16 * FN) < 63 ? (!BKC && FN > 1 ? FM * 16 : FM * 16 * FN) : 63;
-}
-
-// Persistent plain GEMM (unsplit, one or more problems): workgroup g takes
-// the work items g, g + G, g + 2G, ... (G = gridDim.x) of the problem-major,
-// row-major (problem, tile) order, and the two-stage LDS pipeline runs on
-// across tile boundaries: the first slice of the next tile is in flight
-// while the last slice of the current one is multiplied and its results are
-// stored, so no tile waits for its first load or a fresh dispatch.  The
-// activation is a template argument (the kernel dispatches once at entry).
-//
-// The first wait of a tile must cover that prefetch but not the stores
-// issued after it.  Vector memory operations of a wave retire in issue order
-// (the compiler's own waits rely on it: a load followed by two stores is
-// awaited with vmcnt(2)), so after a tile that lay wholly inside C, whose
-// epilogue issued at least S = interior_stores() stores after the prefetch,
-// vmcnt(S) leaves only those stores in flight; after an edge tile (fewer
-// stores) it waits for everything.
-// `lds` holds the two A stages, then the two B stages (2 * (BM + BN) * BK
-// floats, 1 KB aligned), declared by the kernel once for all activations.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, int ACT>
-__device__ __forceinline__ void gemm_persistent(const ZnGemmArgs &p, float *lds) {
-    constexpr int NT = WM * WN * kWave;
-    constexpr int WTM = BM / WM, WTN = BN / WN;
-    constexpr int FM = WTM / 32, FN = WTN / 32;
-    constexpr int S = interior_stores<FM, FN, BKC>();
-    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    typedef DmaStage<BM, BK, NT, AK, WA> SA;
-    typedef DmaStage<BN, BK, NT, BKC, WB> SB;
-    float(*lds_a)[SA::kFloats] = reinterpret_cast<float(*)[SA::kFloats]>(lds);
-    float(*lds_b)[SB::kFloats] = reinterpret_cast<float(*)[SB::kFloats]>(lds + 2 * SA::kFloats);
-
-    const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
-    const int ntiles = p.tiles_m * p.tiles_n;
-    const int total = ntiles * p.batch;
-    const int step = gridDim.x;
-    int w = blockIdx.x;
-    if (w >= total) return;  // the host launches at most `total` workgroups
-
-    const int ktiles = (p.k + BK - 1) / BK;  // >= 1: the host sends K = 0 to the plain kernels
-    const int lda = (int)p.lda, ldb = (int)p.ldb;
-    constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
-    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
-    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
-
-    // work item -> problem and tile origin (wave-uniform)
-    auto decode = [&](int wi, int &bz, int &m0, int &n0) {
-        bz = wi / ntiles;
-        const int pid = wi - bz * ntiles;
-        const int tm = pid / p.tiles_n;
-        m0 = tm * BM;
-        n0 = (pid - tm * p.tiles_n) * BN;
-    };
-    auto issue = [&](int bz, int m0, int n0, int k0, int st) {
-        SA::issue(make_rsrc(p.a + (int64_t)bz * p.stride_a, a_bytes), lds_a[st], lda, m0, k0, p.m, p.k, wave, lane);
-        SB::issue(make_rsrc(p.b + (int64_t)bz * p.stride_b, b_bytes), lds_b[st], ldb, n0, k0, p.n, p.k, wave, lane);
-    };
-
-    zn_f32x16 acc[FM][FN];
-    {
-        int bz, m0, n0;
-        decode(w, bz, m0, n0);
-        issue(bz, m0, n0, 0, 0);
-    }
-    int stage = 0;
-    bool after_interior = false;  // the previous tile's epilogue issued >= S stores after the prefetch
-    for (;;) {
-        int bz, m0, n0;
-        decode(w, bz, m0, n0);
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-            for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-        const bool has_next = w + step < total;
-        for (int kt = 0; kt < ktiles; ++kt) {
-            if (kt == 0 && after_interior)
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(S) : "memory");  // the prefetch has landed
-            else
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();  // every wave's part of this stage is in LDS; the other stage is free
-            if (kt + 1 < ktiles) {
-                issue(bz, m0, n0, (kt + 1) * BK, stage ^ 1);
-            } else if (has_next) {  // the next tile's first slice
-                int bz2, m2, n2;
-                decode(w + step, bz2, m2, n2);
-                issue(bz2, m2, n2, 0, stage ^ 1);
-            }
-            const float *la = lds_a[stage];
-            const float *lb = lds_b[stage];
-#pragma unroll
-            for (int kg = 0; kg < BK; kg += 8) {
-                float fa[FM][4], fb[FN][4];
-                read_frags_dma<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
-                read_frags_dma<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-#pragma unroll
-                    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-                        for (int fn = 0; fn < FN; ++fn)
-                            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
-            }
-            stage ^= 1;
-        }
-        store_tile_act<BM, BN, WM, WN, AK, BKC, ACT>(p, acc, bz, m0, n0, wm0, wn0, lane, 0);
-        if (!has_next) break;
-        after_interior = m0 + BM <= p.m && n0 + BN <= p.n;
-        w += step;
-    }
-}
-
-}  // namespace
+// Exported fp32 GEMM kernels for gfx950: the plain, persistent and
+// intra-workgroup split-K GEMMs, the split-K reduce and the grouped Dense
+// backward launches (device code in gemm_core.h).
+#include "gemm_core.h"
 
 // Exported kernels: zn_sgemm_<layout>_<tile>[_v].  Layout letters follow
 // the reference: nn = Backend.matMul, nt = matMulTransposeB, tn =
@@ -1073,100 +78,6 @@ ZN_GEMMP_TILE(x, 256, 128, 16, 4, 2, 1)
 ZN_GEMMP_TILE(l, 128, 128, 16, 2, 2, 4)
 ZN_GEMMP_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_GEMMP_TILE(m, 64, 64, 32, 2, 2, 1)
-
-// Implicit-GEMM convolution, per image b = blockIdx.y:
-// out_b[OC][OH*OW] = W[OC][K] . im2col(input_b)^T (+ bias[oc]), an NN GEMM
-// whose B operand is gathered from the NCHW input (ZnConvGeom).  _v: W rows
-// are 16-byte aligned; _g: the input is gathered in chunks of 4 pixels with
-// 16-byte loads (stride_w == 1, out_w % 4 == 0), otherwise element by element.
-#define ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, G, SUFFIX)                             \
-    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_conv_nn_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, true, false, WA, 4, G>(p);                              \
-    }
-#define ZN_CONV_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, kGIm2col, _v)                             \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, kGIm2col, )                                \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, kGIm2col4, _v_g)                          \
-    ZN_CONV_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, kGIm2col4, _g)
-
-ZN_CONV_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_CONV_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_CONV_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_CONV_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_CONV_TILE(s, 32, 32, 32, 1, 1, 1)
-
-// Input gradient of a stride-1 convolution, per image b = blockIdx.y:
-// grad_input_b[C][H*W] = W'[C][K] . B^T, NT, W' = weights regrouped as
-// [ic][(kh*kW + kw)*OC + oc] and B gathered from grad_output rows
-// (ConvTGatherStage).  _v: W' rows are 16-byte aligned.
-#define ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
-    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convt_nt_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, true, true, WA, 16, kGTransposed>(p);                  \
-    }
-#define ZN_CONVT_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
-    ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
-    ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
-
-ZN_CONVT_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_CONVT_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_CONVT_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_CONVT_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_CONVT_TILE(s, 32, 32, 32, 1, 1, 1)
-
-// Weight gradient of a convolution with stride_w == 1 and out_w % 4 == 0:
-// grad_W[OC][taps] = go2^T . col with K = the output pixels of all images,
-// A = grad_output read as [pixels][OC] rows (X-contiguous, like TN) and
-// B = col gathered from the NCHW input (ConvWGatherStage).  _v: OC % 4 == 0
-// and grad_output 16-byte aligned.
-#define ZN_CONVW_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
-    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convw_tn_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, false, true, WA, 16, kGWeight>(p);                     \
-    }
-#define ZN_CONVW_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
-    ZN_CONVW_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
-    ZN_CONVW_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
-
-ZN_CONVW_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_CONVW_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_CONVW_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_CONVW_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_CONVW_TILE(s, 32, 32, 32, 1, 1, 1)
-
-// Convolution forward on an NHWC copy of the input, per image b = blockIdx.y:
-// out_b[OC][OH*OW] = W[OC][K] . B^T (+ bias[oc]), NT, W in the im2col K order
-// and B gathered 4 channels at a time (ConvNhwcGatherStage, C % 4 == 0, any
-// stride).  _v: W rows are 16-byte aligned.
-#define ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
-    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convf_nt_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, true, true, WA, 16, kGNhwc>(p);                        \
-    }
-#define ZN_CONVF_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
-    ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
-    ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
-
-ZN_CONVF_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_CONVF_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_CONVF_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_CONVF_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_CONVF_TILE(s, 32, 32, 32, 1, 1, 1)
-
-// Weight gradient from an NHWC copy of the input: grad_W[OC][taps] =
-// go2^T . col, TN, K = the output pixels of all images, B gathered 4 channels
-// at a time (ConvNhwcWGatherStage, C % 4 == 0, any stride).  _v: OC % 4 == 0
-// and grad_output 16-byte aligned.
-#define ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                               \
-    extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convwn_tn_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, false, false, WA, 16, kGNhwcW>(p);                     \
-    }
-#define ZN_CONVWN_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                             \
-    ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                      \
-    ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
-
-ZN_CONVWN_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_CONVWN_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_CONVWN_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_CONVWN_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_CONVWN_TILE(s, 32, 32, 32, 1, 1, 1)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not

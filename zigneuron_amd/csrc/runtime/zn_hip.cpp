@@ -57,6 +57,7 @@ constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", 
                                            "zn_weight_regroup", "zn_pack_rows", "zn_nchw_to_nhwc"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
+constexpr const char *kConvObject = "zn_conv_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
 constexpr const char *kAttnObject = "zn_attention_gfx950.hsaco";
 // Fused attention kernels by padded head dim (zn_attention_d<dim>[_v]).
@@ -132,6 +133,7 @@ struct zn_ctx {
     int device = -1;
     hipStream_t stream = nullptr;
     hipModule_t gemm_module = nullptr;
+    hipModule_t conv_module = nullptr;
     hipModule_t elt_module = nullptr;
     hipModule_t attn_module = nullptr;
     hipFunction_t attn[3][2] = {};             // fused attention [head dim 32/64/128][16-byte I/O]
@@ -993,6 +995,7 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     else
         dir = library_dir();
     const std::string gemm_path = dir + "/" + kGemmObject;
+    const std::string conv_path = dir + "/" + kConvObject;
     const std::string elt_path = dir + "/" + kEltObject;
     const std::string attn_path = dir + "/" + kAttnObject;
 
@@ -1020,6 +1023,10 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
         ctx->gemm_module = nullptr;
         return bail(ZN_ERR_CODE_OBJECT);
     }
+    if (hipModuleLoad(&ctx->conv_module, conv_path.c_str()) != hipSuccess) {
+        ctx->conv_module = nullptr;
+        return bail(ZN_ERR_CODE_OBJECT);
+    }
     if (hipModuleLoad(&ctx->elt_module, elt_path.c_str()) != hipSuccess) {
         ctx->elt_module = nullptr;
         return bail(ZN_ERR_CODE_OBJECT);
@@ -1042,23 +1049,23 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             for (int g = 0; g < 2; ++g) {
                 char name[64];
                 std::snprintf(name, sizeof(name), "zn_conv_nn_%s%s%s", kTiles[t].suffix, v ? "_v" : "", g ? "_g" : "");
-                if (hipModuleGetFunction(&ctx->conv[t][v][g], ctx->gemm_module, name) != hipSuccess)
+                if (hipModuleGetFunction(&ctx->conv[t][v][g], ctx->conv_module, name) != hipSuccess)
                     return bail(ZN_ERR_SYMBOL);
             }
     for (int t = 0; t < kNumTiles; ++t)
         for (int v = 0; v < 2; ++v) {
             char name[64];
             std::snprintf(name, sizeof(name), "zn_convt_nt_%s%s", kTiles[t].suffix, v ? "_v" : "");
-            if (hipModuleGetFunction(&ctx->convt[t][v], ctx->gemm_module, name) != hipSuccess)
+            if (hipModuleGetFunction(&ctx->convt[t][v], ctx->conv_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
             std::snprintf(name, sizeof(name), "zn_convw_tn_%s%s", kTiles[t].suffix, v ? "_v" : "");
-            if (hipModuleGetFunction(&ctx->convw[t][v], ctx->gemm_module, name) != hipSuccess)
+            if (hipModuleGetFunction(&ctx->convw[t][v], ctx->conv_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
             std::snprintf(name, sizeof(name), "zn_convf_nt_%s%s", kTiles[t].suffix, v ? "_v" : "");
-            if (hipModuleGetFunction(&ctx->convf[t][v], ctx->gemm_module, name) != hipSuccess)
+            if (hipModuleGetFunction(&ctx->convf[t][v], ctx->conv_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
             std::snprintf(name, sizeof(name), "zn_convwn_tn_%s%s", kTiles[t].suffix, v ? "_v" : "");
-            if (hipModuleGetFunction(&ctx->convwn[t][v], ctx->gemm_module, name) != hipSuccess)
+            if (hipModuleGetFunction(&ctx->convwn[t][v], ctx->conv_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
         }
     for (int l = 0; l < 3; ++l)
@@ -1144,6 +1151,7 @@ int zn_hip_destroy(zn_ctx *ctx) {
     if (ctx->ws) (void)hipFree(ctx->ws);
     ctx->ws = nullptr;
     if (ctx->gemm_module) (void)hipModuleUnload(ctx->gemm_module);
+    if (ctx->conv_module) (void)hipModuleUnload(ctx->conv_module);
     if (ctx->elt_module) (void)hipModuleUnload(ctx->elt_module);
     if (ctx->attn_module) (void)hipModuleUnload(ctx->attn_module);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
