@@ -204,13 +204,18 @@ def test_c5_im2col_conv_gemm(ctx):
     checksum_property(c, col, w.T, K, "conv")
 
 
+@pytest.mark.parametrize("path", ["auto", "prologue"])
 @pytest.mark.parametrize("act", ["linear", "relu", "sigmoid", "tanh"])
 @pytest.mark.parametrize("shape", [(256, 784, 128), (33, 17, 5), (4096, 1024, 1024), (1, 9, 300), (96, 200, 2048),
-                                   (2048, 64, 12)])
-def test_dense_backward_fused(ctx, act, shape):
+                                   (2048, 64, 12), (256, 128, 10)])
+def test_dense_backward_fused(ctx, act, shape, path):
     """zn_hip_dense_backward against the reference's four steps: the
     activation derivative bit-exact, grad_bias (+= onto a non-zero start)
-    within the GEMM tolerance, the NT / TN products componentwise."""
+    within the GEMM tolerance, the NT / TN products componentwise.  "auto"
+    runs small layers' GEMMs in one grouped launch of 32x32 tiles whose waves
+    split K; "prologue" (wave split off) the grouped launch of unsplit 64x64
+    tiles.  Both follow the prologue kernel."""
+    ctx.set_gemm_wave_split(-1 if path == "auto" else 0)
     batch, d_in, d_out = shape
     rng = np.random.default_rng(batch + d_in + d_out)
     x, w = uniform(rng, (batch, d_in)), uniform(rng, (d_in, d_out))
@@ -232,8 +237,11 @@ def test_dense_backward_fused(ctx, act, shape):
     assert_close(gw, oracle.matmul_tn(x, gaa, d_in, d_out, batch, threads=THREADS), "tn", x, gaa, d_in, d_out, batch,
                  what="grad_weights")
     # first layer: no grad_input; grad_weights is overwritten (deterministically), not accumulated
+    dgaa.fill(np.nan)
     ctx.dense_backward(act, dx, dw, dy, dgo, dgaa, None, dgw, dgb, batch, d_in, d_out)
     np.testing.assert_array_equal(dgw.download().reshape(d_in, d_out), gw)
+    np.testing.assert_array_equal(dgaa.download().reshape(batch, d_out), gaa)  # written without grad_input too
+    ctx.set_gemm_wave_split(-1)
     for buf in (dx, dw, dy, dgo, dgaa, dgi, dgw, dgb):
         buf.close()
 

@@ -745,6 +745,79 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
     store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
 }
 
+// The end of an intra-workgroup split-K tile (gemm_ksplit and the fused
+// Dense backward tile): the KS partial BM x BN tiles go to LDS (which the
+// staging no longer uses), each output is the sum of its partials in wave
+// order, and the epilogue applies C_old, the bias and the activation; wave w
+// finishes the (row block, register) items w, w + KS, ...
+template <int BM, int BN, int KS, bool AK, bool BKC, int ACT>
+__device__ __forceinline__ void ksplit_finish(const ZnGemmArgs &p, float *lds,
+                                              const zn_f32x16 (&acc)[BM / 32][BN / 32], int64_t bz, int m0, int n0,
+                                              int wave, int lane) {
+    constexpr int FM = BM / 32, FN = BN / 32;
+    // partial tiles to LDS: part[wave][fm][fn][r][lane], lanes contiguous
+    __syncthreads();  // every wave is done with every staging region
+    float *part = lds + wave * (FM * FN * 16 * kWave);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[((fm * FN + fn) * 16 + r) * kWave + lane] = acc[fm][fn][r];
+    __syncthreads();
+
+    float *gc = p.c + bz * p.stride_c;
+    const int64_t ldc = p.ldc;
+    const int j = lane & 31, h = lane >> 5;
+    const bool has_bias = p.bias != nullptr;
+    const bool vec = !BKC && FN > 1 && p.vec_c != 0;
+    constexpr int kPart = FM * FN * 16 * kWave;
+    for (int item = wave; item < FM * 16; item += KS) {
+        const int fm = item >> 4, r = item & 15;
+        const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
+        const int row = m0 + (AK ? 32 * fm + bi : FM * bi + fm);
+        if (row >= p.m) continue;
+        float *crow = gc + (int64_t)row * ldc;
+        const float rbias = has_bias && p.bias_rows ? p.bias[row] : 0.0f;
+        float v[FN];
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const int off = ((fm * FN + fn) * 16 + r) * kWave + lane;
+            float x = lds[off];
+#pragma unroll
+            for (int w = 1; w < KS; ++w) x = x + lds[w * kPart + off];
+            v[fn] = x;
+        }
+        if constexpr (!BKC && FN > 1) {
+            const int col0 = n0 + FN * j;
+            if (vec && col0 + FN <= p.n) {
+                typedef typename FVec<FN>::type VT;
+                VT *dst = reinterpret_cast<VT *>(crow + col0);
+                VT o;
+                if (p.accumulate) o = *dst;
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    float x = v[fn];
+                    if (p.accumulate) x = o[fn] + x;
+                    if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col0 + fn]);
+                    o[fn] = zn_activate(x, ACT);
+                }
+                *dst = o;
+                continue;
+            }
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const int col = n0 + (BKC ? 32 * fn + j : FN * j + fn);
+            if (col >= p.n) continue;
+            float x = v[fn];
+            if (p.accumulate) x = crow[col] + x;
+            if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col]);
+            crow[col] = zn_activate(x, ACT);
+        }
+    }
+}
+
 // Intra-workgroup split-K, for problems of few tiles and long K: each of the
 // KS waves of a workgroup multiplies the whole BM x BN tile over its own
 // contiguous range of K (the ranges of a K split into KS slices of whole BK
@@ -818,67 +891,7 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
         }
     }
 
-    // partial tiles to LDS: part[wave][fm][fn][r][lane], lanes contiguous
-    __syncthreads();  // every wave is done with every staging region
-    float *part = lds + wave * (FM * FN * 16 * kWave);
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) part[((fm * FN + fn) * 16 + r) * kWave + lane] = acc[fm][fn][r];
-    __syncthreads();
-
-    float *gc = p.c + bz * p.stride_c;
-    const int64_t ldc = p.ldc;
-    const int j = lane & 31, h = lane >> 5;
-    const bool has_bias = p.bias != nullptr;
-    const bool vec = !BKC && FN > 1 && p.vec_c != 0;
-    constexpr int kPart = FM * FN * 16 * kWave;
-    for (int item = wave; item < FM * 16; item += KS) {
-        const int fm = item >> 4, r = item & 15;
-        const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
-        const int row = m0 + (AK ? 32 * fm + bi : FM * bi + fm);
-        if (row >= p.m) continue;
-        float *crow = gc + (int64_t)row * ldc;
-        const float rbias = has_bias && p.bias_rows ? p.bias[row] : 0.0f;
-        float v[FN];
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            const int off = ((fm * FN + fn) * 16 + r) * kWave + lane;
-            float x = lds[off];
-#pragma unroll
-            for (int w = 1; w < KS; ++w) x = x + lds[w * kPart + off];
-            v[fn] = x;
-        }
-        if constexpr (!BKC && FN > 1) {
-            const int col0 = n0 + FN * j;
-            if (vec && col0 + FN <= p.n) {
-                typedef typename FVec<FN>::type VT;
-                VT *dst = reinterpret_cast<VT *>(crow + col0);
-                VT o;
-                if (p.accumulate) o = *dst;
-#pragma unroll
-                for (int fn = 0; fn < FN; ++fn) {
-                    float x = v[fn];
-                    if (p.accumulate) x = o[fn] + x;
-                    if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col0 + fn]);
-                    o[fn] = zn_activate(x, ACT);
-                }
-                *dst = o;
-                continue;
-            }
-        }
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            const int col = n0 + (BKC ? 32 * fn + j : FN * j + fn);
-            if (col >= p.n) continue;
-            float x = v[fn];
-            if (p.accumulate) x = crow[col] + x;
-            if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col]);
-            crow[col] = zn_activate(x, ACT);
-        }
-    }
+    ksplit_finish<BM, BN, KS, AK, BKC, ACT>(p, lds, acc, bz, m0, n0, wave, lane);
 }
 
 // Store instructions a wave issues for a tile that lies wholly inside C:
