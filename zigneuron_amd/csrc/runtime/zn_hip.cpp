@@ -351,25 +351,44 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t bat
     return kTileM;
 }
 
-// Split-K factor, from the same measurements.  Each split costs a pass of
-// the reduce kernel (a few us), so:
-//  * 2*CUs or more (problem, tile) pairs: no split;
-//  * CUs/2 .. 2*CUs pairs: split only deep K, keeping >= 1024 per slice
-//    (1024x1024x4096 TN: 4 slices; 1000^3: none);
-//  * fewer pairs: aim at 2*CUs workgroups with >= 128 of K per slice
-//    (>= 64 when there are at most 8 tiles).
-// At most 16 slices, 64 when K >= 16384 (long reductions such as a conv
-// weight gradient over a whole batch).
+// Split-K factor.  A problem of at least half a workgroup per CU takes the
+// split S that minimises its makespan, ceil(T*S/CUs) workgroups on the
+// busiest CU each running K/S: min over S of ceil(T*S/CUs) / S (a larger S
+// must gain at least 5%, which the reduce pass costs: 3000^3 TN is 446 us
+// unsplit against 467 us in 3 for a 3.7% smaller makespan), with at
+// least 768 of K per slice (below that the reduce costs more than it saves:
+// 1000^3 26.0 us unsplit, 30.3 us in 2) and at most 16 slices.  On a tie the
+// smaller S wins, except that an S giving two or more workgroups per CU beats
+// one that leaves a single workgroup (4 waves) per CU (1024x1024x4096 TN:
+// 84.7 us unsplit, 78 us in 2-4).  Measured on MI355X: 1000x600x3000 TN
+// 59 -> 44 us (2 -> 3 slices), 1536^3 NN 81.6 -> 74.3 us (1 -> 3),
+// 4097^2 x 4096 NN 1495 -> 1256 us (1 -> 3), 1280^2 x 2560 NN 91.8 -> 83.6 us
+// (1 -> 3).  The partial sums may take at most 256 MiB of workspace.
+// Fewer tiles than half the CUs: aim at 2*CUs workgroups with >= 128 of K
+// per slice (>= 64 when there are at most 8 tiles), at most 16 slices, 64
+// when K >= 16384 (long reductions such as a conv weight gradient over a
+// whole batch).
 int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k, int64_t batch) {
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     const TileShape &ts = kTiles[tile];
     const int64_t tiles = cdiv(m, ts.bm) * cdiv(n, ts.bn) * batch;
-    if (tiles >= 2 * cus) return 1;
-    int64_t splits;
-    if (tiles >= cus / 2)
-        splits = std::min<int64_t>(4 * cus / tiles, k / 1024);
-    else
-        splits = std::min<int64_t>(2 * cus / tiles, k / (tiles <= 8 ? 64 : 128));
+    if (tiles >= cus / 2) {
+        int64_t best = 1, best_load = cdiv(tiles, cus);  // workgroups on the busiest CU
+        const int64_t max_s = std::min<int64_t>(16, k / 768);
+        constexpr int64_t kMaxWorkspaceFloats = (int64_t)1 << 26;  // 256 MiB of partial sums
+        for (int64_t sp = 2; sp <= max_s && sp * batch * m * n <= kMaxWorkspaceFloats; ++sp) {
+            const int64_t load = cdiv(tiles * sp, cus);
+            // load / sp at least 5% below best_load / best (the reduce pass costs a few percent)
+            const bool faster = load * best * 20 < best_load * sp * 19;
+            const bool tie_more_waves = load * best == best_load * sp && best_load < 2 && load >= 2;
+            if (faster || tie_more_waves) {
+                best = sp;
+                best_load = load;
+            }
+        }
+        return (int)best;
+    }
+    int64_t splits = std::min<int64_t>(2 * cus / tiles, k / (tiles <= 8 ? 64 : 128));
     const int64_t cap = k >= 16384 ? 64 : 16;
     if (splits > cap) splits = cap;
     return splits < 2 ? 1 : (int)splits;
