@@ -95,3 +95,36 @@ def test_persistent_against_oracle(ctx):
     (plain, pers), a, b, c0, _ = _both(ctx, "nt", m, n, k, 1, "128x128", acc=True, seed=3)
     ref = ref_gemm("nt", a[0], b[0], m, n, k, c0=c0[0], accumulate=True)
     assert_close(pers[0], ref, "nt", a[0], b[0], m, n, k, c0=c0[0], accumulate=True, what="persistent")
+
+
+@pytest.mark.parametrize("layout,m,n,k", [("nn", 4097, 1023, 777), ("tn", 2049, 2048, 512), ("nt", 4100, 1000, 256)])
+def test_row_tail_split(ctx, layout, m, n, k):
+    """A last row of 64x64 tiles that would put one more workgroup on the
+    busiest CU runs as a second, small GEMM: the rows above it are
+    bit-identical to the unsplit launch (forcing the tile turns the row split
+    off), and sampled rows, the tail included, match the oracle."""
+    rng = np.random.default_rng(m + n)
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    outs = []
+    for tile in ("auto", "64x64"):
+        announce(f"row tail {layout} {m}x{n}x{k} tile {tile}")
+        ctx.set_gemm_tile(tile)
+        dc = ctx.alloc(m * n).fill(np.nan)
+        ctx.sgemm(layout, m, n, k, da, lda, db, ldb, dc, n)
+        outs.append(dc.download().reshape(m, n))
+        dc.close()
+    ctx.set_gemm_tile("auto")
+    da.close()
+    db.close()
+    split, whole = outs
+    main = (m - 1) // 64 * 64
+    assert np.isfinite(split).all()
+    np.testing.assert_array_equal(split[:main].view(np.uint32), whole[:main].view(np.uint32))
+    rows = np.unique(np.r_[np.linspace(0, m - 1, 16).astype(int), np.arange(main, m)])
+    a_rows = np.ascontiguousarray(a[:, rows] if layout == "tn" else a[rows])
+    ref = ref_gemm(layout, a_rows, b, len(rows), n, k)
+    assert_close(split[rows], ref, layout, a_rows, b, len(rows), n, k, what="row tail")

@@ -430,7 +430,8 @@ constexpr double kPackMinMacs = 536870912.0;  // 2^29 multiply-adds: the copy co
 int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                    int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
                    int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows,
-                   const ZnConvGeom *conv = nullptr, GatherMode mode = kGatherIm2col) {
+                   const ZnConvGeom *conv = nullptr, GatherMode mode = kGatherIm2col, bool split_rows = true,
+                   int padded = 0) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
     if (layout < ZN_LAYOUT_NN || layout > ZN_LAYOUT_TN) return ZN_ERR_INVALID_ARG;
     if (act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
@@ -484,7 +485,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // 16-byte staging); the padding adds exact zeros past K, which the 4-byte
     // path stages as well, so the result is the same.
     Lease pack_a(ctx), pack_b(ctx);
-    bool a_packed = false, b_packed = false;  // rows padded with zeros to whole float4s
+    // rows padded with zeros to whole float4s (here, or by the caller: padded bit 0 = A, bit 1 = B)
+    bool a_packed = (padded & 1) != 0, b_packed = (padded & 2) != 0;
     if (!conv && batch == 1 && k > 0 && (double)m * n * k >= kPackMinMacs) {
         const bool a_vec = aligned16(a) && lda % 4 == 0 && a_row % 4 == 0;
         const bool b_vec = aligned16(b) && ldb % 4 == 0 && b_row % 4 == 0;
@@ -511,8 +513,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
             return ZN_OK;
         };
         int rcp;
-        if (!a_vec && (rcp = pack(pack_a, a, lda, a_outer, a_row, a_packed))) return rcp;
-        if (!b_vec && (rcp = pack(pack_b, b, ldb, b_outer, b_row, b_packed))) return rcp;
+        if (!a_vec && !a_packed && (rcp = pack(pack_a, a, lda, a_outer, a_row, a_packed))) return rcp;
+        if (!b_vec && !b_packed && (rcp = pack(pack_b, b, ldb, b_outer, b_row, b_packed))) return rcp;
     }
 
     ZnGemmArgs args;
@@ -555,6 +557,28 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     if (rc) return rc;
     constexpr int64_t kMaxGridY = 65535;
     const int64_t chunk_batch = batch < kMaxGridY ? batch : kMaxGridY;
+    // Row tail: when the last row of tiles is what puts one more workgroup on
+    // the busiest CU (1040 tiles of 64x64 for 4097 x 1023: 5 on some CUs, 4
+    // on the rest), the rows above it run as one GEMM and the tail rows as a
+    // second, small one (usually the intra-workgroup split-K kernel).  Each
+    // part is an ordinary GEMM of its rows, so no element changes its K order
+    // in the first part.
+    if (split_rows && !conv && batch == 1 && k > 0 && ctx->forced_tile < 0 && ctx->forced_splits == 0 &&
+        ctx->forced_wave_split < 0 && tiles_m >= 2) {
+        const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+        const int64_t per_cu = cdiv(ntiles, cus);
+        if (per_cu >= 2 && cdiv(ntiles - tiles_n, cus) < per_cu) {
+            const int64_t m_main = (tiles_m - 1) * ts.bm;
+            const int pad = (a_packed ? 1 : 0) | (b_packed ? 2 : 0);  // the packed copies stay leased until return
+            rc = gemm_launch_ex(ctx, layout, m_main, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias, act,
+                                bias_rows, nullptr, mode, false, pad);
+            if (rc) return rc;
+            const float *a_tail = layout == ZN_LAYOUT_TN ? a + m_main : a + m_main * lda;
+            return gemm_launch_ex(ctx, layout, m - m_main, n, k, a_tail, lda, 0, b, ldb, 0, c + m_main * ldc, ldc, 0, 1,
+                                  accumulate, bias_rows ? bias + m_main : bias, act, bias_rows, nullptr, mode, false,
+                                  pad);
+        }
+    }
     int splits = ctx->forced_splits > 0 ? (int)std::min<int64_t>(ctx->forced_splits, std::max<int64_t>(1, k / ts.bk))
                                         : choose_splits(ctx, tile, m, n, k, batch);
     int64_t k_chunk = k;
