@@ -263,6 +263,44 @@ def test_backend_elementwise_helpers(backend):
     np.testing.assert_array_equal(gb, oracle.accumulate_bias(gb0, out))  # same row order: bit-exact
 
 
+def test_host_slice_staging_paths(ctx, backend):
+    """Host-slice calls take three routes by size: small ones stage their
+    inputs through one pinned block (one DMA) and, for small results, let the
+    kernel write straight into it; streaming elementwise ops run on the pinned
+    block itself; large ones copy through the pinned ring.  Every route must
+    give the device-pointer path's (or the oracle's) bits."""
+    rng = np.random.default_rng(44)
+    cases = [(100, 200, 300), (1024, 512, 64), (1500, 1400, 700)]  # zero-copy C, C by DMA, large
+    for m, n, k in cases:
+        a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+        bias, c0 = uniform(rng, (n,)), uniform(rng, (m, n))
+        announce(f"host-slice staging {m}x{n}x{k}")
+        c = np.empty(m * n, np.float32)
+        backend.matMulBiasRelu(a, b, bias, c, m, n, k)
+        np.testing.assert_array_equal(c.reshape(m, n), run_gemm(ctx, "nn", a, b, m, n, k, bias=bias, act="relu"))
+        c = c0.ravel().copy()
+        backend.matMulTransposeB(a, np.ascontiguousarray(b.T), c, m, n, k, True)
+        np.testing.assert_array_equal(c.reshape(m, n), run_gemm(ctx, "nt", a, np.ascontiguousarray(b.T), m, n, k,
+                                                                c0=c0, accumulate=True))
+    for rows, cols in ((30, 1000), (300, 1000), (1200, 1000)):  # zero-copy, copies, pinned ring
+        announce(f"host-slice elementwise {rows}x{cols}")
+        out, bias = uniform(rng, (rows, cols)), uniform(rng, (cols,))
+        o = out.ravel().copy()
+        backend.addBias(o, bias)
+        np.testing.assert_array_equal(o, oracle.add_bias(out, bias).ravel())
+        y = oracle.activation_forward("sigmoid", out.ravel())
+        got = np.empty_like(y)
+        backend.activationForward("sigmoid", out.ravel(), got)
+        assert np.all(np.abs(got - y) <= 2 * np.spacing(np.abs(y)) + 1e-45)
+        g, gi = uniform(rng, (rows * cols,)), np.empty(rows * cols, np.float32)
+        backend.activationBackward("tanh", y, g, gi)
+        np.testing.assert_array_equal(gi, oracle.activation_backward("tanh", y, g))
+        gb0 = uniform(rng, (cols,))
+        gb = gb0.copy()
+        backend.accumulateBias(gb, out.ravel())
+        np.testing.assert_array_equal(gb, oracle.accumulate_bias(gb0, out))
+
+
 # ------------------------------------------------------ strided batched
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
 def test_strided_batched_against_oracle(ctx, layout):
