@@ -97,6 +97,9 @@ def test_null_and_bad_arguments_without_device(lib):
     """Argument checks that run before any device call."""
     from zigneuron_amd import _lib
     assert lib.zn_hip_set_gemm_tile(None, 0) == _lib.ZN_ERR_INVALID_ARG
+    assert lib.zn_hip_set_gemm_splits(None, 0) == _lib.ZN_ERR_INVALID_ARG
+    assert lib.zn_hip_set_gemm_persistent(None, -1) == _lib.ZN_ERR_INVALID_ARG
+    assert lib.zn_hip_set_gemm_wave_split(None, 4) == _lib.ZN_ERR_INVALID_ARG
     assert lib.zn_hip_create(0, None, None) == _lib.ZN_ERR_INVALID_ARG
     assert lib.zn_hip_destroy(None) == _lib.ZN_OK
     assert lib.zn_hip_sgemm(None, 0, 1, 1, 1, None, 1, None, 1, None, 1, 0, None, 0) == _lib.ZN_ERR_INVALID_ARG

@@ -104,3 +104,15 @@ def test_policy_small_problems_against_oracle(ctx):
         got = _run(ctx, layout, m, n, k, 1, a[None], b[None], np.full((1, m, n), np.nan, np.float32), None, "linear",
                    False, m if layout == "tn" else k, k if layout == "nt" else n)[0]
         assert_close(got, ref_gemm(layout, a, b, m, n, k), layout, a, b, m, n, k, what="wave split policy")
+
+
+def test_tuning_hooks_reject_bad_values(ctx):
+    from zigneuron_amd import InvalidArgumentError
+    for bad in (1, 2, 5, 16, -2):
+        with pytest.raises(InvalidArgumentError):
+            ctx.set_gemm_wave_split(bad)
+    for bad in (2, -2):
+        with pytest.raises(InvalidArgumentError):
+            ctx.set_gemm_persistent(bad)
+    ctx.set_gemm_wave_split(-1)
+    ctx.set_gemm_persistent(-1)
