@@ -540,7 +540,9 @@ struct ConvNhwcWGatherStage {
 // more than repeating one).  ACT = -1 reads it at run time; the 128x128 and
 // 256x128 tiles keep that form (the specialised copies made the 8192^3 main
 // loop 0.9-1.3% slower in NN and NT).
-template <int BM, int BN, int WM, int WN, bool AK, bool BKC, int ACT>
+// STREAM: C is written with non-temporal stores (the persistent kernels,
+// whose short-K problems are bound by writing C).
+template <int BM, int BN, int WM, int WN, bool AK, bool BKC, int ACT, bool STREAM = false>
 __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
                                                int64_t bz, int m0, int n0, int wm0, int wn0, int lane, int slice) {
     constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
@@ -585,7 +587,10 @@ __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32
                         if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
                         v[fn] = zn_activate(x, act);
                     }
-                    *dst = v;
+                    if constexpr (STREAM)
+                        __builtin_nontemporal_store(v, dst);
+                    else
+                        *dst = v;
                     continue;
                 }
             }
@@ -597,7 +602,10 @@ __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32
                     float x = acc[fm][fn][r];
                     if (accumulate) x = crow[col] + x;
                     if (has_bias) x = x + (row_bias ? rb : bias_v[fn]);
-                    crow[col] = zn_activate(x, act);
+                    if constexpr (STREAM)
+                        __builtin_nontemporal_store(zn_activate(x, act), &crow[col]);
+                    else
+                        crow[col] = zn_activate(x, act);
                 }
             }
         }
@@ -918,6 +926,11 @@ constexpr int interior_stores() {
 // epilogue issued at least S = interior_stores() stores after the prefetch,
 // vmcnt(S) leaves only those stores in flight; after an edge tile (fewer
 // stores) it waits for everything.
+//
+// These problems are bound by writing C (C5 QK^T: K = 64, 512 MiB of C, at
+// 2 * 64 flops per 4 bytes written), so C goes out with non-temporal stores:
+// on MI355X that took the QK^T batch from 217 to 201 us.  The same stores in
+// the other kernels changed nothing beyond run-to-run noise.
 // `lds` holds the two A stages, then the two B stages (2 * (BM + BN) * BK
 // floats, 1 KB aligned), declared by the kernel once for all activations.
 template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, int ACT>
@@ -1008,7 +1021,7 @@ __device__ __forceinline__ void gemm_persistent(const ZnGemmArgs &p, float *lds)
             }
             stage ^= 1;
         }
-        store_tile_act<BM, BN, WM, WN, AK, BKC, ACT>(p, acc, bz, m0, n0, wm0, wn0, lane, 0);
+        store_tile_act<BM, BN, WM, WN, AK, BKC, ACT, true>(p, acc, bz, m0, n0, wm0, wn0, lane, 0);
         if (!has_next) break;
         after_interior = m0 + BM <= p.m && n0 + BN <= p.n;
         w += step;
