@@ -48,8 +48,10 @@ def uniform(rng, shape, lo=-1.0, hi=1.0):
 
 def time_launches(ctx, fn, steps, warmup, rounds=3):
     """Milliseconds per call from HIP events on the context stream: after the
-    warmup calls (and at least ~20 ms of device work, so clocks have settled),
-    the fastest of `rounds` timed runs of `steps` back-to-back calls."""
+    warmup calls (and about 100 ms of device work, so clocks have settled:
+    after the host-side set-up of a new configuration, the first ~40 ms of
+    launches ran up to 5% slower), the fastest of `rounds` timed runs of
+    `steps` back-to-back calls."""
     for _ in range(warmup):
         fn()
     ctx.sync()
@@ -58,7 +60,7 @@ def time_launches(ctx, fn, steps, warmup, rounds=3):
     fn()
     e1.record()
     first = max(e0.elapsed_ms(e1), 1e-3)
-    for _ in range(min(2000, int(20.0 / first))):
+    for _ in range(min(5000, int(100.0 / first))):
         fn()
     best = float("inf")
     for _ in range(rounds):

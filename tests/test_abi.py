@@ -60,7 +60,7 @@ def test_code_objects_hold_every_kernel():
     for blob in (gemm, conv, elt, attn):  # an offload bundle (hipcc --genco) or a bare ELF code object
         assert blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or blob[:4] == b"\x7fELF"
     for lay in ("nn", "nt", "tn"):
-        for t in ("x", "l", "n", "m", "s"):
+        for t in ("x", "l", "n", "m", "s", "r", "h"):
             for v in ("", "_v"):
                 assert f"zn_sgemm_{lay}_{t}{v}".encode() in gemm
         for t in ("x", "l", "n", "m"):

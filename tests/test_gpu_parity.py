@@ -416,7 +416,7 @@ def test_invalid_arguments_are_errors(ctx, backend):
 
 
 # ------------------------------------------------ every kernel variant
-TILES = ["256x128", "128x128", "128x64", "64x64", "32x32"]
+TILES = ["256x128", "128x128", "128x64", "64x64", "32x32", "128x128k32", "64x64k16"]
 
 
 @pytest.mark.parametrize("aligned", [True, False], ids=["vec16", "vec4"])
@@ -441,6 +441,38 @@ def test_every_tile_variant(ctx, tile, layout, aligned):
     pre = (ref_gemm(layout, a, b, m, n, k, c0=c0, accumulate=True) + bias[None, :]).astype(np.float32)
     ref = np.tanh(pre.astype(np.float64)).astype(np.float32)
     assert_close(c, ref, layout, a, b, m, n, k, c0=c0, accumulate=True, bias=bias, act="tanh", what=tile + " epi")
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+def test_pinned_tiles_bit_identical(ctx, layout):
+    """The three-stage pinned loop (64x64, 128x128k32, 64x64k16 tiles) keeps the
+    two-stage loop's K order per element: unsplit results are bit-identical
+    to the 128x128 two-stage kernel's, on interior tiles (short store path)
+    and edge tiles alike; split into K slices they match the oracle."""
+    m, n, k = 520, 392, 1040
+    rng = np.random.default_rng(zlib.crc32(f"pinned-{layout}".encode()))
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    out = {}
+    try:
+        ctx.set_gemm_splits(1)
+        for tile in ("128x128", "64x64", "128x128k32", "64x64k16"):
+            announce(f"pinned {layout} {tile} unsplit")
+            ctx.set_gemm_tile(tile)
+            out[tile] = run_gemm(ctx, layout, a, b, m, n, k)
+        for tile in ("64x64", "128x128k32", "64x64k16"):
+            assert np.array_equal(out[tile].view(np.uint32), out["128x128"].view(np.uint32)), tile
+        ref = ref_gemm(layout, a, b, m, n, k)
+        assert_close(out["128x128"], ref, layout, a, b, m, n, k, what="128x128")
+        ctx.set_gemm_splits(3)
+        for tile in ("64x64", "128x128k32", "64x64k16"):
+            announce(f"pinned {layout} {tile} split 3")
+            ctx.set_gemm_tile(tile)
+            c = run_gemm(ctx, layout, a, b, m, n, k)
+            assert_close(c, ref, layout, a, b, m, n, k, what=tile + " split")
+    finally:
+        ctx.set_gemm_tile("auto")
+        ctx.set_gemm_splits(0)
 
 
 @pytest.mark.parametrize("tile", TILES)

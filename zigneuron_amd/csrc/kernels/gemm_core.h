@@ -612,6 +612,63 @@ __device__ __forceinline__ void store_tile_act(const ZnGemmArgs &p, const zn_f32
     }
 }
 
+// Epilogue of gemm_tile_pinned.  A tile with nothing to add or apply (a
+// plain GEMM, or a split-K slice's raw partial sums) takes a short path of
+// stores, predicated on the edges of C; everything else goes through
+// store_tile_act with the activation as a template argument.  One-round
+// problems run the epilogue once per CU, all at the end and with a cold
+// instruction cache, so the length of the executed code shows:
+// 2048x2048x1024 NN on 128x128 tiles took 72.4 us with this path, 77.3 us
+// through store_tile_act<ACT = 0> and 87.5 us through the run-time
+// activation form.
+template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
+__device__ __forceinline__ void store_tile_fast(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+                                                int64_t bz, int m0, int n0, int wm0, int wn0, int lane, int slice) {
+    constexpr int FM = BM / WM / 32, FN = BN / WN / 32;
+    const bool split = p.splits > 1;
+    if (split || (!p.accumulate && !p.bias && p.act == 0)) {
+        float *gc = split ? p.ws + ((int64_t)bz * p.splits + slice) * (int64_t)p.m * p.n : p.c + bz * p.stride_c;
+        const int64_t ldc = split ? (int64_t)p.n : p.ldc;
+        const bool vec_c = split ? p.n % 4 == 0 : p.vec_c != 0;
+        const bool full_n = n0 + BN <= p.n;
+        const int j = lane & 31, h = lane >> 5;
+        const int c0 = n0 + wn0 + (BKC ? j : FN * j);  // this lane's first column
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
+                const int row = m0 + wm0 + (AK ? 32 * fm + bi : FM * bi + fm);
+                if (row >= p.m) continue;
+                float *crow = gc + (int64_t)row * ldc;
+                if constexpr (BKC || FN == 1) {
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+                        if (full_n || c0 + 32 * fn < p.n) crow[c0 + 32 * fn] = acc[fm][fn][r];
+                } else {
+                    if (vec_c && (full_n || c0 + FN <= p.n)) {
+                        typedef typename FVec<FN>::type VT;
+                        VT v;
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn) v[fn] = acc[fm][fn][r];
+                        *reinterpret_cast<VT *>(crow + c0) = v;
+                    } else {
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn)
+                            if (c0 + fn < p.n) crow[c0 + fn] = acc[fm][fn][r];
+                    }
+                }
+            }
+        return;
+    }
+    switch (split ? 0 : p.act) {
+    case 1: store_tile_act<BM, BN, WM, WN, AK, BKC, 1>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
+    case 2: store_tile_act<BM, BN, WM, WN, AK, BKC, 2>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
+    case 3: store_tile_act<BM, BN, WM, WN, AK, BKC, 3>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
+    default: store_tile_act<BM, BN, WM, WN, AK, BKC, 0>(p, acc, bz, m0, n0, wm0, wn0, lane, slice); break;
+    }
+}
+
 template <int BM, int BN, int WM, int WN, bool AK, bool BKC>
 __device__ __forceinline__ void store_tile(const ZnGemmArgs &p, const zn_f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
                                            int64_t bz, int m0, int n0, int wm0, int wn0, int lane, int slice) {
@@ -751,6 +808,117 @@ __device__ __forceinline__ void gemm_tile_dma(const ZnGemmArgs &p, int wg = -1) 
         }
     }
     store_tile<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "6-bit vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// The plain GEMM main loop with a fixed instruction schedule, for problems
+// of about one round of tiles, where each SIMD holds one or two waves and
+// every stall of a wave idles its matrix core.  Three LDS stages; slice
+// kt + 2 is loaded while slice kt is multiplied.  The slice barrier sits
+// before the last k group of a slice: the wave waits for its part of slice
+// kt + 1, meets the others, refills the stage of slice kt - 1, reads the
+// first fragments of slice kt + 1, and only then multiplies the last group
+// of slice kt, whose fragments it read before the barrier.  Fragments are
+// double-buffered across groups, and sched_barrier keeps the compiler from
+// moving the LDS reads, the barrier or the DMA into the MFMA runs.  The
+// barrier section runs in every iteration (the last one reads a stage it
+// never uses), so the fragment waits of the last group see one set of
+// pending reads.  Same K order per element as gemm_tile_dma, so the results
+// are bit-identical to it.  On MI355X against gemm_tile_dma's two-stage
+// loop: 4096x1024x1024 NT 76.4 -> 70.9 us (128x128, BK 32), 1024^3
+// 26.0 -> 23.7 us (64x64, BK 32).
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB>
+__device__ __forceinline__ void gemm_tile_pinned(const ZnGemmArgs &p, int wg = -1) {
+    constexpr int NT = WM * WN * kWave;
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int FM = WTM / 32, FN = WTN / 32;
+    constexpr int R = 3, G = BK / 8;
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+    static_assert(G >= 2 && G % 2 == 0, "an even number of k groups per slice");
+    typedef DmaStage<BM, BK, NT, AK, WA> SA;
+    typedef DmaStage<BN, BK, NT, BKC, WB> SB;
+    constexpr int L = SA::kPerWave + SB::kPerWave;  // DMA instructions per slice and wave
+    __shared__ __attribute__((aligned(1024))) float lds_a[R][SA::kFloats];
+    __shared__ __attribute__((aligned(1024))) float lds_b[R][SB::kFloats];
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+    int tm, tn, slice;
+    tile_coords(p, tm, tn, slice, wg);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int64_t bz = blockIdx.y;
+
+    const int kbeg = slice * p.k_chunk;
+    const int kend = min(p.k, kbeg + p.k_chunk);
+    const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
+    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + bz * p.stride_a, a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + bz * p.stride_b, b_bytes);
+    auto issue = [&](int s, int st) {
+        SA::issue(ra, lds_a[st], lda, m0, kbeg + s * BK, p.m, kend, wave, lane);
+        SB::issue(rb, lds_b[st], ldb, n0, kbeg + s * BK, p.n, kend, wave, lane);
+    };
+
+    zn_f32x16 acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+    float fa[2][FM][4], fb[2][FN][4];
+    auto multiply = [&](const float(&xa)[FM][4], const float(&xb)[FN][4]) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn)
+                    acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[fm][t], xb[fn][t], acc[fm][fn], 0, 0, 0);
+    };
+    if (ktiles > 0) {
+        issue(0, 0);
+        if (ktiles > 1) {
+            issue(1, 1);
+            vm_wait<L>();  // slice 0 is in; slice 1 may still be in flight
+        } else {
+            vm_wait<0>();
+        }
+        __syncthreads();
+        read_frags_dma<BM, BK, FM, AK>(lds_a[0], wm0, 0, lane, fa[0]);
+        read_frags_dma<BN, BK, FN, BKC>(lds_b[0], wn0, 0, lane, fb[0]);
+    }
+    int st = 0;
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int nst = st + 1 == R ? 0 : st + 1;
+#pragma unroll
+        for (int g = 0; g + 1 < G; ++g) {
+            read_frags_dma<BM, BK, FM, AK>(lds_a[st], wm0, 8 * (g + 1), lane, fa[(g + 1) & 1]);
+            read_frags_dma<BN, BK, FN, BKC>(lds_b[st], wn0, 8 * (g + 1), lane, fb[(g + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(fa[g & 1], fb[g & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        vm_wait<0>();     // this wave's part of slice kt + 1 is in LDS (the only DMA in flight)
+        __syncthreads();  // every wave's part is; every wave is done with slice kt - 1
+        if (kt + 2 < ktiles) issue(kt + 2, nst + 1 == R ? 0 : nst + 1);
+        read_frags_dma<BM, BK, FM, AK>(lds_a[nst], wm0, 0, lane, fa[0]);
+        read_frags_dma<BN, BK, FN, BKC>(lds_b[nst], wn0, 0, lane, fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(fa[1], fb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        st = nst;
+    }
+    store_tile_fast<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
 }
 
 // The end of an intra-workgroup split-K tile (gemm_ksplit and the fused

@@ -5,34 +5,41 @@
 
 // Exported kernels: zn_sgemm_<layout>_<tile>[_v].  Layout letters follow
 // the reference: nn = Backend.matMul, nt = matMulTransposeB, tn =
-// matMulTransposeA.  Tiles (macro tile, waves x wave tile):
-//   x = 256x128, 8 waves of 64x64   large problems (two workgroups per CU)
+// matMulTransposeA.  Tiles (macro tile, waves x wave tile, main loop):
+//   x = 256x128, 8 waves of 64x64    large problems (two workgroups per CU)
 //   l = 128x128, 4 waves of 64x64
-//   n = 128x64,  2 waves of 64x64   narrow N (attention P.V, N = 64)
-//   m = 64x64,   4 waves of 32x32   mid-size problems (BK 32)
-//   s = 32x32,   1 wave             small problems (BK 32)
-// The _v variants stage operands with 16-byte loads straight into LDS
-// (aligned rows, contiguous extents a multiple of 4); the plain ones with
-// 4-byte loads straight into LDS.
-#define ZN_GEMM_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                            \
+//   n = 128x64,  2 waves of 64x64    narrow N (attention P.V, N = 64)
+//   m = 64x64,   4 waves of 32x32    mid-size problems (BK 32, pinned loop)
+//   s = 32x32,   1 wave              small problems (BK 32)
+//   r = 128x128, 4 waves of 64x64    one round of tiles (BK 32, pinned loop,
+//                                    one workgroup per CU)
+//   h = 64x64,   4 waves of 32x32    several rounds (BK 16, pinned loop,
+//                                    six workgroups per CU)
+// x, l, n and s run gemm_tile_dma's two-stage loop, m, r and h
+// gemm_tile_pinned's three-stage one.  The _v variants stage operands with
+// 16-byte loads straight into LDS (aligned rows, contiguous extents a
+// multiple of 4); the plain ones with 4-byte loads straight into LDS.
+#define ZN_GEMM_KERNEL(NAME, LOOP, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                      \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void NAME(ZnGemmArgs p) {        \
-        gemm_tile_dma<BM, BN, BK, WM, WN, AK, BKC, (VEC) ? 16 : 4, (VEC) ? 16 : 4>(p);           \
+        LOOP<BM, BN, BK, WM, WN, AK, BKC, (VEC) ? 16 : 4, (VEC) ? 16 : 4>(p);                    \
     }
 
-#define ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, VEC, SUFFIX)                            \
-    ZN_GEMM_KERNEL(zn_sgemm_nn_##TILE##SUFFIX, BM, BN, BK, WM, WN, true, false, VEC, MINB)      \
-    ZN_GEMM_KERNEL(zn_sgemm_nt_##TILE##SUFFIX, BM, BN, BK, WM, WN, true, true, VEC, MINB)       \
-    ZN_GEMM_KERNEL(zn_sgemm_tn_##TILE##SUFFIX, BM, BN, BK, WM, WN, false, false, VEC, MINB)
+#define ZN_GEMM_LAYOUTS(TILE, LOOP, BM, BN, BK, WM, WN, MINB, VEC, SUFFIX)                      \
+    ZN_GEMM_KERNEL(zn_sgemm_nn_##TILE##SUFFIX, LOOP, BM, BN, BK, WM, WN, true, false, VEC, MINB) \
+    ZN_GEMM_KERNEL(zn_sgemm_nt_##TILE##SUFFIX, LOOP, BM, BN, BK, WM, WN, true, true, VEC, MINB)  \
+    ZN_GEMM_KERNEL(zn_sgemm_tn_##TILE##SUFFIX, LOOP, BM, BN, BK, WM, WN, false, false, VEC, MINB)
 
-#define ZN_GEMM_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                            \
-    ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, true, _v)                                   \
-    ZN_GEMM_LAYOUTS(TILE, BM, BN, BK, WM, WN, MINB, false, )
+#define ZN_GEMM_TILE(TILE, LOOP, BM, BN, BK, WM, WN, MINB)                                      \
+    ZN_GEMM_LAYOUTS(TILE, LOOP, BM, BN, BK, WM, WN, MINB, true, _v)                              \
+    ZN_GEMM_LAYOUTS(TILE, LOOP, BM, BN, BK, WM, WN, MINB, false, )
 
-ZN_GEMM_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_GEMM_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_GEMM_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_GEMM_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_GEMM_TILE(s, 32, 32, 32, 1, 1, 1)
+ZN_GEMM_TILE(x, gemm_tile_dma, 256, 128, 16, 4, 2, 1)
+ZN_GEMM_TILE(l, gemm_tile_dma, 128, 128, 16, 2, 2, 4)
+ZN_GEMM_TILE(n, gemm_tile_dma, 128, 64, 16, 2, 1, 1)
+ZN_GEMM_TILE(m, gemm_tile_pinned, 64, 64, 32, 2, 2, 1)
+ZN_GEMM_TILE(s, gemm_tile_dma, 32, 32, 32, 1, 1, 1)
+ZN_GEMM_TILE(r, gemm_tile_pinned, 128, 128, 32, 2, 2, 1)
+ZN_GEMM_TILE(h, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
 
 // Intra-workgroup split-K GEMMs (gemm_ksplit) on 32x32 tiles, BK 32, with
 // KS = 4 or 8 waves: zn_sgemmk<KS>_<layout>[_v], for problems of at most one

@@ -37,16 +37,20 @@
 namespace {
 
 // Macro tiles of the GEMM code object (kernels/gemm_f32.hip).
-enum Tile { kTileX = 0, kTileL, kTileN, kTileM, kTileS, kNumTiles };
+enum Tile { kTileX = 0, kTileL, kTileN, kTileM, kTileS, kTileR, kTileH, kNumTiles };
 struct TileShape {
     int bm, bn, bk, threads;
     const char *suffix;
+    bool conv;        // the convolution code object has kernels for it
+    bool persistent;  // zn_sgemmp_<layout>_<suffix>_v exists
 };
-constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x"},
-                                         {128, 128, 16, 256, "l"},
-                                         {128, 64, 16, 128, "n"},
-                                         {64, 64, 32, 256, "m"},
-                                         {32, 32, 32, 64, "s"}};
+constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x", true, true},
+                                         {128, 128, 16, 256, "l", true, true},
+                                         {128, 64, 16, 128, "n", true, true},
+                                         {64, 64, 32, 256, "m", true, true},
+                                         {32, 32, 32, 64, "s", true, false},
+                                         {128, 128, 32, 256, "r", false, false},
+                                         {64, 64, 16, 256, "h", false, false}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
 enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kPack, kToNhwc, kNumElt };
@@ -332,8 +336,8 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // graph replays): the largest tiles win once they give every CU two or more
 // workgroups; below that, 64x64 tiles (4 waves) are the fastest down to the
 // smallest problems and for N <= 64 (C5 P.V: 169 us against 184 us for
-// 128x64); 32x32 and 128x64 tiles never beat them and are left to explicit
-// selection.  A tile
+// 128x64), except for exactly one round of 128x128 tiles (below); 32x32 and
+// 128x64 tiles never beat them and are left to explicit selection.  A tile
 // whose padding wastes more than a quarter of its MFMA work (for example
 // 256-row tiles over M = 128) is skipped for the next smaller one.
 // A gathered (implicit convolution) operand costs more per staged element, so
@@ -348,6 +352,19 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t bat
     if (k <= 256 && tiles(kTileL) >= 2 * cus && useful(kTileL)) return kTileL;
     if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
     if (tiles(kTileL) >= (gathered ? 2 : 4) * cus && useful(kTileL)) return kTileL;
+    // One full round of 128x128 tiles with K up to 1536: one workgroup per
+    // CU on the three-stage 128x128 loop (4096x1024x1024 NT 76.6 -> 71.9 us,
+    // 2048x2048x1024 NN 74.7 -> 73.5 us against 64x64).  Longer K, or fewer
+    // or more tiles, stay on 64x64 (2048^3 NN: 144 us against 152 us;
+    // 2048x1536x1024, 192 tiles: 56 us against 72 us).
+    if (!gathered && 10 * tiles(kTileR) >= 9 * cus && tiles(kTileR) <= cus && k <= 1536 && useful(kTileR))
+        return kTileR;
+    // 64x64: BK 32 while the tiles fit one round at its three workgroups per
+    // CU, BK 16 (six per CU) beyond (3072x2048x1024 NN: 108.8 -> 106.3 us,
+    // 4096x1024x777 NN: 65.4 -> 60.1 us; 1024^3 stays at 23.9 us on BK 32,
+    // 29.9 us on BK 16).  Short K stays on 64x64 BK 32, which has the
+    // persistent kernel.
+    if (!gathered && tiles(kTileM) > 3 * cus && k > 256) return kTileH;
     return kTileM;
 }
 
@@ -471,9 +488,11 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
 
     // The NHWC forward gather runs best on 64x64 tiles (C5 forward, rocprofv3 trace: 156 us against 172 us for
     // 128x128 and 314 us for 256x128).
-    const Tile tile = ctx->forced_tile >= 0                       ? (Tile)ctx->forced_tile
+    // A forced tile without convolution kernels leaves convolutions to the policy.
+    const bool forced = ctx->forced_tile >= 0 && (!conv || kTiles[ctx->forced_tile].conv);
+    const Tile tile = forced                        ? (Tile)ctx->forced_tile
                       : conv && mode == kGatherNhwc ? kTileM
-                                                                  : choose_tile(ctx, m, n, k, batch, conv != nullptr);
+                                                    : choose_tile(ctx, m, n, k, batch, conv != nullptr);
     const TileShape &ts = kTiles[tile];
     const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
     if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
@@ -647,7 +666,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // 232 -> 215 us).  Longer tiles keep the hardware's dynamic assignment,
     // which balances the CUs better (C5 convolution GEMM, K = 576: 132 us
     // plain, 150 us persistent; 8192^3 0.6% slower persistent).
-    if (!conv && splits == 1 && vec && k > 0 && tile != kTileS && ctx->forced_persistent != 0) {
+    if (!conv && splits == 1 && vec && k > 0 && kTiles[tile].persistent && ctx->forced_persistent != 0) {
         const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
         const int64_t resident = cus * ctx->gemmp_occ[layout][tile];
         const int64_t total = ntiles * batch;
@@ -1150,7 +1169,7 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                     return bail(ZN_ERR_SYMBOL);
             }
     for (int t = 0; t < kNumTiles; ++t)
-        for (int v = 0; v < 2; ++v)
+        for (int v = 0; v < 2 && kTiles[t].conv; ++v)
             for (int g = 0; g < 2; ++g) {
                 char name[64];
                 std::snprintf(name, sizeof(name), "zn_conv_nn_%s%s%s", kTiles[t].suffix, v ? "_v" : "", g ? "_g" : "");
@@ -1158,7 +1177,7 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                     return bail(ZN_ERR_SYMBOL);
             }
     for (int t = 0; t < kNumTiles; ++t)
-        for (int v = 0; v < 2; ++v) {
+        for (int v = 0; v < 2 && kTiles[t].conv; ++v) {
             char name[64];
             std::snprintf(name, sizeof(name), "zn_convt_nt_%s%s", kTiles[t].suffix, v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->convt[t][v], ctx->conv_module, name) != hipSuccess)
@@ -1183,7 +1202,7 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             }
     for (int l = 0; l < 3; ++l)
         for (int t = 0; t < kNumTiles; ++t) {
-            if (t == kTileS) continue;
+            if (!kTiles[t].persistent) continue;
             char name[64];
             std::snprintf(name, sizeof(name), "zn_sgemmp_%s_%s_v", kLayoutName[l], kTiles[t].suffix);
             if (hipModuleGetFunction(&ctx->gemmp[l][t], ctx->gemm_module, name) != hipSuccess)
