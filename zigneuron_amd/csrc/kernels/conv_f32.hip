@@ -1,5 +1,12 @@
 // Exported implicit-GEMM convolution kernels for gfx950 (forward, input and
 // weight gradients), on the GEMM core of gemm_core.h with gathered B operands.
+// The 64x64 kernels of the three gathers that load only by DMA (transposed,
+// NHWC forward, NHWC weight gradient) run the pinned three-stage loop at
+// BK 16 (24 KB of LDS, six workgroups per CU): on MI355X, C5 forward
+// 160.3 -> 156.6 us, a 4 x 128 x 14 x 14 -> 256 convolution 21.9 -> 19.8 us
+// forward and 50.6 -> 46.5 us backward, bit-identical results.  The host's
+// K granularity for the 64x64 tile (32: split-K chunks, the NHWC forward's
+// one-tap slices) is a multiple of that BK.
 #include "gemm_core.h"
 
 // Implicit-GEMM convolution, per image b = blockIdx.y:
@@ -27,19 +34,19 @@ ZN_CONV_TILE(s, 32, 32, 32, 1, 1, 1)
 // grad_input_b[C][H*W] = W'[C][K] . B^T, NT, W' = weights regrouped as
 // [ic][(kh*kW + kw)*OC + oc] and B gathered from grad_output rows
 // (ConvTGatherStage).  _v: W' rows are 16-byte aligned.
-#define ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
+#define ZN_CONVT_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                       \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convt_nt_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, true, true, WA, 16, kGTransposed>(p);                  \
+        LOOP<BM, BN, BK, WM, WN, true, true, WA, 16, kGTransposed>(p); \
     }
-#define ZN_CONVT_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
-    ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
-    ZN_CONVT_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+#define ZN_CONVT_TILE(TILE, LOOP, BM, BN, BK, WM, WN, MINB) \
+    ZN_CONVT_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, 16, _v) \
+    ZN_CONVT_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, 4, )
 
-ZN_CONVT_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_CONVT_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_CONVT_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_CONVT_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_CONVT_TILE(s, 32, 32, 32, 1, 1, 1)
+ZN_CONVT_TILE(x, gemm_tile_dma, 256, 128, 16, 4, 2, 1)
+ZN_CONVT_TILE(l, gemm_tile_dma, 128, 128, 16, 2, 2, 4)
+ZN_CONVT_TILE(n, gemm_tile_dma, 128, 64, 16, 2, 1, 1)
+ZN_CONVT_TILE(m, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
+ZN_CONVT_TILE(s, gemm_tile_dma, 32, 32, 32, 1, 1, 1)
 
 // Weight gradient of a convolution with stride_w == 1 and out_w % 4 == 0:
 // grad_W[OC][taps] = go2^T . col with K = the output pixels of all images,
@@ -64,34 +71,34 @@ ZN_CONVW_TILE(s, 32, 32, 32, 1, 1, 1)
 // out_b[OC][OH*OW] = W[OC][K] . B^T (+ bias[oc]), NT, W in the im2col K order
 // and B gathered 4 channels at a time (ConvNhwcGatherStage, C % 4 == 0, any
 // stride).  _v: W rows are 16-byte aligned.
-#define ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                                \
+#define ZN_CONVF_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                       \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convf_nt_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, true, true, WA, 16, kGNhwc>(p);                        \
+        LOOP<BM, BN, BK, WM, WN, true, true, WA, 16, kGNhwc>(p); \
     }
-#define ZN_CONVF_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                              \
-    ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                       \
-    ZN_CONVF_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+#define ZN_CONVF_TILE(TILE, LOOP, BM, BN, BK, WM, WN, MINB) \
+    ZN_CONVF_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, 16, _v) \
+    ZN_CONVF_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, 4, )
 
-ZN_CONVF_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_CONVF_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_CONVF_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_CONVF_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_CONVF_TILE(s, 32, 32, 32, 1, 1, 1)
+ZN_CONVF_TILE(x, gemm_tile_dma, 256, 128, 16, 4, 2, 1)
+ZN_CONVF_TILE(l, gemm_tile_dma, 128, 128, 16, 2, 2, 4)
+ZN_CONVF_TILE(n, gemm_tile_dma, 128, 64, 16, 2, 1, 1)
+ZN_CONVF_TILE(m, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
+ZN_CONVF_TILE(s, gemm_tile_dma, 32, 32, 32, 1, 1, 1)
 
 // Weight gradient from an NHWC copy of the input: grad_W[OC][taps] =
 // go2^T . col, TN, K = the output pixels of all images, B gathered 4 channels
 // at a time (ConvNhwcWGatherStage, C % 4 == 0, any stride).  _v: OC % 4 == 0
 // and grad_output 16-byte aligned.
-#define ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                               \
+#define ZN_CONVWN_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, WA, SUFFIX)                      \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void zn_convwn_tn_##TILE##SUFFIX(ZnGemmArgs p) { \
-        gemm_tile_dma<BM, BN, BK, WM, WN, false, false, WA, 16, kGNhwcW>(p);                     \
+        LOOP<BM, BN, BK, WM, WN, false, false, WA, 16, kGNhwcW>(p); \
     }
-#define ZN_CONVWN_TILE(TILE, BM, BN, BK, WM, WN, MINB)                                             \
-    ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 16, _v)                                      \
-    ZN_CONVWN_KERNEL(TILE, BM, BN, BK, WM, WN, MINB, 4, )
+#define ZN_CONVWN_TILE(TILE, LOOP, BM, BN, BK, WM, WN, MINB) \
+    ZN_CONVWN_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, 16, _v) \
+    ZN_CONVWN_KERNEL(TILE, LOOP, BM, BN, BK, WM, WN, MINB, 4, )
 
-ZN_CONVWN_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_CONVWN_TILE(l, 128, 128, 16, 2, 2, 4)
-ZN_CONVWN_TILE(n, 128, 64, 16, 2, 1, 1)
-ZN_CONVWN_TILE(m, 64, 64, 32, 2, 2, 1)
-ZN_CONVWN_TILE(s, 32, 32, 32, 1, 1, 1)
+ZN_CONVWN_TILE(x, gemm_tile_dma, 256, 128, 16, 4, 2, 1)
+ZN_CONVWN_TILE(l, gemm_tile_dma, 128, 128, 16, 2, 2, 4)
+ZN_CONVWN_TILE(n, gemm_tile_dma, 128, 64, 16, 2, 1, 1)
+ZN_CONVWN_TILE(m, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
+ZN_CONVWN_TILE(s, gemm_tile_dma, 32, 32, 32, 1, 1, 1)

@@ -832,16 +832,24 @@ __device__ __forceinline__ void vm_wait() {
 // are bit-identical to it.  On MI355X against gemm_tile_dma's two-stage
 // loop: 4096x1024x1024 NT 76.4 -> 70.9 us (128x128, BK 32), 1024^3
 // 26.0 -> 23.7 us (64x64, BK 32).
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int WA, int WB, int G = kGNone>
 __device__ __forceinline__ void gemm_tile_pinned(const ZnGemmArgs &p, int wg = -1) {
+    constexpr bool CONVT = G == kGTransposed, NHWC = G == kGNhwc, NHWCW = G == kGNhwcW;
+    // gathers whose loads all go straight to LDS (no register-staged step)
+    static_assert(G == kGNone || CONVT || NHWC || NHWCW, "gather not supported by the pinned loop");
+    static_assert(!(CONVT || NHWC) || (BKC && WB == 16), "K-contiguous gathered operand");
+    static_assert(!NHWCW || (!BKC && WB == 16), "X-contiguous gathered operand");
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
-    constexpr int R = 3, G = BK / 8;
+    constexpr int R = 3, GR = BK / 8;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    static_assert(G >= 2 && G % 2 == 0, "an even number of k groups per slice");
+    static_assert(GR >= 2 && GR % 2 == 0, "an even number of k groups per slice");
     typedef DmaStage<BM, BK, NT, AK, WA> SA;
-    typedef DmaStage<BN, BK, NT, BKC, WB> SB;
+    typedef DmaStage<BN, BK, NT, BKC, WB> SB;  // the gathers issue as many loads per wave as SB
+    typedef ConvTGatherStage<BN, BK, NT> ST;
+    typedef ConvNhwcGatherStage<BN, BK, NT> SN;
+    typedef ConvNhwcWGatherStage<BN, BK, NT> SNW;
     constexpr int L = SA::kPerWave + SB::kPerWave;  // DMA instructions per slice and wave
     __shared__ __attribute__((aligned(1024))) float lds_a[R][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[R][SB::kFloats];
@@ -860,12 +868,27 @@ __device__ __forceinline__ void gemm_tile_pinned(const ZnGemmArgs &p, int wg = -
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     constexpr int RA = WA == 16 ? 3 : 0, RB = WB == 16 ? 3 : 0;
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RA) & ~RA) : (p.k - 1) * lda + ((p.m + RA) & ~RA)) * 4u;
-    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
+    const uint32_t b_bytes =
+        NHWCW ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+        : (CONVT || NHWC) ? (uint32_t)(p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+                          : (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RB) & ~RB) : (p.k - 1) * ldb + ((p.n + RB) & ~RB)) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + bz * p.stride_a, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + bz * p.stride_b, b_bytes);
+    typename SN::Lane cln{};
+    if constexpr (NHWC) cln = SN::lane_setup(p.conv, n0, p.n, wave, lane);
+    typename SNW::Lane clnw{};
+    if constexpr (NHWCW) clnw = SNW::lane_setup(p.conv, n0, p.n, lane);
     auto issue = [&](int s, int st) {
-        SA::issue(ra, lds_a[st], lda, m0, kbeg + s * BK, p.m, kend, wave, lane);
-        SB::issue(rb, lds_b[st], ldb, n0, kbeg + s * BK, p.n, kend, wave, lane);
+        const int k0 = kbeg + s * BK;
+        SA::issue(ra, lds_a[st], lda, m0, k0, p.m, kend, wave, lane);
+        if constexpr (NHWC)
+            SN::issue(rb, lds_b[st], p.conv, cln, k0, kend, wave, lane);
+        else if constexpr (NHWCW)
+            SNW::issue(rb, lds_b[st], p.conv, clnw, k0, kend, wave);
+        else if constexpr (CONVT)
+            ST::issue(rb, lds_b[st], p.conv, n0, k0, p.n, kend, wave, lane);
+        else
+            SB::issue(rb, lds_b[st], ldb, n0, k0, p.n, kend, wave, lane);
     };
 
     zn_f32x16 acc[FM][FN];
@@ -901,7 +924,7 @@ __device__ __forceinline__ void gemm_tile_pinned(const ZnGemmArgs &p, int wg = -
     for (int kt = 0; kt < ktiles; ++kt) {
         const int nst = st + 1 == R ? 0 : st + 1;
 #pragma unroll
-        for (int g = 0; g + 1 < G; ++g) {
+        for (int g = 0; g + 1 < GR; ++g) {
             read_frags_dma<BM, BK, FM, AK>(lds_a[st], wm0, 8 * (g + 1), lane, fa[(g + 1) & 1]);
             read_frags_dma<BN, BK, FN, BKC>(lds_b[st], wn0, 8 * (g + 1), lane, fb[(g + 1) & 1]);
             __builtin_amdgcn_sched_barrier(0);
