@@ -363,8 +363,8 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t bat
     // CU, BK 16 (six per CU) beyond (3072x2048x1024 NN: 108.8 -> 106.3 us,
     // 4096x1024x777 NN: 65.4 -> 60.1 us; 1024^3 stays at 23.9 us on BK 32,
     // 29.9 us on BK 16).  Short K stays on 64x64 BK 32, which has the
-    // persistent kernel.
-    if (!gathered && tiles(kTileM) > 3 * cus && k > 256) return kTileH;
+    // persistent kernel, and so does N <= 64 (C5 P.V: 170.3 us against 174.0).
+    if (!gathered && tiles(kTileM) > 3 * cus && k > 256 && n > 64) return kTileH;
     return kTileM;
 }
 
