@@ -114,5 +114,12 @@ def test_tuning_hooks_reject_bad_values(ctx):
     for bad in (2, -2):
         with pytest.raises(InvalidArgumentError):
             ctx.set_gemm_persistent(bad)
+    from zigneuron_amd import _lib
+    for bad in (max(_lib.TILES.values()) + 1, -2):
+        with pytest.raises(InvalidArgumentError):
+            ctx.set_gemm_tile(bad)
+    for name in _lib.TILES:
+        ctx.set_gemm_tile(name)
+    ctx.set_gemm_tile("auto")
     ctx.set_gemm_wave_split(-1)
     ctx.set_gemm_persistent(-1)
