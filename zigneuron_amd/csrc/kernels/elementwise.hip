@@ -294,7 +294,8 @@ extern "C" __global__ __launch_bounds__(256) void zn_row_sum(ZnEltArgs p) {
 // copied into rows of ld_dst floats with a zero tail, so the GEMM can stage
 // it with 16-byte loads.  A copy (bit-exact); one float4 of dst per thread
 // and step.
-extern "C" __global__ __launch_bounds__(256) void zn_pack_rows(ZnPackArgs p) {
+extern "C" __global__ __launch_bounds__(256) void zn_pack_rows(ZnPack2Args a) {
+    const ZnPackArgs &p = a.op[blockIdx.y];  // both GEMM operands in one launch (gridDim.y <= 2)
     const int64_t per_row = p.ld_dst >> 2;
     const int64_t total = p.rows * per_row;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {

@@ -509,23 +509,24 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     if (!conv && batch == 1 && k > 0 && (double)m * n * k >= kPackMinMacs) {
         const bool a_vec = aligned16(a) && lda % 4 == 0 && a_row % 4 == 0;
         const bool b_vec = aligned16(b) && ldb % 4 == 0 && b_row % 4 == 0;
+        // both packings go into one launch (blockIdx.y selects the operand)
+        ZnPack2Args jobs;
+        std::memset(&jobs, 0, sizeof(jobs));
+        int njobs = 0;
+        int64_t most = 0;  // float4s of the larger packed operand
         auto pack = [&](Lease &l, const float *&src, int64_t &ld, int64_t rows, int64_t cols, bool &packed) -> int {
             const int64_t ld_dst = (cols + 3) & ~(int64_t)3;
             if ((rows - 1) * ld_dst + ld_dst > kLimit) return ZN_OK;  // stays on the 4-byte path
             int rc2 = l.get((size_t)(rows * ld_dst));
             if (rc2) return rc2;
-            ZnPackArgs pa;
+            ZnPackArgs &pa = jobs.op[njobs++];
             pa.src = src;
             pa.dst = l.ptr;
             pa.rows = rows;
             pa.cols = cols;
             pa.ld_src = ld;
             pa.ld_dst = ld_dst;
-            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
-            if ((rc2 = select_device(ctx)) ||
-                (rc2 = launch(ctx, ctx->elt[kPack], (unsigned)std::min<int64_t>(cdiv(rows * ld_dst / 4, 256), cap), 1,
-                              256, &pa)))
-                return rc2;
+            most = std::max<int64_t>(most, rows * ld_dst / 4);
             src = l.ptr;
             ld = ld_dst;
             packed = true;
@@ -534,6 +535,13 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         int rcp;
         if (!a_vec && !a_packed && (rcp = pack(pack_a, a, lda, a_outer, a_row, a_packed))) return rcp;
         if (!b_vec && !b_packed && (rcp = pack(pack_b, b, ldb, b_outer, b_row, b_packed))) return rcp;
+        if (njobs > 0) {
+            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+            if ((rcp = select_device(ctx)) ||
+                (rcp = launch(ctx, ctx->elt[kPack], (unsigned)std::min<int64_t>(cdiv(most, 256), cap), (unsigned)njobs,
+                              256, &jobs)))
+                return rcp;
+        }
     }
 
     ZnGemmArgs args;

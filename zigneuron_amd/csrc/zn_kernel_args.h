@@ -131,6 +131,11 @@ struct ZnPackArgs {
     int64_t rows, cols, ld_src, ld_dst;
 };
 
+// Up to two row packings in one launch: blockIdx.y selects op[blockIdx.y].
+struct ZnPack2Args {
+    ZnPackArgs op[2];
+};
+
 // Per image b < batch: dst_b[p][c] = src_b[c][p] for c < channels, p < pixels
 // (NCHW -> NHWC).
 struct ZnTransposeArgs {
