@@ -11,7 +11,7 @@
 //   n = 128x64,  2 waves of 64x64    narrow N (attention P.V, N = 64)
 //   m = 64x64,   4 waves of 32x32    mid-size problems (BK 32, pinned loop)
 //   s = 32x32,   1 wave              small problems (BK 32)
-//   r = 128x128, 4 waves of 64x64    one round of tiles (BK 32, pinned loop,
+//   r = 128x128, 8 waves of 32x64    one round of tiles (BK 32, pinned loop,
 //                                    one workgroup per CU)
 //   h = 64x64,   4 waves of 32x32    several rounds (BK 16, pinned loop,
 //                                    six workgroups per CU)
@@ -38,7 +38,7 @@ ZN_GEMM_TILE(l, gemm_tile_dma, 128, 128, 16, 2, 2, 4)
 ZN_GEMM_TILE(n, gemm_tile_dma, 128, 64, 16, 2, 1, 1)
 ZN_GEMM_TILE(m, gemm_tile_pinned, 64, 64, 32, 2, 2, 1)
 ZN_GEMM_TILE(s, gemm_tile_dma, 32, 32, 32, 1, 1, 1)
-ZN_GEMM_TILE(r, gemm_tile_pinned, 128, 128, 32, 2, 2, 1)
+ZN_GEMM_TILE(r, gemm_tile_pinned, 128, 128, 32, 4, 2, 1)
 ZN_GEMM_TILE(h, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
 
 // Intra-workgroup split-K GEMMs (gemm_ksplit) on 32x32 tiles, BK 32, with

@@ -49,7 +49,7 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x", true, true},
                                          {128, 64, 16, 128, "n", true, true},
                                          {64, 64, 32, 256, "m", true, true},
                                          {32, 32, 32, 64, "s", true, false},
-                                         {128, 128, 32, 256, "r", false, false},
+                                         {128, 128, 32, 512, "r", false, false},
                                          {64, 64, 16, 256, "h", false, false}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
@@ -397,7 +397,11 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
             const int64_t load = cdiv(tiles * sp, cus);
             // load / sp at least 5% below best_load / best (the reduce pass costs a few percent)
             const bool faster = load * best * 20 < best_load * sp * 19;
-            const bool tie_more_waves = load * best == best_load * sp && best_load < 2 && load >= 2;
+            // (not for the 128x128 BK 32 tile, one workgroup per CU: a second
+            // one per CU is a second round; 2048x2048x1536 NN 119.9 us in 2
+            // slices against 106.8 us unsplit)
+            const bool tie_more_waves =
+                tile != kTileR && load * best == best_load * sp && best_load < 2 && load >= 2;
             if (faster || tie_more_waves) {
                 best = sp;
                 best_load = load;
