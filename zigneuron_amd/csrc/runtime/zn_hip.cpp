@@ -352,12 +352,13 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t bat
     if (k <= 256 && tiles(kTileL) >= 2 * cus && useful(kTileL)) return kTileL;
     if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
     if (tiles(kTileL) >= (gathered ? 2 : 4) * cus && useful(kTileL)) return kTileL;
-    // One full round of 128x128 tiles with K up to 1536: one workgroup per
-    // CU on the three-stage 128x128 loop (4096x1024x1024 NT 76.6 -> 71.9 us,
-    // 2048x2048x1024 NN 74.7 -> 73.5 us against 64x64).  Longer K, or fewer
-    // or more tiles, stay on 64x64 (2048^3 NN: 144 us against 152 us;
-    // 2048x1536x1024, 192 tiles: 56 us against 72 us).
-    if (!gathered && 10 * tiles(kTileR) >= 9 * cus && tiles(kTileR) <= cus && k <= 1536 && useful(kTileR))
+    // One round of 128x128 tiles (at least 85% of the CUs): one workgroup of
+    // 8 waves per CU on the three-stage 128x128 loop, at any K (against the
+    // 64x64 tiles: 4096x1024x1024 NT 74.0 -> 70.4 us, 2048^3 NN 139.8 ->
+    // 135.5 us, 2048x2048x4096 TN 277.1 -> 257.8 us, 2048x1792x1024 NN (224
+    // tiles) 72.5 -> 70.8 us).  Fewer tiles stay on 64x64 (2048x1536x1024,
+    // 192 tiles: 56.0 us against 70.4 us).
+    if (!gathered && 20 * tiles(kTileR) >= 17 * cus && tiles(kTileR) <= cus && useful(kTileR))
         return kTileR;
     // 64x64: BK 32 while the tiles fit one round at its three workgroups per
     // CU, BK 16 (six per CU) beyond (3072x2048x1024 NN: 108.8 -> 106.3 us,
