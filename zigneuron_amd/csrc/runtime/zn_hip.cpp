@@ -332,6 +332,16 @@ int launch(zn_ctx *ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned thre
 // ------------------------------------------------------------ GEMM policy
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// K slices for the 128x128 BK 32 tile (one workgroup per CU): the most, up
+// to 16 and with at least 768 of K each, that keep tiles x slices within one
+// round of workgroups.
+int64_t round_splits(int64_t tiles, int64_t k, int64_t cus) {
+    const int64_t max_s = std::max<int64_t>(1, std::min<int64_t>(16, k / 768));
+    int64_t s = 1;
+    while (s < max_s && tiles * (s + 1) <= cus) ++s;
+    return s;
+}
+
 // Tile choice, from measurements on MI355X (256 CUs, per-launch times from
 // graph replays): the largest tiles win once they give every CU two or more
 // workgroups; below that, 64x64 tiles (4 waves) are the fastest down to the
@@ -352,13 +362,16 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t bat
     if (k <= 256 && tiles(kTileL) >= 2 * cus && useful(kTileL)) return kTileL;
     if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
     if (tiles(kTileL) >= (gathered ? 2 : 4) * cus && useful(kTileL)) return kTileL;
-    // One round of 128x128 tiles (at least 85% of the CUs): one workgroup of
-    // 8 waves per CU on the three-stage 128x128 loop, at any K (against the
-    // 64x64 tiles: 4096x1024x1024 NT 74.0 -> 70.4 us, 2048^3 NN 139.8 ->
-    // 135.5 us, 2048x2048x4096 TN 277.1 -> 257.8 us, 2048x1792x1024 NN (224
-    // tiles) 72.5 -> 70.8 us).  Fewer tiles stay on 64x64 (2048x1536x1024,
-    // 192 tiles: 56.0 us against 70.4 us).
-    if (!gathered && 20 * tiles(kTileR) >= 17 * cus && tiles(kTileR) <= cus && useful(kTileR))
+    // One round of 128x128 tiles (at least 85% of the CUs, counting K slices
+    // of at least 768): one workgroup of 8 waves per CU on the three-stage
+    // 128x128 loop (against the 64x64 tiles: 4096x1024x1024 NT 74.0 -> 70.4
+    // us, 2048^3 NN 139.8 -> 135.5 us, 2048x2048x4096 TN 277.1 -> 257.8 us,
+    // 2048x1792x1024 NN (224 tiles) 72.5 -> 70.8 us; C3 dW 1024x1024x4096 TN
+    // in 4 slices 76.7 -> 74.5 us, 1024x1024x8192 TN 144.6 -> 137.5 us).
+    // Fewer tiles stay on 64x64 (2048x1536x1024, 192 tiles: 56.0 us against
+    // 70.4 us).
+    if (!gathered && tiles(kTileR) <= cus && useful(kTileR) &&
+        20 * tiles(kTileR) * round_splits(tiles(kTileR), k, cus) >= 17 * cus)
         return kTileR;
     // 64x64: BK 32 while the tiles fit one round at its three workgroups per
     // CU, BK 16 (six per CU) beyond (3072x2048x1024 NN: 108.8 -> 106.3 us,
@@ -390,6 +403,10 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     const TileShape &ts = kTiles[tile];
     const int64_t tiles = cdiv(m, ts.bm) * cdiv(n, ts.bn) * batch;
+    // The 128x128 BK 32 tile runs one workgroup per CU: a second workgroup
+    // per CU is a second round (2048x2048x1536 NN 119.9 us in 2 slices
+    // against 106.8 us unsplit), so its split only fills the first.
+    if (tile == kTileR) return (int)round_splits(tiles, k, cus);
     if (tiles >= cus / 2) {
         int64_t best = 1, best_load = cdiv(tiles, cus);  // workgroups on the busiest CU
         const int64_t max_s = std::min<int64_t>(16, k / 768);
@@ -398,11 +415,7 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
             const int64_t load = cdiv(tiles * sp, cus);
             // load / sp at least 5% below best_load / best (the reduce pass costs a few percent)
             const bool faster = load * best * 20 < best_load * sp * 19;
-            // (not for the 128x128 BK 32 tile, one workgroup per CU: a second
-            // one per CU is a second round; 2048x2048x1536 NN 119.9 us in 2
-            // slices against 106.8 us unsplit)
-            const bool tie_more_waves =
-                tile != kTileR && load * best == best_load * sp && best_load < 2 && load >= 2;
+            const bool tie_more_waves = load * best == best_load * sp && best_load < 2 && load >= 2;
             if (faster || tie_more_waves) {
                 best = sp;
                 best_load = load;
