@@ -59,6 +59,31 @@ def assert_close(c, ref, layout, a, b, m, n, k, c0=None, accumulate=False, bias=
     return err
 
 
+def assert_close_rows(c, ref, a_mk, b_kn, k, what="", block=1024):
+    """assert_close for a large problem, with the fp64 denominators taken in
+    row blocks so host memory stays at a few blocks' worth."""
+    bound = tol(k)
+    abs_b = np.abs(b_kn.astype(np.float64))
+    worst = 0.0
+    for r0 in range(0, c.shape[0], block):
+        r1 = min(c.shape[0], r0 + block)
+        cb = c[r0:r1]
+        assert np.all(np.isfinite(cb)), f"{what}: non-finite output in rows {r0}:{r1}"
+        den = np.abs(a_mk[r0:r1].astype(np.float64)) @ abs_b
+        err = componentwise_error(cb, ref[r0:r1], den)
+        assert err <= bound, f"{what} rows {r0}:{r1}: componentwise err {err:.3e} > tol {bound:.3e}"
+        worst = max(worst, err)
+    return worst
+
+
+def pmap(fn, items, threads=THREADS):
+    """fn over items on a thread pool (the oracle's ctypes calls release the
+    GIL, so single-threaded oracle functions run side by side)."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
+        return list(ex.map(fn, items))
+
+
 def announce(msg: str) -> None:
     """Name the case before each GPU step (flushed), so a failure names it."""
     print(f"[gpu] {msg}", flush=True)

@@ -202,6 +202,27 @@ def test_accumulate_against_oracle(ctx, layout, m, n, k):
     assert_close(c, ref, layout, a, b, m, n, k, c0=c0, accumulate=True)
 
 
+@pytest.mark.parametrize("accumulate", [False, True])
+@pytest.mark.parametrize("batch_size,n,k", [(1, 10, 128), (1, 300, 7), (37, 130, 70), (256, 10, 784),
+                                            (513, 65, 33)])
+def test_backend_mat_mul_batch(backend, batch_size, n, k, accumulate):
+    """Backend.matMulBatch (src/backend.zig:186-195): rows of A against a shared
+    B, against the CPU arm cpuMatMulBatch (:2609-2613) row by row.  Host slices
+    in and out, with and without accumulate, one row and ragged row counts.
+    C is exactly batch_size*n long: the CPU arm's per-row memset clears its
+    slice to the end (:2521), which past batch_size*n is a side effect of that
+    defect, not part of the operator's result."""
+    rng = np.random.default_rng(batch_size * 1000 + n + k)
+    a, b = uniform(rng, (batch_size, k)), uniform(rng, (k, n))
+    c0 = uniform(rng, (batch_size * n,))
+    announce(f"Backend.matMulBatch {batch_size}x{n}x{k} acc={accumulate}")
+    c = c0.copy()
+    backend.matMulBatch(a.ravel(), b.ravel(), c, batch_size, n, k, accumulate)
+    ref = oracle.matmul_batch(a, b, batch_size, n, k, accumulate, c0)
+    assert_close(c.reshape(batch_size, n), ref, "nn", a, b, batch_size, n, k,
+                 c0=c0 if accumulate else None, accumulate=accumulate, what="matMulBatch")
+
+
 def test_k_zero_and_empty(ctx):
     announce("k=0 and empty shapes")
     rng = np.random.default_rng(2)

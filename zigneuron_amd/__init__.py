@@ -4,9 +4,11 @@ The product is the C-ABI library ``lib/libzn_hip.so`` (include/zn_hip.h) and
 its offline-built gfx950 code objects; this package is the host-side mirror
 of the reference ``Backend``/``Dense`` interfaces over that ABI.
 """
-from ._lib import ZnError, NoDeviceError, CodeObjectError, InvalidArgumentError  # noqa: F401
+from ._lib import (ZnError, NoDeviceError, CodeObjectError, SymbolError, InvalidArgumentError,  # noqa: F401
+                   OutOfMemoryError, LaunchError, HipError)
 from .backend import Backend, Context, DeviceBuffer, available  # noqa: F401
 from .layer import Dense, DenseDevice  # noqa: F401
 
 __all__ = ["Backend", "Context", "DeviceBuffer", "Dense", "DenseDevice", "available", "ZnError",
-           "NoDeviceError", "CodeObjectError", "InvalidArgumentError"]
+           "NoDeviceError", "CodeObjectError", "SymbolError", "InvalidArgumentError", "OutOfMemoryError",
+           "LaunchError", "HipError"]

@@ -15,7 +15,6 @@
 #include <hip/hip_runtime.h>
 
 #include <dlfcn.h>
-#include <sys/stat.h>
 
 #include <climits>
 #include <cstdio>
@@ -218,9 +217,62 @@ bool mul_ok(size_t a, size_t b, size_t *out) {
     return true;
 }
 
-bool file_exists(const std::string &path) {
-    struct stat st;
-    return stat(path.c_str(), &st) == 0 && S_ISREG(st.st_mode);
+// Host-side check of a code object before the runtime sees it: a clang
+// offload bundle (what `hipcc --genco` writes) with an amdgcn gfx950 entry,
+// or a bare ELF, whose AMDGPU ELF header and program and section header
+// tables lie inside the file.  A missing, truncated or foreign file is then
+// ZN_ERR_CODE_OBJECT without ever reaching hipModuleLoad.
+constexpr uint16_t kEmAmdgpu = 224;          // ELF e_machine of AMDGPU code objects
+constexpr uint32_t kMachGfx950 = 0x04f;      // e_flags & 0xff (EF_AMDGPU_MACH) for gfx950
+
+template <typename T>
+T load_le(const unsigned char *p) {
+    T v;
+    std::memcpy(&v, p, sizeof(T));
+    return v;
+}
+
+bool amdgpu_elf_ok(const unsigned char *p, size_t n) {
+    if (n < 64 || std::memcmp(p, "\x7f" "ELF", 4) != 0 || p[4] != 2 || p[5] != 1) return false;  // 64-bit, LE
+    if (load_le<uint16_t>(p + 18) != kEmAmdgpu) return false;
+    if ((load_le<uint32_t>(p + 48) & 0xff) != kMachGfx950) return false;
+    const uint64_t phoff = load_le<uint64_t>(p + 32), shoff = load_le<uint64_t>(p + 40);
+    const uint64_t ph = (uint64_t)load_le<uint16_t>(p + 54) * load_le<uint16_t>(p + 56);
+    const uint64_t sh = (uint64_t)load_le<uint16_t>(p + 58) * load_le<uint16_t>(p + 60);
+    return phoff <= n && ph <= n - phoff && shoff <= n && sh <= n - shoff;
+}
+
+bool code_object_ok(const std::string &path) {
+    FILE *f = std::fopen(path.c_str(), "rb");
+    if (!f) return false;
+    std::vector<unsigned char> buf;
+    unsigned char chunk[1 << 16];
+    size_t got;
+    while ((got = std::fread(chunk, 1, sizeof(chunk), f)) > 0) buf.insert(buf.end(), chunk, chunk + got);
+    std::fclose(f);
+    const size_t n = buf.size();
+    const unsigned char *p = buf.data();
+    static const char kBundle[] = "__CLANG_OFFLOAD_BUNDLE__";
+    const size_t magic = sizeof(kBundle) - 1;
+    if (n < magic || std::memcmp(p, kBundle, magic) != 0) return amdgpu_elf_ok(p, n);
+    if (n < magic + 8) return false;
+    const uint64_t entries = load_le<uint64_t>(p + magic);
+    size_t at = magic + 8;
+    bool found = false;
+    for (uint64_t i = 0; i < entries; ++i) {
+        if (n - at < 24) return false;
+        const uint64_t off = load_le<uint64_t>(p + at), size = load_le<uint64_t>(p + at + 8);
+        const uint64_t tlen = load_le<uint64_t>(p + at + 16);
+        at += 24;
+        if (tlen > n - at || off > n || size > n - off) return false;
+        const std::string triple((const char *)p + at, (size_t)tlen);
+        at += (size_t)tlen;
+        if (triple.find("amdgcn") != std::string::npos) {
+            if (triple.find("gfx950") == std::string::npos || !amdgpu_elf_ok(p + off, (size_t)size)) return false;
+            found = true;
+        }
+    }
+    return found;
 }
 
 // Directory holding this shared library (the default code-object location).
@@ -764,16 +816,57 @@ int elt_launch(zn_ctx *ctx, EltKernel kernel, int64_t work_items, const Args &ar
 constexpr size_t kStageBytes = (size_t)32 << 20;  // per pinned staging buffer
 constexpr size_t kStageMin = (size_t)4 << 20;      // smaller copies stay pageable
 
-int ensure_staging(zn_ctx *ctx) {
-    if (ctx->pinned[0]) return ZN_OK;
+// Set-up fault injection for the error-path tests: ZN_HIP_TEST_SETUP_FAULT=n
+// makes step n of the staging (1-5) or pipeline (11-21) set-up fail as if
+// the HIP call had run out of memory.  Read at each set-up attempt.
+hipError_t setup_step(int step, hipError_t real) {
+    const char *env = std::getenv("ZN_HIP_TEST_SETUP_FAULT");
+    if (env && std::atoi(env) == step) return hipErrorOutOfMemory;
+    return real;
+}
+
+void release_staging(zn_ctx *ctx) {
+    ctx->copier.reset();
     for (int i = 0; i < 2; ++i) {
-        ZN_HIP_TRY(ctx, hipHostMalloc((void **)&ctx->pinned[i], kStageBytes, hipHostMallocDefault));
-        ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->pinned_done[i], hipEventDisableTiming));
+        if (ctx->pinned_done[i]) (void)hipEventDestroy(ctx->pinned_done[i]);
+        if (ctx->pinned[i]) (void)hipHostFree(ctx->pinned[i]);
+        ctx->pinned_done[i] = nullptr;
+        ctx->pinned[i] = nullptr;
+    }
+}
+
+// The staging set is ready only when complete (the copier is made last); a
+// failed set-up releases what it made, so a later call starts afresh.
+int ensure_staging(zn_ctx *ctx) {
+    if (ctx->copier) return ZN_OK;
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        e = setup_step(1 + 2 * i, hipHostMalloc((void **)&ctx->pinned[i], kStageBytes, hipHostMallocDefault));
+        if (e == hipSuccess)
+            e = setup_step(2 + 2 * i, hipEventCreateWithFlags(&ctx->pinned_done[i], hipEventDisableTiming));
+    }
+    if (e == hipSuccess) e = setup_step(5, hipSuccess);
+    if (e != hipSuccess) {
+        release_staging(ctx);
+        return fail_hip(ctx, e, e == hipErrorOutOfMemory ? ZN_ERR_OOM : ZN_ERR_HIP);
     }
     const unsigned hw = std::thread::hardware_concurrency();
     ctx->copier.reset(new HostCopier((int)std::min(15u, hw > 1 ? hw - 1 : 0u)));
     return ZN_OK;
 }
+
+// Work queued on a stream that reads or writes pinned staging memory must be
+// finished before that memory is used again, also when the call returns
+// early with an error.  Declared after the call's leases, so it waits before
+// they go back to the pool.
+struct PinnedFence {
+    zn_ctx *ctx;
+    hipStream_t stream = nullptr;  // the context stream when null
+    bool done = false;
+    ~PinnedFence() {
+        if (!done) (void)hipStreamSynchronize(stream ? stream : ctx->stream);
+    }
+};
 
 // Host -> device on `stream` (the context stream by default).  Large copies:
 // chunk i is copied into pinned buffer i % 2 once that buffer's previous DMA
@@ -791,6 +884,7 @@ int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n, hipStream_t str
     }
     int rc = ensure_staging(ctx);
     if (rc) return rc;
+    PinnedFence fence{ctx, stream};
     for (size_t off = 0, i = 0; off < bytes; off += kStageBytes, ++i) {
         const size_t len = std::min(kStageBytes, bytes - off);
         const int s = (int)(i & 1);
@@ -799,6 +893,7 @@ int copy_in(zn_ctx *ctx, float *dst, const float *src, size_t n, hipStream_t str
         ZN_HIP_TRY(ctx, hipMemcpyAsync((char *)dst + off, ctx->pinned[s], len, hipMemcpyHostToDevice, stream));
         ZN_HIP_TRY(ctx, hipEventRecord(ctx->pinned_done[s], stream));
     }
+    fence.done = true;  // the last DMAs may run on; pinned_done orders the ring's reuse
     return ZN_OK;
 }
 
@@ -815,6 +910,7 @@ int copy_out_and_wait(zn_ctx *ctx, float *dst, const float *src, size_t n) {
     }
     int rc = ensure_staging(ctx);
     if (rc) return rc;
+    PinnedFence fence{ctx};
     const size_t chunks = (bytes + kStageBytes - 1) / kStageBytes;
     auto issue = [&](size_t i) -> int {
         const size_t off = i * kStageBytes, len = std::min(kStageBytes, bytes - off);
@@ -834,22 +930,53 @@ int copy_out_and_wait(zn_ctx *ctx, float *dst, const float *src, size_t n) {
         ctx->copier->copy((char *)dst + off, ctx->pinned[s], len);
     }
     ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    fence.done = true;
     return ZN_OK;
 }
 
+void release_pipeline(zn_ctx *ctx) {
+    if (ctx->up) (void)hipStreamSynchronize(ctx->up);
+    if (ctx->down) (void)hipStreamSynchronize(ctx->down);
+    for (int i = 0; i < 2; ++i) {
+        if (ctx->pinned_out_done[i]) (void)hipEventDestroy(ctx->pinned_out_done[i]);
+        if (ctx->pinned_out[i]) (void)hipHostFree(ctx->pinned_out[i]);
+        if (ctx->chunk_in[i]) (void)hipEventDestroy(ctx->chunk_in[i]);
+        if (ctx->chunk_out[i]) (void)hipEventDestroy(ctx->chunk_out[i]);
+        ctx->pinned_out_done[i] = ctx->chunk_in[i] = ctx->chunk_out[i] = nullptr;
+        ctx->pinned_out[i] = nullptr;
+    }
+    if (ctx->entry) (void)hipEventDestroy(ctx->entry);
+    ctx->entry = nullptr;
+    if (ctx->up) (void)hipStreamDestroy(ctx->up);
+    if (ctx->down) (void)hipStreamDestroy(ctx->down);
+    ctx->up = ctx->down = nullptr;
+}
+
+// Ready only when complete (the upload stream is made last); a failed
+// set-up releases what it made.
 int ensure_pipeline(zn_ctx *ctx) {
     int rc = ensure_staging(ctx);
     if (rc) return rc;
     if (ctx->up) return ZN_OK;
-    for (int i = 0; i < 2; ++i) {
-        ZN_HIP_TRY(ctx, hipHostMalloc((void **)&ctx->pinned_out[i], kStageBytes, hipHostMallocDefault));
-        ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->pinned_out_done[i], hipEventDisableTiming));
-        ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->chunk_in[i], hipEventDisableTiming));
-        ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->chunk_out[i], hipEventDisableTiming));
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        const int s0 = 11 + 4 * i;
+        e = setup_step(s0, hipHostMalloc((void **)&ctx->pinned_out[i], kStageBytes, hipHostMallocDefault));
+        if (e == hipSuccess)
+            e = setup_step(s0 + 1, hipEventCreateWithFlags(&ctx->pinned_out_done[i], hipEventDisableTiming));
+        if (e == hipSuccess) e = setup_step(s0 + 2, hipEventCreateWithFlags(&ctx->chunk_in[i], hipEventDisableTiming));
+        if (e == hipSuccess) e = setup_step(s0 + 3, hipEventCreateWithFlags(&ctx->chunk_out[i], hipEventDisableTiming));
     }
-    ZN_HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->entry, hipEventDisableTiming));
-    ZN_HIP_TRY(ctx, hipStreamCreateWithFlags(&ctx->down, hipStreamNonBlocking));
-    ZN_HIP_TRY(ctx, hipStreamCreateWithFlags(&ctx->up, hipStreamNonBlocking));
+    if (e == hipSuccess) e = setup_step(19, hipEventCreateWithFlags(&ctx->entry, hipEventDisableTiming));
+    if (e == hipSuccess) e = setup_step(20, hipStreamCreateWithFlags(&ctx->down, hipStreamNonBlocking));
+    hipStream_t up = nullptr;
+    if (e == hipSuccess) e = setup_step(21, hipStreamCreateWithFlags(&up, hipStreamNonBlocking));
+    if (e != hipSuccess) {
+        if (up) (void)hipStreamDestroy(up);
+        release_pipeline(ctx);
+        return fail_hip(ctx, e, e == hipErrorOutOfMemory ? ZN_ERR_OOM : ZN_ERR_HIP);
+    }
+    ctx->up = up;
     return ZN_OK;
 }
 
@@ -1044,6 +1171,7 @@ int host_gemm(zn_ctx *ctx, int layout, const float *a, size_t a_len, const float
         if (bias) std::memcpy(pbias, bias, n * sizeof(float));
         if (accumulate) std::memcpy(pc, c, mn * sizeof(float));
         Lease din(ctx), dc(ctx);
+        PinnedFence fence{ctx};
         if ((rc = din.get(in_floats))) return rc;
         ZN_HIP_TRY(ctx, hipMemcpyAsync(din.ptr, pa, in_floats * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
         const bool zero_copy = mn * sizeof(float) <= kZeroCopyBytes;
@@ -1061,6 +1189,7 @@ int host_gemm(zn_ctx *ctx, int layout, const float *a, size_t a_len, const float
         if (!zero_copy)
             ZN_HIP_TRY(ctx, hipMemcpyAsync(pc, dc.ptr, mn * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
         ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        fence.done = true;
         std::memcpy(c, pc, mn * sizeof(float));
         return ZN_OK;
     }
@@ -1130,13 +1259,6 @@ const char *zn_hip_status_string(int status) {
 int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     if (!out) return ZN_ERR_INVALID_ARG;
     *out = nullptr;
-    int count = 0;
-    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
-        (void)hipGetLastError();
-        return ZN_ERR_NO_DEVICE;
-    }
-    if (device < 0 || device >= count) return ZN_ERR_INVALID_ARG;
-
     std::string dir;
     if (code_object_dir && *code_object_dir)
         dir = code_object_dir;
@@ -1148,6 +1270,17 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     const std::string conv_path = dir + "/" + kConvObject;
     const std::string elt_path = dir + "/" + kEltObject;
     const std::string attn_path = dir + "/" + kAttnObject;
+    // The code objects are checked on the host first, so a bad directory is
+    // reported the same way with or without a device.
+    for (const std::string *path : {&gemm_path, &conv_path, &elt_path, &attn_path})
+        if (!code_object_ok(*path)) return ZN_ERR_CODE_OBJECT;
+
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        return ZN_ERR_NO_DEVICE;
+    }
+    if (device < 0 || device >= count) return ZN_ERR_INVALID_ARG;
 
     zn_ctx *ctx = new (std::nothrow) zn_ctx();
     if (!ctx) return ZN_ERR_OOM;
@@ -1166,7 +1299,6 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     ctx->info.total_mem = (int64_t)prop.totalGlobalMem;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return bail(ZN_ERR_NO_DEVICE);
 
-    if (!file_exists(gemm_path) || !file_exists(elt_path) || !file_exists(attn_path)) return bail(ZN_ERR_CODE_OBJECT);
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) return bail(fail_hip(ctx, e));
     if (hipModuleLoad(&ctx->gemm_module, gemm_path.c_str()) != hipSuccess) {
@@ -1270,28 +1402,8 @@ int zn_hip_destroy(zn_ctx *ctx) {
         ctx->captured.clear();
     }
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->up) (void)hipStreamSynchronize(ctx->up);
-    if (ctx->down) (void)hipStreamSynchronize(ctx->down);
-    ctx->copier.reset();
-    for (int i = 0; i < 2; ++i) {
-        if (ctx->pinned_out_done[i]) (void)hipEventDestroy(ctx->pinned_out_done[i]);
-        if (ctx->pinned_out[i]) (void)hipHostFree(ctx->pinned_out[i]);
-        if (ctx->chunk_in[i]) (void)hipEventDestroy(ctx->chunk_in[i]);
-        if (ctx->chunk_out[i]) (void)hipEventDestroy(ctx->chunk_out[i]);
-        ctx->pinned_out_done[i] = ctx->chunk_in[i] = ctx->chunk_out[i] = nullptr;
-        ctx->pinned_out[i] = nullptr;
-    }
-    if (ctx->entry) (void)hipEventDestroy(ctx->entry);
-    ctx->entry = nullptr;
-    if (ctx->up) (void)hipStreamDestroy(ctx->up);
-    if (ctx->down) (void)hipStreamDestroy(ctx->down);
-    ctx->up = ctx->down = nullptr;
-    for (int i = 0; i < 2; ++i) {
-        if (ctx->pinned_done[i]) (void)hipEventDestroy(ctx->pinned_done[i]);
-        if (ctx->pinned[i]) (void)hipHostFree(ctx->pinned[i]);
-        ctx->pinned_done[i] = nullptr;
-        ctx->pinned[i] = nullptr;
-    }
+    release_pipeline(ctx);
+    release_staging(ctx);
     while (!ctx->graphs.empty()) (void)zn_hip_graph_destroy(ctx->graphs.back());
     for (void *w : ctx->retired_ws) (void)hipFree(w);
     ctx->retired_ws.clear();
@@ -2240,8 +2352,10 @@ int zn_hip_add_bias_host(zn_ctx *ctx, float *out, size_t out_len, const float *b
         float *po = pb.take(used), *pbias = pb.take(bias_len);
         std::memcpy(po, out, used * sizeof(float));
         std::memcpy(pbias, bias, bias_len * sizeof(float));
+        PinnedFence fence{ctx};
         if ((rc = zn_hip_add_bias(ctx, po, pbias, (int64_t)rows, (int64_t)bias_len))) return rc;
         ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        fence.done = true;
         std::memcpy(out, po, used * sizeof(float));
         return ZN_OK;
     }
@@ -2264,8 +2378,10 @@ int zn_hip_activation_forward_host(zn_ctx *ctx, int act, const float *in, size_t
         PinnedBlock pb{ctx->pinned[0]};
         float *pi = pb.take(in_len), *po = pb.take(in_len);
         std::memcpy(pi, in, in_len * sizeof(float));
+        PinnedFence fence{ctx};
         if ((rc = zn_hip_activation_forward(ctx, act, pi, po, (int64_t)in_len))) return rc;
         ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        fence.done = true;
         std::memcpy(out, po, in_len * sizeof(float));
         return ZN_OK;
     }
@@ -2291,8 +2407,10 @@ int zn_hip_activation_backward_host(zn_ctx *ctx, int act, const float *y, size_t
         float *py = pb.take(y_len), *pgo = pb.take(y_len), *pgi = pb.take(y_len);
         std::memcpy(py, y, y_len * sizeof(float));
         std::memcpy(pgo, grad_out, y_len * sizeof(float));
+        PinnedFence fence{ctx};
         if ((rc = zn_hip_activation_backward(ctx, act, py, pgo, pgi, (int64_t)y_len))) return rc;
         ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        fence.done = true;
         std::memcpy(grad_in, pgi, y_len * sizeof(float));
         return ZN_OK;
     }
@@ -2321,11 +2439,13 @@ int zn_hip_accumulate_bias_host(zn_ctx *ctx, float *grad_bias, size_t grad_bias_
         std::memcpy(pgaa, gaa, rows * grad_bias_len * sizeof(float));
         std::memcpy(pgb, grad_bias, grad_bias_len * sizeof(float));
         Lease dgaa(ctx);
+        PinnedFence fence{ctx};
         if ((rc = dgaa.get(rows * grad_bias_len))) return rc;
         ZN_HIP_TRY(ctx, hipMemcpyAsync(dgaa.ptr, pgaa, rows * grad_bias_len * sizeof(float), hipMemcpyHostToDevice,
                                        ctx->stream));
         if ((rc = zn_hip_accumulate_bias(ctx, pgb, dgaa.ptr, (int64_t)rows, (int64_t)grad_bias_len))) return rc;
         ZN_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        fence.done = true;
         std::memcpy(grad_bias, pgb, grad_bias_len * sizeof(float));
         return ZN_OK;
     }
