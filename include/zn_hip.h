@@ -200,6 +200,28 @@ int zn_hip_set_gemm_wave_split(zn_ctx *ctx, int waves);
 int zn_hip_sgemm(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                  const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias, int act);
 
+/* zn_hip_sgemm without any allocation: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * results as zn_hip_sgemm, except:
+ *  - split-K partial sums go to a fixed 64 MiB per-device scratch array in
+ *    the library (held until the process ends) instead of the context's
+ *    growable workspace.  When the launch policy's split would need more,
+ *    the GEMM runs unsplit; a split forced with zn_hip_set_gemm_splits that
+ *    needs more is refused with ZN_ERR_INVALID_ARG;
+ *  - operands are never copied into padded rows: rows that are not whole
+ *    16-byte float4s are staged with 4-byte loads (the same result).
+ * Results equal zn_hip_sgemm's bit for bit whenever both split K alike.
+ * Nothing in the scratch needs clearing between calls (each slice writes all
+ * of its partial sums).  All contexts on one device share its scratch, so
+ * calls whose executions overlap on one device (different streams or
+ * threads) race; calls ordered on one stream do not.  Returns ZN_ERR_OOM or
+ * ZN_ERR_HIP if the scratch could not be set up when the context was
+ * created. */
+int zn_hip_sgemm_noalloc(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
+                         const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias,
+                         int act);
+
 /* `batch` independent problems; operand p of problem i starts at
  * p + i*stride_p (elements).  stride_a or stride_b may be 0 (a shared
  * operand, as in CudaBackend.matMulBatch's shared B, src/cuda.zig:729-797).

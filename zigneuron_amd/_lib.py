@@ -125,6 +125,7 @@ SIGNATURES = {
     "zn_hip_set_gemm_persistent": (I, [P, I]),
     "zn_hip_set_gemm_wave_split": (I, [P, I]),
     "zn_hip_sgemm": (I, [P, I, I64, I64, I64, P, I64, P, I64, P, I64, I, P, I]),
+    "zn_hip_sgemm_noalloc": (I, [P, I, I64, I64, I64, P, I64, P, I64, P, I64, I, P, I]),
     "zn_hip_sgemm_strided_batched": (I, [P, I, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, I64, I, P, I]),
     "zn_hip_add_bias": (I, [P, P, P, I64, I64]),
     "zn_hip_activation_forward": (I, [P, I, P, P, I64]),

@@ -5,9 +5,10 @@
 // and device context (src/cuda_driver.zig, src/cuda_nvrtc.zig,
 // src/cuda_context.zig) and the CudaBackend GEMM wrappers (src/cuda.zig).
 // Design:
-//  * one context = one device + one HIP stream + the two offline-built gfx950
-//    code objects (zn_gemm_gfx950.hsaco, zn_elementwise_gfx950.hsaco) loaded
-//    with hipModuleLoad; no runtime compilation, no CPU fallback;
+//  * one context = one device + one HIP stream + the four offline-built
+//    gfx950 code objects (zn_gemm_gfx950.hsaco, zn_conv_gfx950.hsaco,
+//    zn_elementwise_gfx950.hsaco, zn_attention_gfx950.hsaco) loaded with
+//    hipModuleLoad; no runtime compilation, no CPU fallback;
 //  * a size-bucketed device-buffer cache for the host-slice entry points
 //    (the role of the pow2 pool in src/cuda_context.zig:773-852);
 //  * the launch policy (tile choice, raster, vector-load eligibility) lives
@@ -32,6 +33,14 @@
 
 #include "../../../include/zn_hip.h"
 #include "../zn_kernel_args.h"
+
+// Scratch of zn_hip_sgemm_noalloc: the split-K partial sums of a GEMM whose
+// caller cannot allocate.  One copy per device, held until the process ends.
+// In host code `scratch` only names the symbol; its device address on each
+// device comes from hipGetSymbolAddress (resolve_scratch below), and only
+// that address is ever passed to a kernel.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {
 
@@ -186,6 +195,12 @@ struct zn_ctx {
     hipEvent_t pinned_out_done[2] = {};
     hipEvent_t chunk_in[2] = {}, chunk_out[2] = {};
     hipEvent_t entry = nullptr;
+    // This device's copy of `scratch` (resolved at create) and, while
+    // zn_hip_sgemm_noalloc runs, the flag that routes its split-K partial
+    // sums there and turns operand packing off.
+    float *scratch = nullptr;
+    int scratch_status = ZN_OK;
+    bool no_alloc = false;
 };
 
 struct zn_event {
@@ -290,6 +305,46 @@ int select_device(zn_ctx *ctx) {
     ZN_HIP_TRY(ctx, hipSetDevice(ctx->device));
     return ZN_OK;
 }
+
+// Device address of `scratch`, resolved once per device with that device
+// current and kept for the process (each device holds its own copy at its
+// own address).  Every context on the device shares it.
+struct ScratchAddress {
+    bool resolved = false;
+    int status = ZN_OK;
+    int hip_error = 0;
+    float *ptr = nullptr;
+};
+std::mutex g_scratch_mu;
+std::map<int, ScratchAddress> g_scratch;
+
+int resolve_scratch(zn_ctx *ctx) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ScratchAddress &s = g_scratch[ctx->device];
+    if (!s.resolved) {
+        s.resolved = true;
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            s.status = e == hipErrorOutOfMemory ? ZN_ERR_OOM : ZN_ERR_HIP;
+            s.hip_error = (int)e;
+        } else {
+            s.ptr = static_cast<float *>(p);
+        }
+    }
+    ctx->scratch = s.ptr;
+    ctx->scratch_status = s.status;
+    if (s.status != ZN_OK) ctx->last_hip_error = s.hip_error;
+    return s.status;
+}
+
+// Marks a context as running zn_hip_sgemm_noalloc for one call.
+struct NoAllocScope {
+    zn_ctx *ctx;
+    explicit NoAllocScope(zn_ctx *c) : ctx(c) { ctx->no_alloc = true; }
+    ~NoAllocScope() { ctx->no_alloc = false; }
+};
 
 size_t bucket_of(size_t bytes) {
     size_t b = 256;
@@ -576,7 +631,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     Lease pack_a(ctx), pack_b(ctx);
     // rows padded with zeros to whole float4s (here, or by the caller: padded bit 0 = A, bit 1 = B)
     bool a_packed = (padded & 1) != 0, b_packed = (padded & 2) != 0;
-    if (!conv && batch == 1 && k > 0 && (double)m * n * k >= kPackMinMacs) {
+    if (!conv && !ctx->no_alloc && batch == 1 && k > 0 && (double)m * n * k >= kPackMinMacs) {
         const bool a_vec = aligned16(a) && lda % 4 == 0 && a_row % 4 == 0;
         const bool b_vec = aligned16(b) && ldb % 4 == 0 && b_row % 4 == 0;
         // both packings go into one launch (blockIdx.y selects the operand)
@@ -683,7 +738,16 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         k_chunk = cdiv(cdiv(k, splits), ts.bk) * ts.bk;
         splits = (int)cdiv(k, k_chunk);
         const size_t need = (size_t)splits * (size_t)chunk_batch * (size_t)m * (size_t)n * sizeof(float);
-        if (splits > 1 && ensure_workspace(ctx, need) != ZN_OK) splits = 1;  // fall back to one pass
+        if (ctx->no_alloc) {
+            // partial sums in the fixed scratch: a split the caller forced
+            // must fit it; the policy's own split falls back to one pass
+            if (need > kScratchBytes) {
+                if (ctx->forced_splits > 0) return ZN_ERR_INVALID_ARG;
+                splits = 1;
+            }
+        } else if (splits > 1 && ensure_workspace(ctx, need) != ZN_OK) {
+            splits = 1;  // fall back to one pass
+        }
         if (splits <= 1) {
             splits = 1;
             k_chunk = k;
@@ -691,7 +755,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     }
     args.splits = splits;
     args.k_chunk = (int32_t)k_chunk;
-    args.ws = ctx->ws;
+    float *const ws = ctx->no_alloc ? ctx->scratch : ctx->ws;
+    args.ws = ws;
     // 4-pixel (16-byte) gather: unit column stride, and whole chunks of 4 pixels per output row
     const int gather4 = conv && conv->stride_w == 1 && conv->out_w % 4 == 0 ? 1 : 0;
     hipFunction_t f = !conv                     ? ctx->gemm[layout][tile][vec ? 1 : 0]
@@ -769,7 +834,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         if (splits > 1) {
             ZnReduceArgs r;
             std::memset(&r, 0, sizeof(r));
-            r.ws = ctx->ws;
+            r.ws = ws;
             r.c = part.c;
             r.bias = bias;
             r.ldc = ldc;
@@ -1298,6 +1363,9 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     ctx->info.clock_khz = prop.clockRate;
     ctx->info.total_mem = (int64_t)prop.totalGlobalMem;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return bail(ZN_ERR_NO_DEVICE);
+    // The no-allocation GEMM's scratch: a failure here is kept and reported
+    // by zn_hip_sgemm_noalloc; every other entry point works without it.
+    (void)resolve_scratch(ctx);
 
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) return bail(fail_hip(ctx, e));
@@ -1652,6 +1720,15 @@ int zn_hip_set_gemm_persistent(zn_ctx *ctx, int mode) {
 
 int zn_hip_sgemm(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                  const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias, int act) {
+    return gemm_launch(ctx, layout, m, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias, act);
+}
+
+int zn_hip_sgemm_noalloc(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
+                         const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias,
+                         int act) {
+    if (!ctx) return ZN_ERR_INVALID_ARG;
+    if (!ctx->scratch) return ctx->scratch_status != ZN_OK ? ctx->scratch_status : ZN_ERR_HIP;
+    NoAllocScope scope(ctx);
     return gemm_launch(ctx, layout, m, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias, act);
 }
 
