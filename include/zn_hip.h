@@ -172,6 +172,8 @@ int zn_hip_event_destroy(zn_event *ev);
 #define ZN_TILE_32x32 4
 #define ZN_TILE_128x128_K32 5 /* 128x128, BK 32, one workgroup per CU; not for convolutions */
 #define ZN_TILE_64x64_K16 6   /* 64x64, BK 16, six workgroups per CU; not for convolutions */
+#define ZN_TILE_256x256 7     /* 256x256, BK 16, one workgroup per CU; 16-byte rows only (otherwise 256x128); not for
+                                 convolutions */
 int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile);
 /* Split-K override: 0 (the default) lets the policy choose, 1..64 forces that
  * many K slices (at most K / BK) for every following GEMM on this context.

@@ -437,7 +437,7 @@ def test_invalid_arguments_are_errors(ctx, backend):
 
 
 # ------------------------------------------------ every kernel variant
-TILES = ["256x128", "128x128", "128x64", "64x64", "32x32", "128x128k32", "64x64k16"]
+TILES = ["256x128", "128x128", "128x64", "64x64", "32x32", "128x128k32", "64x64k16", "256x256"]
 
 
 @pytest.mark.parametrize("aligned", [True, False], ids=["vec16", "vec4"])
@@ -466,10 +466,11 @@ def test_every_tile_variant(ctx, tile, layout, aligned):
 
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
 def test_pinned_tiles_bit_identical(ctx, layout):
-    """The three-stage pinned loop (64x64, 128x128k32, 64x64k16 tiles) keeps the
-    two-stage loop's K order per element: unsplit results are bit-identical
-    to the 128x128 two-stage kernel's, on interior tiles (short store path)
-    and edge tiles alike; split into K slices they match the oracle."""
+    """The three-stage loops (pinned: 64x64, 128x128k32, 64x64k16; wide:
+    256x256) keep the two-stage loop's K order per element: unsplit results
+    are bit-identical to the 128x128 two-stage kernel's, on interior tiles
+    (short store path) and edge tiles alike; split into K slices they match
+    the oracle."""
     m, n, k = 520, 392, 1040
     rng = np.random.default_rng(zlib.crc32(f"pinned-{layout}".encode()))
     a_shape, b_shape = stored_shapes(layout, m, n, k)
@@ -477,16 +478,16 @@ def test_pinned_tiles_bit_identical(ctx, layout):
     out = {}
     try:
         ctx.set_gemm_splits(1)
-        for tile in ("128x128", "64x64", "128x128k32", "64x64k16"):
+        for tile in ("128x128", "64x64", "128x128k32", "64x64k16", "256x256"):
             announce(f"pinned {layout} {tile} unsplit")
             ctx.set_gemm_tile(tile)
             out[tile] = run_gemm(ctx, layout, a, b, m, n, k)
-        for tile in ("64x64", "128x128k32", "64x64k16"):
+        for tile in ("64x64", "128x128k32", "64x64k16", "256x256"):
             assert np.array_equal(out[tile].view(np.uint32), out["128x128"].view(np.uint32)), tile
         ref = ref_gemm(layout, a, b, m, n, k)
         assert_close(out["128x128"], ref, layout, a, b, m, n, k, what="128x128")
         ctx.set_gemm_splits(3)
-        for tile in ("64x64", "128x128k32", "64x64k16"):
+        for tile in ("64x64", "128x128k32", "64x64k16", "256x256"):
             announce(f"pinned {layout} {tile} split 3")
             ctx.set_gemm_tile(tile)
             c = run_gemm(ctx, layout, a, b, m, n, k)

@@ -21,7 +21,7 @@ from gpu_common import announce, assert_close, stored_shapes
 
 pytestmark = pytest.mark.gpu
 
-TILES = ["auto", "256x128", "128x128", "128x64", "64x64", "32x32", "128x128k32", "64x64k16"]
+TILES = ["auto", "256x128", "128x128", "128x64", "64x64", "32x32", "128x128k32", "64x64k16", "256x256"]
 ACTS = ["linear", "relu", "sigmoid", "tanh"]
 
 

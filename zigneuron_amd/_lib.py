@@ -26,7 +26,8 @@ ZN_ERR_OVERFLOW = -8
 
 LAYOUT_NN, LAYOUT_NT, LAYOUT_TN = 0, 1, 2
 TILE_AUTO = -1
-TILES = {"auto": -1, "256x128": 0, "128x128": 1, "128x64": 2, "64x64": 3, "32x32": 4, "128x128k32": 5, "64x64k16": 6}
+TILES = {"auto": -1, "256x128": 0, "128x128": 1, "128x64": 2, "64x64": 3, "32x32": 4, "128x128k32": 5, "64x64k16": 6,
+         "256x256": 7}
 ACT_LINEAR, ACT_RELU, ACT_SIGMOID, ACT_TANH = 0, 1, 2, 3
 
 

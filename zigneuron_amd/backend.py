@@ -210,7 +210,8 @@ class Context:
         check(_lib.load().zn_hip_copy_f32(self.handle, int(dst), int(src), int(count)), "zn_hip_copy_f32")
 
     def set_gemm_tile(self, tile="auto") -> None:
-        """Force one macro tile ("256x128", "128x128", "128x64", "64x64", "32x32", "128x128k32", "64x64k16") or "auto"."""
+        """Force one macro tile ("256x128", "128x128", "128x64", "64x64", "32x32", "128x128k32", "64x64k16",
+        "256x256") or "auto"."""
         check(_lib.load().zn_hip_set_gemm_tile(self.handle, _lib.TILES[tile] if isinstance(tile, str) else tile),
               "zn_hip_set_gemm_tile")
 

@@ -15,6 +15,9 @@
 //                                    one workgroup per CU)
 //   h = 64x64,   4 waves of 32x32    several rounds (BK 16, pinned loop,
 //                                    six workgroups per CU)
+//   w = 256x256, 8 waves of 128x64   full rounds of large problems (BK 16,
+//                                    gemm_tile_wide, one workgroup per CU;
+//                                    16-byte staging only, no plain variant)
 // x, l, n and s run gemm_tile_dma's two-stage loop, m, r and h
 // gemm_tile_pinned's three-stage one.  The _v variants stage operands with
 // 16-byte loads straight into LDS (aligned rows, contiguous extents a
@@ -40,6 +43,14 @@ ZN_GEMM_TILE(m, gemm_tile_pinned, 64, 64, 32, 2, 2, 1)
 ZN_GEMM_TILE(s, gemm_tile_dma, 32, 32, 32, 1, 1, 1)
 ZN_GEMM_TILE(r, gemm_tile_pinned, 128, 128, 32, 4, 2, 1)
 ZN_GEMM_TILE(h, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
+
+#define ZN_GEMM_WIDE(LAYOUT, AK, BKC)                                                            \
+    extern "C" __global__ __launch_bounds__(512, 1) void zn_sgemm_##LAYOUT##_w_v(ZnGemmArgs p) { \
+        gemm_tile_wide<256, 256, 16, 2, 4, AK, BKC>(p);                                          \
+    }
+ZN_GEMM_WIDE(nn, true, false)
+ZN_GEMM_WIDE(nt, true, true)
+ZN_GEMM_WIDE(tn, false, false)
 
 // Intra-workgroup split-K GEMMs (gemm_ksplit) on 32x32 tiles, BK 32, with
 // KS = 4 or 8 waves: zn_sgemmk<KS>_<layout>[_v], for problems of at most one

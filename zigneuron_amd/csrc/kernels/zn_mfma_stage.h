@@ -158,6 +158,34 @@ __device__ __forceinline__ void read_frags_dma(const float *lds, int w0, int kg,
     }
 }
 
+// One LDS read of the fragments read_frags_dma reads for a K group: for a
+// K-contiguous tile, block `idx` (one 16-byte read of 4 consecutive k); for an
+// X-contiguous tile, MFMA step `idx` (one FX-wide read of FX consecutive rows).
+// Lets a main loop spread a group's reads over the MFMAs of the previous one.
+template <int BX, int BK, int FX, bool KC>
+__device__ __forceinline__ void read_frag_one(const float *lds, int w0, int kg, int lane, int idx, float (&frag)[FX][4]) {
+    const int i = lane & 31;
+    const int h = lane >> 5;
+    if constexpr (KC) {
+        const int row = w0 + 32 * idx + i;
+        const int slot = (kg / 4 + h) ^ DmaStage<BX, BK, kWave, true, 16>::swz(row);
+        const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(lds + row * BK + 4 * slot);
+        frag[idx][0] = v[0];
+        frag[idx][1] = v[1];
+        frag[idx][2] = v[2];
+        frag[idx][3] = v[3];
+    } else {
+        typedef typename FVec<FX>::type VT;
+        const VT v = *reinterpret_cast<const VT *>(lds + (kg + 4 * h + idx) * BX + w0 + FX * i);
+        if constexpr (FX == 1) {
+            frag[0][idx] = v;
+        } else {
+#pragma unroll
+            for (int f = 0; f < FX; ++f) frag[f][idx] = v[f];
+        }
+    }
+}
+
 }  // namespace
 
 #endif

@@ -45,20 +45,22 @@ static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 namespace {
 
 // Macro tiles of the GEMM code object (kernels/gemm_f32.hip).
-enum Tile { kTileX = 0, kTileL, kTileN, kTileM, kTileS, kTileR, kTileH, kNumTiles };
+enum Tile { kTileX = 0, kTileL, kTileN, kTileM, kTileS, kTileR, kTileH, kTileW, kNumTiles };
 struct TileShape {
     int bm, bn, bk, threads;
     const char *suffix;
     bool conv;        // the convolution code object has kernels for it
     bool persistent;  // zn_sgemmp_<layout>_<suffix>_v exists
+    bool plain;       // a 4-byte-staging kernel (no _v suffix) exists
 };
-constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x", true, true},
-                                         {128, 128, 16, 256, "l", true, true},
-                                         {128, 64, 16, 128, "n", true, true},
-                                         {64, 64, 32, 256, "m", true, true},
-                                         {32, 32, 32, 64, "s", true, false},
-                                         {128, 128, 32, 512, "r", false, false},
-                                         {64, 64, 16, 256, "h", false, false}};
+constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x", true, true, true},
+                                         {128, 128, 16, 256, "l", true, true, true},
+                                         {128, 64, 16, 128, "n", true, true, true},
+                                         {64, 64, 32, 256, "m", true, true, true},
+                                         {32, 32, 32, 64, "s", true, false, true},
+                                         {128, 128, 32, 512, "r", false, false, true},
+                                         {64, 64, 16, 256, "h", false, false, true},
+                                         {256, 256, 16, 512, "w", false, false, false}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
 enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kPack, kToNhwc, kNumElt };
@@ -460,10 +462,18 @@ int64_t round_splits(int64_t tiles, int64_t k, int64_t cus) {
 // A gathered (implicit convolution) operand costs more per staged element, so
 // the larger l tile, which reuses each staged element over 128 rows, pays
 // off from 2 instead of 4 tiles per CU (C5 conv: l 221 us, m 227 us).
-Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t batch, bool gathered = false) {
+Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t batch, bool gathered = false,
+                 bool wide_ok = false) {
     const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
     auto tiles = [&](Tile t) { return cdiv(m, kTiles[t].bm) * cdiv(n, kTiles[t].bn) * batch; };
     auto useful = [&](Tile t) { return 4 * m * n * batch >= 3 * tiles(t) * kTiles[t].bm * kTiles[t].bn; };
+    // 256x256 (16-byte staging only, one workgroup per CU): long K and whole
+    // rounds of tiles, the last at least 80% full (8192^3 NN 141.7 -> 145.4
+    // TFLOP/s, 4096^3 125.5 -> 133.7 against 256x128; a ragged last round
+    // would leave CUs idle for a whole 256x256 tile)
+    if (wide_ok && k >= 512 && tiles(kTileW) >= cus && useful(kTileW) &&
+        5 * tiles(kTileW) >= 4 * cdiv(tiles(kTileW), cus) * cus)
+        return kTileW;
     // short K: a tile's epilogue outweighs its K walk, and the smaller l tile
     // overlaps them better (C5 QK^T, K = 64: l 242 us, x 252 us, round-robin A/B)
     if (k <= 256 && tiles(kTileL) >= 2 * cus && useful(kTileL)) return kTileL;
@@ -615,9 +625,14 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // 128x128 and 314 us for 256x128).
     // A forced tile without convolution kernels leaves convolutions to the policy.
     const bool forced = ctx->forced_tile >= 0 && (!conv || kTiles[ctx->forced_tile].conv);
-    const Tile tile = forced                        ? (Tile)ctx->forced_tile
-                      : conv && mode == kGatherNhwc ? kTileM
-                                                    : choose_tile(ctx, m, n, k, batch, conv != nullptr);
+    // 16-byte staging of both operands as they lie (the tiles without a
+    // 4-byte kernel need it; packed copies are not made for them)
+    const bool native_vec = !conv && aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0 && stride_a % 4 == 0 &&
+                            stride_b % 4 == 0 && a_row % 4 == 0 && b_row % 4 == 0;
+    Tile tile = forced                        ? (Tile)ctx->forced_tile
+                : conv && mode == kGatherNhwc ? kTileM
+                                              : choose_tile(ctx, m, n, k, batch, conv != nullptr, native_vec);
+    if (!kTiles[tile].plain && !native_vec) tile = kTileX;  // forced onto a tile it cannot stage: 256x128
     const TileShape &ts = kTiles[tile];
     const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
     if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
@@ -1387,7 +1402,7 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     }
     for (int l = 0; l < 3; ++l)
         for (int t = 0; t < kNumTiles; ++t)
-            for (int v = 0; v < 2; ++v) {
+            for (int v = kTiles[t].plain ? 0 : 1; v < 2; ++v) {
                 char name[64];
                 std::snprintf(name, sizeof(name), "zn_sgemm_%s_%s%s", kLayoutName[l], kTiles[t].suffix,
                               v ? "_v" : "");
