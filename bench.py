@@ -13,18 +13,28 @@ on).  The other BASELINE configurations are timed too and reported under
 
 The CPU baseline is the oracle (a restatement of the reference CPU tiled
 matmul, src/backend.zig:2523-2570) timed on a bounded row sample of the same
-8192^3 workload, single-threaded and on all host cores (OpenMP over row
-blocks, bit-identical to the sequential order).
+8192^3 workload, single-threaded and on the CPUs this job may use (OpenMP
+over row blocks, bit-identical to the sequential order).
+
+roofline.traffic is measured in the same run: before it touches the GPU,
+bench.py runs itself twice under `rocprofv3 --pmc` (FETCH_SIZE, then
+WRITE_SIZE) in --traffic-probe mode, which launches the 8192^3 GEMM and a
+1 GiB zn_copy_f32; each counter is scaled by what it reads for the copy's
+known 1 GiB.  Without rocprofv3 (or if a pass fails) traffic is null.
 
 One GPU only: --gpus N with N > 1 exits with a message.
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import platform
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -35,7 +45,7 @@ sys.path.insert(0, ROOT)
 PEAK_F32_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 PEAK_HBM_GBS = 8000.0
 METRIC = "fp32 GEMM TFLOP/s and % of MFMA peak; MLP train-step GEMM time, 1 MI355X"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_sgemm_nn_8192.json")
+HEADLINE = 8192  # M = N = K of the timed GEMM
 
 
 def log(*a):
@@ -263,7 +273,9 @@ def bench_mlp_step(ctx, rng, reps, warmup):
     ms = time_launches(ctx, step, reps * 5, warmup)
     flops = 2.0 * batch * (784 * 128 + 128 * 10) * 3
     e = {"name": "C2 MLP train step (6 GEMMs + 4 helpers)", "step_ms": round(ms, 5),
-         "gemm_gflop": round(flops / 1e9, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 3)}
+         "gemm_gflop": round(flops / 1e9, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+         "init": ("W1 = U[-1,1)*sqrt(2/784) (relu), W2 = U[-1,1)*sqrt(1/128) (linear): Dense.init's scales, "
+                  "src/layer.zig:331-333; BASELINE's 'Xavier' for W2 would be sqrt(2/138)")}
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us per step (one host call per kernel)")
     if USE_GRAPHS:
         graph = ctx.capture(step)  # the same step, replayed as one HIP graph
@@ -274,13 +286,44 @@ def bench_mlp_step(ctx, rng, reps, warmup):
     return e
 
 
+def host_cpus():
+    """(threads the CPU legs use, description): the CPUs this process may run
+    on, at most OMP_NUM_THREADS when set.  The GPU boxes give a job a 16-CPU
+    share of the host (OMP_NUM_THREADS=16) whatever the host has, so the
+    "all cores" leg runs on that share and says so."""
+    from oracle import oracle
+    affinity = oracle.cpu_count()
+    logical = os.cpu_count() or affinity
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    threads = affinity
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    model = ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if not model:
+        model = platform.processor() or ""
+    desc = {"cpu_model": model, "host_logical_cpus": logical, "affinity_cpus": affinity,
+            "omp_num_threads": omp or None,
+            "threads_used": threads,
+            "cap": (f"{threads} of the host's {logical} logical CPUs: the CPUs this job may use"
+                    + (f" (OMP_NUM_THREADS={omp}, the per-GPU CPU share of the box)" if omp else ""))}
+    return threads, desc
+
+
 def cpu_baseline(target_s=5.0):
     """Oracle (reference CPU tiled matmul restated) on a row sample of the 8192^3 workload."""
     from oracle import oracle
     rng = np.random.default_rng(1)
     n = k = 8192
     b = uniform(rng, (k, n))
-    threads = max(1, min(16, oracle.cpu_count()))
+    threads, host = host_cpus()
     res = {}
     for label, th in (("single", 1), ("all", threads)):
         rows = 32 * th
@@ -295,21 +338,13 @@ def cpu_baseline(target_s=5.0):
         dt = time.perf_counter() - t
         res[label] = {"tflops": 2.0 * rows * n * k / dt / 1e12, "rows": rows, "seconds": dt, "threads": th}
         log(f"  cpu {label}: {rows} rows x 8192 x 8192 in {dt:.2f} s = {res[label]['tflops'] * 1e3:.2f} GFLOP/s")
-    cpu_model = platform.processor() or ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     allc = res["all"]
     return {"value": round(allc["tflops"], 5), "unit": "TFLOP/s", "cores": allc["threads"], "kind": "port",
             "sample": (f"oracle blocked NN (src/backend.zig:2523-2570 restated) on {allc['rows']} of 8192 rows of "
                        f"the 8192^3 workload, {allc['threads']} OpenMP threads; single-thread on "
                        f"{res['single']['rows']} rows: {res['single']['tflops']:.5f} TFLOP/s"),
-            "single_thread_tflops": round(res["single"]["tflops"], 5), "cpu_model": cpu_model}
+            "single_thread_tflops": round(res["single"]["tflops"], 5), "cpu_model": host["cpu_model"],
+            "host": host}
 
 
 def cpu_rows():
@@ -331,7 +366,7 @@ def cpu_rows():
 
     # The GEMM configurations: one thread on a row block of C (rows of A, or columns of A for TN), and
     # the whole GEMM on all host cores (OpenMP over row blocks, bit-identical to one thread).
-    threads = max(1, min(16, oracle.cpu_count()))
+    threads, _ = host_cpus()
 
     def gemm(layout, a, b, m, n, k, th):
         if layout == "nn":
@@ -409,13 +444,151 @@ def copy_calibration(ctx, steps, warmup) -> int:
     return 0
 
 
-def load_traffic():
+def traffic_probe(ctx) -> int:
+    """--traffic-probe: one warm and one counted 8192^3 NN GEMM, then one 1 GiB
+    zn_copy_f32 (the known-size reference), for measure_traffic's rocprofv3
+    passes."""
+    n = HEADLINE
+    a, b, c = ctx.alloc(n * n).fill(0.5), ctx.alloc(n * n).fill(0.25), ctx.alloc(n * n)
+    for _ in range(2):
+        ctx.sgemm("nn", n, n, n, a, n, b, n, c, n)
+    ctx.sync()
+    for buf in (a, b, c):
+        buf.close()
+    count = (1 << 30) // 4
+    src, dst = ctx.alloc(count).fill(1.0), ctx.alloc(count)
+    ctx.copy(dst.ptr, src.ptr, count)
+    ctx.sync()
+    src.close()
+    dst.close()
+    ctx.close()
+    return 0
+
+
+def counter_rows(path):
+    """{kernel name: [counter value per dispatch, in dispatch order]} of a rocprofv3 counter CSV."""
+    out = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            out.setdefault(r["Kernel_Name"].split("(")[0].strip(), []).append(float(r["Counter_Value"]))
+    return out
+
+
+def measure_traffic(timeout_s=120):
+    """HBM traffic of one 8192^3 launch from two rocprofv3 --pmc passes over
+    --traffic-probe (FETCH_SIZE, then WRITE_SIZE, in KiB per dispatch), each
+    scaled so that the copy kernel's counter reads the 1 GiB it moves.  Runs
+    before this process touches the GPU.  Returns (traffic dict or None, note)."""
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None, "rocprofv3 not found"
+    reads = {}
+    work = tempfile.mkdtemp(prefix="zn_traffic_", dir="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp")
     try:
-        with open(TRAFFIC_FILE) as f:
-            t = json.load(f)
-        return float(t["hbm_bytes_per_launch"])
-    except (OSError, ValueError, KeyError):
-        return None
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            out_dir = os.path.join(work, counter.lower())
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out_dir, "-o", "p", "--",
+                   sys.executable, os.path.join(ROOT, "bench.py"), "--traffic-probe"]
+            log(f"traffic pass: {' '.join(cmd[:4])} ... --traffic-probe")
+            r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True, timeout=timeout_s)
+            files = [os.path.join(dp, f) for dp, _, fs in os.walk(out_dir) for f in fs
+                     if f.endswith("counter_collection.csv")]
+            if not files:
+                return None, f"{counter} pass wrote no counters (rc {r.returncode}): {r.stderr[-300:]}"
+            reads[counter] = counter_rows(files[0])
+    except (OSError, subprocess.SubprocessError) as e:
+        return None, f"rocprofv3 pass failed: {e}"
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
+    gemm = [k for k in reads["FETCH_SIZE"] if k.startswith("zn_sgemm")]
+    if len(gemm) != 1 or "zn_copy_f32" not in reads["FETCH_SIZE"] or "zn_copy_f32" not in reads["WRITE_SIZE"]:
+        return None, f"unexpected kernels in the probe: {sorted(reads['FETCH_SIZE'])}"
+    kern = gemm[0]
+    gib = float(1 << 30)
+    fetch_scale = gib / (reads["FETCH_SIZE"]["zn_copy_f32"][-1] * 1024)
+    write_scale = gib / (reads["WRITE_SIZE"]["zn_copy_f32"][-1] * 1024)
+    fetch = reads["FETCH_SIZE"][kern][-1] * 1024 * fetch_scale  # the counted (second) launch
+    write = reads["WRITE_SIZE"][kern][-1] * 1024 * write_scale
+    return {"kernel": kern, "bytes": fetch + write, "fetch_bytes": round(fetch), "write_bytes": round(write),
+            "fetch_kib": reads["FETCH_SIZE"][kern][-1], "write_kib": reads["WRITE_SIZE"][kern][-1],
+            "fetch_scale": round(fetch_scale, 5), "write_scale": round(write_scale, 5)}, "measured"
+
+
+def counter_pass(ctx) -> int:
+    """--counter-pass: every BASELINE configuration's kernels three times each,
+    eagerly (no graphs, no timing loops), plus the 1 GiB copy, for rocprofv3
+    --pmc / --kernel-trace runs that attribute counters per kernel."""
+    rng = np.random.default_rng(3)
+
+    def gemm(layout, m, n, k, batch=1, bias=None, act="linear", lo=-1.0):
+        a_shape = (k, m) if layout == "tn" else (m, k)
+        b_shape = (n, k) if layout == "nt" else (k, n)
+        a = ctx.to_device(uniform(rng, (batch,) + a_shape, lo=lo))
+        b = ctx.to_device(uniform(rng, (batch,) + b_shape))
+        c = ctx.alloc(batch * m * n)
+        db = ctx.to_device(bias) if bias is not None else None
+        lda, ldb = (m if layout == "tn" else k), (k if layout == "nt" else n)
+        for _ in range(3):
+            if batch == 1:
+                ctx.sgemm(layout, m, n, k, a, lda, b, ldb, c, n, False, db, act)
+            else:
+                ctx.sgemm_strided_batched(layout, m, n, k, a, lda, a_shape[0] * a_shape[1], b, ldb,
+                                          b_shape[0] * b_shape[1], c, n, m * n, batch)
+        ctx.sync()
+        for buf in (a, b, c, db):
+            if buf is not None:
+                buf.close()
+
+    log("counter pass: GEMM configurations")
+    gemm("nn", 512, 512, 512)
+    gemm("nn", 256, 128, 784, bias=np.zeros(128, np.float32), act="relu", lo=0.0)
+    gemm("nn", 256, 10, 128, bias=np.zeros(10, np.float32))
+    gemm("nt", 256, 128, 10)
+    gemm("tn", 128, 10, 256)
+    gemm("nt", 256, 784, 128)
+    gemm("tn", 784, 128, 256)
+    gemm("tn", 1024, 1024, 4096)
+    gemm("nt", 4096, 1024, 1024)
+    gemm("nn", 1000, 1000, 1000)
+    gemm("nn", 4097, 1023, 777)
+    gemm("nn", HEADLINE, HEADLINE, HEADLINE)
+    gemm("nt", 1024, 1024, 64, batch=128)
+    gemm("nn", 1024, 64, 1024, batch=128)
+    gemm("nt", 100352, 128, 576)
+    log("counter pass: C2 step, C5 convolution and attention")
+    from zigneuron_amd import DenseDevice
+    x = ctx.to_device(uniform(rng, (256, 784), 0.0, 1.0))
+    dy = ctx.to_device(uniform(rng, (256, 10)))
+    l1 = DenseDevice(ctx, 784, 128, "relu", 256, seed=1)
+    l2 = DenseDevice(ctx, 128, 10, "linear", 256, seed=2)
+    for _ in range(3):
+        h = l1.forward(x)
+        l2.forward(h)
+        l1.backward(x, l2.backward(h, dy))
+    ctx.sync()
+    B, C, H, W, OC = 32, 64, 56, 56, 128
+    xi, w, bias = ctx.to_device(uniform(rng, (B, C, H, W))), ctx.to_device(uniform(rng, (OC, 9 * C))), \
+        ctx.to_device(uniform(rng, (OC,)))
+    o, go = ctx.alloc(B * OC * H * W), ctx.to_device(uniform(rng, (B, OC, H, W)))
+    gi, gw, gb = ctx.alloc(B * C * H * W), ctx.alloc(OC * 9 * C), ctx.alloc(OC)
+    for _ in range(3):
+        ctx.conv2d_forward_im2col(xi, w, bias, o, B, C, OC, 3, 3, H, W, H, W, 1, 1, 1, 1)
+        ctx.conv2d_backward_im2col(xi, w, go, gi, gw, gb, B, C, OC, 3, 3, H, W, H, W, 1, 1, 1, 1)
+    BH, S, D = 128, 1024, 64
+    q, k, v = (ctx.to_device(uniform(rng, (BH, S, D))) for _ in range(3))
+    ao = ctx.alloc(BH * S * D)
+    for _ in range(3):
+        ctx.attention_forward(q, k, v, ao, BH, S, D, 0.125)
+    ctx.sync()
+    count = (1 << 30) // 4
+    src, dst = ctx.alloc(count).fill(1.0), ctx.alloc(count)
+    for _ in range(3):
+        ctx.copy(dst.ptr, src.ptr, count)
+    ctx.sync()
+    ctx.close()
+    log("counter pass: done")
+    return 0
 
 
 def main() -> int:
@@ -431,6 +604,10 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time only a 1 GiB device-to-device copy (zn_copy_f32): the known-size reference "
                          "for scaling FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
+    ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--counter-pass", action="store_true",
+                    help="run every configuration's kernels three times, untimed (for rocprofv3 runs)")
     args = ap.parse_args()
     global USE_GRAPHS, CHECK
     USE_GRAPHS = not args.no_graph
@@ -440,13 +617,22 @@ def main() -> int:
               "design-only here.", file=sys.stderr)
         return 2
 
+    traffic, traffic_note = None, "skipped (--no-traffic)"
+    if not (args.no_traffic or args.traffic_probe or args.counter_pass or args.copy_calibration):
+        traffic, traffic_note = measure_traffic()  # child processes, before this one touches the GPU
+        log(f"traffic: {traffic_note}")
+
     from zigneuron_amd import Context
     ctx = Context(0)
     log(f"device {ctx.arch}, {ctx.compute_units} CUs, {ctx.clock_khz / 1e3:.0f} MHz")
     if args.copy_calibration:
         return copy_calibration(ctx, args.steps, args.warmup)
+    if args.traffic_probe:
+        return traffic_probe(ctx)
+    if args.counter_pass:
+        return counter_pass(ctx)
     rng = np.random.default_rng(42)
-    m = n = k = 8192
+    m = n = k = HEADLINE
     log("allocating 8192^3 operands")
     a_h, b_h = uniform(rng, (m, k)), uniform(rng, (k, n))
     a, b, c = ctx.to_device(a_h), ctx.to_device(b_h), ctx.alloc(m * n)
@@ -492,18 +678,23 @@ def main() -> int:
         cpu = cpu_baseline()
         cpu["configs"] = cpu_rows()
 
-    traffic = load_traffic()
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic U[-1,1) operands, seed 42, resident in HBM",
         "config": {"workload": "NN fp32 GEMM 8192x8192x8192 row-major (BASELINE configs[3], C4 large)",
-                   "m": m, "n": n, "k": k, "layout": "nn", "kernel": "zn_sgemm_nn_x_v",
+                   "m": m, "n": n, "k": k, "layout": "nn", "kernel": traffic["kernel"] if traffic else None,
                    "pct_f32_peak": round(100 * value / PEAK_F32_TFLOPS, 2),
                    "sampled_rows_max_componentwise_err": rel, "tolerance": 1e-5 * np.sqrt(k),
                    "device": ctx.arch, "compute_units": ctx.compute_units},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_F32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_F32_TFLOPS, 4), "traffic": traffic,
+                     "frac": round(achieved / PEAK_F32_TFLOPS, 4),
+                     "traffic": round(traffic["bytes"]) if traffic else None,
+                     "traffic_detail": dict(traffic, note=("FETCH_SIZE + WRITE_SIZE of the timed kernel in this run, "
+                                                           "each scaled by the counter's reading for a 1 GiB "
+                                                           "zn_copy_f32; L2-miss traffic, part of it served by "
+                                                           "the MALL")) if traffic else traffic_note,
+                     "algorithmic_bytes_per_launch": gemm_bytes(m, n, k),
                      "kernel_ms": round(kernel_ms, 4), "algorithmic_flops_per_launch": flops},
         "cpu_baseline": cpu,
         "configs": configs,

@@ -63,7 +63,11 @@ def check_bias(got, gaa, fused, start=None):
 
 @pytest.mark.parametrize("fused", [False, True])
 def test_c2_mlp_training_step(ctx, fused):
-    """X[256x784] U[0,1) -> W1 He + b1(0) + ReLU -> W2 Xavier + b2(0) linear; dY2 U[-1,1).
+    """X[256x784] U[0,1) -> W1 He + b1(0) + ReLU -> W2 + b2(0) linear; dY2 U[-1,1).
+    W1 = U[-1,1)*sqrt(2/784) and W2 = U[-1,1)*sqrt(1/128): Dense.init's scales
+    for a relu and a linear layer (src/layer.zig:331-333).  BASELINE.json calls
+    W2 "Xavier-init", sqrt(2/138), which the reference uses only for sigmoid,
+    tanh and softmax layers; the scale does not affect parity.
     Each of the six GEMMs is checked against the oracle on the GPU's own inputs.
     The reference's call sequence gives bit-identical bias gradients; the fused
     backward sums them over row splits (within the GEMM tolerance)."""
