@@ -255,8 +255,10 @@ def bench_host_slice(ctx, a_h, b_h):
 
 
 def bench_mlp_step(ctx, rng, reps, warmup):
-    """C2: the six GEMMs of one Dense 784-128-10 training step at batch 256 (plus the
-    relu-mask and bias-gradient kernels between them), device resident, one stream."""
+    """C2: the six GEMMs of one Dense 784-128-10 training step at batch 256 (with the
+    relu derivative and both bias gradients), device resident, one stream: two fused
+    forwards and two chained backwards (L2's launch also writes L1's relu derivative),
+    four launches."""
     from zigneuron_amd import DenseDevice
     batch = 256
     x = ctx.to_device(uniform(rng, (batch, 784), 0.0, 1.0))
@@ -267,12 +269,12 @@ def bench_mlp_step(ctx, rng, reps, warmup):
     def step():
         h = l1.forward(x)
         l2.forward(h)
-        g = l2.backward(h, dy)
-        l1.backward(x, g)
+        l2.backward(h, dy, below=l1)
+        l1.backward(x, None)
 
     ms = time_launches(ctx, step, reps * 5, warmup)
     flops = 2.0 * batch * (784 * 128 + 128 * 10) * 3
-    e = {"name": "C2 MLP train step (6 GEMMs + 4 helpers)", "step_ms": round(ms, 5),
+    e = {"name": "C2 MLP train step (6 GEMMs, 4 launches)", "step_ms": round(ms, 5),
          "gemm_gflop": round(flops / 1e9, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
          "init": ("W1 = U[-1,1)*sqrt(2/784) (relu), W2 = U[-1,1)*sqrt(1/128) (linear): Dense.init's scales, "
                   "src/layer.zig:331-333; BASELINE's 'Xavier' for W2 would be sqrt(2/138)")}

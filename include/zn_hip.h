@@ -263,6 +263,23 @@ int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float 
                           const float *activated_output, const float *grad_output, float *grad_after_act,
                           float *grad_input, float *grad_weights, float *grad_bias, int64_t batch, int64_t in_size,
                           int64_t out_size);
+/* zn_hip_dense_backward for a stack of Dense layers walked top-down, with
+ * fewer launches.  No counterpart in the reference, whose backward loop
+ * (src/network.zig:455-477) calls Dense.backward layer by layer; this gives
+ * the same bits as zn_hip_dense_backward called that way.
+ *   gaa_ready = 1: grad_after_act already holds this layer's derivative
+ *     (written by the layer above's call); activated_output and grad_output
+ *     are not read and may be null.
+ *   prev_grad_after_act != null: also writes the layer below's
+ *     prev_grad_after_act = activationBackward(prev_act,
+ *     prev_activated_output, grad_input) (grad_input must be non-null), so
+ *     that layer's call can pass gaa_ready = 1.
+ * Results are bit-identical to zn_hip_dense_backward on the same layers. */
+int zn_hip_dense_backward_chain(zn_ctx *ctx, int act, const float *input, const float *weights,
+                                const float *activated_output, const float *grad_output, float *grad_after_act,
+                                float *grad_input, float *grad_weights, float *grad_bias, int64_t batch,
+                                int64_t in_size, int64_t out_size, int gaa_ready, int prev_act,
+                                const float *prev_activated_output, float *prev_grad_after_act);
 
 /* ------------------------------------- conv and attention (device pointers) */
 

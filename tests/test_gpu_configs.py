@@ -61,7 +61,7 @@ def check_bias(got, gaa, fused, start=None):
     assert np.all(np.abs(got.astype(np.float64) - ref) <= tol(gaa.shape[0]) * den)
 
 
-@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("fused", [False, True, "chain"])
 def test_c2_mlp_training_step(ctx, fused):
     """X[256x784] U[0,1) -> W1 He + b1(0) + ReLU -> W2 + b2(0) linear; dY2 U[-1,1).
     W1 = U[-1,1)*sqrt(2/784) and W2 = U[-1,1)*sqrt(1/128): Dense.init's scales
@@ -70,7 +70,9 @@ def test_c2_mlp_training_step(ctx, fused):
     tanh and softmax layers; the scale does not affect parity.
     Each of the six GEMMs is checked against the oracle on the GPU's own inputs.
     The reference's call sequence gives bit-identical bias gradients; the fused
-    backward sums them over row splits (within the GEMM tolerance)."""
+    backward sums them over row splits (within the GEMM tolerance).  "chain":
+    L2's backward also writes L1's activation derivative, and L1's backward
+    takes it as ready (the bench's step)."""
     from zigneuron_amd import DenseDevice
     batch, d_in, d_h, d_out = 256, 784, 128, 10
     rng = np.random.default_rng(42)
@@ -82,8 +84,12 @@ def test_c2_mlp_training_step(ctx, fused):
     dx, ddy = ctx.to_device(x), ctx.to_device(dy)
     h1 = l1.forward(dx)
     logits = l2.forward(h1)
-    g_h1 = l2.backward(h1, ddy, fused=fused)
-    g_x = l1.backward(dx, g_h1, fused=fused)
+    if fused == "chain":
+        g_h1 = l2.backward(h1, ddy, below=l1)
+        g_x = l1.backward(dx, None)
+    else:
+        g_h1 = l2.backward(h1, ddy, fused=fused)
+        g_x = l1.backward(dx, g_h1, fused=fused)
     ctx.sync()
     W1 = l1.weights.download().reshape(d_in, d_h)
     W2 = l2.weights.download().reshape(d_h, d_out)
@@ -103,7 +109,7 @@ def test_c2_mlp_training_step(ctx, fused):
     dW2 = l2.grad_weights.download().reshape(d_h, d_out)
     assert_close(dW2, oracle.matmul_tn(H1, gaa2, d_h, d_out, batch), "tn", H1, gaa2, d_h, d_out, batch,
                  what="L2 dW (TN)")
-    check_bias(l2.grad_bias.download(), gaa2, fused)
+    check_bias(l2.grad_bias.download(), gaa2, bool(fused))
     # L1 backward: gaa1 = relu'(H1) * GH1, dX1 = gaa1 . W1^T (NT), dW1 = X^T . gaa1 (TN)
     gaa1 = l1.gaa.download().reshape(batch, d_h)
     np.testing.assert_array_equal(gaa1, oracle.activation_backward("relu", H1, GH1).reshape(batch, d_h))
@@ -113,7 +119,7 @@ def test_c2_mlp_training_step(ctx, fused):
     dW1 = l1.grad_weights.download().reshape(d_in, d_h)
     assert_close(dW1, oracle.matmul_tn(x, gaa1, d_in, d_h, batch, threads=THREADS), "tn", x, gaa1, d_in, d_h, batch,
                  what="L1 dW (TN)")
-    check_bias(l1.grad_bias.download(), gaa1, fused)
+    check_bias(l1.grad_bias.download(), gaa1, bool(fused))
 
 
 @pytest.mark.parametrize("which", ["dW_TN", "dX_NT"])
@@ -251,9 +257,63 @@ def test_dense_backward_fused(ctx, act, shape, path):
         buf.close()
 
 
+@pytest.mark.parametrize("path", ["auto", "wide", "large"])
+@pytest.mark.parametrize("acts", [("relu", "linear"), ("tanh", "sigmoid"), ("sigmoid", "relu"), ("linear", "tanh")])
+@pytest.mark.parametrize("shape", [(256, 784, 128, 10), (33, 17, 5, 7), (1, 9, 300, 4), (96, 200, 64, 2048),
+                                   (3000, 64, 48, 20)])
+def test_dense_backward_chain_bit_identical(ctx, shape, acts, path):
+    """Two stacked layers' backward, chained (the upper call writes the lower
+    layer's activation derivative, the lower call takes it as ready) against
+    the unchained calls: every output bit-identical (both derivatives, both
+    grad_inputs, weight and bias gradients).  "auto": 32x32 wave-split tiles
+    (the derivative written as the NT tiles finish); "wide": 64x64 tiles (a
+    separate activation pass); "large": the ungrouped path (forced tile), as
+    is the 3000-row shape on every path.  The unchained results themselves are
+    checked against the oracle by test_dense_backward_fused."""
+    from zigneuron_amd import DenseDevice
+    batch, d_in, d_mid, d_out = shape
+    act_lo, act_hi = acts
+    rng = np.random.default_rng(batch + d_in + d_mid + d_out)
+    x = uniform(rng, (batch, d_in), 0.0, 1.0)
+    go = uniform(rng, (batch, d_out))
+    gb_lo, gb_hi = uniform(rng, (d_mid,)), uniform(rng, (d_out,))
+    announce(f"dense backward chain {shape} {acts} {path}")
+    ctx.set_gemm_wave_split(0 if path == "wide" else -1)
+    if path == "large":
+        ctx.set_gemm_tile("64x64")
+    dx, dgo = ctx.to_device(x), ctx.to_device(go)
+    lo = DenseDevice(ctx, d_in, d_mid, act_lo, batch, seed=3)
+    hi = DenseDevice(ctx, d_mid, d_out, act_hi, batch, seed=4)
+    lo.forward(dx)
+    hi.forward(lo.out)
+    results = {}
+    for mode in ("plain", "chain"):
+        lo.grad_bias.upload(gb_lo)
+        hi.grad_bias.upload(gb_hi)
+        for b in (lo.gaa, hi.gaa, lo.grad_input, hi.grad_input, lo.grad_weights, hi.grad_weights):
+            b.fill(np.nan)
+        if mode == "plain":
+            g = hi.backward(lo.out, dgo)
+            lo.backward(dx, g)
+        else:
+            hi.backward(lo.out, dgo, below=lo)
+            lo.backward(dx, None)
+        results[mode] = [b.download() for b in (hi.gaa, lo.gaa, hi.grad_input, lo.grad_input, hi.grad_weights,
+                                                lo.grad_weights, hi.grad_bias, lo.grad_bias)]
+    names = ("hi.gaa", "lo.gaa", "hi.grad_input", "lo.grad_input", "hi.grad_weights", "lo.grad_weights",
+             "hi.grad_bias", "lo.grad_bias")
+    for name, a, b in zip(names, results["plain"], results["chain"]):
+        assert not np.isnan(a).any(), name
+        np.testing.assert_array_equal(b, a, err_msg=name)
+    ctx.set_gemm_tile("auto")
+    ctx.set_gemm_wave_split(-1)
+    for b in (dx, dgo):
+        b.close()
+
+
 def test_graph_replay_of_mlp_step_matches_eager(ctx):
     """The C2 training step (bias-gradient reset by a fill kernel, two fused
-    forwards, two fused backwards) captured once and replayed three times,
+    forwards, two chained backwards) captured once and replayed three times,
     with unrelated eager GEMMs and synchronisations between the replays:
     every replay reproduces the eager step bit for bit."""
     from zigneuron_amd import DenseDevice, InvalidArgumentError
@@ -269,8 +329,8 @@ def test_graph_replay_of_mlp_step_matches_eager(ctx):
         l2.grad_bias.fill(0.0)
         h = l1.forward(x)
         l2.forward(h)
-        g = l2.backward(h, dy)
-        l1.backward(x, g)
+        l2.backward(h, dy, below=l1)
+        l1.backward(x, None)
 
     def outputs():
         return [b.download() for b in (l1.out, l2.out, l2.grad_input, l1.grad_input, l1.grad_weights,

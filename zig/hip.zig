@@ -80,6 +80,7 @@ pub extern fn zn_hip_activation_forward(ctx: ?*Ctx, act: c_int, in: ?[*]const f3
 pub extern fn zn_hip_activation_backward(ctx: ?*Ctx, act: c_int, y: ?[*]const f32, grad_out: ?[*]const f32, grad_in: ?[*]f32, len: i64) c_int;
 pub extern fn zn_hip_accumulate_bias(ctx: ?*Ctx, grad_bias: ?[*]f32, gaa: ?[*]const f32, rows: i64, n: i64) c_int;
 pub extern fn zn_hip_dense_backward(ctx: ?*Ctx, act: c_int, input: ?[*]const f32, weights: ?[*]const f32, activated_output: ?[*]const f32, grad_output: ?[*]const f32, grad_after_act: ?[*]f32, grad_input: ?[*]f32, grad_weights: ?[*]f32, grad_bias: ?[*]f32, batch: i64, in_size: i64, out_size: i64) c_int;
+pub extern fn zn_hip_dense_backward_chain(ctx: ?*Ctx, act: c_int, input: ?[*]const f32, weights: ?[*]const f32, activated_output: ?[*]const f32, grad_output: ?[*]const f32, grad_after_act: ?[*]f32, grad_input: ?[*]f32, grad_weights: ?[*]f32, grad_bias: ?[*]f32, batch: i64, in_size: i64, out_size: i64, gaa_ready: c_int, prev_act: c_int, prev_activated_output: ?[*]const f32, prev_grad_after_act: ?[*]f32) c_int;
 pub extern fn zn_hip_im2col(ctx: ?*Ctx, input: ?[*]const f32, col: ?[*]f32, batch: i64, channels: i64, in_h: i64, in_w: i64, k_h: i64, k_w: i64, out_h: i64, out_w: i64, stride_h: i64, stride_w: i64, pad_h: i64, pad_w: i64) c_int;
 pub extern fn zn_hip_conv2d_forward_im2col(ctx: ?*Ctx, input: ?[*]const f32, weights: ?[*]const f32, bias: ?[*]const f32, output: ?[*]f32, batch: i64, in_channels: i64, out_channels: i64, k_h: i64, k_w: i64, in_h: i64, in_w: i64, out_h: i64, out_w: i64, stride_h: i64, stride_w: i64, pad_h: i64, pad_w: i64) c_int;
 pub extern fn zn_hip_conv2d_forward_direct(ctx: ?*Ctx, input: ?[*]const f32, weights: ?[*]const f32, bias: ?[*]const f32, output: ?[*]f32, batch: i64, in_channels: i64, out_channels: i64, k_h: i64, k_w: i64, in_h: i64, in_w: i64, out_h: i64, out_w: i64, stride_h: i64, stride_w: i64, pad_h: i64, pad_w: i64) c_int;
@@ -247,6 +248,13 @@ pub const HipBackend = struct {
     /// null for a first layer.
     pub fn denseBackward(self: *HipBackend, act: Act, input: [*]const f32, weights: [*]const f32, activated_output: [*]const f32, grad_output: [*]const f32, grad_after_act: [*]f32, grad_input: ?[*]f32, grad_weights: [*]f32, grad_bias: [*]f32, batch: i64, in_size: i64, out_size: i64) HipError!void {
         try check(zn_hip_dense_backward(self.ctx, @intFromEnum(act), input, weights, activated_output, grad_output, grad_after_act, grad_input, grad_weights, grad_bias, batch, in_size, out_size));
+    }
+    /// denseBackward for layers walked top-down: with gaa_ready the layer's
+    /// grad_after_act was written by the call of the layer above (y and
+    /// grad_output unread); a non-null prev_grad_after_act also receives the
+    /// layer below's activation derivative.  Same bits as denseBackward.
+    pub fn denseBackwardChain(self: *HipBackend, act: Act, input: [*]const f32, weights: [*]const f32, activated_output: ?[*]const f32, grad_output: ?[*]const f32, grad_after_act: [*]f32, grad_input: ?[*]f32, grad_weights: [*]f32, grad_bias: [*]f32, batch: i64, in_size: i64, out_size: i64, gaa_ready: bool, prev_act: Act, prev_activated_output: ?[*]const f32, prev_grad_after_act: ?[*]f32) HipError!void {
+        try check(zn_hip_dense_backward_chain(self.ctx, @intFromEnum(act), input, weights, activated_output, grad_output, grad_after_act, grad_input, grad_weights, grad_bias, batch, in_size, out_size, @intFromBool(gaa_ready), @intFromEnum(prev_act), prev_activated_output, prev_grad_after_act));
     }
     pub fn attentionForwardDevice(self: *HipBackend, q: [*]const f32, k: [*]const f32, v: [*]const f32, out: [*]f32, batch: i64, seq_len: i64, d_k: i64, scale: f32) HipError!void {
         try check(zn_hip_attention_forward(self.ctx, q, k, v, out, batch, seq_len, d_k, scale));

@@ -265,6 +265,19 @@ class Context:
             _dptr(grad_after_act), _dptr(grad_input), _dptr(grad_weights), _dptr(grad_bias), batch, in_size, out_size),
             "zn_hip_dense_backward")
 
+    def dense_backward_chain(self, act, inp, weights, activated_output, grad_output, grad_after_act, grad_input,
+                             grad_weights, grad_bias, batch, in_size, out_size, gaa_ready=False, prev_act="linear",
+                             prev_activated_output=None, prev_grad_after_act=None) -> None:
+        """dense_backward for layers walked top-down: gaa_ready means grad_after_act already holds
+        this layer's derivative (written by the layer above's call); prev_grad_after_act (with
+        prev_act and prev_activated_output) receives the layer below's derivative from grad_input.
+        Bit-identical to dense_backward layer by layer."""
+        check(_lib.load().zn_hip_dense_backward_chain(
+            self.handle, act_id(act), _dptr(inp), _dptr(weights), _dptr(activated_output), _dptr(grad_output),
+            _dptr(grad_after_act), _dptr(grad_input), _dptr(grad_weights), _dptr(grad_bias), batch, in_size, out_size,
+            int(bool(gaa_ready)), act_id(prev_act), _dptr(prev_activated_output), _dptr(prev_grad_after_act)),
+            "zn_hip_dense_backward_chain")
+
     # --- convolution and attention on device pointers
     def im2col(self, inp, col, batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h=1, stride_w=1,
                pad_h=0, pad_w=0) -> None:

@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include "../zn_kernel_args.h"
+#include "zn_activation.h"
 
 typedef float zn_f32x4 __attribute__((ext_vector_type(4)));
 
@@ -28,15 +29,6 @@ __device__ __forceinline__ float act_forward(float x, int act) {
     }
 }
 
-// Activation backward from the activated output y (src/optimization.zig:229-303).
-__device__ __forceinline__ float act_backward(float y, float go, int act) {
-    switch (act) {
-    case 1: return y > 0.0f ? go : 0.0f;
-    case 2: return (go * y) * (1.0f - y);
-    case 3: return go * (1.0f - y * y);
-    default: return go;
-    }
-}
 
 __device__ __forceinline__ int64_t gtid() { return (int64_t)blockIdx.x * blockDim.x + threadIdx.x; }
 __device__ __forceinline__ int64_t gstride() { return (int64_t)gridDim.x * blockDim.x; }
@@ -90,7 +82,7 @@ extern "C" __global__ __launch_bounds__(256) void zn_activation_forward(ZnEltArg
 // in0 = activated output y, in1 = grad_out, out = grad_in.
 extern "C" __global__ __launch_bounds__(256) void zn_activation_backward(ZnEltArgs p) {
     const int64_t total = p.rows * p.n;
-    for (int64_t i = gtid(); i < total; i += gstride()) p.out[i] = act_backward(p.in0[i], p.in1[i], p.act);
+    for (int64_t i = gtid(); i < total; i += gstride()) p.out[i] = zn_act_backward(p.in0[i], p.in1[i], p.act);
 }
 
 // grad_bias[i] += sum_r gaa[r*n + i], rows ascending exactly like
@@ -135,14 +127,14 @@ extern "C" __global__ __launch_bounds__(256) void zn_dense_grad_prologue(ZnDense
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float d = act_backward(y[q], g[q], p.act);
-            p.gaa[(r + q) * p.n + col] = d;
+            const float d = zn_act_backward(y[q], g[q], p.act);
+            if (p.gaa) p.gaa[(r + q) * p.n + col] = d;
             s = s + d;
         }
     }
     for (; r < r1; ++r) {
-        const float d = act_backward(p.y[r * p.n + col], p.go[r * p.n + col], p.act);
-        p.gaa[r * p.n + col] = d;
+        const float d = zn_act_backward(p.y[r * p.n + col], p.go[r * p.n + col], p.act);
+        if (p.gaa) p.gaa[r * p.n + col] = d;
         s = s + d;
     }
     p.partial[(int64_t)blockIdx.y * p.n + col] = s;

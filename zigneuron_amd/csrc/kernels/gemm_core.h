@@ -38,6 +38,7 @@
 #include "../zn_kernel_args.h"
 
 #include "zn_mfma_stage.h"
+#include "zn_activation.h"
 
 namespace {
 
@@ -1162,7 +1163,7 @@ __device__ __forceinline__ void ksplit_finish(const ZnGemmArgs &p, float *lds,
         }
         if constexpr (!BKC && FN > 1) {
             const int col0 = n0 + FN * j;
-            if (vec && col0 + FN <= p.n) {
+            if (vec && col0 + FN <= p.n && !p.chain_gaa) {  // a chained derivative takes the scalar path
                 typedef typename FVec<FN>::type VT;
                 VT *dst = reinterpret_cast<VT *>(crow + col0);
                 VT o;
@@ -1185,7 +1186,12 @@ __device__ __forceinline__ void ksplit_finish(const ZnGemmArgs &p, float *lds,
             float x = v[fn];
             if (p.accumulate) x = crow[col] + x;
             if (has_bias) x = x + (p.bias_rows ? rbias : p.bias[col]);
-            crow[col] = zn_activate(x, ACT);
+            x = zn_activate(x, ACT);
+            crow[col] = x;
+            if (p.chain_gaa) {
+                const int64_t at = (int64_t)row * ldc + col;
+                p.chain_gaa[at] = zn_act_backward(p.chain_y[at], x, p.chain_act);
+            }
         }
     }
 }

@@ -138,16 +138,49 @@ extern "C" __global__ __launch_bounds__(256) void zn_splitk_reduce(ZnReduceArgs 
     splitk_reduce_body(p, blockIdx.x, gridDim.x);
 }
 
+// The bias gradient of a Dense backward as column sums (ZnColSumArgs), for
+// the grouped launches that run without a prologue: workgroup `block` takes
+// 16 columns; thread t sums the rows of splits t / 16, t / 16 + 16, ... of
+// column t % 16 in row order (and copies them when asked), then 16 threads
+// add each column's split sums in split order onto dst.  `lds` holds
+// splits x 16 floats.
+__device__ __forceinline__ void dense_colsum_body(const ZnColSumArgs &p, int block, float *lds) {
+    const int t = threadIdx.x;
+    const int col = block * 16 + (t & 15);
+    for (int s = t >> 4; s < p.splits; s += 16) {
+        float sum = 0.0f;
+        if (col < p.n) {
+            const int r1 = min(p.rows, (s + 1) * p.per);
+            for (int r = s * p.per; r < r1; ++r) {
+                const float v = p.src[(int64_t)r * p.n + col];
+                if (p.copy) p.copy[(int64_t)r * p.n + col] = v;
+                sum = sum + v;
+            }
+        }
+        lds[s * 16 + (t & 15)] = sum;
+    }
+    __syncthreads();
+    if (t < 16 && col < p.n) {
+        float total = lds[t];
+        for (int s = 1; s < p.splits; ++s) total = total + lds[s * 16 + t];
+        p.dst[col] = p.dst[col] + total;
+    }
+}
+
 // Dense backward GEMMs in one launch (ZnDenseBwdArgs): grad_input = gaa . W^T
-// (NT), grad_weights = input^T . gaa (TN), and the bias reduce.  _v: both
+// (NT), grad_weights = input^T . gaa (TN), and the bias gradient (the reduce
+// of the prologue's partials, or the column sums themselves).  _v: both
 // GEMMs stage with 16-byte loads.
 #define ZN_DENSE_BWD_KERNEL(SUFFIX, W)                                                              \
     extern "C" __global__ __launch_bounds__(256, 1) void zn_dense_bwd_m##SUFFIX(ZnDenseBwdArgs p) { \
+        __shared__ float colsum_lds[kMaxColSumSplits * 16];                                          \
         const int b = blockIdx.x;                                                                    \
         if (b < p.wg_nt)                                                                             \
             gemm_tile_dma<64, 64, 32, 2, 2, true, true, W, W>(p.nt, b);                             \
         else if (b < p.wg_nt + p.wg_tn)                                                              \
             gemm_tile_dma<64, 64, 32, 2, 2, false, false, W, W>(p.tn, b - p.wg_nt);                 \
+        else if (p.wg_colsum)                                                                        \
+            dense_colsum_body(p.colsum, b - p.wg_nt - p.wg_tn, colsum_lds);                          \
         else                                                                                         \
             splitk_reduce_body(p.bias, b - p.wg_nt - p.wg_tn, p.wg_bias);                           \
     }
@@ -164,6 +197,8 @@ ZN_DENSE_BWD_KERNEL(, 4)
             gemm_ksplit<32, 32, 32, 4, true, true, W, W, 0>(p.nt, lds, b);                           \
         else if (b < p.wg_nt + p.wg_tn)                                                              \
             gemm_ksplit<32, 32, 32, 4, false, false, W, W, 0>(p.tn, lds, b - p.wg_nt);               \
+        else if (p.wg_colsum)                                                                        \
+            dense_colsum_body(p.colsum, b - p.wg_nt - p.wg_tn, lds);                                 \
         else                                                                                         \
             splitk_reduce_body(p.bias, b - p.wg_nt - p.wg_tn, p.wg_bias);                           \
     }

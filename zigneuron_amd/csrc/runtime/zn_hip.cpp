@@ -1978,26 +1978,39 @@ static ZnGemmArgs grouped_gemm_args(const float *a, int64_t lda, const float *b,
 }
 
 // zn_dense_bwd_m[_v]: grad_input = gaa . W^T (NT, skipped when null),
-// grad_weights = input^T . gaa (TN) and grad_bias += the ordered sum of the
-// prologue's partials (r), in one launch.
-// tile 32: zn_dense_bwd_k[_v], the same on 32x32 tiles whose four waves split K.
+// grad_weights = input^T . gaa (TN) and the bias gradient in one launch: the
+// ordered sum of a prologue's partials (r, bias_blocks workgroups), or, with
+// cs.splits > 0, the column sums of gaa themselves (cs).
+// tile 32: zn_dense_bwd_k[_v], the same on 32x32 tiles whose four waves split
+// K; only these tiles can also write the layer below's grad_after_act
+// (chain_*) as they finish grad_input.
 static int dense_backward_grouped(zn_ctx *ctx, const float *input, const float *weights, const float *gaa,
                                   float *grad_input, float *grad_weights, const ZnReduceArgs &r, int bias_blocks,
-                                  int64_t batch, int64_t in_size, int64_t out_size, int wg_nt, int wg_tn, int tile) {
+                                  const ZnColSumArgs &cs, int64_t batch, int64_t in_size, int64_t out_size, int wg_nt,
+                                  int wg_tn, int tile, int chain_act, const float *chain_y, float *chain_gaa) {
     ZnDenseBwdArgs d;
     std::memset(&d, 0, sizeof(d));
-    if (grad_input)
+    if (grad_input) {
         d.nt = grouped_gemm_args(gaa, out_size, weights, out_size, grad_input, in_size, batch, in_size, out_size, tile);
+        d.nt.chain_y = chain_y;
+        d.nt.chain_gaa = chain_gaa;
+        d.nt.chain_act = chain_act;
+    }
     d.tn = grouped_gemm_args(input, in_size, gaa, out_size, grad_weights, out_size, in_size, out_size, batch, tile);
-    d.bias = r;
     d.wg_nt = wg_nt;
     d.wg_tn = wg_tn;
-    d.wg_bias = bias_blocks;
+    if (cs.splits > 0) {
+        d.colsum = cs;
+        d.wg_colsum = (int32_t)cdiv(out_size, 16);
+    } else {
+        d.bias = r;
+        d.wg_bias = bias_blocks;
+    }
     // 16-byte staging when every staged row is a whole number of aligned float4s
     const bool vec_tn = aligned16(input) && aligned16(gaa) && in_size % 4 == 0 && out_size % 4 == 0;
     const bool vec_nt = !grad_input || (aligned16(weights) && out_size % 4 == 0);
     hipFunction_t f = (tile == 32 ? ctx->dense_bwd_k : ctx->dense_bwd)[vec_tn && vec_nt ? 1 : 0];
-    return launch(ctx, f, (unsigned)(wg_nt + wg_tn + bias_blocks), 1, 256, &d);
+    return launch(ctx, f, (unsigned)(wg_nt + wg_tn + (cs.splits > 0 ? d.wg_colsum : bias_blocks)), 1, 256, &d);
 }
 
 // Dense.backward (src/layer.zig:411-475) on device pointers:
@@ -2006,18 +2019,33 @@ static int dense_backward_grouped(zn_ctx *ctx, const float *input, const float *
 // split-K reduce adds the splits in ascending order onto grad_bias), then
 // grad_input = gaa . W^T (NT) and grad_weights = input^T . gaa (TN,
 // overwritten like the reference).  grad_input may be null (first layer).
-int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float *weights,
-                          const float *activated_output, const float *grad_output, float *grad_after_act,
-                          float *grad_input, float *grad_weights, float *grad_bias, int64_t batch, int64_t in_size,
-                          int64_t out_size) {
+//
+// Chaining (zn_hip_dense_backward_chain): with gaa_ready, grad_after_act
+// already holds this layer's gaa (y and grad_output are not read) and only
+// its column sums are taken; with prev_gaa, the layer below's
+// prev_gaa = activationBackward(prev_act, prev_y, grad_input) is written too.
+// A linear layer's gaa is grad_output itself, so it needs no prologue either:
+// the GEMMs read grad_output and the column-sum workgroups copy it into
+// grad_after_act.  Every sum keeps the unchained order (the same row splits,
+// rows ascending within a split, splits ascending), so both ways give the
+// same bits.
+static int dense_backward_impl(zn_ctx *ctx, int act, const float *input, const float *weights,
+                               const float *activated_output, const float *grad_output, float *grad_after_act,
+                               float *grad_input, float *grad_weights, float *grad_bias, int64_t batch,
+                               int64_t in_size, int64_t out_size, bool gaa_ready, int prev_act, const float *prev_y,
+                               float *prev_gaa) {
     if (!ctx || act < ZN_ACT_LINEAR || act > ZN_ACT_TANH || batch < 0 || in_size < 0 || out_size < 0)
         return ZN_ERR_INVALID_ARG;
+    if (prev_gaa && (prev_act < ZN_ACT_LINEAR || prev_act > ZN_ACT_TANH)) return ZN_ERR_INVALID_ARG;
     if (batch > INT_MAX || in_size > INT_MAX || out_size > INT_MAX) return ZN_ERR_OVERFLOW;
     if (out_size == 0) return ZN_OK;
-    if (batch > 0 && (!activated_output || !grad_output || !grad_after_act || !grad_bias)) return ZN_ERR_INVALID_ARG;
+    if (batch > 0 && (!grad_after_act || !grad_bias || (!gaa_ready && (!activated_output || !grad_output))))
+        return ZN_ERR_INVALID_ARG;
     if (in_size > 0 && (!grad_weights || (batch > 0 && (!input || !weights)))) return ZN_ERR_INVALID_ARG;
+    if (prev_gaa && batch > 0 && in_size > 0 && (!grad_input || !prev_y)) return ZN_ERR_INVALID_ARG;
     int rc = select_device(ctx);
     if (rc) return rc;
+    const bool chain = prev_gaa && batch > 0 && in_size > 0;
     if (batch > 0) {
         const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
         const int64_t col_groups = cdiv(out_size, 256);
@@ -2026,16 +2054,65 @@ int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float 
         if (splits > 65535) splits = 65535;
         const int64_t per = cdiv(batch, splits);
         splits = cdiv(batch, per);
+        // gaa without a prologue: a ready buffer, or grad_output of a linear layer
+        const bool no_prologue = gaa_ready || act == ZN_ACT_LINEAR;
+        const float *gaa = gaa_ready ? grad_after_act : (act == ZN_ACT_LINEAR ? grad_output : grad_after_act);
+        // Small layers: grad_input, grad_weights and the bias gradient in one
+        // launch (C2's layers: 5 launches -> 2, or 1 without a prologue).  Up
+        // to 2 workgroups per CU of 32x32 tiles whose four waves split K (C2
+        // step 44 -> 33 us), else up to 2 per CU of unsplit 64x64 tiles.
+        const bool small = in_size > 0 && batch <= 2048 && out_size <= 2048 && ctx->forced_tile < 0 &&
+                           ctx->forced_splits == 0 && in_size <= INT_MAX / 4 / std::max<int64_t>(batch, out_size);
+        int tile = 0;
+        int64_t wg_nt = 0, wg_tn = 0;
+        for (int t : {32, 64}) {
+            wg_nt = grad_input ? cdiv(batch, t) * cdiv(in_size, t) : 0;
+            wg_tn = cdiv(in_size, t) * cdiv(out_size, t);
+            if (t == 32 && ctx->forced_wave_split == 0) continue;
+            if (small && wg_nt + wg_tn <= 2 * cus) {
+                tile = t;
+                break;
+            }
+        }
+        ZnColSumArgs cs;
+        std::memset(&cs, 0, sizeof(cs));
+        if (tile && no_prologue && splits <= kMaxColSumSplits) {
+            // one launch: the column sums run beside the GEMMs
+            cs.src = gaa;
+            cs.dst = grad_bias;
+            cs.copy = gaa_ready ? nullptr : grad_after_act;
+            cs.rows = (int32_t)batch;
+            cs.n = (int32_t)out_size;
+            cs.per = (int32_t)per;
+            cs.splits = (int32_t)splits;
+            ZnReduceArgs none;
+            std::memset(&none, 0, sizeof(none));
+            const bool fused_chain = chain && tile == 32;
+            if ((rc = dense_backward_grouped(ctx, input, weights, gaa, grad_input, grad_weights, none, 0, cs, batch,
+                                             in_size, out_size, (int)wg_nt, (int)wg_tn, tile, prev_act,
+                                             fused_chain ? prev_y : nullptr, fused_chain ? prev_gaa : nullptr)))
+                return rc;
+            if (chain && !fused_chain)
+                return zn_hip_activation_backward(ctx, prev_act, prev_y, grad_input, prev_gaa, batch * in_size);
+            return ZN_OK;
+        }
         Lease part(ctx);
         if ((rc = part.get((size_t)(splits * out_size)))) return rc;
         ZnDenseGradArgs g;
-        g.y = activated_output;
-        g.go = grad_output;
-        g.gaa = grad_after_act;
+        if (gaa_ready) {  // the sums only: gaa read as the grad_output of a linear activation
+            g.y = grad_after_act;
+            g.go = grad_after_act;
+            g.gaa = nullptr;
+            g.act = ZN_ACT_LINEAR;
+        } else {
+            g.y = activated_output;
+            g.go = grad_output;
+            g.gaa = grad_after_act;
+            g.act = act;
+        }
         g.partial = part.ptr;
         g.rows = batch;
         g.n = out_size;
-        g.act = act;
         g.rows_per_split = (int32_t)per;
         if ((rc = launch(ctx, ctx->elt[kDenseGrad], (unsigned)col_groups, (unsigned)splits, 256, &g))) return rc;
         ZnReduceArgs r;
@@ -2051,19 +2128,16 @@ int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float 
         r.act = ZN_ACT_LINEAR;
         r.vec = (out_size % 4 == 0 && aligned16(grad_bias) && aligned16(part.ptr)) ? 1 : 0;
         const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(cdiv(out_size / (r.vec ? 4 : 1), 256), 8 * cus));
-        // Small layers: grad_input, grad_weights and the bias reduce in one
-        // launch (C2's layers: 5 launches -> 2).  Up to 2 workgroups per CU
-        // of 32x32 tiles whose four waves split K (C2 step 44 -> 33 us), else
-        // up to 2 per CU of unsplit 64x64 tiles.
-        const bool small = in_size > 0 && batch <= 2048 && out_size <= 2048 && ctx->forced_tile < 0 &&
-                           ctx->forced_splits == 0 && in_size <= INT_MAX / 4 / std::max<int64_t>(batch, out_size);
-        for (int tile : {32, 64}) {
-            const int64_t wg_nt = grad_input ? cdiv(batch, tile) * cdiv(in_size, tile) : 0;
-            const int64_t wg_tn = cdiv(in_size, tile) * cdiv(out_size, tile);
-            if (tile == 32 && ctx->forced_wave_split == 0) continue;
-            if (small && wg_nt + wg_tn <= 2 * cus)
-                return dense_backward_grouped(ctx, input, weights, grad_after_act, grad_input, grad_weights, r,
-                                              (int)blocks, batch, in_size, out_size, (int)wg_nt, (int)wg_tn, tile);
+        if (tile) {
+            const bool fused_chain = chain && tile == 32;
+            if ((rc = dense_backward_grouped(ctx, input, weights, grad_after_act, grad_input, grad_weights, r,
+                                             (int)blocks, cs, batch, in_size, out_size, (int)wg_nt, (int)wg_tn, tile,
+                                             prev_act, fused_chain ? prev_y : nullptr,
+                                             fused_chain ? prev_gaa : nullptr)))
+                return rc;
+            if (chain && !fused_chain)
+                return zn_hip_activation_backward(ctx, prev_act, prev_y, grad_input, prev_gaa, batch * in_size);
+            return ZN_OK;
         }
         if ((rc = launch(ctx, ctx->splitk_reduce, (unsigned)blocks, 1, 256, &r))) return rc;
     }
@@ -2072,9 +2146,31 @@ int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float 
         (rc = gemm_launch(ctx, ZN_LAYOUT_NT, batch, in_size, out_size, grad_after_act, out_size, 0, weights, out_size,
                           0, grad_input, in_size, 0, 1, 0, nullptr, ZN_ACT_LINEAR)))
         return rc;
+    if (chain && (rc = zn_hip_activation_backward(ctx, prev_act, prev_y, grad_input, prev_gaa, batch * in_size)))
+        return rc;
     if (batch == 0) return zn_hip_fill_f32(ctx, grad_weights, 0.0f, in_size * out_size);
     return gemm_launch(ctx, ZN_LAYOUT_TN, in_size, out_size, batch, input, in_size, 0, grad_after_act, out_size, 0,
                        grad_weights, out_size, 0, 1, 0, nullptr, ZN_ACT_LINEAR);
+}
+
+int zn_hip_dense_backward(zn_ctx *ctx, int act, const float *input, const float *weights,
+                          const float *activated_output, const float *grad_output, float *grad_after_act,
+                          float *grad_input, float *grad_weights, float *grad_bias, int64_t batch, int64_t in_size,
+                          int64_t out_size) {
+    return dense_backward_impl(ctx, act, input, weights, activated_output, grad_output, grad_after_act, grad_input,
+                               grad_weights, grad_bias, batch, in_size, out_size, false, ZN_ACT_LINEAR, nullptr,
+                               nullptr);
+}
+
+int zn_hip_dense_backward_chain(zn_ctx *ctx, int act, const float *input, const float *weights,
+                                const float *activated_output, const float *grad_output, float *grad_after_act,
+                                float *grad_input, float *grad_weights, float *grad_bias, int64_t batch,
+                                int64_t in_size, int64_t out_size, int gaa_ready, int prev_act,
+                                const float *prev_activated_output, float *prev_grad_after_act) {
+    if (gaa_ready != 0 && gaa_ready != 1) return ZN_ERR_INVALID_ARG;
+    return dense_backward_impl(ctx, act, input, weights, activated_output, grad_output, grad_after_act, grad_input,
+                               grad_weights, grad_bias, batch, in_size, out_size, gaa_ready == 1, prev_act,
+                               prev_activated_output, prev_grad_after_act);
 }
 
 // ------------------------------------------------------- conv backward

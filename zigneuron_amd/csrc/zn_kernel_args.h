@@ -53,6 +53,12 @@ struct ZnGemmArgs {
     int32_t bias_rows;         // 1: bias is indexed by row (length m), else by column (length n)
     int32_t batch;             // problems; the persistent kernels walk batch * tiles_m * tiles_n work items
     ZnConvGeom conv;           // the zn_conv_* kernels only
+    // Chained activation derivative (intra-workgroup split-K tiles only):
+    // when chain_gaa is set, each finished element v of C also gives
+    // chain_gaa[i] = act'(chain_y[i]) * v (act = chain_act), both laid out like C.
+    const float *chain_y;
+    float *chain_gaa;
+    int32_t chain_act;
 };
 
 // Split-K reduction: C = act((accumulate ? C : 0) + sum_s ws[s] + bias), the
@@ -67,15 +73,30 @@ struct ZnReduceArgs {
     int32_t bias_rows;
 };
 
-// The GEMMs of one Dense backward in one launch (after the prologue that
-// wrote grad_after_act and the bias partial sums): workgroups [0, wg_nt)
-// compute grad_input (NT), the next wg_tn grad_weights (TN), the last wg_bias
-// reduce the bias partial sums.  Both GEMMs use the 64x64 tile, unsplit.
+// Bias gradient as column sums in one launch: dst[c] += sum over row splits
+// s (ascending) of (sum over the split's rows r, ascending, of src[r*n + c]),
+// splits of `per` rows; the same sums as zn_dense_grad_prologue's partials
+// added by the split-K reduce.  copy (optional) receives src.
+constexpr int kMaxColSumSplits = 256;  // row splits the grouped launches' column sums take
+
+struct ZnColSumArgs {
+    const float *src;
+    float *dst;
+    float *copy;
+    int32_t rows, n, per, splits;
+};
+
+// The GEMMs of one Dense backward in one launch: workgroups [0, wg_nt)
+// compute grad_input (NT), the next wg_tn grad_weights (TN), and the last
+// ones the bias gradient: wg_bias reduce the partial sums a prologue wrote
+// (the prologue also wrote grad_after_act), or, without a prologue,
+// wg_colsum sum the columns of grad_after_act themselves.
 struct ZnDenseBwdArgs {
     ZnGemmArgs nt;
     ZnGemmArgs tn;
-    ZnReduceArgs bias;
-    int32_t wg_nt, wg_tn, wg_bias;
+    ZnReduceArgs bias;     // reduce of the prologue's partial sums (wg_bias workgroups), or
+    ZnColSumArgs colsum;   // the column sums themselves (wg_colsum workgroups)
+    int32_t wg_nt, wg_tn, wg_bias, wg_colsum;
 };
 
 // Elementwise helpers (fill, copy, bias, activations, bias gradient, row
@@ -106,7 +127,7 @@ struct ZnAttnArgs {
 struct ZnDenseGradArgs {
     const float *y;        // activated output [rows x n]
     const float *go;       // grad_output [rows x n]
-    float *gaa;            // grad after activation [rows x n]
+    float *gaa;            // grad after activation [rows x n]; null: only the sums
     float *partial;        // [splits x n] column sums
     int64_t rows, n;
     int32_t act;

@@ -93,6 +93,7 @@ class DenseDevice:
         self.out = ctx.alloc(batch * output_size)
         self.gaa = ctx.alloc(batch * output_size)
         self.grad_input = ctx.alloc(batch * input_size)
+        self._gaa_ready = False  # self.gaa was written by the layer above's chained backward
 
     def forward(self, x: DeviceBuffer) -> DeviceBuffer:
         """Fused NN + bias + activation into self.out (asynchronous)."""
@@ -100,16 +101,38 @@ class DenseDevice:
                        self.output_size, self.out, self.output_size, False, self.bias, self.act)
         return self.out
 
-    def backward(self, x: DeviceBuffer, grad_out: DeviceBuffer, fused: bool = True) -> DeviceBuffer:
+    def backward(self, x: DeviceBuffer, grad_out: Optional[DeviceBuffer], fused: bool = True,
+                 below: Optional["DenseDevice"] = None) -> DeviceBuffer:
         """activationBackward -> NT (grad_input) -> accumulateBias -> TN (grad_weights).
 
         fused: one zn_hip_dense_backward call (activation derivative and bias
         sums in one pass, bias summed over row splits); otherwise the
-        reference's four calls, with the row-by-row bias sum."""
+        reference's four calls, with the row-by-row bias sum.
+        below: the layer whose output is x; this call then also writes that
+        layer's activation derivative (zn_hip_dense_backward_chain), and that
+        layer's own backward takes it as ready (its grad_out is not read).
+        The results are the same bits as the unchained calls."""
         if fused:
-            self.ctx.dense_backward(self.act, x, self.weights, self.out, grad_out, self.gaa, self.grad_input,
-                                    self.grad_weights, self.grad_bias, self.batch, self.input_size, self.output_size)
+            ready = self._gaa_ready
+            self._gaa_ready = False
+            if below is None and not ready:
+                self.ctx.dense_backward(self.act, x, self.weights, self.out, grad_out, self.gaa, self.grad_input,
+                                        self.grad_weights, self.grad_bias, self.batch, self.input_size,
+                                        self.output_size)
+                return self.grad_input
+            if below is not None and (below.output_size != self.input_size or below.batch != self.batch):
+                raise _lib.InvalidArgumentError(_lib.ZN_ERR_INVALID_ARG, "DenseDevice.backward", "below")
+            self.ctx.dense_backward_chain(
+                self.act, x, self.weights, None if ready else self.out, None if ready else grad_out, self.gaa,
+                self.grad_input, self.grad_weights, self.grad_bias, self.batch, self.input_size, self.output_size,
+                ready, below.act if below is not None else "linear", below.out if below is not None else None,
+                below.gaa if below is not None else None)
+            if below is not None:
+                below._gaa_ready = True
             return self.grad_input
+        if self._gaa_ready:
+            raise _lib.InvalidArgumentError(_lib.ZN_ERR_INVALID_ARG, "DenseDevice.backward",
+                                            "the chained derivative needs fused=True")
         n_out = self.batch * self.output_size
         self.ctx.activation_backward(self.act, self.out, grad_out, self.gaa, n_out)
         self.ctx.sgemm("nt", self.batch, self.input_size, self.output_size, self.gaa, self.output_size,
