@@ -175,9 +175,10 @@ int zn_hip_event_destroy(zn_event *ev);
 #define ZN_TILE_256x256 7     /* 256x256, BK 16, one workgroup per CU; 16-byte rows only (otherwise 256x128); not for
                                  convolutions */
 int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile);
-/* Split-K override: 0 (the default) lets the policy choose, 1..64 forces that
- * many K slices (at most K / BK) for every following GEMM on this context.
- * Like the tile override, a tuning and test hook with no reference
+/* Split-K override: 0 (the default) lets the policy choose, 1..256 asks for
+ * that many K slices (at most ceil(K / BK)) for every following GEMM on this
+ * context; K is cut into equal slices of whole BK multiples, which can give
+ * fewer.  Like the tile override, a tuning and test hook with no reference
  * counterpart. */
 int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits);
 /* Persistent-kernel override: -1 (the default) lets the policy choose, 0

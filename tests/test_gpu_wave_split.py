@@ -5,7 +5,9 @@ K and sum the partial tiles in wave order, then apply C_old, the bias and the
 activation.  That is the arithmetic of the 32x32 tile split into as many K
 slices by separate workgroups and finished by the ordered reduce, so the two
 paths must agree bit for bit whenever every wave has a non-empty slice; the
-automatic policy is checked against the oracle.
+automatic policy is checked against the oracle.  Problems of at most half
+the CUs of tiles split K over workgroups too; the last workgroup of a tile
+adds the partial tiles in slice order, again the split-K arithmetic.
 """
 from __future__ import annotations
 
@@ -91,6 +93,68 @@ def test_wave_split_matches_split_k(ctx, layout, m, n, k, batch, waves, bias, ac
         if ref is not None:
             assert_close(got[0], ref, layout, a[0], b[0], m, n, k, c0=c0[0] if acc else None, accumulate=acc,
                          bias=bv, act=act, what="wave split")
+
+
+WG_CASES = [
+    # layout, m, n, k, batch, bias, act, acc: at most half the CUs of 32x32 tiles, K >= 1536
+    ("nn", 256, 128, 1600, 1, True, "relu", False),     # 7 workgroups per tile, 25 slices of 64
+    ("nt", 100, 70, 2000, 1, True, "sigmoid", True),    # ragged everywhere
+    ("nn", 64, 64, 4096, 1, True, "linear", True),      # 32 slices of 128 (two stages per wave)
+    ("nn", 300, 200, 3000, 1, False, "tanh", False),    # 256-wide slices
+    ("nt", 32, 32, 1537, 1, False, "linear", False),    # 4-byte staging; the last slice is one column of K
+    ("tn", 64, 96, 2048, 3, False, "linear", False),
+    ("nn", 33, 65, 1800, 5, False, "linear", False),    # the last workgroup has one slice
+]
+
+
+@pytest.mark.parametrize("layout,m,n,k,batch,bias,act,acc", WG_CASES)
+def test_workgroup_split_matches_split_k(ctx, layout, m, n, k, batch, bias, act, acc):
+    """Small problems whose K the policy also splits over workgroups: slice q
+    (chunk floats of K) goes to wave q % 4 of workgroup q / 4, and the last
+    workgroup of each tile adds the slices in order.  That is the 32x32 tile
+    split into the same slices by split-K launches and the ordered reduce,
+    so the two agree bit for bit; run twice in a row (the tile counters are
+    set back to zero by each launch), and checked against the oracle."""
+    cus = ctx.compute_units
+    tiles = -(-m // 32) * -(-n // 32) * batch
+    assert tiles * 2 <= cus
+    assert k >= 1536
+    s0 = min(cus // tiles, -(-k // 128), 8)
+    chunk = -(-(-(-k // (4 * s0))) // 32) * 32
+    slices = -(-k // chunk)
+    assert slices > 4, "more than one workgroup per tile"
+    assert -(-(-(-k // slices)) // 32) * 32 == chunk, "split-K with this many slices cuts K the same way"
+    rng = np.random.default_rng(m * 3 + n + k)
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a = uniform(rng, (batch,) + a_shape)
+    b = uniform(rng, (batch,) + b_shape)
+    c0 = uniform(rng, (batch, m, n))
+    bv = uniform(rng, (n,)) if bias else None
+    if batch > 1:
+        bv, act, acc = None, "linear", False
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    announce(f"workgroup split {layout} {m}x{n}x{k} batch {batch}: {slices} slices of {chunk}")
+    got = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
+    again = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
+    ctx.set_gemm_wave_split(0)
+    ctx.set_gemm_tile("32x32")
+    ctx.set_gemm_splits(slices)
+    want = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
+    ctx.set_gemm_tile("auto")
+    ctx.set_gemm_splits(0)
+    ctx.set_gemm_wave_split(-1)
+    assert np.isfinite(got).all()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
+    # an activation without bias is checked as the oracle's fused form with a zero bias
+    rb = bv if bv is not None or act == "linear" else np.zeros(n, np.float32)
+    for i in range(batch):
+        if rb is not None and (layout != "nn" or acc):
+            continue  # the oracle's fused form: NN, bias, no accumulate
+        ref = ref_gemm(layout, a[i], b[i], m, n, k, c0=c0[i] if acc else None, accumulate=acc, bias=rb, act=act)
+        assert_close(got[i], ref, layout, a[i], b[i], m, n, k, c0=c0[i] if acc else None, accumulate=acc, bias=rb,
+                     act=act, what=f"workgroup split problem {i}")
 
 
 def test_policy_small_problems_against_oracle(ctx):

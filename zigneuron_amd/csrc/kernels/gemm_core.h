@@ -1123,21 +1123,64 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
 // staging no longer uses), each output is the sum of its partials in wave
 // order, and the epilogue applies C_old, the bias and the activation; wave w
 // finishes the (row block, register) items w, w + KS, ...
-template <int BM, int BN, int KS, bool AK, bool BKC, int ACT>
+//
+// XS (the zn_sgemmk4s_* kernels): the workgroups split K as well; wave w of
+// workgroup s multiplied K slice q = s * KS + w, each non-empty slice's
+// partial tile goes to its own block of p.ws, and the workgroup that arrives
+// last at the tile's counter (whichever it is) adds the blocks in slice
+// order, runs the epilogue and sets the counter back to zero.  The blocks
+// are written and read as agent-scope atomics (stores and loads coherent
+// across the XCDs' L2 caches), and every store has completed (vmcnt 0)
+// before the workgroup arrives, so the last arrival reads finished blocks.
+// Device-scope fences would write back and invalidate a whole L2 per
+// workgroup instead (36 us against 14 us for 224 workgroups on MI355X).
+// Kept out of the other kernels: in C2's small launches the unused code
+// alone cost about 2 us per launch.
+template <int BM, int BN, int KS, bool AK, bool BKC, int ACT, bool XS = false>
 __device__ __forceinline__ void ksplit_finish(const ZnGemmArgs &p, float *lds,
                                               const zn_f32x16 (&acc)[BM / 32][BN / 32], int64_t bz, int m0, int n0,
-                                              int wave, int lane) {
+                                              int wave, int lane, int tile = 0, int split = 0) {
     constexpr int FM = BM / 32, FN = BN / 32;
-    // partial tiles to LDS: part[wave][fm][fn][r][lane], lanes contiguous
-    __syncthreads();  // every wave is done with every staging region
-    float *part = lds + wave * (FM * FN * 16 * kWave);
+    int slices = KS;
+    float *src = lds;
+    if constexpr (XS) {
+        constexpr int kWavePart = FM * FN * 16 * kWave;
+        slices = (p.k + p.k_chunk - 1) / p.k_chunk;
+        const int64_t slot = bz * ((int64_t)p.tiles_m * p.tiles_n) + tile;
+        src = p.ws + slot * p.splits * KS * kWavePart;
+        const int q = split * KS + wave;
+        if (q < slices) {
+            float *mine = src + (int64_t)q * kWavePart;
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
+            for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
+                for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) part[((fm * FN + fn) * 16 + r) * kWave + lane] = acc[fm][fn][r];
-    __syncthreads();
+                    for (int r = 0; r < 16; ++r)
+                        __hip_atomic_store(mine + ((fm * FN + fn) * 16 + r) * kWave + lane, acc[fm][fn][r],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __shared__ int last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's block is written
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(p.counters + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   p.splits - 1;
+        __syncthreads();
+        if (!last) return;
+        if (threadIdx.x == 0) __hip_atomic_store(p.counters + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        // partial tiles to LDS: part[wave][fm][fn][r][lane], lanes contiguous
+        __syncthreads();  // every wave is done with every staging region
+        float *part = lds + wave * (FM * FN * 16 * kWave);
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) part[((fm * FN + fn) * 16 + r) * kWave + lane] = acc[fm][fn][r];
+        __syncthreads();
+    }
 
     float *gc = p.c + bz * p.stride_c;
     const int64_t ldc = p.ldc;
@@ -1156,9 +1199,26 @@ __device__ __forceinline__ void ksplit_finish(const ZnGemmArgs &p, float *lds,
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
             const int off = ((fm * FN + fn) * 16 + r) * kWave + lane;
-            float x = lds[off];
+            float x;
+            if constexpr (XS) {
+                // in groups of 16 loads, so the loads of a group are in flight together
+                x = __hip_atomic_load(src + off, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int q0 = 1; q0 < slices; q0 += 16) {
+                    float t[16];
 #pragma unroll
-            for (int w = 1; w < KS; ++w) x = x + lds[w * kPart + off];
+                    for (int i = 0; i < 16; ++i)
+                        t[i] = q0 + i < slices ? __hip_atomic_load(src + (int64_t)(q0 + i) * kPart + off,
+                                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                               : 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (q0 + i < slices) x = x + t[i];
+                }
+            } else {
+                x = lds[off];
+#pragma unroll
+                for (int w = 1; w < KS; ++w) x = x + lds[w * kPart + off];
+            }
             v[fn] = x;
         }
         if constexpr (!BKC && FN > 1) {
@@ -1208,7 +1268,14 @@ __device__ __forceinline__ void ksplit_finish(const ZnGemmArgs &p, float *lds,
 //
 // `lds` holds KS private regions of two A and two B stages each
 // (KS * 2 * (BM + BN) * BK floats); the partial tiles reuse it.
-template <int BM, int BN, int BK, int KS, bool AK, bool BKC, int WA, int WB, int ACT>
+//
+// XS: K is split over workgroups too (blockIdx.z = split of p.splits): wave
+// w of workgroup s takes slice s * KS + w of p.k_chunk, and ksplit_finish
+// hands the partial tiles over through p.ws.  Both stages are filled before
+// the first wait, so a wave of one or two slices waits for one memory round
+// trip.  (In the plain kernels, whose waves mostly have one or two slices
+// too, that prologue measured 1.5 us slower per launch.)
+template <int BM, int BN, int BK, int KS, bool AK, bool BKC, int WA, int WB, int ACT, bool XS = false>
 __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int wg = -1) {
     constexpr int FM = BM / 32, FN = BN / 32;
     typedef DmaStage<BM, BK, kWave, AK, WA> SA;
@@ -1225,8 +1292,9 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
     const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
     const int m0 = tm * BM, n0 = tn * BN;
     const int64_t bz = wg >= 0 ? 0 : blockIdx.y;
-    const int chunk = ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
-    const int kbeg = min(p.k, wave * chunk);
+    const int split = XS ? (int)blockIdx.z : 0;
+    const int chunk = XS ? p.k_chunk : ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
+    const int kbeg = min(p.k, (split * KS + wave) * chunk);
     const int kend = min(p.k, kbeg + chunk);
     const int ktiles = (kend - kbeg + BK - 1) / BK;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
@@ -1243,16 +1311,24 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
         for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-    if (ktiles > 0) {
-        SA::issue(ra, lds_a[0], lda, m0, kbeg, p.m, kend, 0, lane);
-        SB::issue(rb, lds_b[0], ldb, n0, kbeg, p.n, kend, 0, lane);
+    constexpr int kSliceLoads = SA::kPerWave + SB::kPerWave;  // this wave's load instructions per slice
+    for (int kt = 0; kt < (XS ? 2 : 1) && kt < ktiles; ++kt) {
+        SA::issue(ra, lds_a[kt], lda, m0, kbeg + kt * BK, p.m, kend, 0, lane);
+        SB::issue(rb, lds_b[kt], ldb, n0, kbeg + kt * BK, p.n, kend, 0, lane);
     }
     for (int kt = 0; kt < ktiles; ++kt) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // slice kt is in this wave's stage
         const int cur = kt & 1;
-        if (kt + 1 < ktiles) {  // the other stage was last read by slice kt - 1, whose MFMAs consumed those reads
-            SA::issue(ra, lds_a[cur ^ 1], lda, m0, kbeg + (kt + 1) * BK, p.m, kend, 0, lane);
-            SB::issue(rb, lds_b[cur ^ 1], ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, 0, lane);
+        if constexpr (XS) {
+            if (kt + 1 < ktiles)
+                vm_wait<kSliceLoads>();  // slice kt is in its stage; slice kt + 1 may still be in flight
+            else
+                vm_wait<0>();
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // slice kt is in this wave's stage
+            if (kt + 1 < ktiles) {  // the other stage was last read by slice kt - 1, whose MFMAs consumed those reads
+                SA::issue(ra, lds_a[cur ^ 1], lda, m0, kbeg + (kt + 1) * BK, p.m, kend, 0, lane);
+                SB::issue(rb, lds_b[cur ^ 1], ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, 0, lane);
+            }
         }
 #pragma unroll
         for (int kg = 0; kg < BK; kg += 8) {
@@ -1267,9 +1343,14 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
                     for (int fn = 0; fn < FN; ++fn)
                         acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
         }
+        if (XS && kt + 2 < ktiles) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's fragment reads have returned
+            SA::issue(ra, lds_a[cur], lda, m0, kbeg + (kt + 2) * BK, p.m, kend, 0, lane);
+            SB::issue(rb, lds_b[cur], ldb, n0, kbeg + (kt + 2) * BK, p.n, kend, 0, lane);
+        }
     }
 
-    ksplit_finish<BM, BN, KS, AK, BKC, ACT>(p, lds, acc, bz, m0, n0, wave, lane);
+    ksplit_finish<BM, BN, KS, AK, BKC, ACT, XS>(p, lds, acc, bz, m0, n0, wave, lane, pid, split);
 }
 
 // Store instructions a wave issues for a tile that lies wholly inside C:

@@ -55,25 +55,30 @@ ZN_GEMM_WIDE(tn, false, false)
 // Intra-workgroup split-K GEMMs (gemm_ksplit) on 32x32 tiles, BK 32, with
 // KS = 4 or 8 waves: zn_sgemmk<KS>_<layout>[_v], for problems of at most one
 // workgroup per CU whose tiles would otherwise need a split-K reduce launch.
-#define ZN_GEMMK_KERNEL(NAME, KS, AK, BKC, W)                                                    \
+// zn_sgemmk4s_<layout>[_v]: K split over workgroups as well (blockIdx.z),
+// the last workgroup of each tile adding the partial tiles (p.ws,
+// p.counters).
+#define ZN_GEMMK_KERNEL(NAME, KS, AK, BKC, W, XS)                                                \
     extern "C" __global__ __launch_bounds__(KS * 64, 1) void NAME(ZnGemmArgs p) {               \
         __shared__ __attribute__((aligned(1024))) float lds[KS * 2 * (32 + 32) * 32];            \
         switch (p.act) {                                                                         \
-        case 1: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 1>(p, lds); break;                    \
-        case 2: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 2>(p, lds); break;                    \
-        case 3: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 3>(p, lds); break;                    \
-        default: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 0>(p, lds); break;                   \
+        case 1: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 1, XS>(p, lds); break;                \
+        case 2: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 2, XS>(p, lds); break;                \
+        case 3: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 3, XS>(p, lds); break;                \
+        default: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 0, XS>(p, lds); break;               \
         }                                                                                        \
     }
-#define ZN_GEMMK_LAYOUTS(KS, W, SUFFIX)                                                         \
-    ZN_GEMMK_KERNEL(zn_sgemmk##KS##_nn##SUFFIX, KS, true, false, W)                              \
-    ZN_GEMMK_KERNEL(zn_sgemmk##KS##_nt##SUFFIX, KS, true, true, W)                               \
-    ZN_GEMMK_KERNEL(zn_sgemmk##KS##_tn##SUFFIX, KS, false, false, W)
+#define ZN_GEMMK_LAYOUTS(KS, W, SUFFIX, XS, S)                                                  \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_nn##SUFFIX, KS, true, false, W, XS)                       \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_nt##SUFFIX, KS, true, true, W, XS)                        \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_tn##SUFFIX, KS, false, false, W, XS)
 
-ZN_GEMMK_LAYOUTS(4, 16, _v)
-ZN_GEMMK_LAYOUTS(4, 4, )
-ZN_GEMMK_LAYOUTS(8, 16, _v)
-ZN_GEMMK_LAYOUTS(8, 4, )
+ZN_GEMMK_LAYOUTS(4, 16, _v, false, )
+ZN_GEMMK_LAYOUTS(4, 4, , false, )
+ZN_GEMMK_LAYOUTS(8, 16, _v, false, )
+ZN_GEMMK_LAYOUTS(8, 4, , false, )
+ZN_GEMMK_LAYOUTS(4, 16, _v, true, s)
+ZN_GEMMK_LAYOUTS(4, 4, , true, s)
 
 // Persistent plain GEMMs (gemm_persistent), 16-byte staging only:
 // zn_sgemmp_<layout>_<tile>_v, for problems of several rounds of tiles.

@@ -40,6 +40,7 @@
 // device comes from hipGetSymbolAddress (resolve_scratch below), and only
 // that address is ever passed to a kernel.
 constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr int64_t kCounterSlots = 4096;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {
@@ -155,6 +156,7 @@ struct zn_ctx {
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
+    hipFunction_t gemmks[3][2] = {};           // [layout][16-byte]: 32x32 wave-split tiles with K split over workgroups too
     hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
     hipFunction_t dense_bwd_k[2] = {};         // the same on 32x32 tiles with K split over 4 waves [16-byte]
     hipFunction_t convf[kNumTiles][2] = {};    // convolution forward on NHWC [tile][16-byte W rows]
@@ -166,6 +168,7 @@ struct zn_ctx {
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
     size_t ws_bytes = 0;
+    int32_t *counters = nullptr;  // kCounterSlots tile counters of the split wave-split kernels, zero between launches
     hipFunction_t elt[kNumElt] = {};
     int last_hip_error = 0;
     // Graph capture (zn_hip_graph_begin .. _end): leased buffers go to
@@ -746,7 +749,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
                                   pad);
         }
     }
-    int splits = ctx->forced_splits > 0 ? (int)std::min<int64_t>(ctx->forced_splits, std::max<int64_t>(1, k / ts.bk))
+    int splits = ctx->forced_splits > 0 ? (int)std::min<int64_t>(ctx->forced_splits, std::max<int64_t>(1, cdiv(k, ts.bk)))
                                         : choose_splits(ctx, tile, m, n, k, batch);
     int64_t k_chunk = k;
     if (splits > 1) {
@@ -786,6 +789,13 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // separate workgroups plus a reduce launch.  On MI355X: C1 512^3 12.6 ->
     // 6.3 us, the C2 GEMMs 7.7-12.2 -> 4.1-9.3 us; with 1024 tiles (1000^3)
     // or more the tiled kernels win.  Four waves below K = 512, eight above.
+    // Tiles for at most half the CUs with K >= 1536 also split K over up to
+    // cus / tiles workgroups of four waves (at most 32 slices of 32 or more),
+    // whose partial tiles the last workgroup of each tile adds in slice order
+    // in the same launch.  On MI355X: 300 x 200 x 3000 27.4 -> 20.1 us; the
+    // hand-over (stores, counter, the last workgroup's loads) costs about
+    // 5 us, so below K = 1536 (C2's 256 x 128 x 784: 9.7 us unsplit, 14.1
+    // split 7 ways) one workgroup per tile stays faster.
     {
         const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
         const int64_t tiles32 = cdiv(m, 32) * cdiv(n, 32) * batch;
@@ -801,7 +811,27 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
             kargs.tiles_n = (int32_t)cdiv(n, 32);
             kargs.splits = 1;
             kargs.k_chunk = (int32_t)k;
-            hipFunction_t fk = ctx->gemmk[layout][waves == 8 ? 1 : 0][vec ? 1 : 0];
+            // K in slices of `chunk` (a multiple of 32), slice q to wave q % 4
+            // of workgroup q / 4: the slices of the 32x32 tile split into as
+            // many parts by the split-K launches, added in the same order
+            int64_t wsplits = 1;
+            if (ctx->forced_wave_split < 0 && tiles32 * 2 <= cus && tiles32 <= kCounterSlots && k >= 1536)
+                wsplits = std::min<int64_t>({cus / tiles32, cdiv(k, 4 * 32), 8});
+            if (wsplits >= 2) {
+                const int64_t chunk = cdiv(cdiv(k, 4 * wsplits), 32) * 32;
+                wsplits = cdiv(cdiv(k, chunk), 4);
+                const size_t need = (size_t)(tiles32 * wsplits) * 4 * 32 * 32 * sizeof(float);
+                if (ctx->no_alloc ? need > kScratchBytes : ensure_workspace(ctx, need) != ZN_OK) wsplits = 1;
+                if (wsplits >= 2) {
+                    waves = 4;
+                    kargs.splits = (int32_t)wsplits;
+                    kargs.k_chunk = (int32_t)chunk;
+                    kargs.ws = ctx->no_alloc ? ctx->scratch : ctx->ws;
+                    kargs.counters = ctx->counters;
+                }
+            }
+            hipFunction_t fk = kargs.splits > 1 ? ctx->gemmks[layout][vec ? 1 : 0]
+                                                : ctx->gemmk[layout][waves == 8 ? 1 : 0][vec ? 1 : 0];
             for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
                 const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
                 ZnGemmArgs part = kargs;
@@ -810,7 +840,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
                 part.b = b + b0 * stride_b;
                 part.c = c + b0 * stride_c;
                 rc = launch(ctx, fk, (unsigned)(kargs.tiles_m * kargs.tiles_n), (unsigned)nb, (unsigned)(waves * 64),
-                            &part);
+                            &part, (unsigned)kargs.splits);
                 if (rc) return rc;
             }
             return ZN_OK;
@@ -1442,6 +1472,13 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                     return bail(ZN_ERR_SYMBOL);
             }
     for (int l = 0; l < 3; ++l)
+        for (int v = 0; v < 2; ++v) {
+            char name[64];
+            std::snprintf(name, sizeof(name), "zn_sgemmk4s_%s%s", kLayoutName[l], v ? "_v" : "");
+            if (hipModuleGetFunction(&ctx->gemmks[l][v], ctx->gemm_module, name) != hipSuccess)
+                return bail(ZN_ERR_SYMBOL);
+        }
+    for (int l = 0; l < 3; ++l)
         for (int t = 0; t < kNumTiles; ++t) {
             if (!kTiles[t].persistent) continue;
             char name[64];
@@ -1469,6 +1506,13 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             std::snprintf(name, sizeof(name), "zn_attention_d%d%s", kAttnDims[d], v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->attn[d][v], ctx->attn_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
         }
+    void *counters = nullptr;
+    if ((e = hipMalloc(&counters, kCounterSlots * sizeof(int32_t))) != hipSuccess) {
+        (void)hipGetLastError();
+        return bail(fail_hip(ctx, e, ZN_ERR_OOM));
+    }
+    ctx->counters = static_cast<int32_t *>(counters);
+    if ((e = hipMemset(counters, 0, kCounterSlots * sizeof(int32_t))) != hipSuccess) return bail(fail_hip(ctx, e));
     *out = ctx;
     return ZN_OK;
 }
@@ -1495,6 +1539,8 @@ int zn_hip_destroy(zn_ctx *ctx) {
     ctx->pool.clear();
     if (ctx->ws) (void)hipFree(ctx->ws);
     ctx->ws = nullptr;
+    if (ctx->counters) (void)hipFree(ctx->counters);
+    ctx->counters = nullptr;
     if (ctx->gemm_module) (void)hipModuleUnload(ctx->gemm_module);
     if (ctx->conv_module) (void)hipModuleUnload(ctx->conv_module);
     if (ctx->elt_module) (void)hipModuleUnload(ctx->elt_module);

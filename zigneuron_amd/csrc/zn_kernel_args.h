@@ -59,6 +59,10 @@ struct ZnGemmArgs {
     const float *chain_y;
     float *chain_gaa;
     int32_t chain_act;
+    // Intra-workgroup split-K kernels with splits > 1: one counter per
+    // (problem, tile), zero between launches (the last workgroup of a tile
+    // resets it).
+    int32_t *counters;
 };
 
 // Split-K reduction: C = act((accumulate ? C : 0) + sum_s ws[s] + bias), the
