@@ -191,7 +191,8 @@ int zn_hip_set_gemm_persistent(zn_ctx *ctx, int mode);
  * (problems of at most one 32x32 tile per CU, 64 <= K <= 4096), 0 never
  * uses it, 4 or 8 runs every GEMM with K > 0 (other than the convolutions')
  * on 32x32 tiles whose 4 or 8 waves split K and sum their partial tiles in
- * wave order.  A tuning and test hook with no reference counterpart. */
+ * wave order, 16 on 16x16 tiles whose 4 waves do the same.  A tuning and
+ * test hook with no reference counterpart. */
 int zn_hip_set_gemm_wave_split(zn_ctx *ctx, int waves);
 
 /* C = act((accumulate ? C : 0) + op(A).op(B) + bias) for one problem.

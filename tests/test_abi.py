@@ -69,6 +69,8 @@ def test_code_objects_hold_every_kernel():
         for waves in ("4", "8", "4s"):
             for v in ("", "_v"):
                 assert f"zn_sgemmk{waves}_{lay}{v}".encode() in gemm
+        for v in ("", "_v"):
+            assert f"zn_sgemmq4_{lay}{v}".encode() in gemm
     for t in ("x", "l", "n", "m", "s"):
         for v in ("", "_v"):
             for g in ("", "_g"):

@@ -8,6 +8,8 @@ paths must agree bit for bit whenever every wave has a non-empty slice; the
 automatic policy is checked against the oracle.  Problems of at most half
 the CUs of tiles split K over workgroups too; the last workgroup of a tile
 adds the partial tiles in slice order, again the split-K arithmetic.
+Problems of at most one 16x16 tile per CU run on 16x16 tiles whose four
+waves split K (unless K >= 1536 and the tiles fill under half the CUs).
 """
 from __future__ import annotations
 
@@ -97,10 +99,10 @@ def test_wave_split_matches_split_k(ctx, layout, m, n, k, batch, waves, bias, ac
 
 WG_CASES = [
     # layout, m, n, k, batch, bias, act, acc: at most half the CUs of 32x32 tiles, K >= 1536
-    ("nn", 256, 128, 1600, 1, True, "relu", False),     # 7 workgroups per tile, 25 slices of 64
+    ("nn", 256, 96, 1600, 1, True, "relu", False),      # 7 workgroups per tile, 25 slices of 64
     ("nt", 100, 70, 2000, 1, True, "sigmoid", True),    # ragged everywhere
     ("nn", 64, 64, 4096, 1, True, "linear", True),      # 32 slices of 128 (two stages per wave)
-    ("nn", 300, 200, 3000, 1, False, "tanh", False),    # 256-wide slices
+    ("nn", 128, 200, 3000, 1, False, "tanh", False),    # 96-wide slices
     ("nt", 32, 32, 1537, 1, False, "linear", False),    # 4-byte staging; the last slice is one column of K
     ("tn", 64, 96, 2048, 3, False, "linear", False),
     ("nn", 33, 65, 1800, 5, False, "linear", False),    # the last workgroup has one slice
@@ -118,6 +120,7 @@ def test_workgroup_split_matches_split_k(ctx, layout, m, n, k, batch, bias, act,
     cus = ctx.compute_units
     tiles = -(-m // 32) * -(-n // 32) * batch
     assert tiles * 2 <= cus
+    assert 2 * (-(-m // 16) * -(-n // 16) * batch) < cus, "too few 16x16 tiles for the 16x16 kernels"
     assert k >= 1536
     s0 = min(cus // tiles, -(-k // 128), 8)
     chunk = -(-(-(-k // (4 * s0))) // 32) * 32
@@ -157,6 +160,57 @@ def test_workgroup_split_matches_split_k(ctx, layout, m, n, k, batch, bias, act,
                      act=act, what=f"workgroup split problem {i}")
 
 
+Q_CASES = [
+    # layout, m, n, k, batch, bias, act, acc
+    ("nn", 256, 128, 784, 1, True, "relu", False),     # the C2 first layer (the policy's choice)
+    ("nn", 256, 10, 128, 1, True, "linear", False),    # the C2 second layer (4-byte B rows)
+    ("nt", 256, 784, 128, 1, False, "linear", True),
+    ("tn", 784, 128, 256, 1, False, "linear", False),
+    ("nn", 100, 70, 1000, 1, True, "sigmoid", False),  # ragged
+    ("tn", 64, 96, 300, 3, False, "linear", False),
+    ("nn", 33, 65, 200, 5, False, "linear", False),
+    ("nn", 17, 9, 3000, 1, False, "tanh", False),      # 24 slices per wave through 4 stages (4-byte B)
+    ("nt", 31, 47, 4099, 1, False, "linear", True),    # 4-byte staging, 33 slices per wave
+    ("nn", 64, 64, 2048, 1, False, "linear", False),   # 16 slices per wave through 8 stages
+]
+
+
+@pytest.mark.parametrize("layout,m,n,k,batch,bias,act,acc", Q_CASES)
+def test_quarter_tiles_against_oracle(ctx, layout, m, n, k, batch, bias, act, acc):
+    """16x16 tiles whose four waves split K (zn_sgemmq4_*), forced on every
+    case: against the oracle, the same bits on a second run, and the same
+    bits as the automatic choice where the policy picks them (at most one
+    16x16 tile per CU, 64 <= K <= 4096, and K < 1536 or tiles for at least
+    half the CUs)."""
+    rng = np.random.default_rng(m * 5 + n + k)
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a = uniform(rng, (batch,) + a_shape)
+    b = uniform(rng, (batch,) + b_shape)
+    c0 = uniform(rng, (batch, m, n))
+    bv = uniform(rng, (n,)) if bias else None
+    if batch > 1:
+        bv, act, acc = None, "linear", False
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    announce(f"16x16 wave split {layout} {m}x{n}x{k} batch {batch} act {act} acc {acc}")
+    ctx.set_gemm_wave_split(16)
+    got = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
+    again = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
+    ctx.set_gemm_wave_split(-1)
+    assert np.isfinite(got).all()
+    np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
+    cus = ctx.compute_units
+    tiles16 = -(-m // 16) * -(-n // 16) * batch
+    if tiles16 <= cus and 64 <= k <= 4096 and (k < 1536 or 2 * tiles16 >= cus):
+        auto = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
+        np.testing.assert_array_equal(auto.view(np.uint32), got.view(np.uint32))
+    rb = bv if bv is not None or act == "linear" else np.zeros(n, np.float32)
+    for i in range(batch):
+        ref = ref_gemm(layout, a[i], b[i], m, n, k, c0=c0[i] if acc else None, accumulate=acc, bias=rb, act=act)
+        assert_close(got[i], ref, layout, a[i], b[i], m, n, k, c0=c0[i] if acc else None, accumulate=acc, bias=rb,
+                     act=act, what=f"16x16 wave split problem {i}")
+
+
 def test_policy_small_problems_against_oracle(ctx):
     """The automatic choice for problems of at most one 32x32 tile per CU."""
     rng = np.random.default_rng(5)
@@ -172,7 +226,7 @@ def test_policy_small_problems_against_oracle(ctx):
 
 def test_tuning_hooks_reject_bad_values(ctx):
     from zigneuron_amd import InvalidArgumentError
-    for bad in (1, 2, 5, 16, -2):
+    for bad in (1, 2, 5, 32, -2):
         with pytest.raises(InvalidArgumentError):
             ctx.set_gemm_wave_split(bad)
     for bad in (2, -2):

@@ -1353,6 +1353,131 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
     ksplit_finish<BM, BN, KS, AK, BKC, ACT, XS>(p, lds, acc, bz, m0, n0, wave, lane, pid, split);
 }
 
+// Wait until at most `ahead` slices' loads (of kSliceLoads instructions
+// each) are still in flight: vmcnt takes an immediate, so one branch per
+// possible count.
+template <int kSliceLoads, int NS>
+__device__ __forceinline__ void vm_wait_slices(int ahead) {
+    static_assert((NS - 1) * kSliceLoads < 64, "6-bit vmcnt");
+    switch (ahead) {
+    case 0: vm_wait<0>(); break;
+    case 1: vm_wait<kSliceLoads>(); break;
+    case 2: if constexpr (NS > 2) vm_wait<2 * kSliceLoads>(); break;
+    case 3: if constexpr (NS > 3) vm_wait<3 * kSliceLoads>(); break;
+    case 4: if constexpr (NS > 4) vm_wait<4 * kSliceLoads>(); break;
+    case 5: if constexpr (NS > 5) vm_wait<5 * kSliceLoads>(); break;
+    case 6: if constexpr (NS > 6) vm_wait<6 * kSliceLoads>(); break;
+    default: if constexpr (NS > 7) vm_wait<7 * kSliceLoads>(); break;
+    }
+}
+
+// Intra-workgroup split-K on 16x16 tiles (v_mfma_f32_16x16x4f32), for
+// problems whose 32x32 tiles would leave most CUs idle: C2's 256 x 128 x 784
+// forward is 32 tiles of 32x32 (at least 2.6 us of matrix-core time on each
+// of 32 CUs) but 128 tiles of 16x16.  Each of the KS = 4 waves multiplies
+// the 16x16 tile over its own contiguous range of K (whole BK = 32 slices),
+// with up to NS slices in flight in NS private LDS stages (8 with 16-byte
+// loads: every slice of a wave of up to 8 slices is requested before the
+// first wait), then the partial tiles meet in LDS and are added in wave
+// order, and the epilogue (C_old, bias, activation) runs on the sums.
+//
+// 16x16x4 operands: in MFMA step t of a k group kg (16 values of k), lane
+// (i = lane % 16, h = lane / 16) supplies A[i][kg + 4h + t] and
+// B[kg + 4h + t][i]; lane (j, h) receives D[4h + r][j] in register r.
+// `lds` holds KS * NS stages of (16 + 16) * BK floats.
+template <int KS, bool AK, bool BKC, int W, int ACT>
+__device__ __forceinline__ void gemm_ksplit16(const ZnGemmArgs &p, float *lds) {
+    constexpr int BM = 16, BN = 16, BK = 32;
+    constexpr int NS = W == 16 ? 8 : 4;
+    typedef DmaStage<BM, BK, kWave, AK, W> SA;
+    typedef DmaStage<BN, BK, kWave, BKC, W> SB;
+    constexpr int kStage = SA::kFloats + SB::kFloats;
+    constexpr int kSliceLoads = SA::kPerWave + SB::kPerWave;
+    static_assert(KS * kWave == 256, "one output element per thread in the epilogue");
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+    float *region = lds + wave * NS * kStage;
+
+    const int pid = blockIdx.x;
+    const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int64_t bz = blockIdx.y;
+    const int chunk = ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
+    const int kbeg = min(p.k, wave * chunk);
+    const int kend = min(p.k, kbeg + chunk);
+    const int ktiles = (kend - kbeg + BK - 1) / BK;
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    constexpr int RW = W == 16 ? 3 : 0;
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RW) & ~RW) : (p.k - 1) * lda + ((p.m + RW) & ~RW)) * 4u;
+    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RW) & ~RW) : (p.k - 1) * ldb + ((p.n + RW) & ~RW)) * 4u;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + bz * p.stride_a, a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + bz * p.stride_b, b_bytes);
+
+    for (int kt = 0; kt < NS && kt < ktiles; ++kt) {
+        float *st = region + kt * kStage;
+        SA::issue(ra, st, lda, m0, kbeg + kt * BK, p.m, kend, 0, lane);
+        SB::issue(rb, st + SA::kFloats, ldb, n0, kbeg + kt * BK, p.n, kend, 0, lane);
+    }
+    const int i = lane & 15, h = lane >> 4;
+    zn_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kt = 0; kt < ktiles; ++kt) {
+        vm_wait_slices<kSliceLoads, NS>(min(ktiles - 1 - kt, NS - 1));  // slice kt is in its stage
+        const float *sa = region + (kt % NS) * kStage;
+        const float *sb = sa + SA::kFloats;
+#pragma unroll
+        for (int kg = 0; kg < BK; kg += 16) {
+            float fa[4], fb[4];
+            if constexpr (AK) {
+                const int slot = (kg / 4 + h) ^ SA::swz(i);
+                const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(sa + i * BK + 4 * slot);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) fa[t] = v[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) fa[t] = sa[(kg + 4 * h + t) * BM + i];
+            }
+            if constexpr (BKC) {
+                const int slot = (kg / 4 + h) ^ SB::swz(i);
+                const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(sb + i * BK + 4 * slot);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) fb[t] = v[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) fb[t] = sb[(kg + 4 * h + t) * BN + i];
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[t], fb[t], acc, 0, 0, 0);
+        }
+        if (kt + NS < ktiles) {  // refill this stage once its fragment reads have returned
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            float *st = region + (kt % NS) * kStage;
+            SA::issue(ra, st, lda, m0, kbeg + (kt + NS) * BK, p.m, kend, 0, lane);
+            SB::issue(rb, st + SA::kFloats, ldb, n0, kbeg + (kt + NS) * BK, p.n, kend, 0, lane);
+        }
+    }
+
+    // partial tiles to LDS, part[wave][r][lane]; thread t finishes element
+    // (t / 16, t % 16), held by lane 16 * (t / 64) + t % 16 in register (t / 16) % 4
+    __syncthreads();  // every wave is done with every stage
+    float *part = lds + wave * 4 * kWave;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[r * kWave + lane] = acc[r];
+    __syncthreads();
+    const int t = threadIdx.x;
+    const int rr = t >> 4, cc = t & 15;
+    const int off = (rr & 3) * kWave + (rr >> 2) * 16 + cc;
+    float x = lds[off];
+#pragma unroll
+    for (int w = 1; w < KS; ++w) x = x + lds[w * 4 * kWave + off];
+    const int row = m0 + rr, col = n0 + cc;
+    if (row < p.m && col < p.n) {
+        float *dst = p.c + bz * p.stride_c + (int64_t)row * p.ldc + col;
+        if (p.accumulate) x = *dst + x;
+        if (p.bias) x = x + p.bias[p.bias_rows ? row : col];
+        *dst = zn_activate(x, ACT);
+    }
+}
+
 // Store instructions a wave issues for a tile that lies wholly inside C:
 // one per (row block, accumulator register) on the vector-store path of an
 // X-contiguous B, one per element column otherwise (fewest of the two, since

@@ -80,6 +80,24 @@ ZN_GEMMK_LAYOUTS(8, 4, , false, )
 ZN_GEMMK_LAYOUTS(4, 16, _v, true, s)
 ZN_GEMMK_LAYOUTS(4, 4, , true, s)
 
+// The same on 16x16 tiles (gemm_ksplit16): zn_sgemmq4_<layout>[_v].
+#define ZN_GEMMQ_KERNEL(NAME, AK, BKC, W)                                                        \
+    extern "C" __global__ __launch_bounds__(256, 1) void NAME(ZnGemmArgs p) {                   \
+        __shared__ __attribute__((aligned(1024))) float lds[4 * (W == 16 ? 8 : 4) * 32 * 32];    \
+        switch (p.act) {                                                                         \
+        case 1: gemm_ksplit16<4, AK, BKC, W, 1>(p, lds); break;                                  \
+        case 2: gemm_ksplit16<4, AK, BKC, W, 2>(p, lds); break;                                  \
+        case 3: gemm_ksplit16<4, AK, BKC, W, 3>(p, lds); break;                                  \
+        default: gemm_ksplit16<4, AK, BKC, W, 0>(p, lds); break;                                 \
+        }                                                                                        \
+    }
+ZN_GEMMQ_KERNEL(zn_sgemmq4_nn_v, true, false, 16)
+ZN_GEMMQ_KERNEL(zn_sgemmq4_nt_v, true, true, 16)
+ZN_GEMMQ_KERNEL(zn_sgemmq4_tn_v, false, false, 16)
+ZN_GEMMQ_KERNEL(zn_sgemmq4_nn, true, false, 4)
+ZN_GEMMQ_KERNEL(zn_sgemmq4_nt, true, true, 4)
+ZN_GEMMQ_KERNEL(zn_sgemmq4_tn, false, false, 4)
+
 // Persistent plain GEMMs (gemm_persistent), 16-byte staging only:
 // zn_sgemmp_<layout>_<tile>_v, for problems of several rounds of tiles.
 #define ZN_GEMMP_KERNEL(NAME, BM, BN, BK, WM, WN, AK, BKC, MINB)                                 \

@@ -156,6 +156,7 @@ struct zn_ctx {
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
+    hipFunction_t gemmq[3][2] = {};            // [layout][16-byte]: 16x16 wave-split tiles
     hipFunction_t gemmks[3][2] = {};           // [layout][16-byte]: 32x32 wave-split tiles with K split over workgroups too
     hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
     hipFunction_t dense_bwd_k[2] = {};         // the same on 32x32 tiles with K split over 4 waves [16-byte]
@@ -805,6 +806,34 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         else if (!conv && ctx->forced_wave_split < 0 && ctx->forced_tile < 0 && ctx->forced_splits == 0 &&
                  tiles32 <= cus && k >= 64 && k <= 4096)
             waves = k >= 512 ? 8 : 4;
+        // 16x16 tiles (four waves splitting K) for at most one round of them,
+        // unless they are so few that the workgroup split below does better
+        // (K >= 1536 and 16x16 tiles for under half the CUs).  On MI355X:
+        // C2's 256 x 128 x 784 forward 9.1 -> 5.6 us, 256 x 10 x 128
+        // 5.8 -> 4.0 us, 300 x 200 x 3000 15.3 us (18.7 split over
+        // workgroups); 64 x 64 x 4096 17.7 us against 14.1 split.
+        const int64_t tiles16 = cdiv(m, 16) * cdiv(n, 16) * batch;
+        if (waves == 16 ||
+            (waves && ctx->forced_wave_split < 0 && tiles16 <= cus && (k < 1536 || tiles16 * 2 >= cus))) {
+            ZnGemmArgs q = args;
+            q.tiles_m = (int32_t)cdiv(m, 16);
+            q.tiles_n = (int32_t)cdiv(n, 16);
+            q.splits = 1;
+            q.k_chunk = (int32_t)k;
+            if ((int64_t)q.tiles_m * q.tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
+            for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
+                const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
+                ZnGemmArgs part = q;
+                part.batch = (int32_t)nb;
+                part.a = a + b0 * stride_a;
+                part.b = b + b0 * stride_b;
+                part.c = c + b0 * stride_c;
+                rc = launch(ctx, ctx->gemmq[layout][vec ? 1 : 0], (unsigned)(q.tiles_m * q.tiles_n), (unsigned)nb, 256,
+                            &part);
+                if (rc) return rc;
+            }
+            return ZN_OK;
+        }
         if (waves) {
             ZnGemmArgs kargs = args;
             kargs.tiles_m = (int32_t)cdiv(m, 32);
@@ -1477,6 +1506,9 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             std::snprintf(name, sizeof(name), "zn_sgemmk4s_%s%s", kLayoutName[l], v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->gemmks[l][v], ctx->gemm_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
+            std::snprintf(name, sizeof(name), "zn_sgemmq4_%s%s", kLayoutName[l], v ? "_v" : "");
+            if (hipModuleGetFunction(&ctx->gemmq[l][v], ctx->gemm_module, name) != hipSuccess)
+                return bail(ZN_ERR_SYMBOL);
         }
     for (int l = 0; l < 3; ++l)
         for (int t = 0; t < kNumTiles; ++t) {
@@ -1768,7 +1800,7 @@ int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits) {
 }
 
 int zn_hip_set_gemm_wave_split(zn_ctx *ctx, int waves) {
-    if (!ctx || (waves != -1 && waves != 0 && waves != 4 && waves != 8)) return ZN_ERR_INVALID_ARG;
+    if (!ctx || (waves != -1 && waves != 0 && waves != 4 && waves != 8 && waves != 16)) return ZN_ERR_INVALID_ARG;
     ctx->forced_wave_split = waves;
     return ZN_OK;
 }
