@@ -70,7 +70,8 @@ def test_code_objects_hold_every_kernel():
             for v in ("", "_v"):
                 assert f"zn_sgemmk{waves}_{lay}{v}".encode() in gemm
         for v in ("", "_v"):
-            assert f"zn_sgemmq4_{lay}{v}".encode() in gemm
+            for q in ("q4", "q4m"):
+                assert f"zn_sgemm{q}_{lay}{v}".encode() in gemm
     for t in ("x", "l", "n", "m", "s"):
         for v in ("", "_v"):
             for g in ("", "_g"):

@@ -179,9 +179,10 @@ Q_CASES = [
 def test_quarter_tiles_against_oracle(ctx, layout, m, n, k, batch, bias, act, acc):
     """16x16 tiles whose four waves split K (zn_sgemmq4_*), forced on every
     case: against the oracle, the same bits on a second run, and the same
-    bits as the automatic choice where the policy picks them (at most one
-    16x16 tile per CU, 64 <= K <= 4096, and K < 1536 or tiles for at least
-    half the CUs)."""
+    bits as the automatic choice where the policy picks them (64 <= K <=
+    4096 and at most one 32x32 tile per CU; at most one 16x16 tile per CU
+    and K < 1536 or tiles for at least half the CUs, or two to three 16x16
+    tiles per CU on the two-stage kernels)."""
     rng = np.random.default_rng(m * 5 + n + k)
     a_shape, b_shape = stored_shapes(layout, m, n, k)
     a = uniform(rng, (batch,) + a_shape)
@@ -201,7 +202,9 @@ def test_quarter_tiles_against_oracle(ctx, layout, m, n, k, batch, bias, act, ac
     np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
     cus = ctx.compute_units
     tiles16 = -(-m // 16) * -(-n // 16) * batch
-    if tiles16 <= cus and 64 <= k <= 4096 and (k < 1536 or 2 * tiles16 >= cus):
+    tiles32 = -(-m // 32) * -(-n // 32) * batch
+    picked = (tiles16 <= cus and (k < 1536 or 2 * tiles16 >= cus)) or cus < tiles16 <= 3 * cus
+    if picked and tiles32 <= cus and 64 <= k <= 4096:
         auto = _run(ctx, layout, m, n, k, batch, a, b, c0, bv, act, acc, lda, ldb)
         np.testing.assert_array_equal(auto.view(np.uint32), got.view(np.uint32))
     rb = bv if bv is not None or act == "linear" else np.zeros(n, np.float32)

@@ -1271,11 +1271,11 @@ __device__ __forceinline__ void ksplit_finish(const ZnGemmArgs &p, float *lds,
 //
 // XS: K is split over workgroups too (blockIdx.z = split of p.splits): wave
 // w of workgroup s takes slice s * KS + w of p.k_chunk, and ksplit_finish
-// hands the partial tiles over through p.ws.  Both stages are filled before
-// the first wait, so a wave of one or two slices waits for one memory round
-// trip.  (In the plain kernels, whose waves mostly have one or two slices
-// too, that prologue measured 1.5 us slower per launch.)
-template <int BM, int BN, int BK, int KS, bool AK, bool BKC, int WA, int WB, int ACT, bool XS = false>
+// hands the partial tiles over through p.ws.  PF (with XS): both stages
+// are filled before the first wait, so a wave of one or two slices waits
+// for one memory round trip.  (In C2's small launches that prologue
+// measured 1.5 us slower per launch, and C1's 512^3 0.07 us faster.)
+template <int BM, int BN, int BK, int KS, bool AK, bool BKC, int WA, int WB, int ACT, bool XS = false, bool PF = XS>
 __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int wg = -1) {
     constexpr int FM = BM / 32, FN = BN / 32;
     typedef DmaStage<BM, BK, kWave, AK, WA> SA;
@@ -1312,13 +1312,13 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
     constexpr int kSliceLoads = SA::kPerWave + SB::kPerWave;  // this wave's load instructions per slice
-    for (int kt = 0; kt < (XS ? 2 : 1) && kt < ktiles; ++kt) {
+    for (int kt = 0; kt < (PF ? 2 : 1) && kt < ktiles; ++kt) {
         SA::issue(ra, lds_a[kt], lda, m0, kbeg + kt * BK, p.m, kend, 0, lane);
         SB::issue(rb, lds_b[kt], ldb, n0, kbeg + kt * BK, p.n, kend, 0, lane);
     }
     for (int kt = 0; kt < ktiles; ++kt) {
         const int cur = kt & 1;
-        if constexpr (XS) {
+        if constexpr (PF) {
             if (kt + 1 < ktiles)
                 vm_wait<kSliceLoads>();  // slice kt is in its stage; slice kt + 1 may still be in flight
             else
@@ -1343,7 +1343,7 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
                     for (int fn = 0; fn < FN; ++fn)
                         acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
         }
-        if (XS && kt + 2 < ktiles) {
+        if (PF && kt + 2 < ktiles) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's fragment reads have returned
             SA::issue(ra, lds_a[cur], lda, m0, kbeg + (kt + 2) * BK, p.m, kend, 0, lane);
             SB::issue(rb, lds_b[cur], ldb, n0, kbeg + (kt + 2) * BK, p.n, kend, 0, lane);
@@ -1384,11 +1384,13 @@ __device__ __forceinline__ void vm_wait_slices(int ahead) {
 // 16x16x4 operands: in MFMA step t of a k group kg (16 values of k), lane
 // (i = lane % 16, h = lane / 16) supplies A[i][kg + 4h + t] and
 // B[kg + 4h + t][i]; lane (j, h) receives D[4h + r][j] in register r.
-// `lds` holds KS * NS stages of (16 + 16) * BK floats.
-template <int KS, bool AK, bool BKC, int W, int ACT>
+// `lds` holds KS * NS stages of (16 + 16) * BK floats.  NSMAX = 2 (the
+// zn_sgemmq4m_* kernels): two stages, 32 KB of LDS, so that five
+// workgroups share a CU when there are more tiles than CUs.
+template <int KS, bool AK, bool BKC, int W, int ACT, int NSMAX = 8>
 __device__ __forceinline__ void gemm_ksplit16(const ZnGemmArgs &p, float *lds) {
     constexpr int BM = 16, BN = 16, BK = 32;
-    constexpr int NS = W == 16 ? 8 : 4;
+    constexpr int NS = NSMAX < (W == 16 ? 8 : 4) ? NSMAX : (W == 16 ? 8 : 4);
     typedef DmaStage<BM, BK, kWave, AK, W> SA;
     typedef DmaStage<BN, BK, kWave, BKC, W> SB;
     constexpr int kStage = SA::kFloats + SB::kFloats;

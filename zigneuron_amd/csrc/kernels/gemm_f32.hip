@@ -58,45 +58,51 @@ ZN_GEMM_WIDE(tn, false, false)
 // zn_sgemmk4s_<layout>[_v]: K split over workgroups as well (blockIdx.z),
 // the last workgroup of each tile adding the partial tiles (p.ws,
 // p.counters).
-#define ZN_GEMMK_KERNEL(NAME, KS, AK, BKC, W, XS)                                                \
+#define ZN_GEMMK_KERNEL(NAME, KS, AK, BKC, W, XS, PF)                                            \
     extern "C" __global__ __launch_bounds__(KS * 64, 1) void NAME(ZnGemmArgs p) {               \
         __shared__ __attribute__((aligned(1024))) float lds[KS * 2 * (32 + 32) * 32];            \
         switch (p.act) {                                                                         \
-        case 1: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 1, XS>(p, lds); break;                \
-        case 2: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 2, XS>(p, lds); break;                \
-        case 3: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 3, XS>(p, lds); break;                \
-        default: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 0, XS>(p, lds); break;               \
+        case 1: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 1, XS, PF>(p, lds); break;            \
+        case 2: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 2, XS, PF>(p, lds); break;            \
+        case 3: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 3, XS, PF>(p, lds); break;            \
+        default: gemm_ksplit<32, 32, 32, KS, AK, BKC, W, W, 0, XS, PF>(p, lds); break;           \
         }                                                                                        \
     }
-#define ZN_GEMMK_LAYOUTS(KS, W, SUFFIX, XS, S)                                                  \
-    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_nn##SUFFIX, KS, true, false, W, XS)                       \
-    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_nt##SUFFIX, KS, true, true, W, XS)                        \
-    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_tn##SUFFIX, KS, false, false, W, XS)
+#define ZN_GEMMK_LAYOUTS(KS, W, SUFFIX, XS, PF, S)                                              \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_nn##SUFFIX, KS, true, false, W, XS, PF)                   \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_nt##SUFFIX, KS, true, true, W, XS, PF)                    \
+    ZN_GEMMK_KERNEL(zn_sgemmk##KS##S##_tn##SUFFIX, KS, false, false, W, XS, PF)
 
-ZN_GEMMK_LAYOUTS(4, 16, _v, false, )
-ZN_GEMMK_LAYOUTS(4, 4, , false, )
-ZN_GEMMK_LAYOUTS(8, 16, _v, false, )
-ZN_GEMMK_LAYOUTS(8, 4, , false, )
-ZN_GEMMK_LAYOUTS(4, 16, _v, true, s)
-ZN_GEMMK_LAYOUTS(4, 4, , true, s)
+ZN_GEMMK_LAYOUTS(4, 16, _v, false, false, )
+ZN_GEMMK_LAYOUTS(4, 4, , false, false, )
+ZN_GEMMK_LAYOUTS(8, 16, _v, false, false, )
+ZN_GEMMK_LAYOUTS(8, 4, , false, false, )
+ZN_GEMMK_LAYOUTS(4, 16, _v, true, true, s)
+ZN_GEMMK_LAYOUTS(4, 4, , true, true, s)
 
-// The same on 16x16 tiles (gemm_ksplit16): zn_sgemmq4_<layout>[_v].
-#define ZN_GEMMQ_KERNEL(NAME, AK, BKC, W)                                                        \
-    extern "C" __global__ __launch_bounds__(256, 1) void NAME(ZnGemmArgs p) {                   \
-        __shared__ __attribute__((aligned(1024))) float lds[4 * (W == 16 ? 8 : 4) * 32 * 32];    \
+// The same on 16x16 tiles (gemm_ksplit16): zn_sgemmq4_<layout>[_v] with up
+// to 8 LDS stages per wave, zn_sgemmq4m_<layout>[_v] with 2 (several
+// workgroups per CU).
+#define ZN_GEMMQ_KERNEL(NAME, AK, BKC, W, NSMAX, MINB)                                           \
+    extern "C" __global__ __launch_bounds__(256, MINB) void NAME(ZnGemmArgs p) {                \
+        constexpr int kStages = NSMAX < (W == 16 ? 8 : 4) ? NSMAX : (W == 16 ? 8 : 4);           \
+        __shared__ __attribute__((aligned(1024))) float lds[4 * kStages * 32 * 32];              \
         switch (p.act) {                                                                         \
-        case 1: gemm_ksplit16<4, AK, BKC, W, 1>(p, lds); break;                                  \
-        case 2: gemm_ksplit16<4, AK, BKC, W, 2>(p, lds); break;                                  \
-        case 3: gemm_ksplit16<4, AK, BKC, W, 3>(p, lds); break;                                  \
-        default: gemm_ksplit16<4, AK, BKC, W, 0>(p, lds); break;                                 \
+        case 1: gemm_ksplit16<4, AK, BKC, W, 1, NSMAX>(p, lds); break;                           \
+        case 2: gemm_ksplit16<4, AK, BKC, W, 2, NSMAX>(p, lds); break;                           \
+        case 3: gemm_ksplit16<4, AK, BKC, W, 3, NSMAX>(p, lds); break;                           \
+        default: gemm_ksplit16<4, AK, BKC, W, 0, NSMAX>(p, lds); break;                          \
         }                                                                                        \
     }
-ZN_GEMMQ_KERNEL(zn_sgemmq4_nn_v, true, false, 16)
-ZN_GEMMQ_KERNEL(zn_sgemmq4_nt_v, true, true, 16)
-ZN_GEMMQ_KERNEL(zn_sgemmq4_tn_v, false, false, 16)
-ZN_GEMMQ_KERNEL(zn_sgemmq4_nn, true, false, 4)
-ZN_GEMMQ_KERNEL(zn_sgemmq4_nt, true, true, 4)
-ZN_GEMMQ_KERNEL(zn_sgemmq4_tn, false, false, 4)
+#define ZN_GEMMQ_LAYOUTS(S, NSMAX, MINB)                                                         \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nn_v, true, false, 16, NSMAX, MINB)                          \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nt_v, true, true, 16, NSMAX, MINB)                           \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_tn_v, false, false, 16, NSMAX, MINB)                         \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nn, true, false, 4, NSMAX, MINB)                             \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nt, true, true, 4, NSMAX, MINB)                              \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_tn, false, false, 4, NSMAX, MINB)
+ZN_GEMMQ_LAYOUTS(, 8, 1)
+ZN_GEMMQ_LAYOUTS(m, 2, 4)
 
 // Persistent plain GEMMs (gemm_persistent), 16-byte staging only:
 // zn_sgemmp_<layout>_<tile>_v, for problems of several rounds of tiles.

@@ -156,7 +156,7 @@ struct zn_ctx {
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
-    hipFunction_t gemmq[3][2] = {};            // [layout][16-byte]: 16x16 wave-split tiles
+    hipFunction_t gemmq[3][2][2] = {};         // [layout][2 stages][16-byte]: 16x16 wave-split tiles
     hipFunction_t gemmks[3][2] = {};           // [layout][16-byte]: 32x32 wave-split tiles with K split over workgroups too
     hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
     hipFunction_t dense_bwd_k[2] = {};         // the same on 32x32 tiles with K split over 4 waves [16-byte]
@@ -811,10 +811,14 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         // (K >= 1536 and 16x16 tiles for under half the CUs).  On MI355X:
         // C2's 256 x 128 x 784 forward 9.1 -> 5.6 us, 256 x 10 x 128
         // 5.8 -> 4.0 us, 300 x 200 x 3000 15.3 us (18.7 split over
-        // workgroups); 64 x 64 x 4096 17.7 us against 14.1 split.
+        // workgroups); 64 x 64 x 4096 17.7 us against 14.1 split.  Up to
+        // three per CU run on the two-stage kernels (several workgroups per
+        // CU): 384^3 5.7 -> 4.9 us, 512 x 256 x 1024 9.5 -> 6.5 us; C1's
+        // 512^3 (four per CU) stays on 32x32 tiles (6.2 against 6.4 us).
         const int64_t tiles16 = cdiv(m, 16) * cdiv(n, 16) * batch;
-        if (waves == 16 ||
-            (waves && ctx->forced_wave_split < 0 && tiles16 <= cus && (k < 1536 || tiles16 * 2 >= cus))) {
+        if (waves == 16 || (waves && ctx->forced_wave_split < 0 &&
+                            ((tiles16 <= cus && (k < 1536 || tiles16 * 2 >= cus)) ||
+                             (tiles16 > cus && tiles16 <= 3 * cus)))) {
             ZnGemmArgs q = args;
             q.tiles_m = (int32_t)cdiv(m, 16);
             q.tiles_n = (int32_t)cdiv(n, 16);
@@ -828,8 +832,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
                 part.a = a + b0 * stride_a;
                 part.b = b + b0 * stride_b;
                 part.c = c + b0 * stride_c;
-                rc = launch(ctx, ctx->gemmq[layout][vec ? 1 : 0], (unsigned)(q.tiles_m * q.tiles_n), (unsigned)nb, 256,
-                            &part);
+                rc = launch(ctx, ctx->gemmq[layout][tiles16 > cus ? 1 : 0][vec ? 1 : 0],
+                            (unsigned)(q.tiles_m * q.tiles_n), (unsigned)nb, 256, &part);
                 if (rc) return rc;
             }
             return ZN_OK;
@@ -1506,9 +1510,11 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             std::snprintf(name, sizeof(name), "zn_sgemmk4s_%s%s", kLayoutName[l], v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->gemmks[l][v], ctx->gemm_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
-            std::snprintf(name, sizeof(name), "zn_sgemmq4_%s%s", kLayoutName[l], v ? "_v" : "");
-            if (hipModuleGetFunction(&ctx->gemmq[l][v], ctx->gemm_module, name) != hipSuccess)
-                return bail(ZN_ERR_SYMBOL);
+            for (int r = 0; r < 2; ++r) {
+                std::snprintf(name, sizeof(name), "zn_sgemmq4%s_%s%s", r ? "m" : "", kLayoutName[l], v ? "_v" : "");
+                if (hipModuleGetFunction(&ctx->gemmq[l][r][v], ctx->gemm_module, name) != hipSuccess)
+                    return bail(ZN_ERR_SYMBOL);
+            }
         }
     for (int l = 0; l < 3; ++l)
         for (int t = 0; t < kNumTiles; ++t) {
