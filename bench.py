@@ -567,7 +567,8 @@ def counter_pass(ctx) -> int:
     for _ in range(3):
         h = l1.forward(x)
         l2.forward(h)
-        l1.backward(x, l2.backward(h, dy))
+        l2.backward(h, dy, below=l1)
+        l1.backward(x, None)
     ctx.sync()
     B, C, H, W, OC = 32, 64, 56, 56, 128
     xi, w, bias = ctx.to_device(uniform(rng, (B, C, H, W))), ctx.to_device(uniform(rng, (OC, 9 * C))), \
