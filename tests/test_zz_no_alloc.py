@@ -1,7 +1,8 @@
 """zn_hip_sgemm_noalloc against zn_hip_sgemm, through the C ABI.
 
-The no-allocation GEMM keeps split-K partial sums in the library's fixed
-64 MiB per-device scratch and never packs operands.  Two calls in a row, the
+The no-allocation GEMM keeps split-K partial sums (and the partial tiles of
+the workgroup-split tiles) in the library's fixed 64 MiB per-device scratch
+and never packs operands.  Two calls in a row, the
 second on a smaller problem, must match zn_hip_sgemm bit for bit wherever
 both split K alike, and the oracle within 1e-5*sqrt(K) everywhere; a policy
 split too large for the scratch runs unsplit, and a forced one is refused.
@@ -74,6 +75,30 @@ def test_noalloc_matches_sgemm_two_calls(ctx):
     np.testing.assert_array_equal(got, ref_c)
     assert_close(got, ref_gemm("nt", a, b_nt, m, n, k, c0=c0, accumulate=True), "nt", a, b_nt, m, n, k, c0=c0,
                  accumulate=True, what="noalloc accumulate")
+
+
+def test_noalloc_workgroup_split_tiles(ctx):
+    """Few tiles with deep K take the 32x32 tiles whose K is split over
+    workgroups too; their partial tiles go to the scratch here and to the
+    context's workspace in zn_hip_sgemm, with the same slices and the same
+    order.  Two calls in a row (the tile counters are back at zero after
+    each), then a smaller problem on the 16x16 tiles."""
+    rng = np.random.default_rng(78)
+    for m, n, k, bias in ((64, 64, 4096, False), (100, 70, 2000, True), (32, 96, 1600, False)):
+        a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+        bv = uniform(rng, (n,)) if bias else None
+        announce(f"noalloc workgroup split NN {m}x{n}x{k} bias {bias}")
+        for _ in range(2):
+            ref_c, got = run_both(ctx, "nn", m, n, k, a, b, bias=bv, act="tanh" if bias else "linear")
+            np.testing.assert_array_equal(got.view(np.uint32), ref_c.view(np.uint32))
+        assert_close(got, ref_gemm("nn", a, b, m, n, k, bias=bv, act="tanh" if bias else "linear"), "nn", a, b, m,
+                     n, k, bias=bv, act="tanh" if bias else "linear", what="noalloc workgroup split")
+    m, n, k = 256, 128, 784
+    a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+    announce("noalloc 16x16 tiles NN 256x128x784")
+    ref_c, got = run_both(ctx, "nn", m, n, k, a, b)
+    np.testing.assert_array_equal(got.view(np.uint32), ref_c.view(np.uint32))
+    assert_close(got, ref_gemm("nn", a, b, m, n, k), "nn", a, b, m, n, k, what="noalloc 16x16")
 
 
 def test_noalloc_unaligned_rows_are_not_packed(ctx):
