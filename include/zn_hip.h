@@ -183,9 +183,11 @@ int zn_hip_set_gemm_tile(zn_ctx *ctx, int tile);
 int zn_hip_set_gemm_splits(zn_ctx *ctx, int splits);
 /* Persistent-kernel override: -1 (the default) lets the policy choose, 0
  * never uses the persistent GEMM kernels, 1 uses them for every eligible
- * GEMM (unsplit, 16-byte staging, K > 0, a tile other than 32x32).  Results
- * are bit-identical either way.  A tuning and test hook with no reference
- * counterpart. */
+ * GEMM (unsplit, 16-byte staging, K > 0, a tile other than 32x32) without
+ * deferred stores, 2 the same with deferred stores wherever those apply
+ * (plain GEMMs on 128x128 tiles that all lie inside C, K > 48; the policy
+ * uses them too).  Results are bit-identical in every mode.  A tuning and
+ * test hook with no reference counterpart. */
 int zn_hip_set_gemm_persistent(zn_ctx *ctx, int mode);
 /* Intra-workgroup split-K override: -1 (the default) lets the policy choose
  * (problems of at most one 32x32 tile per CU, 64 <= K <= 4096), 0 never

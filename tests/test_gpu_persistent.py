@@ -5,7 +5,8 @@ pipeline running across tile boundaries; each output element still sums K in
 the same order, so results must be bit-identical to the plain kernels for
 every layout, tile, epilogue, accumulation and batch.  The plain kernels are
 checked against the oracle elsewhere; one case here is also checked against
-the oracle directly.
+the oracle directly.  The deferred-store kernels (zn_sgemmpd_*) are held to
+the same bar.
 """
 from __future__ import annotations
 
@@ -79,6 +80,51 @@ def test_persistent_bit_identical(ctx, layout, m, n, k, batch, tile):
     (plain, pers), *_ = _both(ctx, layout, m, n, k, batch, tile, seed=m + n + k)
     assert np.isfinite(plain).all()
     np.testing.assert_array_equal(pers.view(np.uint32), plain.view(np.uint32))
+
+
+DEFER_CASES = [
+    # layout, m, n, k, batch: plain problems, 128x128 tiles all inside C, K >= 4 slices of 16
+    ("nt", 1024, 1024, 64, 16),    # the C5 QK^T shape, 16 heads (stores spread over all 4 slices)
+    ("nt", 256, 384, 1024, 3),     # long K: stores in the first 4 of 64 slices
+    ("nn", 512, 768, 96, 3),
+    ("tn", 384, 256, 80, 5),
+    ("nn", 128, 128, 49, 7),       # K one past 3 slices; one tile per problem
+    ("nt", 2048, 1024, 64, 1),
+]
+
+
+@pytest.mark.parametrize("layout,m,n,k,batch", DEFER_CASES)
+def test_persistent_deferred_stores_bit_identical(ctx, layout, m, n, k, batch):
+    """zn_sgemmpd_*: each finished tile is stored during the first four slices
+    of the workgroup's next tile.  Against the plain persistent kernel (mode 1)
+    and the plain kernels (mode 0): the same bits, the default policy (mode -1)
+    included, and a second run gives them again."""
+    rng = np.random.default_rng(m + 3 * n + k)
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a = uniform(rng, (batch,) + a_shape)
+    b = uniform(rng, (batch,) + b_shape)
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    outs = []
+    announce(f"deferred stores {layout} {m}x{n}x{k} batch {batch}")
+    ctx.set_gemm_tile("128x128")
+    for mode in (0, 1, 2, 2, -1):
+        ctx.set_gemm_persistent(mode)
+        dc = ctx.alloc(batch * m * n).fill(np.nan)
+        ctx.sgemm_strided_batched(layout, m, n, k, da, lda, a_shape[0] * a_shape[1], db, ldb,
+                                  b_shape[0] * b_shape[1], dc, n, m * n, batch)
+        outs.append(dc.download().reshape(batch, m, n))
+        dc.close()
+    ctx.set_gemm_tile("auto")
+    ctx.set_gemm_persistent(-1)
+    da.close()
+    db.close()
+    assert np.isfinite(outs[0]).all()
+    for got in outs[1:]:
+        np.testing.assert_array_equal(got.view(np.uint32), outs[0].view(np.uint32))
+    ref = ref_gemm(layout, a[-1], b[-1], m, n, k)
+    assert_close(outs[2][-1], ref, layout, a[-1], b[-1], m, n, k, what="deferred stores")
 
 
 @pytest.mark.parametrize("act", ["linear", "relu", "sigmoid", "tanh"])

@@ -232,7 +232,7 @@ def test_tuning_hooks_reject_bad_values(ctx):
     for bad in (1, 2, 5, 32, -2):
         with pytest.raises(InvalidArgumentError):
             ctx.set_gemm_wave_split(bad)
-    for bad in (2, -2):
+    for bad in (3, -2):
         with pytest.raises(InvalidArgumentError):
             ctx.set_gemm_persistent(bad)
     from zigneuron_amd import _lib

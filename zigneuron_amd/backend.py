@@ -224,7 +224,8 @@ class Context:
         check(_lib.load().zn_hip_set_gemm_wave_split(self.handle, int(waves)), "zn_hip_set_gemm_wave_split")
 
     def set_gemm_persistent(self, mode: int = -1) -> None:
-        """-1: the policy decides; 0: never; 1: every eligible GEMM runs on the persistent kernels."""
+        """-1: the policy decides; 0: never; 1: every eligible GEMM runs on the persistent kernels;
+        2: the same, with deferred stores wherever they apply (bit-identical in every mode)."""
         check(_lib.load().zn_hip_set_gemm_persistent(self.handle, int(mode)), "zn_hip_set_gemm_persistent")
 
     # --- GEMM on device pointers (asynchronous on the context stream)

@@ -1606,6 +1606,155 @@ __device__ __forceinline__ void gemm_persistent(const ZnGemmArgs &p, float *lds)
     }
 }
 
+// The persistent GEMM with deferred stores, for plain problems (no bias,
+// no accumulation, linear) whose tiles all lie inside C and span at least
+// kSpread = 4 K slices: a finished tile's results move to a second set of
+// registers and are stored during the first four slices of the workgroup's
+// next tile, an eighth after each of their k groups, instead of in one
+// burst at the end of the tile (C5's QK^T, K = 64: the bursts stalled the
+// next tiles' loads).  Each slice wait leaves the previous slice's stores in
+// flight: the only operations issued after a slice's DMA are those stores,
+// a fixed number (kPerSlice) for an interior tile.  The workgroup's last
+// tile is stored directly.  Each element sums K in the same order as
+// gemm_persistent, so the results are the same bits.
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
+__device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float *lds) {
+    constexpr int NT = WM * WN * kWave;
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int FM = WTM / 32, FN = WTN / 32;
+    constexpr bool kVec = !BKC && FN > 1;
+    constexpr int kItems = FM * 16;                 // (fm, r) row items of a wave tile
+    constexpr int kSpread = 4;                      // slices the stores of a tile are spread over
+    constexpr int kGroup = kItems / (2 * kSpread);  // items stored after each k group
+    constexpr int kPerSlice = 2 * kGroup * (kVec ? 1 : FN);  // store instructions issued in one slice
+    static_assert(kItems % (2 * kSpread) == 0 && kPerSlice < 64, "equal store groups within the vmcnt range");
+    static_assert(BK == 16, "two k groups per slice, one store group after each");
+    typedef DmaStage<BM, BK, NT, AK, 16> SA;
+    typedef DmaStage<BN, BK, NT, BKC, 16> SB;
+    float(*lds_a)[SA::kFloats] = reinterpret_cast<float(*)[SA::kFloats]>(lds);
+    float(*lds_b)[SB::kFloats] = reinterpret_cast<float(*)[SB::kFloats]>(lds + 2 * SA::kFloats);
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+    const int j = lane & 31, h = lane >> 5;
+    const int ntiles = p.tiles_m * p.tiles_n;
+    const int total = ntiles * p.batch;
+    const int step = gridDim.x;
+    int w = blockIdx.x;
+    if (w >= total) return;  // the host launches at most `total` workgroups
+
+    const int ktiles = (p.k + BK - 1) / BK;  // >= kSpread: the host sends shorter K to gemm_persistent
+    const int lda = (int)p.lda, ldb = (int)p.ldb;
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + 3) & ~3) : (p.k - 1) * lda + ((p.m + 3) & ~3)) * 4u;
+    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + 3) & ~3) : (p.k - 1) * ldb + ((p.n + 3) & ~3)) * 4u;
+
+    auto decode = [&](int wi, int &bz, int &m0, int &n0) {
+        bz = wi / ntiles;
+        const int pid = wi - bz * ntiles;
+        const int tm = pid / p.tiles_n;
+        m0 = tm * BM;
+        n0 = (pid - tm * p.tiles_n) * BN;
+    };
+    auto issue = [&](int bz, int m0, int n0, int k0, int st) {
+        SA::issue(make_rsrc(p.a + (int64_t)bz * p.stride_a, a_bytes), lds_a[st], lda, m0, k0, p.m, p.k, wave, lane);
+        SB::issue(make_rsrc(p.b + (int64_t)bz * p.stride_b, b_bytes), lds_b[st], ldb, n0, k0, p.n, p.k, wave, lane);
+    };
+    // non-temporal stores of row items [i0, i1) of v, a tile at (bz, m0, n0)
+    auto store_items = [&](const zn_f32x16(&v)[FM][FN], int bz, int m0, int n0, int i0, int i1) {
+        float *gc = p.c + (int64_t)bz * p.stride_c;
+#pragma unroll
+        for (int it = 0; it < kItems; ++it) {
+            if (it < i0 || it >= i1) continue;
+            const int fm = it >> 4, r = it & 15;
+            const int bi = 8 * (r >> 2) + 4 * h + (r & 3);
+            const int row = m0 + wm0 + (AK ? 32 * fm + bi : FM * bi + fm);
+            float *crow = gc + (int64_t)row * p.ldc;
+            if constexpr (kVec) {
+                typedef typename FVec<FN>::type VT;
+                VT x;
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) x[fn] = v[fm][fn][r];
+                __builtin_nontemporal_store(x, reinterpret_cast<VT *>(crow + n0 + wn0 + FN * j));
+            } else {
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn)
+                    __builtin_nontemporal_store(v[fm][fn][r], crow + n0 + wn0 + (BKC ? 32 * fn + j : FN * j + fn));
+            }
+        }
+    };
+
+    zn_f32x16 acc[FM][FN], pend[FM][FN];
+    int pbz = 0, pm0 = 0, pn0 = 0;
+    bool pending = false;      // pend holds a tile to store during this tile's first kSpread slices
+    bool stored_last = false;  // the previous slice issued stores after this slice's DMA
+    {
+        int bz, m0, n0;
+        decode(w, bz, m0, n0);
+        issue(bz, m0, n0, 0, 0);
+    }
+    int stage = 0;
+    for (;;) {
+        int bz, m0, n0;
+        decode(w, bz, m0, n0);
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+        const bool has_next = w + step < total;
+        for (int kt = 0; kt < ktiles; ++kt) {
+            if (stored_last)
+                vm_wait<kPerSlice>();  // slice kt has landed; the previous slice's stores may still be in flight
+            else
+                vm_wait<0>();
+            stored_last = pending && kt < kSpread;
+            __syncthreads();  // every wave's part of this stage is in LDS; the other stage is free
+            if (kt + 1 < ktiles) {
+                issue(bz, m0, n0, (kt + 1) * BK, stage ^ 1);
+            } else if (has_next) {  // the next tile's first slice
+                int bz2, m2, n2;
+                decode(w + step, bz2, m2, n2);
+                issue(bz2, m2, n2, 0, stage ^ 1);
+            }
+            const float *la = lds_a[stage];
+            const float *lb = lds_b[stage];
+#pragma unroll
+            for (int kg = 0; kg < BK; kg += 8) {
+                float fa[FM][4], fb[FN][4];
+                read_frags_dma<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
+                read_frags_dma<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn)
+                            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[fm][t], fb[fn][t], acc[fm][fn], 0, 0, 0);
+                if (pending && kt < kSpread) {  // an eighth of the previous tile after each k group
+                    const int q = kt * 2 + kg / 8;
+                    store_items(pend, pbz, pm0, pn0, q * kGroup, (q + 1) * kGroup);
+                }
+            }
+            stage ^= 1;
+        }
+        if (!has_next) {
+            store_items(acc, bz, m0, n0, 0, kItems);
+            break;
+        }
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) pend[fm][fn] = acc[fm][fn];
+        pbz = bz;
+        pm0 = m0;
+        pn0 = n0;
+        pending = true;
+        w += step;
+    }
+}
+
 }  // namespace
 
 #endif  // ZN_GEMM_CORE_H

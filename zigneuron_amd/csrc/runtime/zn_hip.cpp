@@ -165,6 +165,8 @@ struct zn_ctx {
     hipFunction_t gemmp[3][kNumTiles] = {};    // persistent plain GEMM, 16-byte staging [layout][tile] (not s)
     hipFunction_t gemmk[3][2][2] = {};         // intra-workgroup split-K, 32x32 tiles [layout][4 or 8 waves][16-byte]
     int gemmp_occ[3][kNumTiles] = {};          // its resident workgroups per CU
+    hipFunction_t gemmpd[3] = {};              // [layout]: persistent 128x128 with deferred stores
+    int gemmpd_occ[3] = {};
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -892,9 +894,19 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         const int64_t resident = cus * ctx->gemmp_occ[layout][tile];
         const int64_t total = ntiles * batch;
         if (total <= INT_MAX &&
-            (ctx->forced_persistent == 1 || (total > resident && k <= 8 * (int64_t)ts.bk))) {
+            (ctx->forced_persistent >= 1 || (total > resident && k <= 8 * (int64_t)ts.bk))) {
             ZnGemmArgs part = args;
             part.batch = (int32_t)batch;
+            // Deferred stores (gemm_persistent_defer) for plain problems whose
+            // 128x128 tiles all lie inside C, K of 4 slices or more: C5 QK^T
+            // 203 -> 184 us, 4096^2 x 64 NN 31.7 -> 26.4 us, 1024^2 x 80 TN
+            // x 32 68.0 -> 53.9 us, 1024^2 x 128 NT x 64 164.9 -> 157.0 us.
+            const bool defer = ctx->forced_persistent != 1 && tile == kTileL && !accumulate && !bias &&
+                               act == ZN_ACT_LINEAR && m % 128 == 0 && n % 128 == 0 && k > 48 &&
+                               (layout == ZN_LAYOUT_NT || args.vec_c);
+            if (defer)
+                return launch(ctx, ctx->gemmpd[layout],
+                              (unsigned)std::min(total, cus * (int64_t)ctx->gemmpd_occ[layout]), 1, 256, &part);
             return launch(ctx, ctx->gemmp[layout][tile], (unsigned)std::min(total, resident), 1,
                           (unsigned)ts.threads, &part);
         }
@@ -1530,6 +1542,15 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                 occ = 1;
             ctx->gemmp_occ[l][t] = occ;
         }
+    for (int l = 0; l < 3; ++l) {
+        char name[64];
+        std::snprintf(name, sizeof(name), "zn_sgemmpd_%s_l_v", kLayoutName[l]);
+        if (hipModuleGetFunction(&ctx->gemmpd[l], ctx->gemm_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
+        int occ = 0;
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, ctx->gemmpd[l], 256, 0) != hipSuccess || occ < 1)
+            occ = 1;
+        ctx->gemmpd_occ[l] = occ;
+    }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess ||
         hipModuleGetFunction(&ctx->dense_bwd[0], ctx->gemm_module, "zn_dense_bwd_m") != hipSuccess ||
         hipModuleGetFunction(&ctx->dense_bwd[1], ctx->gemm_module, "zn_dense_bwd_m_v") != hipSuccess ||
@@ -1812,7 +1833,7 @@ int zn_hip_set_gemm_wave_split(zn_ctx *ctx, int waves) {
 }
 
 int zn_hip_set_gemm_persistent(zn_ctx *ctx, int mode) {
-    if (!ctx || mode < -1 || mode > 1) return ZN_ERR_INVALID_ARG;
+    if (!ctx || mode < -1 || mode > 2) return ZN_ERR_INVALID_ARG;
     ctx->forced_persistent = mode;
     return ZN_OK;
 }
