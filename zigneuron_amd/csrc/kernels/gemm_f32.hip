@@ -122,20 +122,23 @@ ZN_GEMMQ_LAYOUTS(m, 2, 4)
     ZN_GEMMP_KERNEL(zn_sgemmp_tn_##TILE##_v, BM, BN, BK, WM, WN, false, false, MINB)
 
 ZN_GEMMP_TILE(x, 256, 128, 16, 4, 2, 1)
-ZN_GEMMP_TILE(l, 128, 128, 16, 2, 2, 4)
+ZN_GEMMP_TILE(l, 128, 128, 16, 2, 2, 3)  // 3 waves per SIMD: the TN form needs 145 VGPRs (at 4, it spilled)
 ZN_GEMMP_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_GEMMP_TILE(m, 64, 64, 32, 2, 2, 1)
 
 // Persistent plain GEMMs with deferred stores (gemm_persistent_defer) on
-// the 128x128 tile: zn_sgemmpd_<layout>_l_v.
-#define ZN_GEMMPD_KERNEL(NAME, AK, BKC)                                                          \
-    extern "C" __global__ __launch_bounds__(256, 2) void NAME(ZnGemmArgs p) {                   \
-        __shared__ __attribute__((aligned(1024))) float lds[2 * (128 + 128) * 16];               \
-        gemm_persistent_defer<128, 128, 16, 2, 2, AK, BKC>(p, lds);                              \
+// the 128x128 tile: zn_sgemmpd_<layout>_l_v.  (On 256x128 tiles they ran
+// at the same speed.)
+#define ZN_GEMMPD_KERNEL(NAME, BM, BN, WM, WN, AK, BKC)                                          \
+    extern "C" __global__ __launch_bounds__(WM *WN * 64, 2) void NAME(ZnGemmArgs p) {           \
+        __shared__ __attribute__((aligned(1024))) float lds[2 * (BM + BN) * 16];                 \
+        gemm_persistent_defer<BM, BN, 16, WM, WN, AK, BKC>(p, lds);                              \
     }
-ZN_GEMMPD_KERNEL(zn_sgemmpd_nn_l_v, true, false)
-ZN_GEMMPD_KERNEL(zn_sgemmpd_nt_l_v, true, true)
-ZN_GEMMPD_KERNEL(zn_sgemmpd_tn_l_v, false, false)
+#define ZN_GEMMPD_TILE(TILE, BM, BN, WM, WN)                                                     \
+    ZN_GEMMPD_KERNEL(zn_sgemmpd_nn_##TILE##_v, BM, BN, WM, WN, true, false)                      \
+    ZN_GEMMPD_KERNEL(zn_sgemmpd_nt_##TILE##_v, BM, BN, WM, WN, true, true)                       \
+    ZN_GEMMPD_KERNEL(zn_sgemmpd_tn_##TILE##_v, BM, BN, WM, WN, false, false)
+ZN_GEMMPD_TILE(l, 128, 128, 2, 2)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not
