@@ -90,13 +90,15 @@ DEFER_CASES = [
     ("tn", 384, 256, 80, 5),
     ("nn", 128, 128, 49, 7),       # K one past 3 slices; one tile per problem
     ("nt", 2048, 1024, 64, 1),
+    ("nn", 384, 640, 64, 3),       # 45 work items: uneven chunks over the 8 XCDs
 ]
 
 
 @pytest.mark.parametrize("layout,m,n,k,batch", DEFER_CASES)
 def test_persistent_deferred_stores_bit_identical(ctx, layout, m, n, k, batch):
     """zn_sgemmpd_*: each finished tile is stored during the first four slices
-    of the workgroup's next tile.  Against the plain persistent kernel (mode 1)
+    of the workgroup's next tile, each XCD's workgroups walking a contiguous
+    run of work items (8 or more workgroups).  Against the plain persistent kernel (mode 1)
     and the plain kernels (mode 0): the same bits, the default policy (mode -1)
     included, and a second run gives them again."""
     rng = np.random.default_rng(m + 3 * n + k)

@@ -1640,9 +1640,21 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
     const int j = lane & 31, h = lane >> 5;
     const int ntiles = p.tiles_m * p.tiles_n;
     const int total = ntiles * p.batch;
-    const int step = gridDim.x;
-    int w = blockIdx.x;
-    if (w >= total) return;  // the host launches at most `total` workgroups
+    // Work items walked by this workgroup: w, w + step, ... below `end`.
+    // xcd_remap 3 (at least 8 workgroups): the items are cut into 8 equal
+    // contiguous chunks and XCD x's workgroups (linear ids x, x + 8, ...,
+    // dispatched to XCD x) walk chunk x, so the tiles running at once on one
+    // XCD belong to the same few problems and share their operand panels in
+    // that XCD's L2.  Either walk covers every item once.
+    int w = blockIdx.x, step = gridDim.x, end = total;
+    if (p.xcd_remap == 3) {
+        const int x = (int)blockIdx.x & 7;
+        const int begin = (int)((int64_t)total * x / 8);
+        end = (int)((int64_t)total * (x + 1) / 8);
+        step = ((int)gridDim.x - x + 7) / 8;  // workgroups on XCD x
+        w = begin + ((int)blockIdx.x >> 3);
+    }
+    if (w >= end) return;  // the host launches at most `total` workgroups
 
     const int ktiles = (p.k + BK - 1) / BK;  // >= kSpread: the host sends shorter K to gemm_persistent
     const int lda = (int)p.lda, ldb = (int)p.ldb;
@@ -1703,7 +1715,7 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
             for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
-        const bool has_next = w + step < total;
+        const bool has_next = w + step < end;
         for (int kt = 0; kt < ktiles; ++kt) {
             if (stored_last)
                 vm_wait<kPerSlice>();  // slice kt has landed; the previous slice's stores may still be in flight

@@ -44,7 +44,8 @@ struct ZnGemmArgs {
     int32_t vec_c;             // 1: ldc and C allow vector stores
     int32_t group_m;           // tile rows per raster group
     int32_t xcd_remap;         // 1: gridDim.x % 8 == 0, give each XCD a contiguous tile range;
-                               // 2: split-K with gridDim.y == 1, each XCD a contiguous (slice, tile) range
+                               // 2: split-K with gridDim.y == 1, each XCD a contiguous (slice, tile) range;
+                               // 3: deferred-store persistent kernels, each XCD a contiguous run of work items
     // split-K: blockIdx.z = slice of K; splits > 1 writes raw partial sums to
     // ws[(problem * splits + slice)][m][n] and a reduce kernel finishes C.
     int32_t splits;
