@@ -167,6 +167,7 @@ struct zn_ctx {
     int gemmp_occ[3][kNumTiles] = {};          // its resident workgroups per CU
     hipFunction_t gemmpd[3] = {};              // [layout]: persistent 128x128 with deferred stores
     int gemmpd_occ[3] = {};
+    int gemmpd_threads[3] = {};                // its workgroup size (the kernel's launch bound)
     hipFunction_t splitk_reduce = nullptr;
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
@@ -891,29 +892,31 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // plain, 150 us persistent; 8192^3 0.6% slower persistent).
     if (!conv && splits == 1 && vec && k > 0 && kTiles[tile].persistent && ctx->forced_persistent != 0) {
         const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
-        const int64_t resident = cus * ctx->gemmp_occ[layout][tile];
         const int64_t total = ntiles * batch;
+        ZnGemmArgs part = args;
+        part.batch = (int32_t)batch;
+        // Deferred stores (gemm_persistent_defer) for plain problems whose
+        // 128x128 tiles all lie inside C, K of 4 slices or more, and more
+        // tiles than its own resident workgroups (two per CU): C5 QK^T
+        // 203 -> 184 us, 4096^2 x 64 NN 33.5 -> 26.4 us (plain kernels: its
+        // 1024 tiles fit the plain persistent kernel's residency), 1024^2 x
+        // 80 TN x 32 68.0 -> 53.9 us, 1024^2 x 128 NT x 64 164.9 -> 157.0 us.
+        const bool defer_ok = ctx->forced_persistent != 1 && tile == kTileL && !accumulate && !bias &&
+                              act == ZN_ACT_LINEAR && m % 128 == 0 && n % 128 == 0 && k > 48 &&
+                              (layout == ZN_LAYOUT_NT || args.vec_c) && total <= INT_MAX;
+        const int64_t resident_d = cus * (int64_t)ctx->gemmpd_occ[layout];
+        if (defer_ok && (ctx->forced_persistent == 2 || (total > resident_d && k <= 8 * (int64_t)ts.bk))) {
+            const int64_t grid = std::min(total, resident_d);
+            // each XCD walks a contiguous run of items: C5 QK^T fetched 302 MB
+            // per launch, 68 MB with the remap (Q and K are 64 MB), 2% faster
+            if (grid >= 8) part.xcd_remap = 3;
+            return launch(ctx, ctx->gemmpd[layout], (unsigned)grid, 1, (unsigned)ctx->gemmpd_threads[layout], &part);
+        }
+        const int64_t resident = cus * ctx->gemmp_occ[layout][tile];
         if (total <= INT_MAX &&
-            (ctx->forced_persistent >= 1 || (total > resident && k <= 8 * (int64_t)ts.bk))) {
-            ZnGemmArgs part = args;
-            part.batch = (int32_t)batch;
-            // Deferred stores (gemm_persistent_defer) for plain problems whose
-            // 128x128 tiles all lie inside C, K of 4 slices or more: C5 QK^T
-            // 203 -> 184 us, 4096^2 x 64 NN 31.7 -> 26.4 us, 1024^2 x 80 TN
-            // x 32 68.0 -> 53.9 us, 1024^2 x 128 NT x 64 164.9 -> 157.0 us.
-            const bool defer = ctx->forced_persistent != 1 && tile == kTileL && !accumulate && !bias &&
-                               act == ZN_ACT_LINEAR && m % 128 == 0 && n % 128 == 0 && k > 48 &&
-                               (layout == ZN_LAYOUT_NT || args.vec_c);
-            if (defer) {
-                const int64_t grid = std::min(total, cus * (int64_t)ctx->gemmpd_occ[layout]);
-                // each XCD walks a contiguous run of items: C5 QK^T fetched 302 MB
-                // per launch, 68 MB with the remap (Q and K are 64 MB), 2% faster
-                if (grid >= 8) part.xcd_remap = 3;
-                return launch(ctx, ctx->gemmpd[layout], (unsigned)grid, 1, 256, &part);
-            }
+            (ctx->forced_persistent >= 1 || (total > resident && k <= 8 * (int64_t)ts.bk)))
             return launch(ctx, ctx->gemmp[layout][tile], (unsigned)std::min(total, resident), 1,
                           (unsigned)ts.threads, &part);
-        }
     }
     for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int64_t nb = batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY;
@@ -1550,9 +1553,14 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
         char name[64];
         std::snprintf(name, sizeof(name), "zn_sgemmpd_%s_l_v", kLayoutName[l]);
         if (hipModuleGetFunction(&ctx->gemmpd[l], ctx->gemm_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
-        int occ = 0;
-        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, ctx->gemmpd[l], 256, 0) != hipSuccess || occ < 1)
+        int threads = 0, occ = 0;
+        if (hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, ctx->gemmpd[l]) != hipSuccess ||
+            threads < 64)
+            return bail(ZN_ERR_SYMBOL);
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, ctx->gemmpd[l], threads, 0) != hipSuccess ||
+            occ < 1)
             occ = 1;
+        ctx->gemmpd_threads[l] = threads;
         ctx->gemmpd_occ[l] = occ;
     }
     if (hipModuleGetFunction(&ctx->splitk_reduce, ctx->gemm_module, "zn_splitk_reduce") != hipSuccess ||
