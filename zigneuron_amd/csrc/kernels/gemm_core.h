@@ -879,8 +879,67 @@ __device__ __forceinline__ void gemm_tile_pinned(const ZnGemmArgs &p, int wg = -
     if constexpr (NHWC) cln = SN::lane_setup(p.conv, n0, p.n, wave, lane);
     typename SNW::Lane clnw{};
     if constexpr (NHWCW) clnw = SNW::lane_setup(p.conv, n0, p.n, lane);
+    // Plain 16-byte operands: each lane's DMA byte offsets at k = kbeg are
+    // computed once per tile, masked on M and N; slice s adds s * inc, and K
+    // is masked only in a partial last slice (an out-of-range offset plus
+    // s * inc stays past the buffer's end, which is below 2^31 bytes).
+    constexpr bool PRE = G == kGNone && WA == 16 && WB == 16;
+    constexpr int LA = SA::kPerWave, LB = SB::kPerWave;
+    uint32_t offa[LA], offb[LB];
+    const uint32_t inca = (uint32_t)(AK ? BK : BK * lda) * 4u, incb = (uint32_t)(BKC ? BK : BK * ldb) * 4u;
+    auto chunk = [&](int j, int kwaves, int per_inst) { return (j * kwaves + wave) * per_inst + 4 * lane; };
+    if constexpr (PRE) {
+#pragma unroll
+        for (int j = 0; j < LA; ++j) {
+            const int q = chunk(j, SA::kWaves, SA::kPerInst);
+            const int outer = AK ? m0 + q / BK : kbeg + q / BM;
+            const int inner = AK ? kbeg + 4 * (((q % BK) / 4) ^ SA::swz(q / BK)) : m0 + q % BM;
+            offa[j] = (AK ? outer < p.m : inner < p.m) ? (uint32_t)(outer * lda + inner) * 4u : kOutOfRange;
+        }
+#pragma unroll
+        for (int j = 0; j < LB; ++j) {
+            const int q = chunk(j, SB::kWaves, SB::kPerInst);
+            const int outer = BKC ? n0 + q / BK : kbeg + q / BN;
+            const int inner = BKC ? kbeg + 4 * (((q % BK) / 4) ^ SB::swz(q / BK)) : n0 + q % BN;
+            offb[j] = (BKC ? outer < p.n : inner < p.n) ? (uint32_t)(outer * ldb + inner) * 4u : kOutOfRange;
+        }
+    }
+    const uint32_t lds_a0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)&lds_a[0][0]);
+    const uint32_t lds_b0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)&lds_b[0][0]);
     auto issue = [&](int s, int st) {
         const int k0 = kbeg + s * BK;
+        if constexpr (PRE) {
+            const bool partial = k0 + BK > kend;
+#pragma unroll
+            for (int j = 0; j < LA; ++j) {
+                uint32_t off = offa[j] + (uint32_t)s * inca;
+                if (partial) {
+                    const int q = chunk(j, SA::kWaves, SA::kPerInst);
+                    const int kk = AK ? k0 + 4 * (((q % BK) / 4) ^ SA::swz(q / BK)) : k0 + q / BM;
+                    if (kk >= kend) off = kOutOfRange;
+                }
+                const uint32_t dst = lds_a0 + (uint32_t)(st * SA::kFloats + (j * SA::kWaves + wave) * SA::kPerInst) * 4u;
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                             :
+                             : "s"(dst), "v"(off), "s"(ra)
+                             : "memory");
+            }
+#pragma unroll
+            for (int j = 0; j < LB; ++j) {
+                uint32_t off = offb[j] + (uint32_t)s * incb;
+                if (partial) {
+                    const int q = chunk(j, SB::kWaves, SB::kPerInst);
+                    const int kk = BKC ? k0 + 4 * (((q % BK) / 4) ^ SB::swz(q / BK)) : k0 + q / BN;
+                    if (kk >= kend) off = kOutOfRange;
+                }
+                const uint32_t dst = lds_b0 + (uint32_t)(st * SB::kFloats + (j * SB::kWaves + wave) * SB::kPerInst) * 4u;
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                             :
+                             : "s"(dst), "v"(off), "s"(rb)
+                             : "memory");
+            }
+            return;
+        }
         SA::issue(ra, lds_a[st], lda, m0, k0, p.m, kend, wave, lane);
         if constexpr (NHWC)
             SN::issue(rb, lds_b[st], p.conv, cln, k0, kend, wave, lane);
