@@ -817,6 +817,24 @@ __device__ __forceinline__ void vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Wait until at most `ahead` slices' loads (of kSliceLoads instructions
+// each) are still in flight: vmcnt takes an immediate, so one branch per
+// possible count.
+template <int kSliceLoads, int NS>
+__device__ __forceinline__ void vm_wait_slices(int ahead) {
+    static_assert((NS - 1) * kSliceLoads < 64, "6-bit vmcnt");
+    switch (ahead) {
+    case 0: vm_wait<0>(); break;
+    case 1: vm_wait<kSliceLoads>(); break;
+    case 2: if constexpr (NS > 2) vm_wait<2 * kSliceLoads>(); break;
+    case 3: if constexpr (NS > 3) vm_wait<3 * kSliceLoads>(); break;
+    case 4: if constexpr (NS > 4) vm_wait<4 * kSliceLoads>(); break;
+    case 5: if constexpr (NS > 5) vm_wait<5 * kSliceLoads>(); break;
+    case 6: if constexpr (NS > 6) vm_wait<6 * kSliceLoads>(); break;
+    default: if constexpr (NS > 7) vm_wait<7 * kSliceLoads>(); break;
+    }
+}
+
 // The plain GEMM main loop with a fixed instruction schedule, for problems
 // of about one round of tiles, where each SIMD holds one or two waves and
 // every stall of a wave idles its matrix core.  Three LDS stages; slice
@@ -1004,53 +1022,51 @@ __device__ __forceinline__ void gemm_tile_pinned(const ZnGemmArgs &p, int wg = -
     store_tile_fast<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
 }
 
-// The main loop of the 256x256 tile (8 waves of 128x64, BK 16, 16-byte DMA
-// only), for problems of one or more full rounds of such tiles.  Like
-// gemm_tile_pinned it keeps three LDS stages and one barrier per slice, in
-// the middle of the slice, but it is scheduled for the one workgroup per CU
-// (two waves per SIMD, both held by the same barrier) that this tile allows:
-//  * the LDS reads of the next k group are issued one at a time between the
+// The main loop of the 256x256 tile (8 waves of 128x64, BK 16, 16-byte rows
+// only), for problems of one or more full rounds of such tiles: one
+// workgroup per CU, two waves per SIMD, both held by the same barrier.
+//  * Operands are staged through registers, not LDS DMA: during k group 1
+//    of slice kt every wave reads its share of slice kt + 2 (four 16-byte
+//    buffer loads, into 16 registers; lanes out of range read zeros), and
+//    during k group 0 of slice kt + 1 writes it into LDS, before the barrier
+//    after which it is read.  Two LDS stages suffice: slice kt + 1 goes into
+//    slice kt - 1's stage, which no wave has read since the previous
+//    barrier.  MI355X, 8192^3, against the same loop fed by LDS DMA (three
+//    stages, one wave per SIMD issuing a slice as one burst): NN 146.0 ->
+//    149.7, NT 147.2 -> 149.8, TN 144.2 -> 150.5 TFLOP/s.  With its DMA
+//    removed the DMA loop ran at 151.5 (NN), so the DMA cost 3.7%; neither
+//    its latency (a fourth stage lost 1.4%) nor the barrier (removed: no
+//    change) was the cause.  Loading during k group 0 as well was 1% slower,
+//    and one loading wave per SIMD with twice the share 30% slower.
+//  * The LDS reads of the next k group are issued one at a time between the
 //    MFMAs of the current one, rather than as a burst before them.  A burst
 //    of a workgroup's 8 waves filled the CU's LDS command queue, and a wave
 //    whose read cannot issue stalls its later MFMAs (SQ_LDS_CMD_FIFO_FULL:
 //    2e7 -> 0 cycles; 8192^3 NN on 4 waves of 128x128: 137.5 -> 141.4
-//    TFLOP/s);
-//  * half of the waves (one per SIMD) issue all of a slice's DMA, as one
-//    burst at the start of the slice, so that while a burst waits on the
-//    texture unit's queue the other wave of each SIMD keeps its MFMAs going
-//    (spreading the DMA over the MFMAs was 2-3% slower);
-//  * each lane's DMA offsets are computed once per tile (masked on M and N;
-//    K is masked only in a partial last slice), so a slice's DMA is a few
-//    instructions per load.
-// The slice barrier: slice kt + 1's DMA (issued one slice earlier) has
-// landed, every wave has read slice kt - 1's stage for the last time (its
-// reads of group 1 happen before the barrier of iteration kt - 1), so after
-// the barrier the next slice's first group is read while group 1 of slice kt
-// is multiplied.  Each element sums K in the same order as the other tiles,
-// so results are bit-identical to them.  MI355X, 8192^3 NN: 145.4 TFLOP/s
-// against 141.7 for the 256x128 two-stage loop in the same run; 4096^3:
-// 133.7 against 125.5.
+//    TFLOP/s).  The loads and LDS writes take the MFMA runs after the reads.
+//  * Each lane's load offsets are computed once per tile (masked on M and
+//    N); slice s adds s times an increment, and a load whose k lies at or
+//    beyond the end of K reads zeros, without branches.
+// Each element sums K in the same order as the other tiles, so results are
+// bit-identical to them.
 template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
 __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
-    constexpr int R = 3;
     static_assert(BK == 16, "two k groups per slice");
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    constexpr int NTL = NT / 2;  // the DMA-issuing waves
-    typedef DmaStage<BM, BK, NTL, AK, 16> SA;
-    typedef DmaStage<BN, BK, NTL, BKC, 16> SB;
-    constexpr int LA = SA::kPerWave, LB = SB::kPerWave, L = LA + LB;  // DMA per slice and loading wave
+    typedef DmaStage<BM, BK, NT, AK, 16> SA;  // the LDS layout of the DMA loops
+    typedef DmaStage<BN, BK, NT, BKC, 16> SB;
+    constexpr int LA = SA::kPerWave, LB = SB::kPerWave, L = LA + LB;  // 16-byte loads per slice and wave
     constexpr int RA = AK ? FM : 4, RB = BKC ? FN : 4, NR = RA + RB;  // LDS reads per k group
-    static_assert(NR <= 4 * FM, "one read after each (t, fm) MFMA run at most");
-    __shared__ __attribute__((aligned(1024))) float lds_a[R][SA::kFloats];
-    __shared__ __attribute__((aligned(1024))) float lds_b[R][SB::kFloats];
+    static_assert(NR + L <= 4 * FM, "one read, load or write after each (t, fm) MFMA run");
+    __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
+    __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
-    const bool loader = wave < NTL / kWave;
     int tm, tn, slice;
     tile_coords(p, tm, tn, slice, wg);
     const int m0 = tm * BM, n0 = tn * BN;
@@ -1064,59 +1080,42 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + bz * p.stride_a, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + bz * p.stride_b, b_bytes);
 
-    // This lane's DMA chunks (LDS float p .. p + 3 of instruction j) at k = kbeg,
-    // as byte offsets masked on M and N; slice s adds s * inc.
+    // This lane's loads at k = kbeg, as byte offsets masked on M and N, and
+    // the k offset of each within a slice: slice s adds s * inc, and a load
+    // whose k falls at or beyond kend reads zeros.  No branches: the loads
+    // past the last slice read zeros into registers nobody writes out.
     auto chunk = [&](int j, int kwaves, int per_inst) { return (j * kwaves + wave) * per_inst + 4 * lane; };
-    uint32_t offa[LA], offb[LB];
-    const uint32_t inca = (uint32_t)(AK ? BK : BK * lda) * 4u, incb = (uint32_t)(BKC ? BK : BK * ldb) * 4u;
+    uint32_t off0[L], inc[L];
+    int kq[L];
 #pragma unroll
     for (int j = 0; j < LA; ++j) {
         const int q = chunk(j, SA::kWaves, SA::kPerInst);
+        kq[j] = AK ? 4 * (((q % BK) / 4) ^ SA::swz(q / BK)) : q / BM;
         const int outer = AK ? m0 + q / BK : kbeg + q / BM;
-        const int inner = AK ? kbeg + 4 * (((q % BK) / 4) ^ SA::swz(q / BK)) : m0 + q % BM;
-        offa[j] = (AK ? outer < p.m : inner < p.m) ? (uint32_t)(outer * lda + inner) * 4u : kOutOfRange;
+        const int inner = AK ? kbeg + kq[j] : m0 + q % BM;
+        off0[j] = (AK ? outer < p.m : inner < p.m) ? (uint32_t)(outer * lda + inner) * 4u : kOutOfRange;
+        inc[j] = (uint32_t)(AK ? BK : BK * lda) * 4u;
     }
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
         const int q = chunk(j, SB::kWaves, SB::kPerInst);
+        kq[LA + j] = BKC ? 4 * (((q % BK) / 4) ^ SB::swz(q / BK)) : q / BN;
         const int outer = BKC ? n0 + q / BK : kbeg + q / BN;
-        const int inner = BKC ? kbeg + 4 * (((q % BK) / 4) ^ SB::swz(q / BK)) : n0 + q % BN;
-        offb[j] = (BKC ? outer < p.n : inner < p.n) ? (uint32_t)(outer * ldb + inner) * 4u : kOutOfRange;
+        const int inner = BKC ? kbeg + kq[LA + j] : n0 + q % BN;
+        off0[LA + j] = (BKC ? outer < p.n : inner < p.n) ? (uint32_t)(outer * ldb + inner) * 4u : kOutOfRange;
+        inc[LA + j] = (uint32_t)(BKC ? BK : BK * ldb) * 4u;
     }
-    const uint32_t lds_a0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)&lds_a[0][0]);
-    const uint32_t lds_b0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)&lds_b[0][0]);
-    // The DMA of slice s into stage st (loading waves only).
-    auto dma = [&](int s, int st) {
-        const int k0 = kbeg + s * BK;
-        const bool partial = k0 + BK > kend;
-#pragma unroll
-        for (int j = 0; j < LA; ++j) {
-            uint32_t off = offa[j] + (uint32_t)s * inca;
-            if (partial) {
-                const int q = chunk(j, SA::kWaves, SA::kPerInst);
-                const int kk = AK ? k0 + 4 * (((q % BK) / 4) ^ SA::swz(q / BK)) : k0 + q / BM;
-                if (kk >= kend) off = kOutOfRange;
-            }
-            const uint32_t dst = lds_a0 + (uint32_t)(st * SA::kFloats + (j * SA::kWaves + wave) * SA::kPerInst) * 4u;
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(dst), "v"(off), "s"(ra)
-                         : "memory");
-        }
-#pragma unroll
-        for (int j = 0; j < LB; ++j) {
-            uint32_t off = offb[j] + (uint32_t)s * incb;
-            if (partial) {
-                const int q = chunk(j, SB::kWaves, SB::kPerInst);
-                const int kk = BKC ? k0 + 4 * (((q % BK) / 4) ^ SB::swz(q / BK)) : k0 + q / BN;
-                if (kk >= kend) off = kOutOfRange;
-            }
-            const uint32_t dst = lds_b0 + (uint32_t)(st * SB::kFloats + (j * SB::kWaves + wave) * SB::kPerInst) * 4u;
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(dst), "v"(off), "s"(rb)
-                         : "memory");
-        }
+    const int klen = kend - kbeg;
+    zn_f32x4 g[L];  // this wave's share of one slice
+    auto load = [&](int s, int j) {
+        const uint32_t off = s * BK + kq[j] < klen && off0[j] != kOutOfRange ? off0[j] + (uint32_t)s * inc[j] : kOutOfRange;
+        g[j] = __builtin_bit_cast(zn_f32x4, __builtin_amdgcn_raw_buffer_load_b128(j < LA ? ra : rb, off, 0, 0));
+    };
+    auto write = [&](int st, int j) {
+        if (j < LA)
+            *reinterpret_cast<zn_f32x4 *>(&lds_a[st][chunk(j, SA::kWaves, SA::kPerInst)]) = g[j];
+        else
+            *reinterpret_cast<zn_f32x4 *>(&lds_b[st][chunk(j - LA, SB::kWaves, SB::kPerInst)]) = g[j];
     };
 
     zn_f32x16 acc[FM][FN];
@@ -1127,10 +1126,11 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
     float fa[2][FM][4], fb[2][FN][4];
-    // One k group from fragments (xa, xb); after MFMA run q (one (t, fm) pair,
-    // FN MFMAs), read fragment q of the next group from stage rst at k rkg.
+    // One k group from fragments (xa, xb); after MFMA run q (one (t, fm)
+    // pair, FN MFMAs): q < NR reads fragment q of the next group from stage
+    // rst at k rkg; later runs call `extra(q - NR)` (a load or an LDS write).
     auto multiply = [&](const float(&xa)[FM][4], const float(&xb)[FN][4], int rst, int rkg, float(&da)[FM][4],
-                        float(&db)[FN][4]) {
+                        float(&db)[FN][4], auto &&extra) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1139,40 +1139,49 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
                 for (int fn = 0; fn < FN; ++fn)
                     acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[fm][t], xb[fn][t], acc[fm][fn], 0, 0, 0);
                 const int q = t * FM + fm;
+                __builtin_amdgcn_sched_barrier(0);
                 if (q < NR) {
-                    __builtin_amdgcn_sched_barrier(0);
                     if (q < RA)
                         read_frag_one<BM, BK, FM, AK>(lds_a[rst], wm0, rkg, lane, q, da);
                     else
                         read_frag_one<BN, BK, FN, BKC>(lds_b[rst], wn0, rkg, lane, q - RA, db);
-                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    extra(q - NR);
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
     };
+    // Slice kt in stage S = kt % 2: group 0 writes slice kt + 1 (in the
+    // registers since group 1 of slice kt - 1) into stage S ^ 1, the barrier,
+    // group 1 loads slice kt + 2 while reading slice kt + 1's group 0.
+    auto slice_step = [&](int kt, auto sc) {
+        constexpr int S = decltype(sc)::value;
+        auto wr = [&](int x) {
+            if (x < L) write(S ^ 1, x);
+        };
+        auto ld = [&](int x) {
+            if (x < L) load(kt + 2, x);
+        };
+        multiply(fa[0], fb[0], S, 8, fa[1], fb[1], wr);  // group 0; reads group 1
+        __syncthreads();  // slice kt + 1 is in LDS; every wave has read slice kt for the last time
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(fa[1], fb[1], S ^ 1, 0, fa[0], fb[0], ld);  // group 1; reads group 0 of slice kt + 1
+        __builtin_amdgcn_sched_barrier(0);
+    };
     if (ktiles > 0) {
-        if (loader) {
-            dma(0, 0);
-            if (ktiles > 1) dma(1, 1);
-        }
-        if (ktiles > 1) vm_wait<L>(); else vm_wait<0>();  // slice 0 is in; slice 1 may still be in flight
+#pragma unroll
+        for (int j = 0; j < L; ++j) load(0, j);
+#pragma unroll
+        for (int j = 0; j < L; ++j) write(0, j);
+#pragma unroll
+        for (int j = 0; j < L; ++j) load(1, j);
         __syncthreads();
         read_frags_dma<BM, BK, FM, AK>(lds_a[0], wm0, 0, lane, fa[0]);
         read_frags_dma<BN, BK, FN, BKC>(lds_b[0], wn0, 0, lane, fb[0]);
     }
-    int st = 0;
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int nst = st + 1 == R ? 0 : st + 1;
-        const int fst = nst + 1 == R ? 0 : nst + 1;  // slice kt - 1's stage, free since the last barrier
-        const bool refill = kt + 2 < ktiles;
-        if (loader && refill) dma(kt + 2, fst);
-        __builtin_amdgcn_sched_barrier(0);
-        multiply(fa[0], fb[0], st, 8, fa[1], fb[1]);  // group 0; reads group 1
-        if (refill) vm_wait<L>(); else vm_wait<0>();  // this wave's part of slice kt + 1 is in LDS
-        __syncthreads();  // every wave's is; every wave has read slice kt - 1 for the last time
-        __builtin_amdgcn_sched_barrier(0);
-        multiply(fa[1], fb[1], nst, 0, fa[0], fb[0]);  // group 1; reads group 0 of slice kt + 1
-        __builtin_amdgcn_sched_barrier(0);
-        st = nst;
+    for (int kt = 0; kt < ktiles; kt += 2) {
+        slice_step(kt, std::integral_constant<int, 0>());
+        if (kt + 1 < ktiles) slice_step(kt + 1, std::integral_constant<int, 1>());
     }
     store_tile_fast<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
 }
@@ -1410,24 +1419,6 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
     }
 
     ksplit_finish<BM, BN, KS, AK, BKC, ACT, XS>(p, lds, acc, bz, m0, n0, wave, lane, pid, split);
-}
-
-// Wait until at most `ahead` slices' loads (of kSliceLoads instructions
-// each) are still in flight: vmcnt takes an immediate, so one branch per
-// possible count.
-template <int kSliceLoads, int NS>
-__device__ __forceinline__ void vm_wait_slices(int ahead) {
-    static_assert((NS - 1) * kSliceLoads < 64, "6-bit vmcnt");
-    switch (ahead) {
-    case 0: vm_wait<0>(); break;
-    case 1: vm_wait<kSliceLoads>(); break;
-    case 2: if constexpr (NS > 2) vm_wait<2 * kSliceLoads>(); break;
-    case 3: if constexpr (NS > 3) vm_wait<3 * kSliceLoads>(); break;
-    case 4: if constexpr (NS > 4) vm_wait<4 * kSliceLoads>(); break;
-    case 5: if constexpr (NS > 5) vm_wait<5 * kSliceLoads>(); break;
-    case 6: if constexpr (NS > 6) vm_wait<6 * kSliceLoads>(); break;
-    default: if constexpr (NS > 7) vm_wait<7 * kSliceLoads>(); break;
-    }
 }
 
 // Intra-workgroup split-K on 16x16 tiles (v_mfma_f32_16x16x4f32), for

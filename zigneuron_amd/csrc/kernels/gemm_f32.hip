@@ -17,7 +17,8 @@
 //                                    six workgroups per CU)
 //   w = 256x256, 8 waves of 128x64   full rounds of large problems (BK 16,
 //                                    gemm_tile_wide, one workgroup per CU;
-//                                    16-byte staging only, no plain variant)
+//                                    16-byte loads staged through registers,
+//                                    no plain variant)
 // x, l, n and s run gemm_tile_dma's two-stage loop, m, r and h
 // gemm_tile_pinned's three-stage one.  The _v variants stage operands with
 // 16-byte loads straight into LDS (aligned rows, contiguous extents a
