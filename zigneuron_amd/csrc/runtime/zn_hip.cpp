@@ -153,6 +153,7 @@ struct zn_ctx {
     hipModule_t attn_module = nullptr;
     hipFunction_t attn[3][2] = {};             // fused attention [head dim 32/64/128][16-byte I/O]
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
+    int gemm_threads[3][kNumTiles][2] = {};    // their workgroup sizes (the kernels' launch bounds)
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
@@ -926,7 +927,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         part.a = a ? a + b0 * stride_a : nullptr;
         part.b = b ? b + b0 * stride_b : nullptr;
         part.c = c + b0 * stride_c;
-        rc = launch(ctx, f, (unsigned)ntiles, (unsigned)nb, (unsigned)ts.threads, &part, (unsigned)splits);
+        const int threads = conv ? ts.threads : ctx->gemm_threads[layout][tile][vec ? 1 : 0];
+        rc = launch(ctx, f, (unsigned)ntiles, (unsigned)nb, (unsigned)threads, &part, (unsigned)splits);
         if (rc) return rc;
         if (splits > 1) {
             ZnReduceArgs r;
@@ -1490,6 +1492,12 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
                               v ? "_v" : "");
                 if (hipModuleGetFunction(&ctx->gemm[l][t][v], ctx->gemm_module, name) != hipSuccess)
                     return bail(ZN_ERR_SYMBOL);
+                int threads = 0;
+                if (hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, ctx->gemm[l][t][v]) !=
+                        hipSuccess ||
+                    threads < 64 || threads > 1024)
+                    return bail(ZN_ERR_SYMBOL);
+                ctx->gemm_threads[l][t][v] = threads;
             }
     for (int t = 0; t < kNumTiles; ++t)
         for (int v = 0; v < 2 && kTiles[t].conv; ++v)
