@@ -1060,7 +1060,10 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
     typedef DmaStage<BN, BK, NT, BKC, 16> SB;
     constexpr int LA = SA::kPerWave, LB = SB::kPerWave, L = LA + LB;  // 16-byte loads per slice and wave
     constexpr int RA = AK ? FM : 4, RB = BKC ? FN : 4, NR = RA + RB;  // LDS reads per k group
-    static_assert(NR + L <= 4 * FM, "one read, load or write after each (t, fm) MFMA run");
+    // the runs after which a load or LDS write goes: after the reads when
+    // there is room (the 256x256 tile), else the last L runs, after a read
+    constexpr int kX0 = NR + L <= 4 * FM ? NR : 4 * FM - L;
+    static_assert(NR <= 4 * FM && kX0 >= 0, "at most one read and one load or write after each (t, fm) MFMA run");
     __shared__ __attribute__((aligned(1024))) float lds_a[2][SA::kFloats];
     __shared__ __attribute__((aligned(1024))) float lds_b[2][SB::kFloats];
 
@@ -1128,7 +1131,8 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
     float fa[2][FM][4], fb[2][FN][4];
     // One k group from fragments (xa, xb); after MFMA run q (one (t, fm)
     // pair, FN MFMAs): q < NR reads fragment q of the next group from stage
-    // rst at k rkg; later runs call `extra(q - NR)` (a load or an LDS write).
+    // rst at k rkg, and q >= kX0 calls `extra(q - kX0)` (a load or an LDS
+    // write).
     auto multiply = [&](const float(&xa)[FM][4], const float(&xb)[FN][4], int rst, int rkg, float(&da)[FM][4],
                         float(&db)[FN][4], auto &&extra) {
 #pragma unroll
@@ -1145,9 +1149,8 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
                         read_frag_one<BM, BK, FM, AK>(lds_a[rst], wm0, rkg, lane, q, da);
                     else
                         read_frag_one<BN, BK, FN, BKC>(lds_b[rst], wn0, rkg, lane, q - RA, db);
-                } else {
-                    extra(q - NR);
                 }
+                if (q >= kX0) extra(q - kX0);
                 __builtin_amdgcn_sched_barrier(0);
             }
     };

@@ -11,18 +11,21 @@
 //   n = 128x64,  2 waves of 64x64    narrow N (attention P.V, N = 64)
 //   m = 64x64,   4 waves of 32x32    mid-size problems (BK 32, pinned loop)
 //   s = 32x32,   1 wave              small problems (BK 32)
-//   r = 128x128, 8 waves of 32x64    one round of tiles (BK 32, pinned loop,
-//                                    one workgroup per CU)
+//   r = 128x128, 8 waves             one round of tiles, one workgroup per
+//                                    CU (16-byte rows: 64x32 wave tiles,
+//                                    BK 16, gemm_tile_wide; 4-byte rows:
+//                                    32x64, BK 32, pinned loop)
 //   h = 64x64,   4 waves of 32x32    several rounds (BK 16, pinned loop,
 //                                    six workgroups per CU)
 //   w = 256x256, 8 waves of 128x64   full rounds of large problems (BK 16,
 //                                    gemm_tile_wide, one workgroup per CU;
 //                                    16-byte loads staged through registers,
 //                                    no plain variant)
-// x, l, n and s run gemm_tile_dma's two-stage loop, m, r and h
-// gemm_tile_pinned's three-stage one.  The _v variants stage operands with
-// 16-byte loads straight into LDS (aligned rows, contiguous extents a
-// multiple of 4); the plain ones with 4-byte loads straight into LDS.
+// x, l, n and s run gemm_tile_dma's two-stage loop, m, h and the plain r
+// gemm_tile_pinned's three-stage one, w and the 16-byte r gemm_tile_wide.
+// The _v variants load operands 16 bytes at a time (aligned rows, contiguous
+// extents a multiple of 4): straight into LDS, or through registers on
+// gemm_tile_wide; the plain ones 4 bytes at a time straight into LDS.
 #define ZN_GEMM_KERNEL(NAME, LOOP, BM, BN, BK, WM, WN, AK, BKC, VEC, MINB)                      \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, MINB) void NAME(ZnGemmArgs p) {        \
         LOOP<BM, BN, BK, WM, WN, AK, BKC, (VEC) ? 16 : 4, (VEC) ? 16 : 4>(p);                    \
@@ -42,7 +45,17 @@ ZN_GEMM_TILE(l, gemm_tile_dma, 128, 128, 16, 2, 2, 4)
 ZN_GEMM_TILE(n, gemm_tile_dma, 128, 64, 16, 2, 1, 1)
 ZN_GEMM_TILE(m, gemm_tile_pinned, 64, 64, 32, 2, 2, 1)
 ZN_GEMM_TILE(s, gemm_tile_dma, 32, 32, 32, 1, 1, 1)
-ZN_GEMM_TILE(r, gemm_tile_pinned, 128, 128, 32, 4, 2, 1)
+// r: 16-byte rows on gemm_tile_wide (8 waves of 64x32, BK 16, operands
+// staged through registers), 4-byte rows on gemm_tile_pinned (8 waves of
+// 32x64, BK 32); both keep the K order of the other tiles
+ZN_GEMM_LAYOUTS(r, gemm_tile_pinned, 128, 128, 32, 4, 2, 1, false, )
+#define ZN_GEMM_R_WIDE(LAYOUT, AK, BKC)                                                          \
+    extern "C" __global__ __launch_bounds__(512, 1) void zn_sgemm_##LAYOUT##_r_v(ZnGemmArgs p) { \
+        gemm_tile_wide<128, 128, 16, 2, 4, AK, BKC>(p);                                          \
+    }
+ZN_GEMM_R_WIDE(nn, true, false)
+ZN_GEMM_R_WIDE(nt, true, true)
+ZN_GEMM_R_WIDE(tn, false, false)
 ZN_GEMM_TILE(h, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
 
 #define ZN_GEMM_WIDE(LAYOUT, AK, BKC)                                                            \
