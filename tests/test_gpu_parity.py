@@ -496,6 +496,25 @@ def test_pinned_tiles_bit_identical(ctx, layout):
         ctx.set_gemm_tile("auto")
         ctx.set_gemm_splits(0)
 
+@pytest.mark.parametrize("layout,m,n,k", [("nn", 4096, 2048, 192), ("nt", 3840, 2048, 160), ("tn", 2048, 4096, 144)])
+def test_multi_round_128x128_policy(ctx, layout, m, n, k):
+    """Whole rounds of 128x128 tiles with 16-byte rows (two rounds, and 1.9
+    for NT) go to the register-staged 128x128 loop by the policy: the result
+    is bit-identical to the forced two-stage 128x128 kernel's and matches the
+    oracle."""
+    rng = np.random.default_rng(zlib.crc32(f"rounds-{layout}-{m}".encode()))
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    announce(f"multi-round 128x128 {layout} {m}x{n}x{k}")
+    auto = run_gemm(ctx, layout, a, b, m, n, k)
+    ctx.set_gemm_tile("128x128")
+    try:
+        two_stage = run_gemm(ctx, layout, a, b, m, n, k)
+    finally:
+        ctx.set_gemm_tile("auto")
+    assert np.array_equal(auto.view(np.uint32), two_stage.view(np.uint32))
+    assert_close(auto, ref_gemm(layout, a, b, m, n, k), layout, a, b, m, n, k, what="multi-round")
+
 
 @pytest.mark.parametrize("tile", TILES)
 def test_every_tile_strided_batched(ctx, tile):

@@ -483,8 +483,20 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t bat
         5 * tiles(kTileW) >= 4 * cdiv(tiles(kTileW), cus) * cus)
         return kTileW;
     // short K: a tile's epilogue outweighs its K walk, and the smaller l tile
-    // overlaps them better (C5 QK^T, K = 64: l 242 us, x 252 us, round-robin A/B)
-    if (k <= 256 && tiles(kTileL) >= 2 * cus && useful(kTileL)) return kTileL;
+    // overlaps them better (C5 QK^T, K = 64: l 242 us, x 252 us, round-robin
+    // A/B); up to K = 128 its persistent kernels take the problem
+    if (k <= 128 && tiles(kTileL) >= 2 * cus && useful(kTileL)) return kTileL;
+    // Whole rounds of 128x128 tiles (every round at least 85% full on
+    // average) on the register-staged 128x128 loop, one workgroup of 8 waves
+    // per CU: 4096x2048x1024 NN 140.3 -> 126.3 us (against 64x64), 8192x3072
+    // x 1024 390.7 -> 369.1 us and 6144x4096x1024 390.6 -> 368.8 us (against
+    // 256x128 and 128x128 on 4 waves), 4096x2048x256 49.3 -> 38.2 us,
+    // 3840x2048x1024 (1.9 rounds) 138.7 -> 126.4 us; 2.5 rounds stay on
+    // 64x64 (5120x2048x1024: 172.9 against 184.7 us).  16-byte rows only:
+    // 4-byte rows run the 128x128 tile on the pinned loop, kept to one round.
+    if (wide_ok && !gathered && tiles(kTileR) > cus && useful(kTileR) &&
+        20 * tiles(kTileR) >= 17 * cdiv(tiles(kTileR), cus) * cus)
+        return kTileR;
     if (tiles(kTileX) >= 2 * cus && useful(kTileX)) return kTileX;
     if (tiles(kTileL) >= (gathered ? 2 : 4) * cus && useful(kTileL)) return kTileL;
     // One round of 128x128 tiles (at least 85% of the CUs, counting K slices
