@@ -170,8 +170,17 @@ __device__ __forceinline__ void splitk_reduce_body(const ZnReduceArgs &p, int64_
         const float *src = p.ws + b * p.splits * mn + e;
         float *dst = p.c + b * p.stride_c + row * p.ldc + col;
         if (p.vec) {
+            // up to 8 slices' loads in flight at once, added in slice order
             zn_f32x4 s = *reinterpret_cast<const zn_f32x4 *>(src);
-            for (int z = 1; z < p.splits; ++z) s = s + *reinterpret_cast<const zn_f32x4 *>(src + z * mn);
+            for (int z0 = 1; z0 < p.splits; z0 += 8) {
+                zn_f32x4 x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (z0 + u < p.splits) x[u] = *reinterpret_cast<const zn_f32x4 *>(src + (z0 + u) * mn);
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (z0 + u < p.splits) s = s + x[u];
+            }
             zn_f32x4 v = s;
             if (p.accumulate) v = *reinterpret_cast<const zn_f32x4 *>(dst) + v;
 #pragma unroll
@@ -183,7 +192,15 @@ __device__ __forceinline__ void splitk_reduce_body(const ZnReduceArgs &p, int64_
             *reinterpret_cast<zn_f32x4 *>(dst) = v;
         } else {
             float s = src[0];
-            for (int z = 1; z < p.splits; ++z) s = s + src[z * mn];
+            for (int z0 = 1; z0 < p.splits; z0 += 8) {
+                float x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (z0 + u < p.splits) x[u] = src[(z0 + u) * mn];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (z0 + u < p.splits) s = s + x[u];
+            }
             float x = p.accumulate ? dst[0] + s : s;
             if (p.bias) x = x + p.bias[p.bias_rows ? row : col];
             dst[0] = zn_activate(x, p.act);
