@@ -101,4 +101,9 @@ ZN_CONVWN_TILE(x, gemm_tile_dma, 256, 128, 16, 4, 2, 1)
 ZN_CONVWN_TILE(l, gemm_tile_dma, 128, 128, 16, 2, 2, 4)
 ZN_CONVWN_TILE(n, gemm_tile_dma, 128, 64, 16, 2, 1, 1)
 ZN_CONVWN_TILE(m, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
+// 128x128 on the register-staged loop (16-byte grad_output rows only): one
+// round of tiles x K slices
+extern "C" __global__ __launch_bounds__(512, 1) void zn_convwn_tn_r_v(ZnGemmArgs p) {
+    gemm_tile_wide<128, 128, 16, 2, 4, false, false, kGNhwcW>(p);
+}
 ZN_CONVWN_TILE(s, gemm_tile_dma, 32, 32, 32, 1, 1, 1)

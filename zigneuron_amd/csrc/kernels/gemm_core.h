@@ -506,21 +506,28 @@ struct ConvNhwcWGatherStage {
         return l;
     }
 
+    // byte offset of this lane's chunk of load j (a wave-uniform k row pair)
+    // of the slice at k0, or kOutOfRange (padding, or k at or past kmax)
+    __device__ static __forceinline__ uint32_t offset(const ZnConvGeom &g, const Lane &ln, int k0, int kmax, int wave,
+                                                      int j) {
+        const int plane = g.channels * g.in_h * g.in_w;
+        const int row = j * kWaves + wave;  // wave-uniform
+        const int k = k0 + row * kRowsPerInst + ln.kl;
+        const int q = zn_udiv(k, g.ow_mul, g.ow_shift), ow = k - q * g.out_w;
+        const int b = zn_udiv(q, g.oh_mul, g.oh_shift), oh = q - b * g.out_h;
+        const int ohs = oh * g.stride_h, ows = ow * g.stride_w;
+        const int ih = ohs + ln.dh, iw = ows + ln.dw;
+        const bool ok = k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
+        const int src = b * plane + (ohs * g.in_w + ows) * g.channels + ln.tap_off;
+        return ok ? (uint32_t)src * 4u : kOutOfRange;
+    }
+
     __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, const ZnConvGeom &g,
                                                  const Lane &ln, int k0, int kmax, int wave) {
-        const int plane = g.channels * g.in_h * g.in_w;
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
-            const int row = j * kWaves + wave;  // wave-uniform
-            const int p0 = row * Layout::kPerInst;
-            const int k = k0 + row * kRowsPerInst + ln.kl;
-            const int q = zn_udiv(k, g.ow_mul, g.ow_shift), ow = k - q * g.out_w;
-            const int b = zn_udiv(q, g.oh_mul, g.oh_shift), oh = q - b * g.out_h;
-            const int ohs = oh * g.stride_h, ows = ow * g.stride_w;
-            const int ih = ohs + ln.dh, iw = ows + ln.dw;
-            const bool ok = k < kmax && (unsigned)ih < (unsigned)g.in_h && (unsigned)iw < (unsigned)g.in_w;
-            const int src = b * plane + (ohs * g.in_w + ows) * g.channels + ln.tap_off;
-            const uint32_t off = ok ? (uint32_t)src * 4u : kOutOfRange;
+            const int p0 = (j * kWaves + wave) * Layout::kPerInst;
+            const uint32_t off = offset(g, ln, k0, kmax, wave, j);
             const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
             asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                          :
@@ -1049,12 +1056,15 @@ __device__ __forceinline__ void gemm_tile_pinned(const ZnGemmArgs &p, int wg = -
 //    beyond the end of K reads zeros, without branches.
 // Each element sums K in the same order as the other tiles, so results are
 // bit-identical to them.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int G = kGNone>
 __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
     static_assert(BK == 16, "two k groups per slice");
+    constexpr bool NHWCW = G == kGNhwcW;  // B gathered from an NHWC batch (convolution weight gradient)
+    static_assert(G == kGNone || (NHWCW && !BKC), "the NHWC weight-gradient gather only, X-contiguous");
+    typedef ConvNhwcWGatherStage<BN, BK, NT> SNW;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
     typedef DmaStage<BM, BK, NT, AK, 16> SA;  // the LDS layout of the DMA loops
     typedef DmaStage<BN, BK, NT, BKC, 16> SB;
@@ -1079,7 +1089,8 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
     const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + 3) & ~3) : (p.k - 1) * lda + ((p.m + 3) & ~3)) * 4u;
-    const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + 3) & ~3) : (p.k - 1) * ldb + ((p.n + 3) & ~3)) * 4u;
+    const uint32_t b_bytes = NHWCW ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
+                                   : (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + 3) & ~3) : (p.k - 1) * ldb + ((p.n + 3) & ~3)) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + bz * p.stride_a, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + bz * p.stride_b, b_bytes);
 
@@ -1109,9 +1120,12 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
         inc[LA + j] = (uint32_t)(BKC ? BK : BK * ldb) * 4u;
     }
     const int klen = kend - kbeg;
+    typename SNW::Lane clnw{};
+    if constexpr (NHWCW) clnw = SNW::lane_setup(p.conv, n0, p.n, lane);
     zn_f32x4 g[L];  // this wave's share of one slice
     auto load = [&](int s, int j) {
-        const uint32_t off = s * BK + kq[j] < klen && off0[j] != kOutOfRange ? off0[j] + (uint32_t)s * inc[j] : kOutOfRange;
+        uint32_t off = s * BK + kq[j] < klen && off0[j] != kOutOfRange ? off0[j] + (uint32_t)s * inc[j] : kOutOfRange;
+        if (NHWCW && j >= LA) off = SNW::offset(p.conv, clnw, kbeg + s * BK, kend, wave, j - LA);
         g[j] = __builtin_bit_cast(zn_f32x4, __builtin_amdgcn_raw_buffer_load_b128(j < LA ? ra : rb, off, 0, 0));
     };
     auto write = [&](int st, int j) {

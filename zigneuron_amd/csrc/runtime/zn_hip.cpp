@@ -568,6 +568,8 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+int64_t cus_now(const zn_ctx *ctx) { return ctx->info.compute_units > 0 ? ctx->info.compute_units : 256; }
+
 // Multiplier and shift for x / d, 0 <= x < 2^31, d >= 1: shift = ceil(log2 d),
 // mul = ceil(2^(31 + shift) / d), which is below 2^32 (Granlund & Montgomery
 // 1994, Theorem 4.2 with N = 31).
@@ -649,8 +651,16 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // 4-byte kernel need it; packed copies are not made for them)
     const bool native_vec = !conv && aligned16(a) && aligned16(b) && lda % 4 == 0 && ldb % 4 == 0 && stride_a % 4 == 0 &&
                             stride_b % 4 == 0 && a_row % 4 == 0 && b_row % 4 == 0;
+    // The NHWC weight gradient (a long K over every output pixel, few tiles)
+    // runs as one round of 128x128 tiles x K slices on the register-staged
+    // loop when grad_output's rows are whole float4s: up to 64 slices, one
+    // workgroup per CU (MI355X, C5 128 x 576 x 100352: the GEMM 175 -> 155
+    // us against 64x64 tiles in 64 slices, the whole backward 334 -> 323 us).
+    const bool wn_wide = conv && mode == kGatherWeightNhwc && aligned16(a) && lda % 4 == 0 && stride_a % 4 == 0 &&
+                         a_row % 4 == 0 && cdiv(m, 128) * cdiv(n, 128) * 2 <= cus_now(ctx) && k >= 64 * 128;
     Tile tile = forced                        ? (Tile)ctx->forced_tile
                 : conv && mode == kGatherNhwc ? kTileM
+                : wn_wide                     ? kTileR
                                               : choose_tile(ctx, m, n, k, batch, conv != nullptr, native_vec);
     if (!kTiles[tile].plain && !native_vec) tile = kTileX;  // forced onto a tile it cannot stage: 256x128
     const TileShape &ts = kTiles[tile];
@@ -767,7 +777,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         }
     }
     int splits = ctx->forced_splits > 0 ? (int)std::min<int64_t>(ctx->forced_splits, std::max<int64_t>(1, cdiv(k, ts.bk)))
-                                        : choose_splits(ctx, tile, m, n, k, batch);
+                 : wn_wide && !forced ? (int)std::max<int64_t>(1, std::min<int64_t>({64, cus_now(ctx) / (cdiv(m, 128) * cdiv(n, 128)), k / 768}))
+                                      : choose_splits(ctx, tile, m, n, k, batch);
     int64_t k_chunk = k;
     if (splits > 1) {
         k_chunk = cdiv(cdiv(k, splits), ts.bk) * ts.bk;
@@ -1535,6 +1546,9 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             if (hipModuleGetFunction(&ctx->convwn[t][v], ctx->conv_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
         }
+    // the 128x128 tile's only convolution kernel: the NHWC weight gradient, 16-byte rows
+    if (hipModuleGetFunction(&ctx->convwn[kTileR][1], ctx->conv_module, "zn_convwn_tn_r_v") != hipSuccess)
+        return bail(ZN_ERR_SYMBOL);
     for (int l = 0; l < 3; ++l)
         for (int w = 0; w < 2; ++w)
             for (int v = 0; v < 2; ++v) {
