@@ -79,6 +79,7 @@ def test_code_objects_hold_every_kernel():
                 assert f"zn_conv_nn_{t}{v}{g}".encode() in conv
             for fam in ("zn_convt_nt", "zn_convw_tn", "zn_convf_nt", "zn_convwn_tn"):
                 assert f"{fam}_{t}{v}".encode() in conv
+    assert b"zn_convwn_tn_r_v" in conv  # the NHWC weight gradient on the register-staged 128x128 loop
     for k in ("zn_splitk_reduce", "zn_dense_bwd_m", "zn_dense_bwd_m_v", "zn_dense_bwd_k", "zn_dense_bwd_k_v"):
         assert k.encode() in gemm
     for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",
