@@ -483,6 +483,31 @@ def test_backend_conv2d_backward_host(backend, case):
     backward_check((gi, gw, gb), x, w, go, case, "auto", f"host {case}")
 
 
+@pytest.mark.parametrize("case", [(8, 12, 64, 64, 20, 3, 3, 2, 1), (4, 8, 48, 48, 132, 3, 3, 1, 1)])
+def test_conv_backward_weight_grad_long_k(ctx, case):
+    """Weight gradients over a long K (batch*OH*OW >= 8192) with few tiles
+    and 16-byte grad_output rows, which run as one round of 128x128 tiles x
+    K slices on the register-staged loop: grad_weights and grad_bias against
+    fp64, grad_input against the col2im form."""
+    B, C, H, W, OC, kh, kw, stride, pad = case
+    oh, ow = out_hw(H, W, kh, kw, stride, pad)
+    rng = np.random.default_rng(list(case))
+    x, w, go = uniform(rng, (B, C, H, W)), uniform(rng, (OC, kh * kw * C)), uniform(rng, (B, OC, oh, ow))
+    announce(f"conv backward long K {case}")
+    dx, dw, dgo = ctx.to_device(x), ctx.to_device(w), ctx.to_device(go)
+    dgi, dgw, dgb = ctx.alloc(B * C * H * W), ctx.alloc(OC * kh * kw * C), ctx.alloc(OC)
+    ctx.conv2d_backward_im2col(dx, dw, dgo, dgi, dgw, dgb, B, C, OC, kh, kw, H, W, oh, ow, stride, stride, pad, pad)
+    gw, gb = dgw.download().reshape(OC, kh * kw * C), dgb.download()
+    for buf in (dx, dw, dgo, dgi, dgw, dgb):
+        buf.close()
+    go2 = go.reshape(B * oh * ow, OC).astype(np.float64)
+    col = oracle.im2col(x, B, C, H, W, kh, kw, stride=stride, pad=pad).astype(np.float64)
+    gw_ref = go2.T @ col
+    assert np.all(np.abs(gw - gw_ref) <= tol(B * oh * ow) * (np.abs(go2).T @ np.abs(col)))
+    go64 = go.astype(np.float64)
+    assert np.all(np.abs(gb - go64.sum(axis=(0, 2, 3))) <= tol(B * oh * ow) * np.abs(go64).sum(axis=(0, 2, 3)))
+
+
 def test_c5_conv_backward_properties(ctx):
     """C5 (batch 32, 64->128, 3x3, 56x56, pad 1) through the im2col branch,
     checked in fp64: grad_bias = per-channel sums, grad_weights = go2^T . col,
