@@ -348,6 +348,37 @@ def test_strided_batched_against_oracle(ctx, layout):
         buf.close()
 
 
+@pytest.mark.parametrize("layout", ["nn", "tn"])
+def test_strided_batched_multi_round_128x128(ctx, layout):
+    """A batch whose 128x128 tiles fill three whole rounds (64 problems of
+    512 x 384 x 320) goes to the register-staged 128x128 loop: every problem
+    bit-identical to the forced two-stage 128x128 kernel and within the
+    oracle's tolerance."""
+    rng = np.random.default_rng(37)
+    batch, m, n, k = 64, 512, 384, 320
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a = uniform(rng, (batch,) + a_shape)
+    b = uniform(rng, (batch,) + b_shape)
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    dc = ctx.alloc(batch * m * n).fill(np.nan)
+    announce(f"strided batched multi-round {layout}")
+    ctx.sgemm_strided_batched(layout, m, n, k, da, lda, m * k, db, ldb, k * n, dc, n, m * n, batch)
+    auto = dc.download().reshape(batch, m, n)
+    ctx.set_gemm_tile("128x128")
+    try:
+        ctx.sgemm_strided_batched(layout, m, n, k, da, lda, m * k, db, ldb, k * n, dc, n, m * n, batch)
+    finally:
+        ctx.set_gemm_tile("auto")
+    two_stage = dc.download().reshape(batch, m, n)
+    assert np.array_equal(auto.view(np.uint32), two_stage.view(np.uint32))
+    for i in (0, 17, batch - 1):
+        assert_close(auto[i], ref_gemm(layout, a[i], b[i], m, n, k), layout, a[i], b[i], m, n, k, what=f"batch {i}")
+    for buf in (da, db, dc):
+        buf.close()
+
+
 # ------------------------------------------- unaligned pointers / leading dims
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
 def test_padded_and_unaligned_operands(ctx, layout):
