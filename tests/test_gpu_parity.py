@@ -402,13 +402,15 @@ def test_padded_and_unaligned_operands(ctx, layout):
         buf.close()
 
 
-@pytest.mark.parametrize("layout,m,n,k", [("nn", 4097, 1023, 777), ("nt", 1501, 1003, 999), ("tn", 999, 1502, 1001)])
+@pytest.mark.parametrize("layout,m,n,k", [("nn", 4097, 1023, 777), ("nt", 1501, 1003, 999), ("tn", 999, 1502, 1001),
+                                           ("nn", 40000, 1000, 18), ("nt", 30000, 997, 21)])
 def test_large_unaligned_operands_are_packed(ctx, layout, m, n, k):
     """Large problems whose rows are not 16-byte aligned whole float4s are
     first copied into zero-padded aligned rows, then staged with 16-byte
     loads.  Bit-identical to the problem with every dimension padded to a
     multiple of 4 with zeros (16-byte staging, no copy), and within tolerance
-    of fp64.  The base pointer of A is also one float off alignment."""
+    of fp64.  The base pointer of A is also one float off alignment.  The
+    last two pack rows of only 5 and 6 float4s."""
     rng = np.random.default_rng(6)
     a_shape, b_shape = stored_shapes(layout, m, n, k)
     a, b = uniform(rng, a_shape), uniform(rng, b_shape)
