@@ -363,6 +363,49 @@ def test_graph_replay_of_mlp_step_matches_eager(ctx):
         b.close()
 
 
+def test_graph_replay_of_large_tiles_matches_eager(ctx):
+    """The register-staged tiles under graph capture: a 256x256-tile GEMM
+    (4096 x 4096 x 512), whole rounds of 128x128 tiles (4096 x 2048 x 256)
+    and one round of 128x128 tiles in 4 K slices with the split-K reduce
+    (C3's 1024 x 1024 x 4096 TN), captured once and replayed three times
+    with outputs poisoned and unrelated eager GEMMs in between: every replay
+    reproduces the eager results bit for bit."""
+    rng = np.random.default_rng(17)
+    probs = [("nn", 4096, 4096, 512), ("nn", 4096, 2048, 256), ("tn", 1024, 1024, 4096)]
+    bufs = []
+    for lay, m, n, k in probs:
+        a_shape = (k, m) if lay == "tn" else (m, k)
+        a, b = ctx.to_device(uniform(rng, a_shape)), ctx.to_device(uniform(rng, (k, n)))
+        bufs.append((lay, m, n, k, a, b, ctx.alloc(m * n), m if lay == "tn" else k))
+
+    def run():
+        for lay, m, n, k, a, b, c, lda in bufs:
+            ctx.sgemm(lay, m, n, k, a, lda, b, n, c, n)
+
+    announce("graph replay of large tiles")
+    run()
+    ctx.sync()
+    eager = [c.download() for *_, c, _ in bufs]
+    graph = ctx.capture(run)
+    other_a, other_b = ctx.to_device(uniform(rng, (300, 200))), ctx.to_device(uniform(rng, (200, 100)))
+    other_c = ctx.alloc(300 * 100)
+    for _ in range(3):
+        for *_, c, _ in bufs:
+            c.fill(np.nan)
+        graph.launch()
+        ctx.sync()
+        for (*_, c, _), ref in zip(bufs, eager):
+            np.testing.assert_array_equal(c.download(), ref)
+        ctx.sgemm("nn", 300, 100, 200, other_a, 200, other_b, 100, other_c, 100)
+        ctx.sync()
+    graph.close()
+    for lay, m, n, k, a, b, c, lda in bufs:
+        for x in (a, b, c):
+            x.close()
+    for x in (other_a, other_b, other_c):
+        x.close()
+
+
 def test_znn_model_loads_into_hbm_and_matches_oracle(ctx, tmp_path):
     """A C2-shaped MLP (784 -> 128 relu -> 10 linear) written as a .znn file,
     loaded straight into HBM, run forward on the GPU against the oracle's
