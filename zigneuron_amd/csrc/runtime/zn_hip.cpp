@@ -776,9 +776,15 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
                                   pad);
         }
     }
-    int splits = ctx->forced_splits > 0 ? (int)std::min<int64_t>(ctx->forced_splits, std::max<int64_t>(1, cdiv(k, ts.bk)))
-                 : wn_wide && !forced ? (int)std::max<int64_t>(1, std::min<int64_t>({64, cus_now(ctx) / (cdiv(m, 128) * cdiv(n, 128)), k / 768}))
-                                      : choose_splits(ctx, tile, m, n, k, batch);
+    int splits;
+    if (ctx->forced_splits > 0) {
+        splits = (int)std::min<int64_t>(ctx->forced_splits, std::max<int64_t>(1, cdiv(k, ts.bk)));
+    } else if (wn_wide && !forced) {  // one round: CUs / tiles slices, at most 64, at least 768 of K each
+        const int64_t wn_tiles = cdiv(m, 128) * cdiv(n, 128);
+        splits = (int)std::max<int64_t>(1, std::min<int64_t>({64, cus_now(ctx) / wn_tiles, k / 768}));
+    } else {
+        splits = choose_splits(ctx, tile, m, n, k, batch);
+    }
     int64_t k_chunk = k;
     if (splits > 1) {
         k_chunk = cdiv(cdiv(k, splits), ts.bk) * ts.bk;
