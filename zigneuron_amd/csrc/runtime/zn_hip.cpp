@@ -459,6 +459,9 @@ int64_t round_splits(int64_t tiles, int64_t k, int64_t cus) {
     return s;
 }
 
+// The device's compute units, or MI355X's 256 when the query gave none.
+int64_t cus_now(const zn_ctx *ctx) { return ctx->info.compute_units > 0 ? ctx->info.compute_units : 256; }
+
 // Tile choice, from measurements on MI355X (256 CUs, per-launch times from
 // graph replays): the largest tiles win once they give every CU two or more
 // workgroups; below that, 64x64 tiles (4 waves) are the fastest down to the
@@ -472,7 +475,7 @@ int64_t round_splits(int64_t tiles, int64_t k, int64_t cus) {
 // off from 2 instead of 4 tiles per CU (C5 conv: l 221 us, m 227 us).
 Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t batch, bool gathered = false,
                  bool wide_ok = false) {
-    const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+    const int64_t cus = cus_now(ctx);
     auto tiles = [&](Tile t) { return cdiv(m, kTiles[t].bm) * cdiv(n, kTiles[t].bn) * batch; };
     auto useful = [&](Tile t) { return 4 * m * n * batch >= 3 * tiles(t) * kTiles[t].bm * kTiles[t].bn; };
     // 256x256 (16-byte staging only, one workgroup per CU): long K and whole
@@ -537,7 +540,7 @@ Tile choose_tile(const zn_ctx *ctx, int64_t m, int64_t n, int64_t k, int64_t bat
 // when K >= 16384 (long reductions such as a conv weight gradient over a
 // whole batch).
 int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k, int64_t batch) {
-    const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+    const int64_t cus = cus_now(ctx);
     const TileShape &ts = kTiles[tile];
     const int64_t tiles = cdiv(m, ts.bm) * cdiv(n, ts.bn) * batch;
     // The 128x128 BK 32 tile runs one workgroup per CU: a second workgroup
@@ -567,8 +570,6 @@ int choose_splits(const zn_ctx *ctx, Tile tile, int64_t m, int64_t n, int64_t k,
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-int64_t cus_now(const zn_ctx *ctx) { return ctx->info.compute_units > 0 ? ctx->info.compute_units : 256; }
 
 // Multiplier and shift for x / d, 0 <= x < 2^31, d >= 1: shift = ceil(log2 d),
 // mul = ceil(2^(31 + shift) / d), which is below 2^32 (Granlund & Montgomery
@@ -706,7 +707,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         if (!a_vec && !a_packed && (rcp = pack(pack_a, a, lda, a_outer, a_row, a_packed))) return rcp;
         if (!b_vec && !b_packed && (rcp = pack(pack_b, b, ldb, b_outer, b_row, b_packed))) return rcp;
         if (njobs > 0) {
-            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+            const int64_t cap = cus_now(ctx) * 16;
             if ((rcp = select_device(ctx)) ||
                 (rcp = launch(ctx, ctx->elt[kPack], (unsigned)std::min<int64_t>(cdiv(most, 256), cap), (unsigned)njobs,
                               256, &jobs)))
@@ -762,7 +763,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // in the first part.
     if (split_rows && !conv && batch == 1 && k > 0 && ctx->forced_tile < 0 && ctx->forced_splits == 0 &&
         ctx->forced_wave_split < 0 && tiles_m >= 2) {
-        const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+        const int64_t cus = cus_now(ctx);
         const int64_t per_cu = cdiv(ntiles, cus);
         if (per_cu >= 2 && cdiv(ntiles - tiles_n, cus) < per_cu) {
             const int64_t m_main = (tiles_m - 1) * ts.bm;
@@ -831,7 +832,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // 5 us, so below K = 1536 (C2's 256 x 128 x 784: 9.7 us unsplit, 14.1
     // split 7 ways) one workgroup per tile stays faster.
     {
-        const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+        const int64_t cus = cus_now(ctx);
         const int64_t tiles32 = cdiv(m, 32) * cdiv(n, 32) * batch;
         int waves = 0;
         if (!conv && k > 0 && ctx->forced_wave_split > 0)
@@ -921,7 +922,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     // which balances the CUs better (C5 convolution GEMM, K = 576: 132 us
     // plain, 150 us persistent; 8192^3 0.6% slower persistent).
     if (!conv && splits == 1 && vec && k > 0 && kTiles[tile].persistent && ctx->forced_persistent != 0) {
-        const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+        const int64_t cus = cus_now(ctx);
         const int64_t total = ntiles * batch;
         ZnGemmArgs part = args;
         part.batch = (int32_t)batch;
@@ -977,7 +978,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
             r.vec = (n % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && aligned16(part.c)) ? 1 : 0;
             const int64_t items = m * n * nb / (r.vec ? 4 : 1);
             int64_t blocks = cdiv(items, 256);
-            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 8;
+            const int64_t cap = cus_now(ctx) * 8;
             if (blocks > cap) blocks = cap;
             rc = launch(ctx, ctx->splitk_reduce, (unsigned)blocks, 1, 256, &r);
             if (rc) return rc;
@@ -999,7 +1000,7 @@ int elt_launch(zn_ctx *ctx, EltKernel kernel, int64_t work_items, const Args &ar
     if (rc) return rc;
     const int64_t threads = 256;
     int64_t blocks = cdiv(work_items, threads);
-    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+    const int64_t cap = cus_now(ctx) * 16;
     if (blocks > cap) blocks = cap;  // grid-stride loops cover the rest
     if (blocks < 1) blocks = 1;
     Args a = args;
@@ -2002,7 +2003,7 @@ static ZnIm2colArgs col_args(float *image, float *col, int64_t batch, int64_t c,
 static int im2col_launch(zn_ctx *ctx, const ZnIm2colArgs &a) {
     const int rc = select_device(ctx);
     if (rc) return rc;
-    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 32;
+    const int64_t cap = cus_now(ctx) * 32;
     const int64_t units = cdiv((int64_t)a.batch * a.out_h * a.out_w, 64) * cdiv((int64_t)a.k_h * a.k_w * a.channels, 64);
     const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(units, cap));
     ZnIm2colArgs c = a;
@@ -2011,7 +2012,7 @@ static int im2col_launch(zn_ctx *ctx, const ZnIm2colArgs &a) {
 static int col2im_launch(zn_ctx *ctx, const ZnIm2colArgs &a) {
     const int rc = select_device(ctx);
     if (rc) return rc;
-    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 32;
+    const int64_t cap = cus_now(ctx) * 32;
     const int64_t units = (int64_t)a.batch * a.in_h * cdiv(a.in_w, 64);
     const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(units, cap));
     ZnIm2colArgs c = a;
@@ -2079,7 +2080,7 @@ static int conv2d_device(zn_ctx *ctx, const float *input, const float *weights, 
             t.channels = c;
             t.pixels = h * w;
             const int64_t tiles = nb * cdiv(c, 32) * cdiv(h * w, 32);
-            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+            const int64_t cap = cus_now(ctx) * 16;
             if ((rc = select_device(ctx)) ||
                 (rc = launch(ctx, ctx->elt[kToNhwc], (unsigned)std::min<int64_t>(tiles, cap), 1, 256, &t)) ||
                 (rc = gemm_launch_ex(ctx, ZN_LAYOUT_NT, oc, hw, kdim, weights, kdim, 0, nhwc.ptr, kdim, plane,
@@ -2204,7 +2205,7 @@ static int dense_backward_impl(zn_ctx *ctx, int act, const float *input, const f
     if (rc) return rc;
     const bool chain = prev_gaa && batch > 0 && in_size > 0;
     if (batch > 0) {
-        const int64_t cus = ctx->info.compute_units > 0 ? ctx->info.compute_units : 256;
+        const int64_t cus = cus_now(ctx);
         const int64_t col_groups = cdiv(out_size, 256);
         // enough row splits for ~4 workgroups per CU, at least 16 rows each
         int64_t splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(batch, 16), 4 * cus / col_groups));
@@ -2419,7 +2420,7 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
             t.channels = c;
             t.pixels = h * w;
             const int64_t tiles = nb * cdiv(c, 32) * cdiv(h * w, 32);
-            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+            const int64_t cap = cus_now(ctx) * 16;
             if ((rc = launch(ctx, ctx->elt[kToNhwc], (unsigned)std::min<int64_t>(tiles, cap), 1, 256, &t)) ||
                 (rc = gemm_launch_ex(ctx, ZN_LAYOUT_TN, oc, taps, rows, go, oc, 0, nhwc.ptr, taps, 0, grad_weights,
                                      taps, 0, 1, b0 > 0, nullptr, ZN_ACT_LINEAR, 0, &gw, kGatherWeightNhwc)))
@@ -2464,7 +2465,7 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
             r.act = ZN_ACT_LINEAR;
             r.vec = (taps % 4 == 0 && aligned16(grad_weights) && aligned16(part.ptr)) ? 1 : 0;
             int64_t blocks = cdiv(oc * taps / (r.vec ? 4 : 1), 256);
-            const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 8;
+            const int64_t cap = cus_now(ctx) * 8;
             if (blocks > cap) blocks = cap;
             if ((rc = launch(ctx, ctx->splitk_reduce, (unsigned)blocks, 1, 256, &r))) return rc;
             // grad_col_b = go_b^T . W: TN, M = HW, N = taps, K = OC, per image
@@ -2486,7 +2487,7 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
         ra.out_channels = (int32_t)oc;
         ra.channels = (int32_t)c;
         ra.taps_per_channel = (int32_t)(kh * kw);
-        const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 8;
+        const int64_t cap = cus_now(ctx) * 8;
         if ((rc = launch(ctx, ctx->elt[kRegroup], (unsigned)std::min<int64_t>(cdiv(c * kt, 256), cap), 1, 256, &ra)))
             return rc;
         ZnConvGeom g;
@@ -2518,7 +2519,7 @@ static int conv2d_backward_device(zn_ctx *ctx, const float *input, const float *
     ra.in0 = grad_output;
     ra.rows = batch * oc;
     ra.n = hw;
-    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 16;
+    const int64_t cap = cus_now(ctx) * 16;
     if ((rc = launch(ctx, ctx->elt[kRowSum], (unsigned)std::min<int64_t>(batch * oc, cap), 1, 256, &ra))) return rc;
     if (batch > INT_MAX) return ZN_ERR_OVERFLOW;
     ZnReduceArgs r;
@@ -2580,7 +2581,7 @@ int zn_hip_softmax_rows(zn_ctx *ctx, const float *in, float *out, int64_t rows, 
     a.value = scale;
     int rc = select_device(ctx);
     if (rc) return rc;
-    const int64_t cap = (int64_t)(ctx->info.compute_units > 0 ? ctx->info.compute_units : 256) * 8;
+    const int64_t cap = cus_now(ctx) * 8;
     return launch(ctx, ctx->elt[kSoftmax], (unsigned)(rows < cap ? rows : cap), 1, 256, &a);
 }
 
