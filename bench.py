@@ -56,12 +56,19 @@ def uniform(rng, shape, lo=-1.0, hi=1.0):
     return (rng.random(shape, dtype=np.float32) * np.float32(hi - lo) + np.float32(lo)).astype(np.float32)
 
 
-def time_launches(ctx, fn, steps, warmup, rounds=3):
-    """Milliseconds per call from HIP events on the context stream: after the
-    warmup calls (and about 100 ms of device work, so clocks have settled:
+RUNS = 21  # timed runs per configuration; the median, min and max are reported
+
+
+def time_launches(ctx, fn, steps, warmup, runs=RUNS):
+    """Per-call milliseconds from HIP events on the context stream, as
+    {"median", "min", "max", "best_of_3", "runs", "calls_per_run"}.  After
+    `warmup` calls and about 100 ms of further calls (so clocks have settled:
     after the host-side set-up of a new configuration, the first ~40 ms of
-    launches ran up to 5% slower), the fastest of `rounds` timed runs of
-    `steps` back-to-back calls."""
+    launches ran up to 5% slower), `runs` timed runs, each the mean per call
+    of `steps` back-to-back calls; calls of 0.5 ms or more are timed one per
+    run (the reference's convention, src/benchmark/cuda_benchmark.zig:220-231).
+    best_of_3: the fastest of the first three runs (the statistic reported
+    before the median)."""
     for _ in range(warmup):
         fn()
     ctx.sync()
@@ -72,30 +79,47 @@ def time_launches(ctx, fn, steps, warmup, rounds=3):
     first = max(e0.elapsed_ms(e1), 1e-3)
     for _ in range(min(5000, int(100.0 / first))):
         fn()
-    best = float("inf")
-    for _ in range(rounds):
+    calls = 1 if first >= 0.5 else steps
+    times = []
+    for _ in range(runs):
         e0.record()
-        for _ in range(steps):
+        for _ in range(calls):
             fn()
         e1.record()
-        best = min(best, e0.elapsed_ms(e1) / steps)
+        times.append(e0.elapsed_ms(e1) / calls)
     e0.close()
     e1.close()
-    return best
+    return {"median": float(np.median(times)), "min": float(min(times)), "max": float(max(times)),
+            "best_of_3": float(min(times[:3])), "runs": runs, "calls_per_run": calls}
+
+
+def timing_fields(st, prefix="kernel_ms"):
+    """The entry fields of one time_launches result (median first)."""
+    return {prefix: round(st["median"], 5), f"{prefix}_min": round(st["min"], 5),
+            f"{prefix}_max": round(st["max"], 5), f"{prefix}_best_of_3": round(st["best_of_3"], 5),
+            "timed_runs": st["runs"], "calls_per_run": st["calls_per_run"]}
+
+
+def roofline_seconds(flops, byts):
+    return max(flops / (PEAK_F32_TFLOPS * 1e12), byts / (PEAK_HBM_GBS * 1e9))
 
 
 def gemm_bytes(m, n, k, batch=1, bias=False, acc=False):
     return 4 * (m * k + k * n + m * n) * batch + (4 * n if bias else 0) + (4 * m * n * batch if acc else 0)
 
 
-def config_entry(name, layout, m, n, k, batch, ms, extra=None):
+def config_entry(name, layout, m, n, k, batch, st, extra=None):
+    """One configuration row from a time_launches result: rates from the median."""
+    ms = st["median"]
     flops = 2.0 * m * n * k * batch
     byts = gemm_bytes(m, n, k, batch, bias=bool(extra and extra.get("bias")))
-    t_roof = max(flops / (PEAK_F32_TFLOPS * 1e12), byts / (PEAK_HBM_GBS * 1e9))
-    e = {"name": name, "layout": layout, "m": m, "n": n, "k": k, "batch": batch, "kernel_ms": round(ms, 5),
-         "tflops": round(flops / (ms * 1e-3) / 1e12, 3), "pct_f32_peak": round(100 * flops / (ms * 1e-3) / 1e12 /
-                                                                                 PEAK_F32_TFLOPS, 2),
-         "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "roofline_frac": round(t_roof / (ms * 1e-3), 4)}
+    t_roof = roofline_seconds(flops, byts)
+    e = {"name": name, "layout": layout, "m": m, "n": n, "k": k, "batch": batch}
+    e.update(timing_fields(st))
+    e.update({"tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+              "pct_f32_peak": round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_F32_TFLOPS, 2),
+              "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "roofline_ms": round(t_roof * 1e3, 5),
+              "roofline_frac": round(t_roof / (ms * 1e-3), 4)})
     if extra:
         e.update(extra)
     return e
@@ -154,16 +178,18 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
                                                    b_shape[0] * b_shape[1], c, n, m * n, batch)
         if graph and USE_GRAPHS:  # tiny GEMMs: device time from a replayed graph of 20 launches (no host launch cost)
             g = ctx.capture(lambda: [fn() for _ in range(20)])
-            ms = time_launches(ctx, g.launch, reps, warmup) / 20
+            st = {key: (v / 20 if key in ("median", "min", "max", "best_of_3") else v)
+                  for key, v in time_launches(ctx, g.launch, reps, warmup).items()}
             g.close()
         else:
-            ms = time_launches(ctx, fn, reps, warmup)
+            st = time_launches(ctx, fn, reps, warmup)
+        ms = st["median"]
         c_h = c.download().reshape(batch, m, n)
         for buf in (a, b, c, db):
             if buf is not None:
                 buf.close()
         err = sampled_error(layout, a_h[-1], b_h[-1], c_h[-1], m, n, k, bias, act) if CHECK else None
-        e = config_entry(name, layout, m, n, k, batch, ms, {"bias": bias is not None, "act": act})
+        e = config_entry(name, layout, m, n, k, batch, st, {"bias": bias is not None, "act": act})
         if err is not None:
             e["max_rel_err"] = float(f"{err:.3e}")
             e["tol"] = float(f"{1e-5 * np.sqrt(k):.3e}")
@@ -171,8 +197,8 @@ def bench_configs(ctx, rng, reps=10, warmup=3):
                 log(f"  !! {name}: sampled componentwise error {err:.3e} above 1e-5*sqrt(K)")
         if graph and USE_GRAPHS:
             e["timing"] = "graph replay"
-        log(f"  {name:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s  {e['pct_f32_peak']:5.1f}% peak"
-            f"  {e['hbm_gbs']:7.1f} GB/s")
+        log(f"  {name:28s} {ms * 1e3:9.1f} us (min {st['min'] * 1e3:.1f}, max {st['max'] * 1e3:.1f})  "
+            f"{e['tflops']:7.2f} TFLOP/s  {e['pct_f32_peak']:5.1f}% peak  {e['hbm_gbs']:7.1f} GB/s")
         out.append(e)
         return ms
 
@@ -206,19 +232,26 @@ def bench_conv_attention(ctx, rng, reps, warmup):
     w = ctx.to_device(uniform(rng, (OC, 9 * C)))
     bias = ctx.to_device(uniform(rng, (OC,)))
     o = ctx.alloc(B * OC * H * W)
-    ms = time_launches(ctx, lambda: ctx.conv2d_forward_im2col(x, w, bias, o, B, C, OC, 3, 3, H, W, H, W, 1, 1, 1, 1),
+    st = time_launches(ctx, lambda: ctx.conv2d_forward_im2col(x, w, bias, o, B, C, OC, 3, 3, H, W, H, W, 1, 1, 1, 1),
                        reps, warmup)
-    e = config_entry("C5 conv end-to-end (implicit GEMM)", "nn", OC, H * W, 9 * C, B, ms, {"bias": True})
+    ms = st["median"]
+    e = config_entry("C5 conv end-to-end (implicit GEMM)", "nn", OC, H * W, 9 * C, B, st, {"bias": True})
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
     res.append(e)
     go = ctx.to_device(uniform(rng, (B, OC, H, W)))
     gi, gw, gb = ctx.alloc(B * C * H * W), ctx.alloc(OC * 9 * C), ctx.alloc(OC)
-    ms = time_launches(ctx, lambda: ctx.conv2d_backward_im2col(x, w, go, gi, gw, gb, B, C, OC, 3, 3, H, W, H, W,
+    st = time_launches(ctx, lambda: ctx.conv2d_backward_im2col(x, w, go, gi, gw, gb, B, C, OC, 3, 3, H, W, H, W,
                                                                1, 1, 1, 1), reps, warmup)
+    ms = st["median"]
     flops = 2 * 2.0 * B * H * W * OC * 9 * C  # the weight- and input-gradient GEMMs
-    # stride 1, OC % 4 == 0: im2col + TN grad_W GEMM, implicit transposed-conv grad_input GEMM, bias sums
-    e = {"name": "C5 conv backward (im2col branch)", "kernel_ms": round(ms, 5),
-         "tflops": round(flops / (ms * 1e-3) / 1e12, 3)}
+    # algorithmic bytes: read the input, the weights and grad_output, write grad_input, grad_W and grad_bias
+    byts = 4.0 * (2 * B * C * H * W + 2 * OC * 9 * C + B * OC * H * W + OC)
+    t_roof = roofline_seconds(flops, byts)
+    # stride 1, OC % 4 == 0: NHWC weight-gradient GEMM, implicit transposed-conv grad_input GEMM, bias sums
+    e = {"name": "C5 conv backward (im2col branch)", **timing_fields(st),
+         "tflops": round(flops / (ms * 1e-3) / 1e12, 3), "pct_f32_peak": round(100 * flops / (ms * 1e-3) / 1e12 /
+                                                                                 PEAK_F32_TFLOPS, 2),
+         "roofline_ms": round(t_roof * 1e3, 5), "roofline_frac": round(t_roof / (ms * 1e-3), 4)}
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
     res.append(e)
     for buf in (x, w, bias, o, go, gi, gw, gb):
@@ -226,10 +259,15 @@ def bench_conv_attention(ctx, rng, reps, warmup):
     BH, S, D = 128, 1024, 64
     q, k, v = (ctx.to_device(uniform(rng, (BH, S, D))) for _ in range(3))
     o = ctx.alloc(BH * S * D)
-    ms = time_launches(ctx, lambda: ctx.attention_forward(q, k, v, o, BH, S, D, 0.125), reps, warmup)
-    flops = 4.0 * BH * S * S * D
-    e = {"name": "C5 attention end-to-end (fused online softmax)", "kernel_ms": round(ms, 5),
-         "tflops": round(flops / (ms * 1e-3) / 1e12, 3), "batch": BH, "seq_len": S, "d_k": D}
+    st = time_launches(ctx, lambda: ctx.attention_forward(q, k, v, o, BH, S, D, 0.125), reps, warmup)
+    ms = st["median"]
+    flops = 4.0 * BH * S * S * D  # Q.K^T and P.V
+    t_roof = roofline_seconds(flops, 4.0 * 4 * BH * S * D)  # read Q, K, V, write O
+    e = {"name": "C5 attention end-to-end (fused online softmax)", **timing_fields(st),
+         "tflops": round(flops / (ms * 1e-3) / 1e12, 3), "pct_f32_peak": round(100 * flops / (ms * 1e-3) / 1e12 /
+                                                                                 PEAK_F32_TFLOPS, 2),
+         "roofline_ms": round(t_roof * 1e3, 5), "roofline_frac": round(t_roof / (ms * 1e-3), 4),
+         "batch": BH, "seq_len": S, "d_k": D}
     log(f"  {e['name']:28s} {ms * 1e3:9.1f} us  {e['tflops']:7.2f} TFLOP/s (GEMM FLOPs)")
     res.append(e)
     for buf in (q, k, v, o):
@@ -254,12 +292,19 @@ def bench_host_slice(ctx, a_h, b_h):
     return e
 
 
+# The six GEMMs of the C2 step: (m, n, k, bias) of L1 and L2 forward, L2 dX (NT), L2 dW (TN), L1 dX (NT), L1 dW (TN)
+C2_GEMMS = ((256, 128, 784, True), (256, 10, 128, True), (256, 128, 10, False), (128, 10, 256, False),
+            (256, 784, 128, False), (784, 128, 256, False))
+
+
 def bench_mlp_step(ctx, rng, reps, warmup):
-    """C2: the six GEMMs of one Dense 784-128-10 training step at batch 256 (with the
-    relu derivative and both bias gradients), device resident, one stream: two fused
-    forwards and two chained backwards (L2's launch also writes L1's relu derivative),
-    four launches."""
-    from zigneuron_amd import DenseDevice
+    """C2: one training step of the Dense 784-128-10 MLP at batch 256, device
+    resident, one stream: the six GEMMs with the relu derivative and both bias
+    gradients.  The step is two launches (zn_hip_dense_pair_forward: both
+    forwards; zn_hip_dense_pair_backward: both backwards).  The per-layer step
+    (two fused forwards, two chained backwards: four launches) is timed beside
+    it.  roofline_ms: the six GEMMs' roofline times summed."""
+    from zigneuron_amd import DenseDevice, pair_backward, pair_forward
     batch = 256
     x = ctx.to_device(uniform(rng, (batch, 784), 0.0, 1.0))
     dy = ctx.to_device(uniform(rng, (batch, 10)))
@@ -267,24 +312,40 @@ def bench_mlp_step(ctx, rng, reps, warmup):
     l2 = DenseDevice(ctx, 128, 10, "linear", batch, seed=2)
 
     def step():
+        pair_forward(l1, l2, x)
+        pair_backward(l1, l2, x, dy)
+
+    def per_layer_step():
         h = l1.forward(x)
         l2.forward(h)
         l2.backward(h, dy, below=l1)
         l1.backward(x, None)
 
-    ms = time_launches(ctx, step, reps * 5, warmup)
+    st = time_launches(ctx, step, reps * 5, warmup)
+    ms = st["median"]
     flops = 2.0 * batch * (784 * 128 + 128 * 10) * 3
-    e = {"name": "C2 MLP train step (6 GEMMs, 4 launches)", "step_ms": round(ms, 5),
+    t_roof = sum(roofline_seconds(2.0 * m * n * k, gemm_bytes(m, n, k, bias=b)) for m, n, k, b in C2_GEMMS)
+    e = {"name": "C2 MLP train step (6 GEMMs, 2 launches)", **timing_fields(st, "step_ms"),
          "gemm_gflop": round(flops / 1e9, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+         "roofline_ms": round(t_roof * 1e3, 5), "roofline_frac": round(t_roof / (ms * 1e-3), 4),
          "init": ("W1 = U[-1,1)*sqrt(2/784) (relu), W2 = U[-1,1)*sqrt(1/128) (linear): Dense.init's scales, "
                   "src/layer.zig:331-333; BASELINE's 'Xavier' for W2 would be sqrt(2/138)")}
-    log(f"  {e['name']:28s} {ms * 1e3:9.1f} us per step (one host call per kernel)")
+    log(f"  {e['name']:28s} {ms * 1e3:9.1f} us per step (min {st['min'] * 1e3:.1f}, max {st['max'] * 1e3:.1f}); "
+        f"roofline {t_roof * 1e6:.2f} us")
+    fw = time_launches(ctx, lambda: pair_forward(l1, l2, x), reps * 5, warmup)
+    bw = time_launches(ctx, lambda: pair_backward(l1, l2, x, dy), reps * 5, warmup)
+    e["forward_launch_ms"] = round(fw["median"], 5)
+    e["backward_launch_ms"] = round(bw["median"], 5)
+    pl = time_launches(ctx, per_layer_step, reps * 5, warmup)
+    e.update(timing_fields(pl, "per_layer_step_ms"))
+    log(f"  {'C2 forward / backward launch':28s} {fw['median'] * 1e3:9.1f} / {bw['median'] * 1e3:.1f} us; "
+        f"per-layer step (4 launches) {pl['median'] * 1e3:.1f} us")
     if USE_GRAPHS:
         graph = ctx.capture(step)  # the same step, replayed as one HIP graph
-        gms = time_launches(ctx, graph.launch, reps * 5, warmup)
+        gst = time_launches(ctx, graph.launch, reps * 5, warmup)
         graph.close()
-        e["graph_step_ms"] = round(gms, 5)
-        log(f"  {'C2 MLP train step, HIP graph replay':28s} {gms * 1e3:9.1f} us per step")
+        e["graph_step_ms"] = round(gst["median"], 5)
+        log(f"  {'C2 MLP train step, HIP graph replay':28s} {gst['median'] * 1e3:9.1f} us per step")
     return e
 
 
@@ -435,7 +496,7 @@ def copy_calibration(ctx, steps, warmup) -> int:
     """1 GiB read + 1 GiB write per launch with the plain streaming copy kernel."""
     count = (1 << 30) // 4
     src, dst = ctx.alloc(count).fill(1.0), ctx.alloc(count)
-    ms = time_launches(ctx, lambda: ctx.copy(dst.ptr, src.ptr, count), steps, warmup)
+    ms = time_launches(ctx, lambda: ctx.copy(dst.ptr, src.ptr, count), steps, warmup)["median"]
     gbs = 2 * count * 4 / (ms * 1e-3) / 1e9
     log(f"copy 1 GiB: {ms:.3f} ms -> {gbs:.1f} GB/s (read+write)")
     print(json.dumps({"workload": "zn_copy_f32 1 GiB", "bytes_read_per_launch": count * 4,
@@ -564,11 +625,15 @@ def counter_pass(ctx) -> int:
     dy = ctx.to_device(uniform(rng, (256, 10)))
     l1 = DenseDevice(ctx, 784, 128, "relu", 256, seed=1)
     l2 = DenseDevice(ctx, 128, 10, "linear", 256, seed=2)
+    from zigneuron_amd import pair_backward, pair_forward
     for _ in range(3):
         h = l1.forward(x)
         l2.forward(h)
         l2.backward(h, dy, below=l1)
         l1.backward(x, None)
+    for _ in range(3):
+        pair_forward(l1, l2, x)
+        pair_backward(l1, l2, x, dy)
     ctx.sync()
     B, C, H, W, OC = 32, 64, 56, 56, 128
     xi, w, bias = ctx.to_device(uniform(rng, (B, C, H, W))), ctx.to_device(uniform(rng, (OC, 9 * C))), \

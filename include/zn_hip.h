@@ -219,11 +219,15 @@ int zn_hip_sgemm(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const
  *    16-byte float4s are staged with 4-byte loads (the same result).
  * Results equal zn_hip_sgemm's bit for bit whenever both split K alike.
  * Nothing in the scratch needs clearing between calls (each slice writes all
- * of its partial sums).  All contexts on one device share its scratch, so
- * calls whose executions overlap on one device (different streams or
- * threads) race; calls ordered on one stream do not.  Returns ZN_ERR_OOM or
- * ZN_ERR_HIP if the scratch could not be set up when the context was
- * created. */
+ * of its partial sums).  All contexts on one device share its scratch: a
+ * call made by another context than the device's previous one first makes
+ * its stream wait (on the device, hipStreamWaitEvent) for that call's
+ * kernels, so calls from different contexts and threads run one after the
+ * other; the host does not block.  Calls made under stream capture are not
+ * ordered so: replays of a graph that holds one must not overlap other
+ * no-allocation calls on the device.  Returns ZN_ERR_OOM or ZN_ERR_HIP if
+ * the scratch could not be set up when the context was created (the next
+ * context created on the device tries again). */
 int zn_hip_sgemm_noalloc(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                          const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias,
                          int act);
@@ -284,6 +288,36 @@ int zn_hip_dense_backward_chain(zn_ctx *ctx, int act, const float *input, const 
                                 float *grad_input, float *grad_weights, float *grad_bias, int64_t batch,
                                 int64_t in_size, int64_t out_size, int gaa_ready, int prev_act,
                                 const float *prev_activated_output, float *prev_grad_after_act);
+
+/* Two stacked Dense layers, the lower one [in -> hidden] (x, W1 [in x hidden],
+ * b1, act1) and the top one [hidden -> out] (W2 [hidden x out], b2, act2),
+ * with a launch that spans both layers when the top layer has at most 16
+ * outputs (a classifier head).  The reference runs the same work layer by
+ * layer: Network.forward calls Dense.forward per layer
+ * (src/network.zig:309-360, src/layer.zig:380-409), and its backward loop
+ * calls Dense.backward per layer, top first (src/network.zig:455-477,
+ * src/layer.zig:411-475).  Sizes as Dense.init requires: in, hidden and out
+ * of at least 1 (ZN_ERR_INVALID_ARG otherwise, src/layer.zig:304-305).
+ *
+ * Forward: h = act1(x . W1 + b1) [batch x hidden], y = act2(h . W2 + b2)
+ * [batch x out], as Backend.matMulBias* computes each (src/backend.zig:
+ * 200-295), within the GEMM tolerance.  b1 and b2 may be null (no bias). */
+int zn_hip_dense_pair_forward(zn_ctx *ctx, int act1, const float *x, const float *w1, const float *b1, float *h,
+                              int act2, const float *w2, const float *b2, float *y, int64_t batch, int64_t in_size,
+                              int64_t hidden, int64_t out_size);
+/* Backward of the pair, from grad_y [batch x out]:
+ *   gaa2 = activationBackward(act2, y, grad_y), grad_h = gaa2 . W2^T,
+ *   grad_w2 = h^T . gaa2 (overwritten), grad_b2 += column sums of gaa2;
+ *   gaa1 = activationBackward(act1, h, grad_h), grad_x = gaa1 . W1^T
+ *   (skipped when grad_x is null), grad_w1 = x^T . gaa1 (overwritten),
+ *   grad_b1 += column sums of gaa1.
+ * y is read only for a non-linear act2.  gaa2 and gaa1 are
+ * activationBackward's bits on y and on the grad_h written; the GEMMs are
+ * within the GEMM tolerance, and the bias sums are deterministic, within it. */
+int zn_hip_dense_pair_backward(zn_ctx *ctx, int act1, const float *x, const float *w1, const float *h, float *gaa1,
+                               float *grad_x, float *grad_w1, float *grad_b1, int act2, const float *w2,
+                               const float *y, const float *grad_y, float *gaa2, float *grad_h, float *grad_w2,
+                               float *grad_b2, int64_t batch, int64_t in_size, int64_t hidden, int64_t out_size);
 
 /* ------------------------------------- conv and attention (device pointers) */
 

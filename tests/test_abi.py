@@ -57,7 +57,8 @@ def test_code_objects_hold_every_kernel():
     conv = open(os.path.join(_lib.LIB_DIR, "zn_conv_gfx950.hsaco"), "rb").read()
     elt = open(os.path.join(_lib.LIB_DIR, "zn_elementwise_gfx950.hsaco"), "rb").read()
     attn = open(os.path.join(_lib.LIB_DIR, "zn_attention_gfx950.hsaco"), "rb").read()
-    for blob in (gemm, conv, elt, attn):  # an offload bundle (hipcc --genco) or a bare ELF code object
+    mlp = open(os.path.join(_lib.LIB_DIR, "zn_mlp_gfx950.hsaco"), "rb").read()
+    for blob in (gemm, conv, elt, attn, mlp):  # an offload bundle (hipcc --genco) or a bare ELF code object
         assert blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__") or blob[:4] == b"\x7fELF"
     for lay in ("nn", "nt", "tn"):
         for t in ("x", "l", "n", "m", "s", "r", "h"):
@@ -88,7 +89,13 @@ def test_code_objects_hold_every_kernel():
     for d in (32, 64, 128):
         for v in ("", "_v"):
             assert f"zn_attention_d{d}{v}".encode() in attn
-    assert b"gfx950" in gemm and b"gfx950" in conv and b"gfx950" in attn
+    for k in ("zn_dense_pair_fwd", "zn_dense_pair_fwd_v"):
+        assert k.encode() in mlp
+    for a1 in range(4):
+        for a2 in range(2):
+            for v in ("", "_v"):
+                assert f"zn_dense_pair_bwd_{a1}{a2}{v}".encode() in mlp
+    assert b"gfx950" in gemm and b"gfx950" in conv and b"gfx950" in attn and b"gfx950" in mlp
 
 
 def test_abi_version_and_status_strings(lib):
@@ -144,7 +151,7 @@ def test_dense_init_scales_match_reference():
     assert np.abs(w).max() <= (2 / 784) ** 0.5
 
 
-@pytest.mark.parametrize("obj", ["zn_gemm_gfx950.s", "zn_conv_gfx950.s", "zn_attention_gfx950.s"])
+@pytest.mark.parametrize("obj", ["zn_gemm_gfx950.s", "zn_conv_gfx950.s", "zn_attention_gfx950.s", "zn_mlp_gfx950.s"])
 def test_lds_dma_m0_use_is_confined(obj):
     """The LDS-DMA staging sets M0 right before each buffer_load ... lds; no other
     instruction in the code objects that use it may read or write M0."""

@@ -1,6 +1,6 @@
 """Code-object errors of zn_hip_create, on the CPU.
 
-zn_hip_create checks the four gfx950 code objects on the host before it
+zn_hip_create checks the five gfx950 code objects on the host before it
 touches a device (the role of the module checks in CudaBackend.init,
 src/cuda.zig:262-290, and of checkCuda's error mapping,
 src/cuda_driver.zig:1119-1160).  A missing directory, a missing, truncated or
@@ -18,7 +18,7 @@ import struct
 import pytest
 
 OBJECTS = ("zn_gemm_gfx950.hsaco", "zn_conv_gfx950.hsaco", "zn_elementwise_gfx950.hsaco",
-           "zn_attention_gfx950.hsaco")
+           "zn_attention_gfx950.hsaco", "zn_mlp_gfx950.hsaco")
 BUNDLE = b"__CLANG_OFFLOAD_BUNDLE__"
 NO_GPU = not os.path.exists("/dev/kfd")
 

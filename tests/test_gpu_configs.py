@@ -61,7 +61,7 @@ def check_bias(got, gaa, fused, start=None):
     assert np.all(np.abs(got.astype(np.float64) - ref) <= tol(gaa.shape[0]) * den)
 
 
-@pytest.mark.parametrize("fused", [False, True, "chain"])
+@pytest.mark.parametrize("fused", [False, True, "chain", "pair"])
 def test_c2_mlp_training_step(ctx, fused):
     """X[256x784] U[0,1) -> W1 He + b1(0) + ReLU -> W2 + b2(0) linear; dY2 U[-1,1).
     W1 = U[-1,1)*sqrt(2/784) and W2 = U[-1,1)*sqrt(1/128): Dense.init's scales
@@ -72,8 +72,10 @@ def test_c2_mlp_training_step(ctx, fused):
     The reference's call sequence gives bit-identical bias gradients; the fused
     backward sums them over row splits (within the GEMM tolerance).  "chain":
     L2's backward also writes L1's activation derivative, and L1's backward
-    takes it as ready (the bench's step)."""
-    from zigneuron_amd import DenseDevice
+    takes it as ready.  "pair": both layers' forwards in one launch and both
+    backwards in another (zn_hip_dense_pair_forward / _backward, the bench's
+    step), checked to the same bar."""
+    from zigneuron_amd import DenseDevice, pair_backward, pair_forward
     batch, d_in, d_h, d_out = 256, 784, 128, 10
     rng = np.random.default_rng(42)
     x = uniform(rng, (batch, d_in), 0.0, 1.0)
@@ -82,9 +84,16 @@ def test_c2_mlp_training_step(ctx, fused):
     l1 = DenseDevice(ctx, d_in, d_h, "relu", batch, seed=1)
     l2 = DenseDevice(ctx, d_h, d_out, "linear", batch, seed=2)
     dx, ddy = ctx.to_device(x), ctx.to_device(dy)
-    h1 = l1.forward(dx)
-    logits = l2.forward(h1)
-    if fused == "chain":
+    if fused == "pair":
+        logits = pair_forward(l1, l2, dx)
+        h1 = l1.out
+    else:
+        h1 = l1.forward(dx)
+        logits = l2.forward(h1)
+    if fused == "pair":
+        g_x = pair_backward(l1, l2, dx, ddy)
+        g_h1 = l2.grad_input
+    elif fused == "chain":
         g_h1 = l2.backward(h1, ddy, below=l1)
         g_x = l1.backward(dx, None)
     else:
@@ -98,14 +107,14 @@ def test_c2_mlp_training_step(ctx, fused):
     assert_close(H1, oracle.matmul_bias_act(x, W1, b1, batch, d_h, d_in, "relu"), "nn", x, W1, batch, d_h, d_in,
                  bias=b1, act="relu", what="L1 forward")
     L = logits.download().reshape(batch, d_out)
-    assert_close(L, oracle.matmul_bias_act(H1, W2, b2, batch, d_out, d_h, "linear"), "nn", H1, W2, batch, d_out,
-                 d_h, bias=b2, what="L2 forward")
+    L_ref = oracle.matmul_bias_act(H1, W2, b2, batch, d_out, d_h, "linear")
+    assert_close(L, L_ref, "nn", H1, W2, batch, d_out, d_h, bias=b2, what="L2 forward")
     # L2 backward: gaa2 = dY (linear), dX2 = gaa2 . W2^T (NT), dW2 = H1^T . gaa2 (TN)
     gaa2 = l2.gaa.download().reshape(batch, d_out)
     np.testing.assert_array_equal(gaa2, dy)
     GH1 = g_h1.download().reshape(batch, d_h)
-    assert_close(GH1, oracle.matmul_nt(gaa2, W2, batch, d_h, d_out), "nt", gaa2, W2, batch, d_h, d_out,
-                 what="L2 dX (NT)")
+    GH1_ref = oracle.matmul_nt(gaa2, W2, batch, d_h, d_out)
+    assert_close(GH1, GH1_ref, "nt", gaa2, W2, batch, d_h, d_out, what="L2 dX (NT)")
     dW2 = l2.grad_weights.download().reshape(d_h, d_out)
     assert_close(dW2, oracle.matmul_tn(H1, gaa2, d_h, d_out, batch), "tn", H1, gaa2, d_h, d_out, batch,
                  what="L2 dW (TN)")
@@ -311,12 +320,15 @@ def test_dense_backward_chain_bit_identical(ctx, shape, acts, path):
         b.close()
 
 
-def test_graph_replay_of_mlp_step_matches_eager(ctx):
+@pytest.mark.parametrize("pair", [False, True])
+def test_graph_replay_of_mlp_step_matches_eager(ctx, pair):
     """The C2 training step (bias-gradient reset by a fill kernel, two fused
-    forwards, two chained backwards) captured once and replayed three times,
-    with unrelated eager GEMMs and synchronisations between the replays:
-    every replay reproduces the eager step bit for bit."""
-    from zigneuron_amd import DenseDevice, InvalidArgumentError
+    forwards, two chained backwards; or the pair launches, whose forward
+    hands rows over through counters that each launch leaves at zero)
+    captured once and replayed three times, with unrelated eager GEMMs and
+    synchronisations between the replays: every replay reproduces the eager
+    step bit for bit."""
+    from zigneuron_amd import DenseDevice, InvalidArgumentError, pair_backward, pair_forward
     batch = 256
     rng = np.random.default_rng(7)
     x = ctx.to_device(uniform(rng, (batch, 784), 0.0, 1.0))
@@ -327,6 +339,10 @@ def test_graph_replay_of_mlp_step_matches_eager(ctx):
     def step():
         l1.grad_bias.fill(0.0)
         l2.grad_bias.fill(0.0)
+        if pair:
+            pair_forward(l1, l2, x)
+            pair_backward(l1, l2, x, dy)
+            return
         h = l1.forward(x)
         l2.forward(h)
         l2.backward(h, dy, below=l1)
@@ -336,7 +352,7 @@ def test_graph_replay_of_mlp_step_matches_eager(ctx):
         return [b.download() for b in (l1.out, l2.out, l2.grad_input, l1.grad_input, l1.grad_weights,
                                        l2.grad_weights, l1.grad_bias, l2.grad_bias)]
 
-    announce("graph replay MLP step")
+    announce(f"graph replay MLP step pair={pair}")
     step()
     ctx.sync()
     eager = outputs()

@@ -1,7 +1,8 @@
 """Error paths that need a device: a code object that loads but lacks a
 kernel (ZN_ERR_SYMBOL, the role of src/cuda.zig:262-290), and failures while
 the host-slice staging is set up, forced from the host
-(ZN_HIP_TEST_SETUP_FAULT), after which the context must still work.
+(ZN_HIP_TEST_SETUP_FAULT, honoured only with ZN_HIP_ENABLE_TEST_HOOKS=1),
+after which the context must still work.
 
 Every kernel that runs here is an ordinary, valid launch; the faults are
 simulated in host code before any device work uses the staging memory.
@@ -20,7 +21,7 @@ from gpu_common import announce, assert_close, ref_gemm, run_gemm
 pytestmark = pytest.mark.gpu
 
 OBJECTS = ("zn_gemm_gfx950.hsaco", "zn_conv_gfx950.hsaco", "zn_elementwise_gfx950.hsaco",
-           "zn_attention_gfx950.hsaco")
+           "zn_attention_gfx950.hsaco", "zn_mlp_gfx950.hsaco")
 
 
 def copy_objects(dst):
@@ -76,14 +77,36 @@ def test_setup_failure_leaves_a_working_context(monkeypatch, step):
         a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
         out = np.full(m * n, np.nan, np.float32)
         announce(f"staging set-up fault at step {step}")
+        monkeypatch.setenv("ZN_HIP_ENABLE_TEST_HOOKS", "1")
         monkeypatch.setenv("ZN_HIP_TEST_SETUP_FAULT", str(step))
         with pytest.raises(OutOfMemoryError):
             be.matMul(a, b, out, m, n, k)
         monkeypatch.delenv("ZN_HIP_TEST_SETUP_FAULT")
+        monkeypatch.delenv("ZN_HIP_ENABLE_TEST_HOOKS")
         be.matMul(a, b, out, m, n, k)
         assert_close(out.reshape(m, n), ref_gemm("nn", a, b, m, n, k), "nn", a, b, m, n, k, what="after the fault")
         again = np.full(m * n, np.nan, np.float32)
         be.matMul(a, b, again, m, n, k)  # and once more on the set-up it made
         np.testing.assert_array_equal(again, out)
+    finally:
+        c.close()
+
+
+def test_setup_fault_hook_needs_the_opt_in(monkeypatch):
+    """ZN_HIP_TEST_SETUP_FAULT alone changes nothing: without
+    ZN_HIP_ENABLE_TEST_HOOKS=1 a host-slice call sets up and computes."""
+    from zigneuron_amd import Backend, Context
+    c = Context(0)
+    be = Backend(c)
+    try:
+        rng = np.random.default_rng(7)
+        m, n, k = 64, 48, 80
+        a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
+        out = np.full(m * n, np.nan, np.float32)
+        announce("set-up fault variable without the opt-in")
+        monkeypatch.delenv("ZN_HIP_ENABLE_TEST_HOOKS", raising=False)
+        monkeypatch.setenv("ZN_HIP_TEST_SETUP_FAULT", "1")
+        be.matMul(a, b, out, m, n, k)
+        assert_close(out.reshape(m, n), ref_gemm("nn", a, b, m, n, k), "nn", a, b, m, n, k, what="hook off")
     finally:
         c.close()

@@ -284,6 +284,40 @@ def test_backend_elementwise_helpers(backend):
     np.testing.assert_array_equal(gb, oracle.accumulate_bias(gb0, out))  # same row order: bit-exact
 
 
+@pytest.mark.parametrize("act", ["linear", "relu", "sigmoid", "tanh"])
+def test_dense_forward_reference_sequence_in_place(backend, act):
+    """Dense.forward as the reference runs it where the fused dispatch is not
+    taken (src/layer.zig:384-407): host-slice matMul into the output, addBias
+    on the output in place, then activationForward with the output as its own
+    input (`output, output_buf, output, output_buf`).  Each call is checked
+    against the oracle on the GPU's own intermediate: the GEMM within the
+    tolerance, addBias bit for bit, the in-place activation bit for bit for
+    linear and relu and within 2 ulp for sigmoid and tanh; the whole sequence
+    also agrees with the fused Backend.matMulBias* within the tolerance."""
+    rng = np.random.default_rng(31)
+    batch, d_in, d_out = 256, 784, 128  # C2's first layer
+    x, w, bias = uniform(rng, (batch, d_in), 0.0, 1.0), uniform(rng, (d_in, d_out)), uniform(rng, (d_out,))
+    announce(f"Dense.forward reference sequence, in place, {act}")
+    out = np.empty(batch * d_out, np.float32)
+    backend.matMul(x, w, out, batch, d_out, d_in, False)
+    mm = out.reshape(batch, d_out).copy()
+    assert_close(mm, ref_gemm("nn", x, w, batch, d_out, d_in), "nn", x, w, batch, d_out, d_in, what="matMul")
+    backend.addBias(out, bias)
+    np.testing.assert_array_equal(out, oracle.add_bias(mm, bias).ravel())
+    biased = out.copy()
+    backend.activationForward(act, out, out)
+    ref = oracle.activation_forward(act, biased)
+    if act in ("linear", "relu"):
+        np.testing.assert_array_equal(out, ref)
+    else:
+        assert np.all(np.abs(out - ref) <= 2 * np.spacing(np.abs(ref)) + 1e-45), act
+    fused = np.empty_like(out)
+    getattr(backend, {"linear": "matMulBias", "relu": "matMulBiasRelu", "sigmoid": "matMulBiasSigmoid",
+                      "tanh": "matMulBiasTanh"}[act])(x, w, bias, fused, batch, d_out, d_in)
+    assert_close(out.reshape(batch, d_out), fused.reshape(batch, d_out), "nn", x, w, batch, d_out, d_in, bias=bias,
+                 act=act, what="unfused sequence against matMulBias*")
+
+
 def test_host_slice_staging_paths(ctx, backend):
     """Host-slice calls take three routes by size: small ones stage their
     inputs through one pinned block (one DMA) and, for small results, let the

@@ -48,7 +48,8 @@ CHILD = textwrap.dedent(r'''
         assert rc == _lib.ZN_ERR_INVALID_ARG, (name, rc)
     assert L.zn_hip_destroy(None) == 0 and L.zn_hip_event_destroy(None) == 0
     h = ctypes.c_void_p()
-    names = ("zn_gemm_gfx950.hsaco", "zn_conv_gfx950.hsaco", "zn_elementwise_gfx950.hsaco", "zn_attention_gfx950.hsaco")
+    names = ("zn_gemm_gfx950.hsaco", "zn_conv_gfx950.hsaco", "zn_elementwise_gfx950.hsaco", "zn_attention_gfx950.hsaco",
+             "zn_mlp_gfx950.hsaco")
     d = tempfile.mkdtemp()
     for n in names:
         shutil.copyfile(os.path.join(ROOT, "zigneuron_amd", "lib", n), os.path.join(d, n))
@@ -57,7 +58,7 @@ CHILD = textwrap.dedent(r'''
     if good == _lib.ZN_OK:
         L.zn_hip_destroy(h)
     assert L.zn_hip_create(0, b"/nonexistent/dir", ctypes.byref(h)) == _lib.ZN_ERR_CODE_OBJECT
-    path = os.path.join(d, "zn_elementwise_gfx950.hsaco")  # the smallest of the four
+    path = os.path.join(d, "zn_elementwise_gfx950.hsaco")  # the smallest of the five
     blob = open(path, "rb").read()
     rng = random.Random(7)
     outcomes = set()

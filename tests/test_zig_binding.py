@@ -187,12 +187,47 @@ def test_patch_only_inserts_and_calls_existing_methods():
     assert re.search(r'b\.option\(bool, "hip"', added)
 
 
+# Backend's fused Dense-forward methods and their parameter count after self (src/backend.zig:200-295:
+# a, a_buf, b, b_buf, bias, bias_buf, c, c_buf, batch_size, n, k)
+FUSED_FORWARD = {"linear": "matMulBias", "relu": "matMulBiasRelu", "sigmoid": "matMulBiasSigmoid",
+                 "tanh": "matMulBiasTanh"}
+
+
+def layer_hunk():
+    text = patch_text()
+    part = text[text.index("--- a/src/layer.zig"):]
+    nxt = part.find("\n--- a/", 1)
+    return "\n".join(ln[1:] for ln in (part if nxt < 0 else part[:nxt]).splitlines()
+                     if ln.startswith("+") and not ln.startswith("+++"))
+
+
+def test_layer_hunk_routes_dense_forward_to_the_fused_methods():
+    """Dense.forward on the HIP backend dispatches each GEMM activation to its
+    fused Backend.matMulBias* method with the layer's tensors in the
+    method's argument order (the insert sits after Dense.forward's output-size
+    check, src/layer.zig:380-382)."""
+    added = layer_hunk()
+    assert 'const hip_options = @import("hip_options");' in added
+    assert "if (hip_options.enable_hip)" in added and "self.backend.hip_backend != null" in added
+    used = dict(calls(added, "self.backend."))
+    for act, method in FUSED_FORWARD.items():
+        assert re.search(rf"\.{act} => return self\.backend\.{method}\(", added), act
+        assert used[method] == 11, (method, used[method])
+    for method in FUSED_FORWARD.values():
+        args = split_args(re.search(rf"self\.backend\.{method}\((.*?)\),?\n", added).group(1))
+        assert args == ["input", "input_buf", "w", "w_buf", "b", "b_buf", "output", "output_buf", "batch_size",
+                        "self.output_size", "self.input_size"], (method, args)
+    # every other activation (softmax, gelu, ...) keeps the reference's three calls
+    assert "else => {}," in added
+
+
 @pytest.mark.skipif(not os.path.isdir(os.path.join(REFERENCE, "src")), reason="reference tree not present")
 @pytest.mark.skipif(shutil.which("git") is None, reason="git not available")
 def test_patch_applies_to_the_reference(tmp_path):
     os.makedirs(tmp_path / "src")
     shutil.copyfile(os.path.join(REFERENCE, "src", "backend.zig"), tmp_path / "src" / "backend.zig")
     shutil.copyfile(os.path.join(REFERENCE, "build.zig"), tmp_path / "build.zig")
+    shutil.copyfile(os.path.join(REFERENCE, "src", "layer.zig"), tmp_path / "src" / "layer.zig")
     subprocess.run(["git", "init", "-q", str(tmp_path)], check=True)
     r = subprocess.run(["git", "apply", "--unidiff-zero", PATCH], cwd=tmp_path, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
@@ -201,3 +236,12 @@ def test_patch_applies_to_the_reference(tmp_path):
     for name in ("matMul", "matMulBatch", "matMulTransposeA", "matMulTransposeB", "conv2dForward", "addBias"):
         m = re.search(r"pub fn " + name + r"\(self: Backend,[^\n]*\n([^\n]*)", patched)
         assert m and "hip_be." + name + "(" in m.group(1), name
+    # the fused methods the layer hunk calls take 11 arguments after self in the reference
+    for method in FUSED_FORWARD.values():
+        sig = re.search(r"pub fn " + method + r"\(self: Backend, (.*?)\) !void", patched).group(1)
+        assert len(split_args(sig)) == 11, (method, sig)
+    layer = (tmp_path / "src" / "layer.zig").read_text()
+    fwd = layer[layer.index("pub fn forward(self: *Dense"):]
+    fwd = fwd[:fwd.index("pub fn backward(")]
+    check = fwd.index("return error.InvalidOutputSize;")
+    assert check < fwd.index("if (hip_options.enable_hip)") < fwd.index("try self.backend.matMul(")

@@ -141,3 +141,62 @@ def test_noalloc_split_beyond_scratch(ctx):
     finally:
         ctx.set_gemm_splits(0)
     assert_close(got, ref_gemm("nn", a2, b2, m2, n2, k2), "nn", a2, b2, m2, n2, k2, what="noalloc forced split")
+
+
+def test_noalloc_two_contexts_on_one_device():
+    """Two host threads, each with its own context (its own stream) on
+    device 0, issue split-K no-allocation GEMMs at the same time.  Both use
+    the device's one scratch array; each call waits for the previous call of
+    the other context before its kernels run, so every result matches
+    zn_hip_sgemm of the same context bit for bit."""
+    import threading
+
+    from zigneuron_amd import Context, _lib
+    from zigneuron_amd._lib import check
+    from zigneuron_amd.backend import layout_id
+    lib = _lib.load()
+    m, n, k = 1024, 1024, 4096  # TN: four slices of K, 16 MiB of partial sums in the scratch
+    rounds = 6
+    rng = np.random.default_rng(80)
+    a_shape, b_shape = stored_shapes("tn", m, n, k)
+    jobs = []
+    for i in range(2):
+        c = Context(0)
+        a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+        da, db = c.to_device(a), c.to_device(b)
+        ref = c.alloc(m * n).fill(np.nan)
+        check(lib.zn_hip_sgemm(c.handle, layout_id("tn"), m, n, k, da.ptr, m, db.ptr, n, ref.ptr, n, 0, None, 0),
+              "zn_hip_sgemm")
+        outs = [c.alloc(m * n).fill(np.nan) for _ in range(rounds)]
+        c.sync()
+        jobs.append(dict(ctx=c, a=a, b=b, da=da, db=db, ref=ref, outs=outs, rc=[]))
+    start = threading.Barrier(2)
+
+    def issue(job):
+        start.wait()
+        c = job["ctx"]
+        for out in job["outs"]:
+            job["rc"].append(lib.zn_hip_sgemm_noalloc(c.handle, layout_id("tn"), m, n, k, job["da"].ptr, m,
+                                                      job["db"].ptr, n, out.ptr, n, 0, None, 0))
+
+    announce(f"noalloc from two contexts in two threads: TN {m}x{n}x{k}, {rounds} calls each")
+    threads = [threading.Thread(target=issue, args=(job,)) for job in jobs]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    try:
+        for i, job in enumerate(jobs):
+            assert job["rc"] == [0] * rounds, job["rc"]
+            want = job["ref"].download().reshape(m, n)
+            for r, out in enumerate(job["outs"]):
+                got = out.download().reshape(m, n)
+                np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32),
+                                              err_msg=f"context {i}, call {r}")
+            assert_close(want, ref_gemm("tn", job["a"], job["b"], m, n, k), "tn", job["a"], job["b"], m, n, k,
+                         what=f"context {i}")
+    finally:
+        for job in jobs:
+            for buf in [job["da"], job["db"], job["ref"]] + job["outs"]:
+                buf.close()
+            job["ctx"].close()

@@ -81,6 +81,8 @@ pub extern fn zn_hip_activation_backward(ctx: ?*Ctx, act: c_int, y: ?[*]const f3
 pub extern fn zn_hip_accumulate_bias(ctx: ?*Ctx, grad_bias: ?[*]f32, gaa: ?[*]const f32, rows: i64, n: i64) c_int;
 pub extern fn zn_hip_dense_backward(ctx: ?*Ctx, act: c_int, input: ?[*]const f32, weights: ?[*]const f32, activated_output: ?[*]const f32, grad_output: ?[*]const f32, grad_after_act: ?[*]f32, grad_input: ?[*]f32, grad_weights: ?[*]f32, grad_bias: ?[*]f32, batch: i64, in_size: i64, out_size: i64) c_int;
 pub extern fn zn_hip_dense_backward_chain(ctx: ?*Ctx, act: c_int, input: ?[*]const f32, weights: ?[*]const f32, activated_output: ?[*]const f32, grad_output: ?[*]const f32, grad_after_act: ?[*]f32, grad_input: ?[*]f32, grad_weights: ?[*]f32, grad_bias: ?[*]f32, batch: i64, in_size: i64, out_size: i64, gaa_ready: c_int, prev_act: c_int, prev_activated_output: ?[*]const f32, prev_grad_after_act: ?[*]f32) c_int;
+pub extern fn zn_hip_dense_pair_forward(ctx: ?*Ctx, act1: c_int, x: ?[*]const f32, w1: ?[*]const f32, b1: ?[*]const f32, h: ?[*]f32, act2: c_int, w2: ?[*]const f32, b2: ?[*]const f32, y: ?[*]f32, batch: i64, in_size: i64, hidden: i64, out_size: i64) c_int;
+pub extern fn zn_hip_dense_pair_backward(ctx: ?*Ctx, act1: c_int, x: ?[*]const f32, w1: ?[*]const f32, h: ?[*]const f32, gaa1: ?[*]f32, grad_x: ?[*]f32, grad_w1: ?[*]f32, grad_b1: ?[*]f32, act2: c_int, w2: ?[*]const f32, y: ?[*]const f32, grad_y: ?[*]const f32, gaa2: ?[*]f32, grad_h: ?[*]f32, grad_w2: ?[*]f32, grad_b2: ?[*]f32, batch: i64, in_size: i64, hidden: i64, out_size: i64) c_int;
 pub extern fn zn_hip_im2col(ctx: ?*Ctx, input: ?[*]const f32, col: ?[*]f32, batch: i64, channels: i64, in_h: i64, in_w: i64, k_h: i64, k_w: i64, out_h: i64, out_w: i64, stride_h: i64, stride_w: i64, pad_h: i64, pad_w: i64) c_int;
 pub extern fn zn_hip_conv2d_forward_im2col(ctx: ?*Ctx, input: ?[*]const f32, weights: ?[*]const f32, bias: ?[*]const f32, output: ?[*]f32, batch: i64, in_channels: i64, out_channels: i64, k_h: i64, k_w: i64, in_h: i64, in_w: i64, out_h: i64, out_w: i64, stride_h: i64, stride_w: i64, pad_h: i64, pad_w: i64) c_int;
 pub extern fn zn_hip_conv2d_forward_direct(ctx: ?*Ctx, input: ?[*]const f32, weights: ?[*]const f32, bias: ?[*]const f32, output: ?[*]f32, batch: i64, in_channels: i64, out_channels: i64, k_h: i64, k_w: i64, in_h: i64, in_w: i64, out_h: i64, out_w: i64, stride_h: i64, stride_w: i64, pad_h: i64, pad_w: i64) c_int;
@@ -255,6 +257,16 @@ pub const HipBackend = struct {
     /// layer below's activation derivative.  Same bits as denseBackward.
     pub fn denseBackwardChain(self: *HipBackend, act: Act, input: [*]const f32, weights: [*]const f32, activated_output: ?[*]const f32, grad_output: ?[*]const f32, grad_after_act: [*]f32, grad_input: ?[*]f32, grad_weights: [*]f32, grad_bias: [*]f32, batch: i64, in_size: i64, out_size: i64, gaa_ready: bool, prev_act: Act, prev_activated_output: ?[*]const f32, prev_grad_after_act: ?[*]f32) HipError!void {
         try check(zn_hip_dense_backward_chain(self.ctx, @intFromEnum(act), input, weights, activated_output, grad_output, grad_after_act, grad_input, grad_weights, grad_bias, batch, in_size, out_size, @intFromBool(gaa_ready), @intFromEnum(prev_act), prev_activated_output, prev_grad_after_act));
+    }
+    /// Two stacked Dense forwards (Network.forward over a lower layer and a
+    /// narrow top layer): one launch when the top layer has at most 16 outputs.
+    pub fn densePairForward(self: *HipBackend, act1: Act, x: [*]const f32, w1: [*]const f32, b1: ?[*]const f32, h: [*]f32, act2: Act, w2: [*]const f32, b2: ?[*]const f32, y: [*]f32, batch: i64, in_size: i64, hidden: i64, out_size: i64) HipError!void {
+        try check(zn_hip_dense_pair_forward(self.ctx, @intFromEnum(act1), x, w1, b1, h, @intFromEnum(act2), w2, b2, y, batch, in_size, hidden, out_size));
+    }
+    /// The backward of the same pair, top layer first, in one launch under
+    /// the same limit; grad_x may be null (the network's first layer).
+    pub fn densePairBackward(self: *HipBackend, act1: Act, x: [*]const f32, w1: [*]const f32, h: [*]const f32, gaa1: [*]f32, grad_x: ?[*]f32, grad_w1: [*]f32, grad_b1: [*]f32, act2: Act, w2: [*]const f32, y: [*]const f32, grad_y: [*]const f32, gaa2: [*]f32, grad_h: [*]f32, grad_w2: [*]f32, grad_b2: [*]f32, batch: i64, in_size: i64, hidden: i64, out_size: i64) HipError!void {
+        try check(zn_hip_dense_pair_backward(self.ctx, @intFromEnum(act1), x, w1, h, gaa1, grad_x, grad_w1, grad_b1, @intFromEnum(act2), w2, y, grad_y, gaa2, grad_h, grad_w2, grad_b2, batch, in_size, hidden, out_size));
     }
     pub fn attentionForwardDevice(self: *HipBackend, q: [*]const f32, k: [*]const f32, v: [*]const f32, out: [*]f32, batch: i64, seq_len: i64, d_k: i64, scale: f32) HipError!void {
         try check(zn_hip_attention_forward(self.ctx, q, k, v, out, batch, seq_len, d_k, scale));

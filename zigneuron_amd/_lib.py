@@ -146,6 +146,8 @@ SIGNATURES = {
     "zn_hip_accumulate_bias_host": (I, [P, P, S, P, S]),
     "zn_hip_dense_backward": (I, [P, I] + [P] * 8 + [I64] * 3),
     "zn_hip_dense_backward_chain": (I, [P, I] + [P] * 8 + [I64] * 3 + [I, I, P, P]),
+    "zn_hip_dense_pair_forward": (I, [P, I, P, P, P, P, I, P, P, P] + [I64] * 4),
+    "zn_hip_dense_pair_backward": (I, [P, I] + [P] * 7 + [I] + [P] * 7 + [I64] * 4),
     "zn_hip_im2col": (I, [P, P, P] + [I64] * 12),
     "zn_hip_conv2d_forward_im2col": (I, [P, P, P, P, P] + [I64] * 13),
     "zn_hip_conv2d_forward_direct": (I, [P, P, P, P, P] + [I64] * 13),

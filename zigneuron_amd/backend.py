@@ -279,6 +279,21 @@ class Context:
             int(bool(gaa_ready)), act_id(prev_act), _dptr(prev_activated_output), _dptr(prev_grad_after_act)),
             "zn_hip_dense_backward_chain")
 
+    def dense_pair_forward(self, act1, x, w1, b1, h, act2, w2, b2, y, batch, in_size, hidden, out_size) -> None:
+        """Two stacked Dense forwards, h = act1(x.W1 + b1) then y = act2(h.W2 + b2): one launch
+        when the top layer has at most 16 outputs and the lower one is small."""
+        check(_lib.load().zn_hip_dense_pair_forward(
+            self.handle, act_id(act1), _dptr(x), _dptr(w1), _dptr(b1), _dptr(h), act_id(act2), _dptr(w2), _dptr(b2),
+            _dptr(y), batch, in_size, hidden, out_size), "zn_hip_dense_pair_forward")
+
+    def dense_pair_backward(self, act1, x, w1, h, gaa1, grad_x, grad_w1, grad_b1, act2, w2, y, grad_y, gaa2,
+                            grad_h, grad_w2, grad_b2, batch, in_size, hidden, out_size) -> None:
+        """The backward of the same pair (top layer first), in one launch under the same limits."""
+        check(_lib.load().zn_hip_dense_pair_backward(
+            self.handle, act_id(act1), _dptr(x), _dptr(w1), _dptr(h), _dptr(gaa1), _dptr(grad_x), _dptr(grad_w1),
+            _dptr(grad_b1), act_id(act2), _dptr(w2), _dptr(y), _dptr(grad_y), _dptr(gaa2), _dptr(grad_h),
+            _dptr(grad_w2), _dptr(grad_b2), batch, in_size, hidden, out_size), "zn_hip_dense_pair_backward")
+
     # --- convolution and attention on device pointers
     def im2col(self, inp, col, batch, channels, in_h, in_w, k_h, k_w, out_h, out_w, stride_h=1, stride_w=1,
                pad_h=0, pad_w=0) -> None:

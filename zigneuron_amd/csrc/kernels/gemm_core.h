@@ -1255,11 +1255,11 @@ __device__ __forceinline__ void ksplit_finish(const ZnGemmArgs &p, float *lds,
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's block is written
         __syncthreads();
         if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(p.counters + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            last = __hip_atomic_fetch_add(p.counters + slot * kCounterStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                    p.splits - 1;
         __syncthreads();
         if (!last) return;
-        if (threadIdx.x == 0) __hip_atomic_store(p.counters + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) __hip_atomic_store(p.counters + slot * kCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
         // partial tiles to LDS: part[wave][fm][fn][r][lane], lanes contiguous
         __syncthreads();  // every wave is done with every staging region
@@ -1460,8 +1460,10 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
 // `lds` holds KS * NS stages of (16 + 16) * BK floats.  NSMAX = 2 (the
 // zn_sgemmq4m_* kernels): two stages, 32 KB of LDS, so that five
 // workgroups share a CU when there are more tiles than CUs.
-template <int KS, bool AK, bool BKC, int W, int ACT, int NSMAX = 8>
-__device__ __forceinline__ void gemm_ksplit16(const ZnGemmArgs &p, float *lds) {
+// gemm_ksplit16 up to the epilogue: returns the sum (in wave order) of the
+// KS partial values of tile element (threadIdx.x / 16, threadIdx.x % 16).
+template <int KS, bool AK, bool BKC, int W, int NSMAX = 8>
+__device__ __forceinline__ float gemm_ksplit16_sum(const ZnGemmArgs &p, float *lds, int m0, int n0, int64_t bz) {
     constexpr int BM = 16, BN = 16, BK = 32;
     constexpr int NS = NSMAX < (W == 16 ? 8 : 4) ? NSMAX : (W == 16 ? 8 : 4);
     typedef DmaStage<BM, BK, kWave, AK, W> SA;
@@ -1473,10 +1475,6 @@ __device__ __forceinline__ void gemm_ksplit16(const ZnGemmArgs &p, float *lds) {
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
     float *region = lds + wave * NS * kStage;
 
-    const int pid = blockIdx.x;
-    const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int64_t bz = blockIdx.y;
     const int chunk = ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
     const int kbeg = min(p.k, wave * chunk);
     const int kend = min(p.k, kbeg + chunk);
@@ -1544,7 +1542,18 @@ __device__ __forceinline__ void gemm_ksplit16(const ZnGemmArgs &p, float *lds) {
     float x = lds[off];
 #pragma unroll
     for (int w = 1; w < KS; ++w) x = x + lds[w * 4 * kWave + off];
-    const int row = m0 + rr, col = n0 + cc;
+    return x;
+}
+
+template <int KS, bool AK, bool BKC, int W, int ACT, int NSMAX = 8>
+__device__ __forceinline__ void gemm_ksplit16(const ZnGemmArgs &p, float *lds) {
+    const int pid = blockIdx.x;
+    const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
+    const int m0 = tm * 16, n0 = tn * 16;
+    const int64_t bz = blockIdx.y;
+    float x = gemm_ksplit16_sum<KS, AK, BKC, W, NSMAX>(p, lds, m0, n0, bz);
+    const int t = threadIdx.x;
+    const int row = m0 + (t >> 4), col = n0 + (t & 15);
     if (row < p.m && col < p.n) {
         float *dst = p.c + bz * p.stride_c + (int64_t)row * p.ldc + col;
         if (p.accumulate) x = *dst + x;

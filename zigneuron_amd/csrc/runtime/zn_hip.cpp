@@ -7,7 +7,8 @@
 // Design:
 //  * one context = one device + one HIP stream + the four offline-built
 //    gfx950 code objects (zn_gemm_gfx950.hsaco, zn_conv_gfx950.hsaco,
-//    zn_elementwise_gfx950.hsaco, zn_attention_gfx950.hsaco) loaded with
+//    zn_elementwise_gfx950.hsaco, zn_attention_gfx950.hsaco) and the fused
+//    two-layer Dense kernels (zn_mlp_gfx950.hsaco), loaded with
 //    hipModuleLoad; no runtime compilation, no CPU fallback;
 //  * a size-bucketed device-buffer cache for the host-slice entry points
 //    (the role of the pow2 pool in src/cuda_context.zig:773-852);
@@ -74,10 +75,13 @@ constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kConvObject = "zn_conv_gfx950.hsaco";
 constexpr const char *kEltObject = "zn_elementwise_gfx950.hsaco";
+constexpr const char *kMlpObject = "zn_mlp_gfx950.hsaco";
 constexpr const char *kAttnObject = "zn_attention_gfx950.hsaco";
 // Fused attention kernels by padded head dim (zn_attention_d<dim>[_v]).
 constexpr int kAttnDims[3] = {32, 64, 128};
 constexpr int kAttnQueries = 128;  // queries per workgroup (4 waves x 32)
+
+struct ScratchDevice;
 
 }  // namespace
 
@@ -151,6 +155,9 @@ struct zn_ctx {
     hipModule_t conv_module = nullptr;
     hipModule_t elt_module = nullptr;
     hipModule_t attn_module = nullptr;
+    hipModule_t mlp_module = nullptr;
+    hipFunction_t pair_fwd[2] = {};            // fused two-layer Dense forward [16-byte staging]
+    hipFunction_t pair_bwd[4][2][2] = {};      // fused two-layer Dense backward [lower act][non-linear head][16-byte]
     hipFunction_t attn[3][2] = {};             // fused attention [head dim 32/64/128][16-byte I/O]
     hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
     int gemm_threads[3][kNumTiles][2] = {};    // their workgroup sizes (the kernels' launch bounds)
@@ -173,7 +180,7 @@ struct zn_ctx {
     // Split-K workspace (partial sums), grown on demand and kept until destroy.
     float *ws = nullptr;
     size_t ws_bytes = 0;
-    int32_t *counters = nullptr;  // kCounterSlots tile counters of the split wave-split kernels, zero between launches
+    int32_t *counters = nullptr;  // kCounterSlots arrival counters, kCounterStride ints apart, zero between launches
     hipFunction_t elt[kNumElt] = {};
     int last_hip_error = 0;
     // Graph capture (zn_hip_graph_begin .. _end): leased buffers go to
@@ -205,10 +212,11 @@ struct zn_ctx {
     hipEvent_t pinned_out_done[2] = {};
     hipEvent_t chunk_in[2] = {}, chunk_out[2] = {};
     hipEvent_t entry = nullptr;
-    // This device's copy of `scratch` (resolved at create) and, while
-    // zn_hip_sgemm_noalloc runs, the flag that routes its split-K partial
-    // sums there and turns operand packing off.
+    // This device's copy of `scratch` (resolved at create), its ordering
+    // state and, while zn_hip_sgemm_noalloc runs, the flag that routes its
+    // split-K partial sums there and turns operand packing off.
     float *scratch = nullptr;
+    ScratchDevice *scratch_dev = nullptr;
     int scratch_status = ZN_OK;
     bool no_alloc = false;
 };
@@ -316,37 +324,59 @@ int select_device(zn_ctx *ctx) {
     return ZN_OK;
 }
 
-// Device address of `scratch`, resolved once per device with that device
+// One device's `scratch`: its device address, resolved once with that device
 // current and kept for the process (each device holds its own copy at its
-// own address).  Every context on the device shares it.
-struct ScratchAddress {
+// own address), and the ordering of the calls that use it.  Every context on
+// the device shares it.  A call queues its kernels under `use`, after a wait
+// for `done` when another context recorded it last, and records `done`
+// behind them, so calls from different contexts (streams) run one after the
+// other on the device instead of overlapping on the one array.
+struct ScratchDevice {
+    std::mutex use;
     bool resolved = false;
-    int status = ZN_OK;
-    int hip_error = 0;
     float *ptr = nullptr;
+    hipEvent_t done = nullptr;     // recorded behind the last call's kernels
+    bool recorded = false;
+    const zn_ctx *owner = nullptr;  // the context that recorded `done` last (null: gone)
 };
 std::mutex g_scratch_mu;
-std::map<int, ScratchAddress> g_scratch;
+std::map<int, ScratchDevice> g_scratch;  // by device; the map never moves an entry
 
+// Only a success is kept: after a failure the next context created on the
+// device tries again.
 int resolve_scratch(zn_ctx *ctx) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    ScratchAddress &s = g_scratch[ctx->device];
+    ScratchDevice &s = g_scratch[ctx->device];
     if (!s.resolved) {
-        s.resolved = true;
         void *p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !p) {
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e == hipSuccess && !p) e = hipErrorInvalidSymbol;
+        hipEvent_t ev = nullptr;
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) {
             (void)hipGetLastError();
-            s.status = e == hipErrorOutOfMemory ? ZN_ERR_OOM : ZN_ERR_HIP;
-            s.hip_error = (int)e;
-        } else {
-            s.ptr = static_cast<float *>(p);
+            ctx->scratch = nullptr;
+            ctx->scratch_dev = nullptr;
+            ctx->scratch_status = e == hipErrorOutOfMemory ? ZN_ERR_OOM : ZN_ERR_HIP;
+            ctx->last_hip_error = (int)e;
+            return ctx->scratch_status;
         }
+        s.ptr = static_cast<float *>(p);
+        s.done = ev;
+        s.resolved = true;
     }
     ctx->scratch = s.ptr;
-    ctx->scratch_status = s.status;
-    if (s.status != ZN_OK) ctx->last_hip_error = s.hip_error;
-    return s.status;
+    ctx->scratch_dev = &s;
+    ctx->scratch_status = ZN_OK;
+    return ZN_OK;
+}
+
+// A context that goes away no longer owns the device's last scratch record
+// (its stream was drained before this runs).
+void forget_scratch_owner(zn_ctx *ctx) {
+    if (!ctx->scratch_dev) return;
+    std::lock_guard<std::mutex> lock(ctx->scratch_dev->use);
+    if (ctx->scratch_dev->owner == ctx) ctx->scratch_dev->owner = nullptr;
 }
 
 // Marks a context as running zn_hip_sgemm_noalloc for one call.
@@ -1010,10 +1040,14 @@ int elt_launch(zn_ctx *ctx, EltKernel kernel, int64_t work_items, const Args &ar
 constexpr size_t kStageBytes = (size_t)32 << 20;  // per pinned staging buffer
 constexpr size_t kStageMin = (size_t)4 << 20;      // smaller copies stay pageable
 
-// Set-up fault injection for the error-path tests: ZN_HIP_TEST_SETUP_FAULT=n
-// makes step n of the staging (1-5) or pipeline (11-21) set-up fail as if
-// the HIP call had run out of memory.  Read at each set-up attempt.
+// Set-up fault injection for the error-path tests: with
+// ZN_HIP_ENABLE_TEST_HOOKS=1, ZN_HIP_TEST_SETUP_FAULT=n makes step n of the
+// staging (1-5) or pipeline (11-21) set-up fail as if the HIP call had run
+// out of memory.  Both are read at each set-up attempt; without the first
+// the second is ignored, so a stray variable cannot fail a production call.
 hipError_t setup_step(int step, hipError_t real) {
+    const char *on = std::getenv("ZN_HIP_ENABLE_TEST_HOOKS");
+    if (!on || std::strcmp(on, "1") != 0) return real;
     const char *env = std::getenv("ZN_HIP_TEST_SETUP_FAULT");
     if (env && std::atoi(env) == step) return hipErrorOutOfMemory;
     return real;
@@ -1464,9 +1498,10 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     const std::string conv_path = dir + "/" + kConvObject;
     const std::string elt_path = dir + "/" + kEltObject;
     const std::string attn_path = dir + "/" + kAttnObject;
+    const std::string mlp_path = dir + "/" + kMlpObject;
     // The code objects are checked on the host first, so a bad directory is
     // reported the same way with or without a device.
-    for (const std::string *path : {&gemm_path, &conv_path, &elt_path, &attn_path})
+    for (const std::string *path : {&gemm_path, &conv_path, &elt_path, &attn_path, &mlp_path})
         if (!code_object_ok(*path)) return ZN_ERR_CODE_OBJECT;
 
     int count = 0;
@@ -1512,6 +1547,10 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     }
     if (hipModuleLoad(&ctx->attn_module, attn_path.c_str()) != hipSuccess) {
         ctx->attn_module = nullptr;
+        return bail(ZN_ERR_CODE_OBJECT);
+    }
+    if (hipModuleLoad(&ctx->mlp_module, mlp_path.c_str()) != hipSuccess) {
+        ctx->mlp_module = nullptr;
         return bail(ZN_ERR_CODE_OBJECT);
     }
     for (int l = 0; l < 3; ++l)
@@ -1612,6 +1651,17 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
         return bail(ZN_ERR_SYMBOL);
     for (int i = 0; i < kNumElt; ++i)
         if (hipModuleGetFunction(&ctx->elt[i], ctx->elt_module, kEltName[i]) != hipSuccess) return bail(ZN_ERR_SYMBOL);
+    if (hipModuleGetFunction(&ctx->pair_fwd[0], ctx->mlp_module, "zn_dense_pair_fwd") != hipSuccess ||
+        hipModuleGetFunction(&ctx->pair_fwd[1], ctx->mlp_module, "zn_dense_pair_fwd_v") != hipSuccess)
+        return bail(ZN_ERR_SYMBOL);
+    for (int a1 = 0; a1 < 4; ++a1)
+        for (int a2 = 0; a2 < 2; ++a2)
+            for (int v = 0; v < 2; ++v) {
+                char name[64];
+                std::snprintf(name, sizeof(name), "zn_dense_pair_bwd_%d%d%s", a1, a2, v ? "_v" : "");
+                if (hipModuleGetFunction(&ctx->pair_bwd[a1][a2][v], ctx->mlp_module, name) != hipSuccess)
+                    return bail(ZN_ERR_SYMBOL);
+            }
     for (int d = 0; d < 3; ++d)
         for (int v = 0; v < 2; ++v) {
             char name[64];
@@ -1619,12 +1669,13 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             if (hipModuleGetFunction(&ctx->attn[d][v], ctx->attn_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
         }
     void *counters = nullptr;
-    if ((e = hipMalloc(&counters, kCounterSlots * sizeof(int32_t))) != hipSuccess) {
+    if ((e = hipMalloc(&counters, kCounterSlots * kCounterStride * sizeof(int32_t))) != hipSuccess) {
         (void)hipGetLastError();
         return bail(fail_hip(ctx, e, ZN_ERR_OOM));
     }
     ctx->counters = static_cast<int32_t *>(counters);
-    if ((e = hipMemset(counters, 0, kCounterSlots * sizeof(int32_t))) != hipSuccess) return bail(fail_hip(ctx, e));
+    if ((e = hipMemset(counters, 0, kCounterSlots * kCounterStride * sizeof(int32_t))) != hipSuccess)
+        return bail(fail_hip(ctx, e));
     *out = ctx;
     return ZN_OK;
 }
@@ -1641,6 +1692,7 @@ int zn_hip_destroy(zn_ctx *ctx) {
         ctx->captured.clear();
     }
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    forget_scratch_owner(ctx);
     release_pipeline(ctx);
     release_staging(ctx);
     while (!ctx->graphs.empty()) (void)zn_hip_graph_destroy(ctx->graphs.back());
@@ -1657,6 +1709,7 @@ int zn_hip_destroy(zn_ctx *ctx) {
     if (ctx->conv_module) (void)hipModuleUnload(ctx->conv_module);
     if (ctx->elt_module) (void)hipModuleUnload(ctx->elt_module);
     if (ctx->attn_module) (void)hipModuleUnload(ctx->attn_module);
+    if (ctx->mlp_module) (void)hipModuleUnload(ctx->mlp_module);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     (void)hipGetLastError();
     delete ctx;
@@ -1900,9 +1953,34 @@ int zn_hip_sgemm_noalloc(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t 
                          const float *b, int64_t ldb, float *c, int64_t ldc, int accumulate, const float *bias,
                          int act) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
-    if (!ctx->scratch) return ctx->scratch_status != ZN_OK ? ctx->scratch_status : ZN_ERR_HIP;
-    NoAllocScope scope(ctx);
-    return gemm_launch(ctx, layout, m, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias, act);
+    if (!ctx->scratch || !ctx->scratch_dev) return ctx->scratch_status != ZN_OK ? ctx->scratch_status : ZN_ERR_HIP;
+    ScratchDevice &s = *ctx->scratch_dev;
+    std::lock_guard<std::mutex> lock(s.use);
+    // Under stream capture the call becomes graph nodes and is not ordered
+    // here: whoever replays the graph keeps it apart from other users.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    ZN_HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cap));
+    const bool ordered = cap == hipStreamCaptureStatusNone;
+    if (ordered && s.recorded && s.owner != ctx) ZN_HIP_TRY(ctx, hipStreamWaitEvent(ctx->stream, s.done, 0));
+    int rc;
+    {
+        NoAllocScope scope(ctx);
+        rc = gemm_launch(ctx, layout, m, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias, act);
+    }
+    if (ordered) {
+        const hipError_t e = hipEventRecord(s.done, ctx->stream);
+        if (e != hipSuccess) {
+            // the next user can no longer wait for this call: drain it
+            (void)hipGetLastError();
+            (void)hipStreamSynchronize(ctx->stream);
+            s.recorded = false;
+            s.owner = nullptr;
+            return rc == ZN_OK ? fail_hip(ctx, e) : rc;
+        }
+        s.recorded = true;
+        s.owner = ctx;
+    }
+    return rc;
 }
 
 int zn_hip_sgemm_strided_batched(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a,
@@ -2329,6 +2407,172 @@ int zn_hip_dense_backward_chain(zn_ctx *ctx, int act, const float *input, const 
     return dense_backward_impl(ctx, act, input, weights, activated_output, grad_output, grad_after_act, grad_input,
                                grad_weights, grad_bias, batch, in_size, out_size, gaa_ready == 1, prev_act,
                                prev_activated_output, prev_grad_after_act);
+}
+
+// ------------------------------------------------- two stacked Dense layers
+// The pair kernels (kernels/mlp_f32.hip) take a top layer of at most 16
+// outputs.
+constexpr int64_t kPairOutMax = 16;
+// The backward's LDS copies of W2 (all rows, padded to 32) and of gaa2 (all
+// rows, padded to 32), read 16 bytes at a time.
+constexpr int64_t kPairRawW = 2048, kPairRawG = 4096;
+
+static ZnPairGemm pair_gemm(const float *src, int64_t ld, float *c, int64_t ldc, int64_t m, int64_t n, int64_t k) {
+    ZnPairGemm g;
+    g.src = src;
+    g.c = c;
+    g.ld = (int32_t)ld;
+    g.ldc = (int32_t)ldc;
+    g.m = (int32_t)m;
+    g.n = (int32_t)n;
+    g.k = (int32_t)k;
+    g.tiles_n = (int32_t)cdiv(n, 32);
+    return g;
+}
+
+// The path tests force (a tile, a split or no wave split) takes the
+// per-layer launches.
+static bool pair_forced_off(const zn_ctx *ctx) {
+    return ctx->forced_tile >= 0 || ctx->forced_splits != 0 || ctx->forced_wave_split == 0;
+}
+
+static bool pair_extents_ok(int64_t batch, int64_t in_size, int64_t hidden, int64_t out_size) {
+    const int64_t lim = (int64_t)INT_MAX / 4;
+    return batch * in_size <= lim && in_size * hidden <= lim && batch * hidden <= lim &&
+           hidden * out_size <= lim && batch * out_size <= lim;
+}
+
+// Network.forward over two Dense layers (src/network.zig:309-360, which runs
+// Dense.forward, src/layer.zig:380-409, per layer): h = act1(x . W1 + b1),
+// then y = act2(h . W2 + b2).  One launch (zn_dense_pair_fwd) when the top
+// layer has at most 16 outputs and the lower layer's 16x16 tiles are at most
+// one per CU; otherwise the two fused GEMMs of Backend.matMulBias*.
+int zn_hip_dense_pair_forward(zn_ctx *ctx, int act1, const float *x, const float *w1, const float *b1, float *h,
+                              int act2, const float *w2, const float *b2, float *y, int64_t batch, int64_t in_size,
+                              int64_t hidden, int64_t out_size) {
+    if (!ctx || act1 < ZN_ACT_LINEAR || act1 > ZN_ACT_TANH || act2 < ZN_ACT_LINEAR || act2 > ZN_ACT_TANH ||
+        batch < 0 || in_size < 0 || hidden < 0 || out_size < 0)
+        return ZN_ERR_INVALID_ARG;
+    // a Dense layer has at least one input and one output (Dense.init, src/layer.zig:304-305)
+    if (in_size == 0 || hidden == 0 || out_size == 0) return ZN_ERR_INVALID_ARG;
+    if (batch > INT_MAX || in_size > INT_MAX || hidden > INT_MAX || out_size > INT_MAX) return ZN_ERR_OVERFLOW;
+    if (batch == 0) return ZN_OK;
+    if (!x || !w1 || !h || !w2 || !y) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    const int64_t tiles_m = cdiv(batch, 16), tiles_n = cdiv(hidden, 16);
+    // the tiles' partial sums of y go to the workspace (256 floats per tile)
+    const size_t part_bytes = (size_t)(tiles_m * tiles_n) * 256 * sizeof(float);
+    const bool fused = out_size <= kPairOutMax && tiles_m * tiles_n <= cus_now(ctx) && tiles_m <= kCounterSlots &&
+                       !pair_forced_off(ctx) && pair_extents_ok(batch, in_size, hidden, out_size) && !ctx->no_alloc &&
+                       ensure_workspace(ctx, part_bytes) == ZN_OK;
+    if (!fused) {
+        if ((rc = gemm_launch(ctx, ZN_LAYOUT_NN, batch, hidden, in_size, x, in_size, 0, w1, hidden, 0, h, hidden, 0,
+                              1, 0, b1, act1)))
+            return rc;
+        return gemm_launch(ctx, ZN_LAYOUT_NN, batch, out_size, hidden, h, hidden, 0, w2, out_size, 0, y, out_size, 0,
+                           1, 0, b2, act2);
+    }
+    ZnPairFwdArgs a;
+    std::memset(&a, 0, sizeof(a));
+    ZnGemmArgs &p = a.l1;
+    p.a = x;
+    p.b = w1;
+    p.c = h;
+    p.bias = b1;
+    p.lda = in_size;
+    p.ldb = hidden;
+    p.ldc = hidden;
+    p.m = (int32_t)batch;
+    p.n = (int32_t)hidden;
+    p.k = (int32_t)in_size;
+    p.tiles_m = (int32_t)tiles_m;
+    p.tiles_n = (int32_t)tiles_n;
+    p.act = act1;
+    p.group_m = 1;
+    p.splits = 1;
+    p.k_chunk = (int32_t)in_size;
+    p.batch = 1;
+    a.w2 = w2;
+    a.b2 = b2;
+    a.y = y;
+    a.part = ctx->ws;
+    a.counters = ctx->counters;
+    a.out = (int32_t)out_size;
+    a.act2 = act2;
+    const bool vec = aligned16(x) && aligned16(w1) && in_size % 4 == 0 && hidden % 4 == 0;
+    return launch(ctx, ctx->pair_fwd[vec ? 1 : 0], (unsigned)(tiles_m * tiles_n), 1, 256, &a);
+}
+
+// The backward loop of Network over the same two layers (src/network.zig:
+// 455-477: Dense.backward per layer, top first, src/layer.zig:411-475):
+//   gaa2 = act2'(y, grad_y), grad_h = gaa2 . W2^T, grad_w2 = h^T . gaa2,
+//   grad_b2 += column sums of gaa2;
+//   gaa1 = act1'(h, grad_h), grad_x = gaa1 . W1^T (skipped when null),
+//   grad_w1 = x^T . gaa1, grad_b1 += column sums of gaa1.
+// One launch (zn_dense_pair_bwd) when the top layer has at most 16 outputs
+// and the workgroups fit two per CU; otherwise the chained per-layer
+// launches of zn_hip_dense_backward_chain.
+int zn_hip_dense_pair_backward(zn_ctx *ctx, int act1, const float *x, const float *w1, const float *h, float *gaa1,
+                               float *grad_x, float *grad_w1, float *grad_b1, int act2, const float *w2,
+                               const float *y, const float *grad_y, float *gaa2, float *grad_h, float *grad_w2,
+                               float *grad_b2, int64_t batch, int64_t in_size, int64_t hidden, int64_t out_size) {
+    if (!ctx || act1 < ZN_ACT_LINEAR || act1 > ZN_ACT_TANH || act2 < ZN_ACT_LINEAR || act2 > ZN_ACT_TANH ||
+        batch < 0 || in_size < 0 || hidden < 0 || out_size < 0)
+        return ZN_ERR_INVALID_ARG;
+    if (in_size == 0 || hidden == 0 || out_size == 0) return ZN_ERR_INVALID_ARG;  // Dense.init, src/layer.zig:304-305
+    if (batch > INT_MAX || in_size > INT_MAX || hidden > INT_MAX || out_size > INT_MAX) return ZN_ERR_OVERFLOW;
+    if (batch > 0 && (!gaa2 || !grad_b2 || !grad_y || (act2 != ZN_ACT_LINEAR && !y) || !grad_h || !w2 || !h ||
+                      !gaa1 || !grad_b1 || !x || !w1))
+        return ZN_ERR_INVALID_ARG;
+    if (!grad_w2 || !grad_w1) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    const int64_t wg_nt = grad_x ? cdiv(batch, 32) * cdiv(in_size, 64) : 0;
+    const int64_t wg_tn1 = cdiv(in_size, 32) * cdiv(hidden, 32);
+    const int64_t wg_tn2 = cdiv(hidden, 32);
+    // one workgroup per CU (107 KB of LDS each), all resident at once
+    const bool fused = batch >= 1 && out_size <= kPairOutMax && wg_nt + wg_tn1 + wg_tn2 <= cus_now(ctx) &&
+                       !pair_forced_off(ctx) &&
+                       pair_extents_ok(batch, in_size, hidden, out_size) &&
+                       cdiv(hidden, 32) * 32 * out_size <= kPairRawW && cdiv(batch, 32) * 32 * out_size <= kPairRawG &&
+                       aligned16(w2) && aligned16(grad_y) && (act2 == ZN_ACT_LINEAR || aligned16(y));
+    if (!fused) {
+        if ((rc = dense_backward_impl(ctx, act2, h, w2, y, grad_y, gaa2, grad_h, grad_w2, grad_b2, batch, hidden,
+                                      out_size, false, act1, h, gaa1)))
+            return rc;
+        return dense_backward_impl(ctx, act1, x, w1, nullptr, nullptr, gaa1, grad_x, grad_w1, grad_b1, batch, in_size,
+                                   hidden, true, ZN_ACT_LINEAR, nullptr, nullptr);
+    }
+    ZnPairBwdArgs a;
+    std::memset(&a, 0, sizeof(a));
+    if (grad_x) {
+        a.nt = pair_gemm(w1, hidden, grad_x, in_size, batch, in_size, hidden);
+        a.nt.tiles_n = (int32_t)cdiv(in_size, 64);
+    }
+    a.tn1 = pair_gemm(x, in_size, grad_w1, hidden, in_size, hidden, batch);
+    a.tn2 = pair_gemm(h, hidden, grad_w2, out_size, hidden, out_size, batch);
+    a.h = h;
+    a.w2 = w2;
+    a.y = y;
+    a.grad_y = grad_y;
+    a.gaa1 = gaa1;
+    a.grad_h = grad_h;
+    a.gaa2 = gaa2;
+    a.grad_b1 = grad_b1;
+    a.grad_b2 = grad_b2;
+    a.batch = (int32_t)batch;
+    a.hidden = (int32_t)hidden;
+    a.out = (int32_t)out_size;
+    a.act1 = act1;
+    a.act2 = act2;
+    a.wg_nt = (int32_t)wg_nt;
+    a.wg_tn1 = (int32_t)wg_tn1;
+    a.wg_tn2 = (int32_t)wg_tn2;
+    // 16-byte staging of the loaded operands (W1, x and h): aligned rows that are whole float4s
+    const bool vec = aligned16(w1) && aligned16(x) && aligned16(h) && in_size % 4 == 0 && hidden % 4 == 0;
+    return launch(ctx, ctx->pair_bwd[act1][act2 != ZN_ACT_LINEAR ? 1 : 0][vec ? 1 : 0],
+                  (unsigned)(wg_nt + wg_tn1 + wg_tn2), 1, 256, &a);
 }
 
 // ------------------------------------------------------- conv backward

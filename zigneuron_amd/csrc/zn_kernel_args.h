@@ -61,10 +61,16 @@ struct ZnGemmArgs {
     float *chain_gaa;
     int32_t chain_act;
     // Intra-workgroup split-K kernels with splits > 1: one counter per
-    // (problem, tile), zero between launches (the last workgroup of a tile
-    // resets it).
+    // (problem, tile), kCounterStride ints apart, zero between launches (the
+    // last workgroup of a tile resets it).
     int32_t *counters;
 };
+
+// Cross-workgroup arrival counters (the context's counter array): counter i
+// sits at index i * kCounterStride, one 128-byte line each, so that arrivals
+// at different counters do not contend for one line (the atomics of one line
+// are serialised where they execute).
+constexpr int kCounterStride = 32;
 
 // Split-K reduction: C = act((accumulate ? C : 0) + sum_s ws[s] + bias), the
 // slices summed in ascending order.
@@ -102,6 +108,49 @@ struct ZnDenseBwdArgs {
     ZnReduceArgs bias;     // reduce of the prologue's partial sums (wg_bias workgroups), or
     ZnColSumArgs colsum;   // the column sums themselves (wg_colsum workgroups)
     int32_t wg_nt, wg_tn, wg_bias, wg_colsum;
+};
+
+// Two stacked Dense layers whose top layer is narrow (out <= 16), forward
+// in one launch: h = act1(x . W1 + b1) on the 16x16 wave-split tiles (l1,
+// activation in l1.act); each tile's block of h times W2's matching rows is
+// its partial sum of the strip's y, and the last tile to finish each 16-row
+// strip adds the strip's partials into y = act2(h . W2 + b2).
+struct ZnPairFwdArgs {
+    ZnGemmArgs l1;
+    const float *w2;      // [hidden x out]
+    const float *b2;      // [out], or null
+    float *y;             // [batch x out]
+    float *part;          // 256 floats per tile: its 16 x 16 partial sum of y
+    int32_t *counters;    // one per 16-row strip of h, kCounterStride ints apart, zero between launches
+    int32_t out, act2;
+};
+
+// One GEMM of the pair backward on 32x32 tiles: C [m x n] (row stride ldc)
+// over K = k, with one operand staged from `src` (row stride ld) and the
+// other generated in registers.
+struct ZnPairGemm {
+    const float *src;
+    float *c;
+    int32_t ld, ldc, m, n, k, tiles_n;
+};
+
+// The backward of the same pair in one launch.  gaa2 = act2'(y, grad_y),
+// grad_h = gaa2 . W2^T and gaa1 = act1'(h, grad_h) are generated where they
+// are needed (no workgroup waits for another):
+//   [0, wg_nt)    grad_x  = gaa1 . W1^T on 32x64 tiles (nt: W1 staged; none when grad_x is null)
+//   next wg_tn1   grad_w1 = x^T . gaa1 on 32x32 tiles (tn1: x staged); the first row of tiles
+//                 also writes grad_h and gaa1 and adds gaa1's column sums into grad_b1
+//   next wg_tn2   grad_w2 = h^T . gaa2 (tn2: h staged); the first tile also writes gaa2 and
+//                 adds its column sums into grad_b2
+struct ZnPairBwdArgs {
+    ZnPairGemm nt, tn1, tn2;
+    const float *h;       // [batch x hidden], the lower layer's activated output
+    const float *w2;      // [hidden x out]
+    const float *y;       // [batch x out], the top layer's activated output (read unless act2 is linear)
+    const float *grad_y;  // [batch x out]
+    float *gaa1, *grad_h, *gaa2, *grad_b1, *grad_b2;
+    int32_t batch, hidden, out, act1, act2;
+    int32_t wg_nt, wg_tn1, wg_tn2;
 };
 
 // Elementwise helpers (fill, copy, bias, activations, bias gradient, row

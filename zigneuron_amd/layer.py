@@ -96,7 +96,9 @@ class DenseDevice:
         self._gaa_ready = False  # self.gaa was written by the layer above's chained backward
 
     def forward(self, x: DeviceBuffer) -> DeviceBuffer:
-        """Fused NN + bias + activation into self.out (asynchronous)."""
+        """Fused NN + bias + activation into self.out (asynchronous).  A new forward
+        starts a new step: a derivative left by an earlier chained backward is stale."""
+        self._gaa_ready = False
         self.ctx.sgemm("nn", self.batch, self.output_size, self.input_size, x, self.input_size, self.weights,
                        self.output_size, self.out, self.output_size, False, self.bias, self.act)
         return self.out
@@ -114,6 +116,10 @@ class DenseDevice:
         The results are the same bits as the unchained calls."""
         if fused:
             ready = self._gaa_ready
+            if ready and grad_out is not None:
+                raise _lib.InvalidArgumentError(
+                    _lib.ZN_ERR_INVALID_ARG, "DenseDevice.backward",
+                    "grad_out given, but the layer above's chained backward already wrote this layer's derivative")
             self._gaa_ready = False
             if below is None and not ready:
                 self.ctx.dense_backward(self.act, x, self.weights, self.out, grad_out, self.gaa, self.grad_input,
@@ -141,3 +147,36 @@ class DenseDevice:
         self.ctx.sgemm("tn", self.input_size, self.output_size, self.batch, x, self.input_size, self.gaa,
                        self.output_size, self.grad_weights, self.output_size)
         return self.grad_input
+
+
+def _pair_check(lower: DenseDevice, upper: DenseDevice, where: str) -> None:
+    if upper.input_size != lower.output_size or upper.batch != lower.batch or upper.ctx is not lower.ctx:
+        raise _lib.InvalidArgumentError(_lib.ZN_ERR_INVALID_ARG, where, "upper must take lower's output")
+
+
+def pair_forward(lower: DenseDevice, upper: DenseDevice, x: DeviceBuffer) -> DeviceBuffer:
+    """Network.forward over two stacked layers (src/network.zig:309-360): lower.out =
+    act(x.W + b) of the lower layer, then upper.out from it.  One launch when the upper layer
+    has at most 16 outputs (zn_hip_dense_pair_forward), else one fused GEMM per layer."""
+    _pair_check(lower, upper, "pair_forward")
+    lower._gaa_ready = upper._gaa_ready = False
+    lower.ctx.dense_pair_forward(lower.act, x, lower.weights, lower.bias, lower.out, upper.act, upper.weights,
+                                 upper.bias, upper.out, lower.batch, lower.input_size, lower.output_size,
+                                 upper.output_size)
+    return upper.out
+
+
+def pair_backward(lower: DenseDevice, upper: DenseDevice, x: DeviceBuffer, grad_out: DeviceBuffer,
+                  grad_input: bool = True) -> Optional[DeviceBuffer]:
+    """Network's backward loop over the same two layers (src/network.zig:455-477), upper first:
+    every gradient, derivative and grad_input buffer of both layers, in one launch when the upper
+    layer has at most 16 outputs (zn_hip_dense_pair_backward).  grad_input=False skips the lower
+    layer's grad_input (the first layer of a network)."""
+    _pair_check(lower, upper, "pair_backward")
+    lower._gaa_ready = upper._gaa_ready = False
+    lower.ctx.dense_pair_backward(
+        lower.act, x, lower.weights, lower.out, lower.gaa, lower.grad_input if grad_input else None,
+        lower.grad_weights, lower.grad_bias, upper.act, upper.weights, upper.out, grad_out, upper.gaa,
+        upper.grad_input, upper.grad_weights, upper.grad_bias, lower.batch, lower.input_size, lower.output_size,
+        upper.output_size)
+    return lower.grad_input if grad_input else None
