@@ -53,6 +53,18 @@ __device__ __forceinline__ float act_backward_sel(float y, float go, const ActMa
                                          (__builtin_bit_cast(uint32_t, th) & m.th));
 }
 
+// Workgroup b of the grid runs on XCD b % 8 (the dispatcher deals them out
+// in turn); with a grid of whole eights, the ids XCD x runs (x, x + 8, ...)
+// are remapped to the contiguous range [x * G/8, (x + 1) * G/8), so that
+// neighbouring tiles, which share operand blocks, share an L2.  Only the
+// speed depends on this: the forward's 16 strips of C2 (two per XCD) took
+// 6.99 -> 6.92 us; the backward's tiles lost with it (7.08 -> 7.37 us:
+// its grad_x and grad_w1 tiles then crowd half the XCDs each).
+__device__ __forceinline__ int xcd_contiguous(int b) {
+    const int G = (int)gridDim.x;
+    return (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+}
+
 // ---------------------------------------------------------------- forward
 // The lower layer runs on gemm_ksplit16's 16x16 tiles (four waves split K)
 // and stores its block of h = act1(x . W1 + b1).  Each tile then multiplies
@@ -69,7 +81,7 @@ __device__ __forceinline__ float act_backward_sel(float y, float go, const ActMa
 template <int W, int ACT1>
 __device__ __forceinline__ void pair_forward(const ZnPairFwdArgs &a, float *lds) {
     const ZnGemmArgs &p = a.l1;
-    const int pid = blockIdx.x;
+    const int pid = xcd_contiguous((int)blockIdx.x);
     const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
     const int m0 = tm * 16, n0 = tn * 16;
     const int t = threadIdx.x, lane = t & 63;
@@ -86,11 +98,14 @@ __device__ __forceinline__ void pair_forward(const ZnPairFwdArgs &a, float *lds)
         const int k = n0 + 4 * g + s;
         wv[s] = bload(rw, wave == 0 && k < p.n && i < out, k * out + i);
     }
-    float x = gemm_ksplit16_sum<4, true, false, W>(p, lds, m0, n0, 0);
+    // both biases go out before the main loop too, so that their latency hides
     const int row = m0 + (t >> 4), col = n0 + (t & 15);
+    const float b1v = bload(make_rsrc(p.bias, p.bias ? (uint32_t)p.n * 4u : 0u), col < p.n, col);
+    const float b2v = bload(make_rsrc(a.b2, a.b2 ? (uint32_t)out * 4u : 0u), (t & 15) < out, t & 15);
+    float x = gemm_ksplit16_sum<4, true, false, W>(p, lds, m0, n0, 0);
     float hval = 0.0f;
     if (row < p.m && col < p.n) {
-        if (p.bias) x = x + p.bias[col];
+        if (p.bias) x = x + b1v;
         hval = zn_activate(x, ACT1);
         p.c[(int64_t)row * p.ldc + col] = hval;
     }
@@ -132,7 +147,7 @@ __device__ __forceinline__ void pair_forward(const ZnPairFwdArgs &a, float *lds)
     }
     const int r = t >> 4, c = t & 15;
     if (m0 + r < p.m && c < out) {
-        if (a.b2) y = y + a.b2[c];
+        if (a.b2) y = y + b2v;
         a.y[(int64_t)(m0 + r) * out + c] = zn_activate(y, a.act2);
     }
 }
@@ -448,12 +463,13 @@ __device__ __forceinline__ void pair_tile_nt(const ZnPairBwdArgs &a, const PairS
 // grad_w1 = x^T . gaa1 on a 32x32 tile (rows m0: inputs, columns n0:
 // hidden), K = batch: A = x's block staged by DMA (X-contiguous), B = gaa1
 // from the grad_h block over the slice's batch rows and the tile's hidden
-// columns, transposed through LDS into B's fragment layout.  The tiles of
-// the first row (m0 = 0) cover every batch row of their columns between
-// their four waves, so they also write grad_h and gaa1 (stores along the
-// rows, from the transposed blocks) and add the columns' gaa1 sums into
-// grad_b1: lane (n, h) sums its rows of column n in ascending order, and
-// the eight (wave, h) sums are added in that order.
+// columns, transposed through LDS into B's fragment layout.  Every tile
+// covers every batch row of its columns between its four waves, so the
+// tiles of one column share the writes of grad_h and gaa1 (stores along the
+// rows, from the transposed blocks): 32-row block b goes out from the tile
+// in row b % tiles_m.  The first row's tiles (m0 = 0) also add the columns'
+// gaa1 sums into grad_b1: lane (n, h) sums its rows of column n in
+// ascending order, and the eight (wave, h) sums are added in that order.
 template <int WD, int ACT1, int ACT2>
 __device__ __forceinline__ void pair_tile_tn1(const ZnPairBwdArgs &a, const PairSrc &s, float *lds, int wg) {
     const ZnPairGemm &p = a.tn1;  // m = in, n = hidden, k = batch; src = x [batch x in]
@@ -462,6 +478,7 @@ __device__ __forceinline__ void pair_tile_tn1(const ZnPairBwdArgs &a, const Pair
     const int tm = wg / p.tiles_n, tn = wg - tm * p.tiles_n;
     const int m0 = tm * 32, n0 = tn * 32;
     const bool first_row = tm == 0;  // uniform
+    const int tiles_m = (p.m + 31) / 32;
     const PairK K = pair_k(p.k, w.wave);
     constexpr int RD = WD == 16 ? 3 : 0;
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.src, (uint32_t)((p.k - 1) * p.ld + ((p.m + RD) & ~RD)) * 4u);
@@ -473,14 +490,18 @@ __device__ __forceinline__ void pair_tile_tn1(const ZnPairBwdArgs &a, const Pair
     SX::issue(rs, w.st[1], p.ld, m0, K.kbeg + 32, p.m, K.kend, 0, w.lane);
     h_load<WD>(s, K.kbeg + (w.lane & 31), n0, w.lane, hv[0]);
     h_load<WD>(s, K.kbeg + 32 + (w.lane & 31), n0, w.lane, hv[1]);
+    // the first row's old bias gradient, read early so that its latency hides
+    const int t = threadIdx.x;
+    const bool bias_lane = first_row && t < 32 && n0 + t < s.hidden;
+    const float b1_old = bias_lane ? a.grad_b1[n0 + t] : 0.0f;
     raw_store<false>(s, cw, wlen, w.raw_w);
     raw_store<ACT2 != 0>(s, cg, glen, w.raw_g);
     __syncthreads();  // the workgroup's copies are in LDS
     const int n = w.lane & 31, h = w.lane >> 5;
     const int col = n0 + n;
     const int cells = s.batch * s.hidden;
-    const __amdgpu_buffer_rsrc_t rgh = make_rsrc(a.grad_h, first_row ? (uint32_t)cells * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t rga = make_rsrc(a.gaa1, first_row ? (uint32_t)cells * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rgh = make_rsrc(a.grad_h, (uint32_t)cells * 4u);
+    const __amdgpu_buffer_rsrc_t rga = make_rsrc(a.gaa1, (uint32_t)cells * 4u);
     float sum = 0.0f;
     zn_f32x16 acc;
 #pragma unroll
@@ -510,7 +531,7 @@ __device__ __forceinline__ void pair_tile_tn1(const ZnPairBwdArgs &a, const Pair
                 for (int q = 0; q < 4; ++q)
                     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[0][q], gb[4 * e + q], acc, 0, 0, 0);
             }
-            if (first_row) {  // uniform
+            if ((r0 >> 5) % tiles_m == tm) {  // uniform: this tile writes the block
                 float dc[16];
                 transpose_block(d, w.gt, w.lane, dc);
 #pragma unroll
@@ -519,8 +540,11 @@ __device__ __forceinline__ void pair_tile_tn1(const ZnPairBwdArgs &a, const Pair
                     const bool ok = r < s.batch && col < s.hidden;
                     bstore(rgh, ok, r * s.hidden + col, dc[q]);
                     bstore(rga, ok, r * s.hidden + col, gb[q]);
-                    sum = sum + gb[q];  // +0 outside the batch or the columns
                 }
+            }
+            if (first_row) {  // uniform
+#pragma unroll
+                for (int q = 0; q < 16; ++q) sum = sum + gb[q];  // +0 outside the batch or the columns
             }
         }
     }
@@ -528,11 +552,10 @@ __device__ __forceinline__ void pair_tile_tn1(const ZnPairBwdArgs &a, const Pair
         float *red = lds + kPairRed;
         red[w.wave * 64 + w.lane] = sum;
         __syncthreads();
-        const int t = threadIdx.x;
-        if (t < 32 && n0 + t < s.hidden) {
+        if (bias_lane) {
             float total = red[t];
             for (int k = 1; k < 8; ++k) total = total + red[(k >> 1) * 64 + (k & 1) * 32 + t];
-            a.grad_b1[n0 + t] = a.grad_b1[n0 + t] + total;
+            a.grad_b1[n0 + t] = b1_old + total;
         }
     }
     zn_f32x16 accs[1] = {acc};
@@ -557,6 +580,8 @@ __device__ __forceinline__ void pair_tile_tn2(const ZnPairBwdArgs &a, const Pair
     const int j = w.lane & 31, h = w.lane >> 5;
     const int glen = pad32(s.batch) * s.out;
     const RawPart cg = raw_load<ACT2 != 0>(s, s.gy, 0, glen, s.batch * s.out);
+    const bool bias_lane = wg == 0 && (int)threadIdx.x < s.out;
+    const float b2_old = bias_lane ? a.grad_b2[threadIdx.x] : 0.0f;  // read early: its latency hides
     SH::issue(rs, w.st[0], p.ld, m0, K.kbeg, p.m, K.kend, 0, w.lane);
     SH::issue(rs, w.st[1], p.ld, m0, K.kbeg + 32, p.m, K.kend, 0, w.lane);
     raw_store<ACT2 != 0>(s, cg, glen, w.raw_g);
@@ -573,10 +598,10 @@ __device__ __forceinline__ void pair_tile_tn2(const ZnPairBwdArgs &a, const Pair
         float *red = lds + kPairRed;
         red[t] = sum;
         __syncthreads();
-        if (t < s.out) {
+        if (bias_lane) {
             float total = red[t];
             for (int k = 1; k < 16; ++k) total = total + red[k * 16 + t];
-            a.grad_b2[t] = a.grad_b2[t] + total;
+            a.grad_b2[t] = b2_old + total;
         }
     }
     zn_f32x16 acc;

@@ -138,8 +138,9 @@ struct ZnPairGemm {
 // grad_h = gaa2 . W2^T and gaa1 = act1'(h, grad_h) are generated where they
 // are needed (no workgroup waits for another):
 //   [0, wg_nt)    grad_x  = gaa1 . W1^T on 32x64 tiles (nt: W1 staged; none when grad_x is null)
-//   next wg_tn1   grad_w1 = x^T . gaa1 on 32x32 tiles (tn1: x staged); the first row of tiles
-//                 also writes grad_h and gaa1 and adds gaa1's column sums into grad_b1
+//   next wg_tn1   grad_w1 = x^T . gaa1 on 32x32 tiles (tn1: x staged); the tiles of a column
+//                 share the writes of its grad_h and gaa1, and the first row of tiles adds
+//                 gaa1's column sums into grad_b1
 //   next wg_tn2   grad_w2 = h^T . gaa2 (tn2: h staged); the first tile also writes gaa2 and
 //                 adds its column sums into grad_b2
 struct ZnPairBwdArgs {
