@@ -164,6 +164,7 @@ constexpr int kRawW = 2048, kRawG = 4096;  // floats of the W2 and gaa2 copies (
 struct PairSrc {
     __amdgpu_buffer_rsrc_t h, w2, y, gy;
     int batch, hidden, out, act2;
+    bool whole;  // hidden * out and batch * out are multiples of 4: no copy has a straddling float4
     ActMask m2;  // act2 for the bit-select of a non-linear head's derivative
 };
 
@@ -177,6 +178,7 @@ __device__ __forceinline__ PairSrc pair_src(const ZnPairBwdArgs &a) {
     s.hidden = a.hidden;
     s.out = a.out;
     s.act2 = a.act2;
+    s.whole = ((a.hidden * a.out) & 3) == 0 && ((a.batch * a.out) & 3) == 0;
     s.m2 = act_mask(a.act2);
     return s;
 }
@@ -190,8 +192,11 @@ __device__ __forceinline__ zn_f32x4 bload4(__amdgpu_buffer_rsrc_t r, bool ok, in
 // multiple of 4), zero from `valid` on (relative to base); thread t takes
 // floats 4 (t + 256u) .. + 3, u < 4 (len <= 4096), loading whole float4s
 // that lie before `valid` and the one that straddles it float by float.
-// Loaded into registers first (so that every load of the workgroup is in
-// flight together), then written.
+// Every copy's `valid` is a multiple of 4 when s.whole holds (the copies
+// start at multiples of 32 rows and end at the matrix's end): then the
+// straight-line path without the straddle runs.  Loaded into registers
+// first (so that every load of the workgroup is in flight together), then
+// written.
 struct RawPart {
     zn_f32x4 v[4], y[4];
 };
@@ -209,6 +214,16 @@ template <bool GAA>
 __device__ __forceinline__ RawPart raw_load(const PairSrc &s, __amdgpu_buffer_rsrc_t r, int base, int len, int valid) {
     RawPart p;
     const int t = threadIdx.x;
+    if (s.whole) {  // uniform
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = 4 * (t + 256 * u);
+            const bool ok = e < len && e + 4 <= valid;
+            p.v[u] = bload4(r, ok, base + e);
+            if (GAA) p.y[u] = bload4(s.y, ok, base + e);
+        }
+        return p;
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int e = 4 * (t + 256 * u);
@@ -420,9 +435,11 @@ __device__ __forceinline__ void pair_tile_nt(const ZnPairBwdArgs &a, const PairS
     const RawPart cg = raw_load<ACT2 != 0>(s, s.gy, m0 * s.out, glen, (s.batch - m0) * s.out);
     float hv[2][16];
     SW::issue(rs, w.st[0], p.ld, n0, K.kbeg, p.n, K.kend, 0, w.lane);
-    SW::issue(rs, w.st[1], p.ld, n0, K.kbeg + 32, p.n, K.kend, 0, w.lane);
     h_load<WD>(s, row, K.kbeg, w.lane, hv[0]);
-    h_load<WD>(s, row, K.kbeg + 32, w.lane, hv[1]);
+    if (K.ktiles > 1) {  // uniform (one slice per wave for hidden <= 128)
+        SW::issue(rs, w.st[1], p.ld, n0, K.kbeg + 32, p.n, K.kend, 0, w.lane);
+        h_load<WD>(s, row, K.kbeg + 32, w.lane, hv[1]);
+    }
     raw_store<false>(s, cw, wlen, w.raw_w);
     raw_store<ACT2 != 0>(s, cg, glen, w.raw_g);
     __syncthreads();  // the workgroup's copies are in LDS
