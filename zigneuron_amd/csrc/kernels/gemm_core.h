@@ -1375,9 +1375,12 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
     static_assert(FM * FN * 16 * kWave <= kRegion, "a wave's partial tile fits in its staging region");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
-    float *region = lds + wave * kRegion;
-    float *lds_a[2] = {region, region + SA::kFloats};
-    float *lds_b[2] = {region + 2 * SA::kFloats, region + 2 * SA::kFloats + SB::kFloats};
+    // Stage s of A and of B: offsets from the LDS array itself (a pointer
+    // picked from an array of pointers at run time loses its address space,
+    // and the fragment reads became flat loads that also wait for the DMA).
+    float *const region = lds + wave * kRegion;
+    auto stage_a = [region](int s) { return region + s * SA::kFloats; };
+    auto stage_b = [region](int s) { return region + 2 * SA::kFloats + s * SB::kFloats; };
 
     const int pid = wg >= 0 ? wg : (int)blockIdx.x;  // wg >= 0: this workgroup's tile in a grouped launch
     const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
@@ -1404,8 +1407,8 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
     constexpr int kSliceLoads = SA::kPerWave + SB::kPerWave;  // this wave's load instructions per slice
     for (int kt = 0; kt < (PF ? 2 : 1) && kt < ktiles; ++kt) {
-        SA::issue(ra, lds_a[kt], lda, m0, kbeg + kt * BK, p.m, kend, 0, lane);
-        SB::issue(rb, lds_b[kt], ldb, n0, kbeg + kt * BK, p.n, kend, 0, lane);
+        SA::issue(ra, stage_a(kt), lda, m0, kbeg + kt * BK, p.m, kend, 0, lane);
+        SB::issue(rb, stage_b(kt), ldb, n0, kbeg + kt * BK, p.n, kend, 0, lane);
     }
     for (int kt = 0; kt < ktiles; ++kt) {
         const int cur = kt & 1;
@@ -1417,15 +1420,15 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
         } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // slice kt is in this wave's stage
             if (kt + 1 < ktiles) {  // the other stage was last read by slice kt - 1, whose MFMAs consumed those reads
-                SA::issue(ra, lds_a[cur ^ 1], lda, m0, kbeg + (kt + 1) * BK, p.m, kend, 0, lane);
-                SB::issue(rb, lds_b[cur ^ 1], ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, 0, lane);
+                SA::issue(ra, stage_a(cur ^ 1), lda, m0, kbeg + (kt + 1) * BK, p.m, kend, 0, lane);
+                SB::issue(rb, stage_b(cur ^ 1), ldb, n0, kbeg + (kt + 1) * BK, p.n, kend, 0, lane);
             }
         }
 #pragma unroll
         for (int kg = 0; kg < BK; kg += 8) {
             float fa[FM][4], fb[FN][4];
-            read_frags_dma<BM, BK, FM, AK>(lds_a[cur], 0, kg, lane, fa);
-            read_frags_dma<BN, BK, FN, BKC>(lds_b[cur], 0, kg, lane, fb);
+            read_frags_dma<BM, BK, FM, AK>(stage_a(cur), 0, kg, lane, fa);
+            read_frags_dma<BN, BK, FN, BKC>(stage_b(cur), 0, kg, lane, fb);
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1436,8 +1439,8 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
         }
         if (PF && kt + 2 < ktiles) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's fragment reads have returned
-            SA::issue(ra, lds_a[cur], lda, m0, kbeg + (kt + 2) * BK, p.m, kend, 0, lane);
-            SB::issue(rb, lds_b[cur], ldb, n0, kbeg + (kt + 2) * BK, p.n, kend, 0, lane);
+            SA::issue(ra, stage_a(cur), lda, m0, kbeg + (kt + 2) * BK, p.m, kend, 0, lane);
+            SB::issue(rb, stage_b(cur), ldb, n0, kbeg + (kt + 2) * BK, p.n, kend, 0, lane);
         }
     }
 
