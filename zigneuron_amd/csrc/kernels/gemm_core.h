@@ -1707,7 +1707,10 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int FM = WTM / 32, FN = WTN / 32;
-    constexpr bool kVec = !BKC && FN > 1;
+    // A K-contiguous B is read X-permuted (lane j: columns FN j .. FN j + FN - 1),
+    // so that every layout stores FN consecutive columns per lane
+    constexpr bool kXP = BKC && FN > 1;
+    constexpr bool kVec = FN > 1;
     constexpr int kItems = FM * 16;                 // (fm, r) row items of a wave tile
     constexpr int kSpread = 4;                      // slices the stores of a tile are spread over
     constexpr int kGroup = kItems / (2 * kSpread);  // items stored after each k group
@@ -1821,7 +1824,7 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
             for (int kg = 0; kg < BK; kg += 8) {
                 float fa[FM][4], fb[FN][4];
                 read_frags_dma<BM, BK, FM, AK>(la, wm0, kg, lane, fa);
-                read_frags_dma<BN, BK, FN, BKC>(lb, wn0, kg, lane, fb);
+                read_frags_dma<BN, BK, FN, BKC, kXP>(lb, wn0, kg, lane, fb);
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
 #pragma unroll

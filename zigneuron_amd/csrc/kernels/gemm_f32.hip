@@ -141,8 +141,11 @@ ZN_GEMMP_TILE(n, 128, 64, 16, 2, 1, 1)
 ZN_GEMMP_TILE(m, 64, 64, 32, 2, 2, 1)
 
 // Persistent plain GEMMs with deferred stores (gemm_persistent_defer) on
-// the 128x128 tile: zn_sgemmpd_<layout>_l_v.  (On 256x128 tiles they ran
-// at the same speed.)
+// the 128x128 tile, 4 waves of 32x128: zn_sgemmpd_<layout>_l_v.  Each lane
+// then holds 4 consecutive columns of C and stores them as one float4 (C5
+// QK^T 178 -> 169 us against 4 waves of 64x64 storing float2s, 4-byte
+// stores before the X-permuted B fragments).  (On 256x128 tiles of 64x64
+// waves they ran at the same speed.)
 #define ZN_GEMMPD_KERNEL(NAME, BM, BN, WM, WN, AK, BKC)                                          \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, 2) void NAME(ZnGemmArgs p) {           \
         __shared__ __attribute__((aligned(1024))) float lds[2 * (BM + BN) * 16];                 \
@@ -152,7 +155,7 @@ ZN_GEMMP_TILE(m, 64, 64, 32, 2, 2, 1)
     ZN_GEMMPD_KERNEL(zn_sgemmpd_nn_##TILE##_v, BM, BN, WM, WN, true, false)                      \
     ZN_GEMMPD_KERNEL(zn_sgemmpd_nt_##TILE##_v, BM, BN, WM, WN, true, true)                       \
     ZN_GEMMPD_KERNEL(zn_sgemmpd_tn_##TILE##_v, BM, BN, WM, WN, false, false)
-ZN_GEMMPD_TILE(l, 128, 128, 2, 2)
+ZN_GEMMPD_TILE(l, 128, 128, 4, 1)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not

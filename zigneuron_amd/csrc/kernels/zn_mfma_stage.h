@@ -138,14 +138,16 @@ struct DmaStage {
 
 // Fragments from the staged LDS tile: a K-contiguous tile gives one 16-byte
 // read per block (lane i: row w0 + 32f + i, k = kg + 4h .. kg + 4h + 3).
-template <int BX, int BK, int FX, bool KC>
+// XP: lane i of block f takes row w0 + FX * i + f instead, so that a lane
+// holds FX consecutive rows (of B: consecutive columns of C).
+template <int BX, int BK, int FX, bool KC, bool XP = false>
 __device__ __forceinline__ void read_frags_dma(const float *lds, int w0, int kg, int lane, float (&frag)[FX][4]) {
     if constexpr (KC) {
         const int i = lane & 31;
         const int h = lane >> 5;
 #pragma unroll
         for (int f = 0; f < FX; ++f) {
-            const int row = w0 + 32 * f + i;
+            const int row = XP ? w0 + FX * i + f : w0 + 32 * f + i;
             const int slot = (kg / 4 + h) ^ DmaStage<BX, BK, kWave, true, 16>::swz(row);
             const zn_f32x4 v = *reinterpret_cast<const zn_f32x4 *>(lds + row * BK + 4 * slot);
             frag[f][0] = v[0];
