@@ -68,6 +68,7 @@ def test_code_objects_hold_every_kernel():
         for t in ("x", "l", "n", "m"):
             assert f"zn_sgemmp_{lay}_{t}_v".encode() in gemm
         assert f"zn_sgemmpd_{lay}_l_v".encode() in gemm
+        assert f"zn_sgemmpd4_{lay}_l_v".encode() in gemm
         for waves in ("4", "8", "4s"):
             for v in ("", "_v"):
                 assert f"zn_sgemmk{waves}_{lay}{v}".encode() in gemm

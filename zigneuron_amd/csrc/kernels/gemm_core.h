@@ -1701,8 +1701,10 @@ __device__ __forceinline__ void gemm_persistent(const ZnGemmArgs &p, float *lds)
 // flight: the only operations issued after a slice's DMA are those stores,
 // a fixed number (kPerSlice) for an interior tile.  The workgroup's last
 // tile is stored directly.  Each element sums K in the same order as
-// gemm_persistent, so the results are the same bits.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC>
+// gemm_persistent, so the results are the same bits.  KT > 0: K is exactly
+// KT slices (the host checks), so the slice loop unrolls and every store
+// group and wait is fixed at compile time.
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int KT = 0>
 __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float *lds) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -1744,7 +1746,7 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
     }
     if (w >= end) return;  // the host launches at most `total` workgroups
 
-    const int ktiles = (p.k + BK - 1) / BK;  // >= kSpread: the host sends shorter K to gemm_persistent
+    const int ktiles = KT > 0 ? KT : (p.k + BK - 1) / BK;  // >= kSpread: the host sends shorter K to gemm_persistent
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + 3) & ~3) : (p.k - 1) * lda + ((p.m + 3) & ~3)) * 4u;
     const uint32_t b_bytes = (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + 3) & ~3) : (p.k - 1) * ldb + ((p.n + 3) & ~3)) * 4u;
@@ -1804,6 +1806,7 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
         const bool has_next = w + step < end;
+#pragma unroll
         for (int kt = 0; kt < ktiles; ++kt) {
             if (stored_last)
                 vm_wait<kPerSlice>();  // slice kt has landed; the previous slice's stores may still be in flight

@@ -146,16 +146,18 @@ ZN_GEMMP_TILE(m, 64, 64, 32, 2, 2, 1)
 // QK^T 178 -> 169 us against 4 waves of 64x64 storing float2s, 4-byte
 // stores before the X-permuted B fragments).  (On 256x128 tiles of 64x64
 // waves they ran at the same speed.)
-#define ZN_GEMMPD_KERNEL(NAME, BM, BN, WM, WN, AK, BKC)                                          \
+#define ZN_GEMMPD_KERNEL(NAME, BM, BN, WM, WN, AK, BKC, KT)                                      \
     extern "C" __global__ __launch_bounds__(WM *WN * 64, 2) void NAME(ZnGemmArgs p) {           \
         __shared__ __attribute__((aligned(1024))) float lds[2 * (BM + BN) * 16];                 \
-        gemm_persistent_defer<BM, BN, 16, WM, WN, AK, BKC>(p, lds);                              \
+        gemm_persistent_defer<BM, BN, 16, WM, WN, AK, BKC, KT>(p, lds);                          \
     }
-#define ZN_GEMMPD_TILE(TILE, BM, BN, WM, WN)                                                     \
-    ZN_GEMMPD_KERNEL(zn_sgemmpd_nn_##TILE##_v, BM, BN, WM, WN, true, false)                      \
-    ZN_GEMMPD_KERNEL(zn_sgemmpd_nt_##TILE##_v, BM, BN, WM, WN, true, true)                       \
-    ZN_GEMMPD_KERNEL(zn_sgemmpd_tn_##TILE##_v, BM, BN, WM, WN, false, false)
-ZN_GEMMPD_TILE(l, 128, 128, 4, 1)
+#define ZN_GEMMPD_TILE(TILE, BM, BN, WM, WN, KT, S)                                              \
+    ZN_GEMMPD_KERNEL(zn_sgemmpd##S##_nn_##TILE##_v, BM, BN, WM, WN, true, false, KT)             \
+    ZN_GEMMPD_KERNEL(zn_sgemmpd##S##_nt_##TILE##_v, BM, BN, WM, WN, true, true, KT)              \
+    ZN_GEMMPD_KERNEL(zn_sgemmpd##S##_tn_##TILE##_v, BM, BN, WM, WN, false, false, KT)
+ZN_GEMMPD_TILE(l, 128, 128, 4, 1, 0, )
+// zn_sgemmpd4_<layout>_l_v: K of exactly 4 slices (C5 QK^T, K = 64)
+ZN_GEMMPD_TILE(l, 128, 128, 4, 1, 4, 4)
 
 // Split-K finish: C = act((accumulate ? C : 0) + sum over slices s = 0..S-1
 // of ws[s] + bias[col or row]).  Slices are summed in ascending order, so results do not

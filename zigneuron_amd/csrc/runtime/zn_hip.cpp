@@ -174,6 +174,7 @@ struct zn_ctx {
     hipFunction_t gemmk[3][2][2] = {};         // intra-workgroup split-K, 32x32 tiles [layout][4 or 8 waves][16-byte]
     int gemmp_occ[3][kNumTiles] = {};          // its resident workgroups per CU
     hipFunction_t gemmpd[3] = {};              // [layout]: persistent 128x128 with deferred stores
+    hipFunction_t gemmpd4[3] = {};             // [layout]: the same for K of exactly 4 slices
     int gemmpd_occ[3] = {};
     int gemmpd_threads[3] = {};                // its workgroup size (the kernel's launch bound)
     hipFunction_t splitk_reduce = nullptr;
@@ -971,7 +972,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
             // each XCD walks a contiguous run of items: C5 QK^T fetched 302 MB
             // per launch, 68 MB with the remap (Q and K are 64 MB), 2% faster
             if (grid >= 8) part.xcd_remap = 3;
-            return launch(ctx, ctx->gemmpd[layout], (unsigned)grid, 1, (unsigned)ctx->gemmpd_threads[layout], &part);
+            hipFunction_t fd = cdiv(k, 16) == 4 ? ctx->gemmpd4[layout] : ctx->gemmpd[layout];
+            return launch(ctx, fd, (unsigned)grid, 1, (unsigned)ctx->gemmpd_threads[layout], &part);
         }
         const int64_t resident = cus * ctx->gemmp_occ[layout][tile];
         if (total <= INT_MAX &&
@@ -1633,6 +1635,8 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
         char name[64];
         std::snprintf(name, sizeof(name), "zn_sgemmpd_%s_l_v", kLayoutName[l]);
         if (hipModuleGetFunction(&ctx->gemmpd[l], ctx->gemm_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
+        std::snprintf(name, sizeof(name), "zn_sgemmpd4_%s_l_v", kLayoutName[l]);
+        if (hipModuleGetFunction(&ctx->gemmpd4[l], ctx->gemm_module, name) != hipSuccess) return bail(ZN_ERR_SYMBOL);
         int threads = 0, occ = 0;
         if (hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, ctx->gemmpd[l]) != hipSuccess ||
             threads < 64)
