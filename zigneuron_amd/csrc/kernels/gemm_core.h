@@ -1758,13 +1758,84 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
         m0 = tm * BM;
         n0 = (pid - tm * p.tiles_n) * BN;
     };
-    auto issue = [&](int bz, int m0, int n0, int k0, int st) {
-        SA::issue(make_rsrc(p.a + (int64_t)bz * p.stride_a, a_bytes), lds_a[st], lda, m0, k0, p.m, p.k, wave, lane);
-        SB::issue(make_rsrc(p.b + (int64_t)bz * p.stride_b, b_bytes), lds_b[st], ldb, n0, k0, p.n, p.k, wave, lane);
+    // The lane's DMA byte offsets at k = 0 of a tile are computed once per
+    // tile (masked on M and N); slice s adds s times an increment, and K is
+    // masked only in a partial last slice (an out-of-range offset plus
+    // s * inc stays past the operand, which is below 2^31 bytes).
+    constexpr int LA = SA::kPerWave, LB = SB::kPerWave;
+    const uint32_t inca = (uint32_t)(AK ? BK : BK * lda) * 4u, incb = (uint32_t)(BKC ? BK : BK * ldb) * 4u;
+    auto chunk = [&](int q, int kwaves, int per_inst) { return (q * kwaves + wave) * per_inst + 4 * lane; };
+    auto tile_offsets = [&](int m0, int n0, uint32_t(&oa)[LA], uint32_t(&ob)[LB]) {
+#pragma unroll
+        for (int q = 0; q < LA; ++q) {
+            const int c = chunk(q, SA::kWaves, SA::kPerInst);
+            const int outer = AK ? m0 + c / BK : c / BM;
+            const int inner = AK ? 4 * (((c % BK) / 4) ^ SA::swz(c / BK)) : m0 + c % BM;
+            oa[q] = (AK ? outer < p.m : inner < p.m) ? (uint32_t)(outer * lda + inner) * 4u : kOutOfRange;
+        }
+#pragma unroll
+        for (int q = 0; q < LB; ++q) {
+            const int c = chunk(q, SB::kWaves, SB::kPerInst);
+            const int outer = BKC ? n0 + c / BK : c / BN;
+            const int inner = BKC ? 4 * (((c % BK) / 4) ^ SB::swz(c / BK)) : n0 + c % BN;
+            ob[q] = (BKC ? outer < p.n : inner < p.n) ? (uint32_t)(outer * ldb + inner) * 4u : kOutOfRange;
+        }
     };
-    // non-temporal stores of row items [i0, i1) of v, a tile at (bz, m0, n0)
+    const uint32_t lds_a0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)&lds_a[0][0]);
+    const uint32_t lds_b0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)&lds_b[0][0]);
+    auto issue = [&](int bz, const uint32_t(&oa)[LA], const uint32_t(&ob)[LB], int s, int st) {
+        const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)bz * p.stride_a, a_bytes);
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + (int64_t)bz * p.stride_b, b_bytes);
+        const int k0 = s * BK;
+        const bool partial = k0 + BK > p.k;
+#pragma unroll
+        for (int q = 0; q < LA; ++q) {
+            uint32_t off = oa[q] + (uint32_t)s * inca;
+            if (partial) {
+                const int c = chunk(q, SA::kWaves, SA::kPerInst);
+                const int kk = AK ? k0 + 4 * (((c % BK) / 4) ^ SA::swz(c / BK)) : k0 + c / BM;
+                if (kk >= p.k) off = kOutOfRange;
+            }
+            const uint32_t dst = lds_a0 + (uint32_t)(st * SA::kFloats + (q * SA::kWaves + wave) * SA::kPerInst) * 4u;
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "s"(dst), "v"(off), "s"(ra) : "memory");
+        }
+#pragma unroll
+        for (int q = 0; q < LB; ++q) {
+            uint32_t off = ob[q] + (uint32_t)s * incb;
+            if (partial) {
+                const int c = chunk(q, SB::kWaves, SB::kPerInst);
+                const int kk = BKC ? k0 + 4 * (((c % BK) / 4) ^ SB::swz(c / BK)) : k0 + c / BN;
+                if (kk >= p.k) off = kOutOfRange;
+            }
+            const uint32_t dst = lds_b0 + (uint32_t)(st * SB::kFloats + (q * SB::kWaves + wave) * SB::kPerInst) * 4u;
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "s"(dst), "v"(off), "s"(rb) : "memory");
+        }
+    };
+    // Non-temporal stores of row items [i0, i1) of v, a tile at (bz, m0, n0):
+    // buffer stores into one problem's C (below 2^31 bytes), the lane's byte
+    // offset at the wave tile's first row in a vector register and each
+    // item's row offset in a scalar one, so an item costs its store alone.
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int kNt = 2;  // the nt cache-policy bit of the raw buffer builtins
+    const uint32_t ldc4 = (uint32_t)p.ldc * 4u;
+    const uint32_t c_bytes = (uint32_t)((p.m - 1) * p.ldc + p.n) * 4u;
     auto store_items = [&](const zn_f32x16(&v)[FM][FN], int bz, int m0, int n0, int i0, int i1) {
         float *gc = p.c + (int64_t)bz * p.stride_c;
+        if constexpr (kVec && FN == 4) {
+            const __amdgpu_buffer_rsrc_t rc = make_rsrc(gc, c_bytes);
+            const uint32_t voff =
+                ((uint32_t)(m0 + wm0 + (AK ? 4 * h : FM * 4 * h)) * (uint32_t)p.ldc + (uint32_t)(n0 + wn0 + FN * j)) * 4u;
+#pragma unroll
+            for (int it = 0; it < kItems; ++it) {
+                if (it < i0 || it >= i1) continue;
+                const int fm = it >> 4, r = it & 15;
+                const int rr = 8 * (r >> 2) + (r & 3);
+                const int irow = AK ? 32 * fm + rr : FM * rr + fm;
+                const zn_f32x4 x = {v[fm][0][r], v[fm][1][r], v[fm][2][r], v[fm][3][r]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rc, voff, (uint32_t)irow * ldc4, kNt);
+            }
+            return;
+        }
 #pragma unroll
         for (int it = 0; it < kItems; ++it) {
             if (it < i0 || it >= i1) continue;
@@ -1790,15 +1861,15 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
     int pbz = 0, pm0 = 0, pn0 = 0;
     bool pending = false;      // pend holds a tile to store during this tile's first kSpread slices
     bool stored_last = false;  // the previous slice issued stores after this slice's DMA
-    {
-        int bz, m0, n0;
-        decode(w, bz, m0, n0);
-        issue(bz, m0, n0, 0, 0);
-    }
+    int bz, m0, n0;            // the current tile, and its DMA offsets
+    uint32_t ca[LA], cb[LB];
+    decode(w, bz, m0, n0);
+    tile_offsets(m0, n0, ca, cb);
+    issue(bz, ca, cb, 0, 0);
     int stage = 0;
     for (;;) {
-        int bz, m0, n0;
-        decode(w, bz, m0, n0);
+        int nbz = 0, nm0 = 0, nn0 = 0;  // the next tile, and its DMA offsets
+        uint32_t na[LA], nb[LB];
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
@@ -1815,11 +1886,11 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
             stored_last = pending && kt < kSpread;
             __syncthreads();  // every wave's part of this stage is in LDS; the other stage is free
             if (kt + 1 < ktiles) {
-                issue(bz, m0, n0, (kt + 1) * BK, stage ^ 1);
+                issue(bz, ca, cb, kt + 1, stage ^ 1);
             } else if (has_next) {  // the next tile's first slice
-                int bz2, m2, n2;
-                decode(w + step, bz2, m2, n2);
-                issue(bz2, m2, n2, 0, stage ^ 1);
+                decode(w + step, nbz, nm0, nn0);
+                tile_offsets(nm0, nn0, na, nb);
+                issue(nbz, na, nb, 0, stage ^ 1);
             }
             const float *la = lds_a[stage];
             const float *lb = lds_b[stage];
@@ -1855,6 +1926,13 @@ __device__ __forceinline__ void gemm_persistent_defer(const ZnGemmArgs &p, float
         pn0 = n0;
         pending = true;
         w += step;
+        bz = nbz;
+        m0 = nm0;
+        n0 = nn0;
+#pragma unroll
+        for (int q = 0; q < LA; ++q) ca[q] = na[q];
+#pragma unroll
+        for (int q = 0; q < LB; ++q) cb[q] = nb[q];
     }
 }
 
