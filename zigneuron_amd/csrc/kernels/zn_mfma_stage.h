@@ -87,8 +87,17 @@ struct DmaStage {
         else return row & 15;  // one row spans 256 bytes or more
     }
 
+    // Instruction j of a wave covers outer indices kStep further than
+    // instruction j - 1 (its inner index, which the swizzle may change, is
+    // computed as before), so outer * ld is the first instruction's plus
+    // j * kStep * ld: one multiply per stage, not per load.
+    static constexpr int kStep = KC ? kWaves * kPerInst / BK : kWaves * kPerInst / BX;
+    static constexpr bool kStrided = (KC ? (kWaves * kPerInst) % BK : (kWaves * kPerInst) % BX) == 0;
+
     __device__ static __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, float *lds, int ld, int x0, int k0,
                                                  int xmax, int kmax, int wave, int lane) {
+        const int step_ld = kStep * ld;
+        int outer_ld0 = 0;  // outer * ld of instruction 0
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
             const int p0 = (j * kWaves + wave) * kPerInst;  // first LDS float this instruction writes
@@ -119,7 +128,14 @@ struct DmaStage {
                 }
                 ok = outer < (KC ? xmax : kmax) && inner < (KC ? kmax : xmax);
             }
-            const uint32_t off = ok ? (uint32_t)(outer * ld + inner) * 4u : kOutOfRange;
+            int lin;
+            if constexpr (kStrided) {
+                if (j == 0) outer_ld0 = outer * ld;
+                lin = outer_ld0 + j * step_ld + inner;
+            } else {
+                lin = outer * ld + inner;
+            }
+            const uint32_t off = ok ? (uint32_t)lin * 4u : kOutOfRange;
             const uint32_t lds_addr = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(zn_lds_void *)(lds + p0));
             if constexpr (W == 16)
                 asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
