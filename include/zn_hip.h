@@ -2,7 +2,7 @@
  * zn_hip.h -- C ABI of the MI355X (gfx950) fp32 GEMM backend for ZigNeuron.
  *
  * This is the drop-in boundary a Zig `HipBackend` binds with `extern fn`
- * declarations (the binding stub is shown in INTEGRATION.md).  It replaces the
+ * declarations (zig/hip.zig holds them).  It replaces the
  * reference's CUDA stack for the GEMM path: the driver binding
  * (src/cuda_driver.zig:632-931), NVRTC (src/cuda_nvrtc.zig), the device
  * context (src/cuda_context.zig:382-1820) and the CudaBackend GEMM wrappers
