@@ -67,6 +67,11 @@ def time_launches(ctx, fn, steps, warmup, runs=RUNS):
     launches ran up to 5% slower), `runs` timed runs, each the mean per call
     of `steps` back-to-back calls; calls of 0.5 ms or more are timed one per
     run (the reference's convention, src/benchmark/cuda_benchmark.zig:220-231).
+    Each run is queued behind zn_hip_hold_stream, a one-wave kernel that keeps
+    the stream busy for longer than the host takes to queue the run, so the
+    run's calls execute back to back from the device queue: the events time
+    the device, not the host's submission rate (without it, runs of 6 us
+    kernels read 5.9 to 11 us from one run to the next).
     best_of_3: the fastest of the first three runs (the statistic reported
     before the median)."""
     for _ in range(warmup):
@@ -77,14 +82,20 @@ def time_launches(ctx, fn, steps, warmup, runs=RUNS):
     fn()
     e1.record()
     first = max(e0.elapsed_ms(e1), 1e-3)
-    for _ in range(min(5000, int(100.0 / first))):
+    t = time.perf_counter()
+    settle = min(5000, int(100.0 / first))
+    for _ in range(settle):
         fn()
+    host_us = (time.perf_counter() - t) * 1e6 / max(settle, 1)  # an upper bound of the host's time per call
     calls = 1 if first >= 0.5 else steps
     times = []
     for _ in range(runs):
+        ctx.hold_stream(min(50000.0, 30.0 + 2.0 * host_us * calls))
         e0.record()
+        t = time.perf_counter()
         for _ in range(calls):
             fn()
+        host_us = max(host_us, (time.perf_counter() - t) * 1e6 / calls)
         e1.record()
         times.append(e0.elapsed_ms(e1) / calls)
     e0.close()

@@ -126,6 +126,12 @@ int zn_hip_d2h_async(zn_ctx *ctx, void *dst, const void *src, size_t bytes);
 int zn_hip_fill_f32(zn_ctx *ctx, float *dst, float value, int64_t count);
 /* Device-to-device copy of `count` floats with a plain streaming kernel. */
 int zn_hip_copy_f32(zn_ctx *ctx, float *dst, const float *src, int64_t count);
+/* Keep the context's stream busy for `microseconds` (at most 100000) with a
+ * one-wave kernel that sleeps on the device clock.  No counterpart in the
+ * reference: a measurement aid for timing small kernels, so that launches
+ * queued behind it run back to back from the device queue, whatever the
+ * host's submission rate. */
+int zn_hip_hold_stream(zn_ctx *ctx, float microseconds);
 /* Wait for all work on the context's stream. */
 int zn_hip_sync(zn_ctx *ctx);
 

@@ -85,7 +85,8 @@ def test_code_objects_hold_every_kernel():
     for k in ("zn_splitk_reduce", "zn_dense_bwd_m", "zn_dense_bwd_m_v", "zn_dense_bwd_k", "zn_dense_bwd_k_v"):
         assert k.encode() in gemm
     for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",
-              "zn_accumulate_bias", "zn_im2col", "zn_softmax_rows", "zn_col2im", "zn_row_sum", "zn_dense_grad_prologue"):
+              "zn_accumulate_bias", "zn_im2col", "zn_softmax_rows", "zn_col2im", "zn_row_sum", "zn_dense_grad_prologue",
+              "zn_hold_stream"):
         assert k.encode() in elt
     for d in (32, 64, 128):
         for v in ("", "_v"):

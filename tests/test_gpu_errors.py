@@ -110,3 +110,30 @@ def test_setup_fault_hook_needs_the_opt_in(monkeypatch):
         assert_close(out.reshape(m, n), ref_gemm("nn", a, b, m, n, k), "nn", a, b, m, n, k, what="hook off")
     finally:
         c.close()
+
+
+def test_hold_stream_waits_on_the_device_and_checks_its_argument():
+    """zn_hip_hold_stream (the timing aid that keeps the stream busy while
+    the host queues launches): the events around a 300 us hold read at least
+    300 us and well under a millisecond; a negative or over-long hold is
+    refused before anything is launched."""
+    from zigneuron_amd import Context, InvalidArgumentError
+    c = Context(0)
+    try:
+        announce("hold_stream 300 us")
+        e0, e1 = c.event(), c.event()
+        c.hold_stream(1.0)
+        c.sync()
+        e0.record()
+        c.hold_stream(300.0)
+        e1.record()
+        ms = e0.elapsed_ms(e1)
+        assert 0.3 <= ms < 1.0, ms
+        e0.close()
+        e1.close()
+        for bad in (-1.0, 100001.0, float("nan")):
+            with pytest.raises(InvalidArgumentError):
+                c.hold_stream(bad)
+        c.sync()
+    finally:
+        c.close()

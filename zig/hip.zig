@@ -53,6 +53,7 @@ pub extern fn zn_hip_h2d_async(ctx: ?*Ctx, dst: ?*anyopaque, src: ?*const anyopa
 pub extern fn zn_hip_d2h_async(ctx: ?*Ctx, dst: ?*anyopaque, src: ?*const anyopaque, bytes: usize) c_int;
 pub extern fn zn_hip_fill_f32(ctx: ?*Ctx, dst: ?[*]f32, value: f32, count: i64) c_int;
 pub extern fn zn_hip_copy_f32(ctx: ?*Ctx, dst: ?[*]f32, src: ?[*]const f32, count: i64) c_int;
+pub extern fn zn_hip_hold_stream(ctx: ?*Ctx, microseconds: f32) c_int;
 pub extern fn zn_hip_sync(ctx: ?*Ctx) c_int;
 
 // --------------------------------------------------------- graphs, events

@@ -112,6 +112,7 @@ SIGNATURES = {
     "zn_hip_d2h_async": (I, [P, P, P, S]),
     "zn_hip_fill_f32": (I, [P, P, F, I64]),
     "zn_hip_copy_f32": (I, [P, P, P, I64]),
+    "zn_hip_hold_stream": (I, [P, F]),
     "zn_hip_sync": (I, [P]),
     "zn_hip_graph_begin": (I, [P]),
     "zn_hip_graph_end": (I, [P, ctypes.POINTER(P)]),

@@ -206,6 +206,11 @@ class Context:
         check(L.zn_hip_graph_end(self.handle, ctypes.byref(h)), "zn_hip_graph_end")
         return Graph(self, h)
 
+    def hold_stream(self, microseconds: float) -> None:
+        """Keep the context stream busy for `microseconds` (a timing aid: launches queued behind it run back
+        to back on the device)."""
+        check(_lib.load().zn_hip_hold_stream(self.handle, float(microseconds)), "zn_hip_hold_stream")
+
     def copy(self, dst: int, src: int, count: int) -> None:
         check(_lib.load().zn_hip_copy_f32(self.handle, int(dst), int(src), int(count)), "zn_hip_copy_f32")
 

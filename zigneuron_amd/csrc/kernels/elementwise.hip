@@ -459,3 +459,18 @@ extern "C" __global__ __launch_bounds__(256) void zn_softmax_rows(ZnEltArgs p) {
         }
     }
 }
+
+// One wave that returns after p.value microseconds (read from the 100 MHz
+// constant clock, s_memrealtime), sleeping in between.  It keeps a stream
+// busy while the host queues the launches that follow it, so that those run
+// back to back from the queue and their timing measures the device, not the
+// rate at which the host submits (the "blocking kernel" of GPU benchmark
+// harnesses).  At most p.n sleeps: the wait ends even if the clock stalls.
+extern "C" __global__ __launch_bounds__(64) void zn_hold_stream(ZnEltArgs p) {
+    const uint64_t start = __builtin_amdgcn_s_memrealtime();
+    const uint64_t ticks = (uint64_t)(p.value * 100.0f);
+    for (int64_t i = 0; i < p.n; ++i) {
+        __builtin_amdgcn_s_sleep(8);
+        if (__builtin_amdgcn_s_memrealtime() - start >= ticks) break;
+    }
+}

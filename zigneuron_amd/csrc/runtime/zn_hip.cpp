@@ -65,12 +65,13 @@ constexpr TileShape kTiles[kNumTiles] = {{256, 128, 16, 512, "x", true, true, tr
                                          {256, 256, 16, 512, "w", false, false, false}};
 constexpr const char *kLayoutName[3] = {"nn", "nt", "tn"};
 
-enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kPack, kToNhwc, kNumElt };
+enum EltKernel { kFill, kCopy, kAddBias, kActFwd, kActBwd, kAccBias, kIm2col, kSoftmax, kCol2im, kRowSum, kDenseGrad, kRegroup, kPack, kToNhwc, kHold, kNumElt };
 constexpr const char *kEltName[kNumElt] = {"zn_fill_f32",        "zn_copy_f32", "zn_add_bias",
                                            "zn_activation_forward", "zn_activation_backward",
                                            "zn_accumulate_bias", "zn_im2col",   "zn_softmax_rows",
                                            "zn_col2im",          "zn_row_sum",  "zn_dense_grad_prologue",
-                                           "zn_weight_regroup", "zn_pack_rows", "zn_nchw_to_nhwc"};
+                                           "zn_weight_regroup", "zn_pack_rows", "zn_nchw_to_nhwc",
+                                           "zn_hold_stream"};
 
 constexpr const char *kGemmObject = "zn_gemm_gfx950.hsaco";
 constexpr const char *kConvObject = "zn_conv_gfx950.hsaco";
@@ -1802,6 +1803,18 @@ int zn_hip_copy_f32(zn_ctx *ctx, float *dst, const float *src, int64_t count) {
     a.rows = 1;
     a.n = count;
     return elt_launch(ctx, kCopy, (count + 3) / 4, a);
+}
+
+int zn_hip_hold_stream(zn_ctx *ctx, float microseconds) {
+    if (!ctx || !(microseconds >= 0.0f) || microseconds > 100000.0f) return ZN_ERR_INVALID_ARG;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    ZnEltArgs a = {};
+    a.value = microseconds;
+    // one sleep of 8 x 64 clocks is at least 0.2 us below 2.6 GHz: the cap
+    // is several times the requested wait
+    a.n = (int64_t)(microseconds * 20.0f) + 64;
+    return launch(ctx, ctx->elt[kHold], 1, 1, 64, &a);
 }
 
 int zn_hip_sync(zn_ctx *ctx) {
