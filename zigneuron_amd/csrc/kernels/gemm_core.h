@@ -1062,7 +1062,17 @@ __device__ __forceinline__ void gemm_tile_pinned(const ZnGemmArgs &p, int wg = -
 //    beyond the end of K reads zeros, without branches.
 // Each element sums K in the same order as the other tiles, so results are
 // bit-identical to them.
-template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int G = kGNone>
+//  * UA (the _u kernels): rows that are not whole float4s, loaded as they
+//    lie with 16-byte loads at 4-byte aligned offsets, which gfx950 serves.
+//    Each buffer spans the operand exactly; the range check is per dword,
+//    so a load that runs past the end returns zeros for the dwords beyond
+//    it and the data before it.  A load of an X-contiguous operand that
+//    runs past X reads the next row's first values into columns (or rows)
+//    of C that are never stored.  A load of a K-contiguous operand that
+//    runs past K reads the next row's first values as k >= K: those are set
+//    to zero in registers before the LDS write (an Inf or NaN there would
+//    otherwise reach C through a product with a zero).
+template <int BM, int BN, int BK, int WM, int WN, bool AK, bool BKC, int G = kGNone, bool UA = false>
 __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1) {
     constexpr int NT = WM * WN * kWave;
     constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -1094,9 +1104,11 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
     const int kend = min(p.k, kbeg + p.k_chunk);
     const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
-    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + 3) & ~3) : (p.k - 1) * lda + ((p.m + 3) & ~3)) * 4u;
+    static_assert(!(UA && NHWCW), "unaligned rows: plain operands only");
+    constexpr int RU = UA ? 0 : 3;  // whole float4 rows are padded to a multiple of 4 (packed copies)
+    const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RU) & ~RU) : (p.k - 1) * lda + ((p.m + RU) & ~RU)) * 4u;
     const uint32_t b_bytes = NHWCW ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
-                                   : (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + 3) & ~3) : (p.k - 1) * ldb + ((p.n + 3) & ~3)) * 4u;
+                                   : (uint32_t)(BKC ? (p.n - 1) * ldb + ((p.k + RU) & ~RU) : (p.k - 1) * ldb + ((p.n + RU) & ~RU)) * 4u;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + bz * p.stride_a, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + bz * p.stride_b, b_bytes);
 
@@ -1134,11 +1146,20 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
         if (NHWCW && j >= LA) off = SNW::offset(p.conv, clnw, kbeg + s * BK, kend, wave, j - LA);
         g[j] = __builtin_bit_cast(zn_f32x4, __builtin_amdgcn_raw_buffer_load_b128(j < LA ? ra : rb, off, 0, 0));
     };
-    auto write = [&](int st, int j) {
+    // write load j of slice s into stage st
+    auto write = [&](int st, int j, int s) {
+        zn_f32x4 v = g[j];
+        if constexpr (UA) {
+            if ((AK && j < LA) || (BKC && j >= LA)) {  // K-contiguous: zero the values at k >= kend
+                const int rem = klen - (s * BK + kq[j]);
+#pragma unroll
+                for (int e = 1; e < 4; ++e) v[e] = e < rem ? v[e] : 0.0f;
+            }
+        }
         if (j < LA)
-            *reinterpret_cast<zn_f32x4 *>(&lds_a[st][chunk(j, SA::kWaves, SA::kPerInst)]) = g[j];
+            *reinterpret_cast<zn_f32x4 *>(&lds_a[st][chunk(j, SA::kWaves, SA::kPerInst)]) = v;
         else
-            *reinterpret_cast<zn_f32x4 *>(&lds_b[st][chunk(j - LA, SB::kWaves, SB::kPerInst)]) = g[j];
+            *reinterpret_cast<zn_f32x4 *>(&lds_b[st][chunk(j - LA, SB::kWaves, SB::kPerInst)]) = v;
     };
 
     zn_f32x16 acc[FM][FN];
@@ -1180,7 +1201,7 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
     auto slice_step = [&](int kt, auto sc) {
         constexpr int S = decltype(sc)::value;
         auto wr = [&](int x) {
-            if (x < L) write(S ^ 1, x);
+            if (x < L) write(S ^ 1, x, kt + 1);
         };
         auto ld = [&](int x) {
             if (x < L) load(kt + 2, x);
@@ -1195,7 +1216,7 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
 #pragma unroll
         for (int j = 0; j < L; ++j) load(0, j);
 #pragma unroll
-        for (int j = 0; j < L; ++j) write(0, j);
+        for (int j = 0; j < L; ++j) write(0, j, 0);
 #pragma unroll
         for (int j = 0; j < L; ++j) load(1, j);
         __syncthreads();

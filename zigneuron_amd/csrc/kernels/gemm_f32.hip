@@ -56,6 +56,16 @@ ZN_GEMM_LAYOUTS(r, gemm_tile_pinned, 128, 128, 32, 4, 2, 1, false, )
 ZN_GEMM_R_WIDE(nn, true, false)
 ZN_GEMM_R_WIDE(nt, true, true)
 ZN_GEMM_R_WIDE(tn, false, false)
+// zn_sgemm_<layout>_r_u: the same loop for rows that are not whole float4s,
+// loaded as they lie with 16-byte loads (gemm_tile_wide's UA), instead of
+// packed copies or 4-byte loads
+#define ZN_GEMM_R_UNALIGNED(LAYOUT, AK, BKC)                                                     \
+    extern "C" __global__ __launch_bounds__(512, 1) void zn_sgemm_##LAYOUT##_r_u(ZnGemmArgs p) { \
+        gemm_tile_wide<128, 128, 16, 2, 4, AK, BKC, kGNone, true>(p);                            \
+    }
+ZN_GEMM_R_UNALIGNED(nn, true, false)
+ZN_GEMM_R_UNALIGNED(nt, true, true)
+ZN_GEMM_R_UNALIGNED(tn, false, false)
 ZN_GEMM_TILE(h, gemm_tile_pinned, 64, 64, 16, 2, 2, 2)
 
 #define ZN_GEMM_WIDE(LAYOUT, AK, BKC)                                                            \

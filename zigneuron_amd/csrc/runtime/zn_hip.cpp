@@ -160,8 +160,8 @@ struct zn_ctx {
     hipFunction_t pair_fwd[2] = {};            // fused two-layer Dense forward [16-byte staging]
     hipFunction_t pair_bwd[4][2][2] = {};      // fused two-layer Dense backward [lower act][non-linear head][16-byte]
     hipFunction_t attn[3][2] = {};             // fused attention [head dim 32/64/128][16-byte I/O]
-    hipFunction_t gemm[3][kNumTiles][2] = {};  // [layout][tile][16-byte staging]
-    int gemm_threads[3][kNumTiles][2] = {};    // their workgroup sizes (the kernels' launch bounds)
+    hipFunction_t gemm[3][kNumTiles][3] = {};  // [layout][tile][staging: 4-byte, 16-byte, 16-byte unaligned (r only)]
+    int gemm_threads[3][kNumTiles][3] = {};    // their workgroup sizes (the kernels' launch bounds)
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
@@ -700,6 +700,39 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     const int64_t tiles_m = cdiv(m, ts.bm), tiles_n = cdiv(n, ts.bn);
     if (tiles_m * tiles_n > INT_MAX) return ZN_ERR_OVERFLOW;
 
+    // Row tail: when the last row of tiles is what puts one more workgroup on
+    // the busiest CU (1040 tiles of 64x64 for 4097 x 1023: 5 on some CUs, 4
+    // on the rest), the rows above it run as one GEMM and the tail rows as a
+    // second, small one (usually the intra-workgroup split-K kernel).  Each
+    // part is an ordinary GEMM of its rows, so no element changes its K order
+    // in the first part.  Each part then makes its own staging choices.
+    if (split_rows && !conv && batch == 1 && k > 0 && ctx->forced_tile < 0 && ctx->forced_splits == 0 &&
+        ctx->forced_wave_split < 0 && tiles_m >= 2) {
+        const int64_t cus = cus_now(ctx);
+        const int64_t ntiles_all = tiles_m * tiles_n;
+        const int64_t per_cu = cdiv(ntiles_all, cus);
+        if (per_cu >= 2 && cdiv(ntiles_all - tiles_n, cus) < per_cu) {
+            const int64_t m_main = (tiles_m - 1) * ts.bm;
+            int rc = gemm_launch_ex(ctx, layout, m_main, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias,
+                                    act, bias_rows, nullptr, mode, false, padded);
+            if (rc) return rc;
+            const float *a_tail = layout == ZN_LAYOUT_TN ? a + m_main : a + m_main * lda;
+            return gemm_launch_ex(ctx, layout, m - m_main, n, k, a_tail, lda, 0, b, ldb, 0, c + m_main * ldc, ldc, 0, 1,
+                                  accumulate, bias_rows ? bias + m_main : bias, act, bias_rows, nullptr, mode, false,
+                                  padded);
+        }
+    }
+    // The 128x128 register-staged tile loads rows that are not whole float4s
+    // as they lie, 16 bytes at a time (the _u kernels), unless the problem
+    // takes the intra-workgroup split-K kernels below: no packed copies, no
+    // 4-byte staging.
+    const bool wave_split_possible =
+        !conv && k > 0 &&
+        (ctx->forced_wave_split > 0 ||
+         (ctx->forced_wave_split < 0 && ctx->forced_tile < 0 && ctx->forced_splits == 0 &&
+          cdiv(m, 32) * cdiv(n, 32) * batch <= cus_now(ctx) && k >= 64 && k <= 4096));
+    const bool unaligned = !conv && tile == kTileR && !native_vec && k > 0 && !wave_split_possible;
+
     // Operands whose rows are not 16-byte aligned whole float4s would be
     // staged with 4-byte loads (4x the load instructions).  For large single
     // problems they are first copied into zero-padded aligned rows (C4
@@ -709,7 +742,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     Lease pack_a(ctx), pack_b(ctx);
     // rows padded with zeros to whole float4s (here, or by the caller: padded bit 0 = A, bit 1 = B)
     bool a_packed = (padded & 1) != 0, b_packed = (padded & 2) != 0;
-    if (!conv && !ctx->no_alloc && batch == 1 && k > 0 && (double)m * n * k >= kPackMinMacs) {
+    if (!conv && !unaligned && !ctx->no_alloc && batch == 1 && k > 0 && (double)m * n * k >= kPackMinMacs) {
         const bool a_vec = aligned16(a) && lda % 4 == 0 && a_row % 4 == 0;
         const bool b_vec = aligned16(b) && ldb % 4 == 0 && b_row % 4 == 0;
         // both packings go into one launch (blockIdx.y selects the operand)
@@ -787,28 +820,6 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     if (rc) return rc;
     constexpr int64_t kMaxGridY = 65535;
     const int64_t chunk_batch = batch < kMaxGridY ? batch : kMaxGridY;
-    // Row tail: when the last row of tiles is what puts one more workgroup on
-    // the busiest CU (1040 tiles of 64x64 for 4097 x 1023: 5 on some CUs, 4
-    // on the rest), the rows above it run as one GEMM and the tail rows as a
-    // second, small one (usually the intra-workgroup split-K kernel).  Each
-    // part is an ordinary GEMM of its rows, so no element changes its K order
-    // in the first part.
-    if (split_rows && !conv && batch == 1 && k > 0 && ctx->forced_tile < 0 && ctx->forced_splits == 0 &&
-        ctx->forced_wave_split < 0 && tiles_m >= 2) {
-        const int64_t cus = cus_now(ctx);
-        const int64_t per_cu = cdiv(ntiles, cus);
-        if (per_cu >= 2 && cdiv(ntiles - tiles_n, cus) < per_cu) {
-            const int64_t m_main = (tiles_m - 1) * ts.bm;
-            const int pad = (a_packed ? 1 : 0) | (b_packed ? 2 : 0);  // the packed copies stay leased until return
-            rc = gemm_launch_ex(ctx, layout, m_main, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias, act,
-                                bias_rows, nullptr, mode, false, pad);
-            if (rc) return rc;
-            const float *a_tail = layout == ZN_LAYOUT_TN ? a + m_main : a + m_main * lda;
-            return gemm_launch_ex(ctx, layout, m - m_main, n, k, a_tail, lda, 0, b, ldb, 0, c + m_main * ldc, ldc, 0, 1,
-                                  accumulate, bias_rows ? bias + m_main : bias, act, bias_rows, nullptr, mode, false,
-                                  pad);
-        }
-    }
     int splits;
     if (ctx->forced_splits > 0) {
         splits = (int)std::min<int64_t>(ctx->forced_splits, std::max<int64_t>(1, cdiv(k, ts.bk)));
@@ -844,7 +855,8 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     args.ws = ws;
     // 4-pixel (16-byte) gather: unit column stride, and whole chunks of 4 pixels per output row
     const int gather4 = conv && conv->stride_w == 1 && conv->out_w % 4 == 0 ? 1 : 0;
-    hipFunction_t f = !conv                     ? ctx->gemm[layout][tile][vec ? 1 : 0]
+    const int staging = unaligned ? 2 : vec ? 1 : 0;  // 4-byte, 16-byte, 16-byte unaligned
+    hipFunction_t f = !conv                     ? ctx->gemm[layout][tile][staging]
                       : mode == kGatherTransposed ? ctx->convt[tile][vec ? 1 : 0]
                       : mode == kGatherWeightGrad ? ctx->convw[tile][vec ? 1 : 0]
                       : mode == kGatherNhwc       ? ctx->convf[tile][vec ? 1 : 0]
@@ -990,7 +1002,7 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         part.a = a ? a + b0 * stride_a : nullptr;
         part.b = b ? b + b0 * stride_b : nullptr;
         part.c = c + b0 * stride_c;
-        const int threads = conv ? ts.threads : ctx->gemm_threads[layout][tile][vec ? 1 : 0];
+        const int threads = conv ? ts.threads : ctx->gemm_threads[layout][tile][staging];
         rc = launch(ctx, f, (unsigned)ntiles, (unsigned)nb, (unsigned)threads, &part, (unsigned)splits);
         if (rc) return rc;
         if (splits > 1) {
@@ -1558,10 +1570,10 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     }
     for (int l = 0; l < 3; ++l)
         for (int t = 0; t < kNumTiles; ++t)
-            for (int v = kTiles[t].plain ? 0 : 1; v < 2; ++v) {
+            for (int v = kTiles[t].plain ? 0 : 1; v < (t == kTileR ? 3 : 2); ++v) {
                 char name[64];
                 std::snprintf(name, sizeof(name), "zn_sgemm_%s_%s%s", kLayoutName[l], kTiles[t].suffix,
-                              v ? "_v" : "");
+                              v == 2 ? "_u" : v ? "_v" : "");
                 if (hipModuleGetFunction(&ctx->gemm[l][t][v], ctx->gemm_module, name) != hipSuccess)
                     return bail(ZN_ERR_SYMBOL);
                 int threads = 0;
