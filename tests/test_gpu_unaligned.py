@@ -174,3 +174,45 @@ def test_unaligned_strided_batches(ctx, layout):
         bz = b[z * sb:z * sb + b_shape[0] * b_shape[1]].reshape(b_shape)
         cz = out[z * sc:z * sc + m * n].reshape(m, n)
         assert_close(cz, ref_gemm(layout, az, bz, m, n, k), layout, az, bz, m, n, k, what=f"batch {z}")
+
+
+@pytest.mark.parametrize("layout,mode", [(lay, mode) for lay in ("nn", "nt", "tn") for mode in ("plain", "accumulate")]
+                         + [("nn", "bias_relu")])  # the fused bias epilogue is Backend.matMulBias*, NN only
+def test_row_tail_folded_into_unaligned_launch(ctx, layout, mode):
+    """C4's 4097 x 1023 x 777: the automatic choice runs rows 0..4095 on the
+    unaligned 128x128 tiles and the last row as dot products inside the same
+    launch.  The first 4096 rows are bit-identical to one launch of the same
+    kernel over all rows (forcing the tile turns the row split off); the last
+    row and sampled rows match the oracle."""
+    m, n, k = 4097, 1023, 777
+    rng = np.random.default_rng(10 * "nn nt tn".split().index(layout) + "plain accumulate bias_relu".split().index(mode))
+    a_shape, b_shape = stored_shapes(layout, m, n, k)
+    a, b = uniform(rng, a_shape), uniform(rng, b_shape)
+    c0 = uniform(rng, (m, n)) if mode == "accumulate" else None
+    bias = uniform(rng, (n,)) if mode == "bias_relu" else None
+    act = "relu" if mode == "bias_relu" else "linear"
+    lda = m if layout == "tn" else k
+    ldb = k if layout == "nt" else n
+    da, db = ctx.to_device(a), ctx.to_device(b)
+    dbias = ctx.to_device(bias) if bias is not None else None
+    outs = []
+    for tile in ("auto", TILE):
+        announce(f"folded row tail {layout} {mode} tile {tile}")
+        ctx.set_gemm_tile(tile)
+        dc = ctx.to_device(c0) if c0 is not None else ctx.alloc(m * n).fill(np.nan)
+        ctx.sgemm(layout, m, n, k, da, lda, db, ldb, dc, n, c0 is not None, dbias, act)
+        outs.append(dc.download().reshape(m, n))
+        dc.close()
+    ctx.set_gemm_tile("auto")
+    for buf in (da, db, dbias):
+        if buf is not None:
+            buf.close()
+    split, whole = outs
+    assert np.isfinite(split).all()
+    np.testing.assert_array_equal(split[:m - 1].view(np.uint32), whole[:m - 1].view(np.uint32))
+    rows = np.unique(np.r_[np.linspace(0, m - 1, 8).astype(int), m - 1])
+    a_rows = np.ascontiguousarray(a[:, rows] if layout == "tn" else a[rows])
+    c0_rows = np.ascontiguousarray(c0[rows]) if c0 is not None else None
+    ref = ref_gemm(layout, a_rows, b, len(rows), n, k, c0=c0_rows, accumulate=c0 is not None, bias=bias, act=act)
+    assert_close(split[rows], ref, layout, a_rows, b, len(rows), n, k, c0=c0_rows, accumulate=c0 is not None,
+                 bias=bias, act=act, what=f"folded tail {mode}")

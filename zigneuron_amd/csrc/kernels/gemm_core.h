@@ -1162,6 +1162,46 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
             *reinterpret_cast<zn_f32x4 *>(&lds_b[st][chunk(j - LA, SB::kWaves, SB::kPerInst)]) = v;
     };
 
+    // Row tail (UA kernels, p.tail_rows > 0): this workgroup's tail elements
+    // o = w * P + q, q < P <= 4, each over K <= 1024: thread tid multiplies
+    // k = tid and k = tid + NT.  Its operands are loaded here, before the
+    // main loop, so that their latency hides behind it; the products and
+    // the sums come after it.
+    float tail_av[4][2], tail_bv[4][2];
+    int tail_t[4], tail_j[4];
+    const bool has_tail = UA && p.tail_rows > 0;  // uniform
+    if constexpr (UA) {
+        if (has_tail) {
+            const int P = p.tail_per_wg;
+            const int total = p.tail_rows * p.n;
+            const int o0 = (int)(blockIdx.x + gridDim.x * blockIdx.z) * P;
+            int t = o0 / p.n, j = o0 - t * p.n;
+            const __amdgpu_buffer_rsrc_t rt = make_rsrc(
+                p.tail_a, (uint32_t)(AK ? (p.tail_rows - 1) * lda + p.k : (p.k - 1) * lda + p.tail_rows) * 4u);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                tail_t[q] = t;
+                tail_j[q] = j;
+                const bool ok = q < P && o0 + q < total;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int k = tid + i * NT;
+                    const bool in = ok && k < p.k;
+                    const int ao = AK ? t * lda + k : k * lda + t;
+                    const int bo = BKC ? j * ldb + k : k * ldb + j;
+                    tail_av[q][i] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rt, in ? (uint32_t)ao * 4u : kOutOfRange, 0, 0));
+                    tail_bv[q][i] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rb, in ? (uint32_t)bo * 4u : kOutOfRange, 0, 0));
+                }
+                if (++j == p.n) {
+                    j = 0;
+                    ++t;
+                }
+            }
+        }
+    }
+
     zn_f32x16 acc[FM][FN];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
@@ -1226,6 +1266,36 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
     for (int kt = 0; kt < ktiles; kt += 2) {
         slice_step(kt, std::integral_constant<int, 0>());
         if (kt + 1 < ktiles) slice_step(kt + 1, std::integral_constant<int, 1>());
+    }
+    if constexpr (UA) {
+        if (has_tail) {
+            // each thread's products (k ascending), the wave's sum over a fixed
+            // butterfly read from lane 0, then the waves' sums in wave order
+            __shared__ float tail_red[4][NT / kWave];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float v = tail_av[q][0] * tail_bv[q][0];
+                v = v + tail_av[q][1] * tail_bv[q][1];
+#pragma unroll
+                for (int off = kWave / 2; off > 0; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+                if (lane == 0) tail_red[q][wave] = v;
+            }
+            __syncthreads();
+            const int P = p.tail_per_wg;
+            const int o0 = (int)(blockIdx.x + gridDim.x * blockIdx.z) * P;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (tid == q && q < P && o0 + q < p.tail_rows * p.n) {
+                    float v = tail_red[q][0];
+#pragma unroll
+                    for (int w = 1; w < NT / kWave; ++w) v = v + tail_red[q][w];
+                    float *dst = p.tail_c + (int64_t)tail_t[q] * p.ldc + tail_j[q];
+                    if (p.accumulate) v = *dst + v;
+                    if (p.bias) v = v + p.bias[p.bias_rows ? p.m + tail_t[q] : tail_j[q]];
+                    *dst = zn_activate(v, p.act);
+                }
+            }
+        }
     }
     store_tile_fast<BM, BN, WM, WN, AK, BKC>(p, acc, bz, m0, n0, wm0, wn0, lane, slice);
 }

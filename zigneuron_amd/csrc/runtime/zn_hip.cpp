@@ -634,11 +634,21 @@ enum GatherMode { kGatherIm2col, kGatherTransposed, kGatherWeightGrad, kGatherNh
 
 constexpr double kPackMinMacs = 536870912.0;  // 2^29 multiply-adds: the copy costs a few us
 
+// Rows of C after the m rows of a launch that the launch may compute as
+// well (folded row tail): A's first tail row (TN: column), C's first tail
+// row, their count.  `folded` reports whether it did.
+struct RowTail {
+    const float *a;
+    float *c;
+    int64_t rows;
+    bool folded;
+};
+
 int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                    int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
                    int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows,
                    const ZnConvGeom *conv = nullptr, GatherMode mode = kGatherIm2col, bool split_rows = true,
-                   int padded = 0) {
+                   int padded = 0, RowTail *row_tail = nullptr) {
     if (!ctx) return ZN_ERR_INVALID_ARG;
     if (layout < ZN_LAYOUT_NN || layout > ZN_LAYOUT_TN) return ZN_ERR_INVALID_ARG;
     if (act < ZN_ACT_LINEAR || act > ZN_ACT_TANH) return ZN_ERR_INVALID_ARG;
@@ -713,10 +723,12 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         const int64_t per_cu = cdiv(ntiles_all, cus);
         if (per_cu >= 2 && cdiv(ntiles_all - tiles_n, cus) < per_cu) {
             const int64_t m_main = (tiles_m - 1) * ts.bm;
-            int rc = gemm_launch_ex(ctx, layout, m_main, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias,
-                                    act, bias_rows, nullptr, mode, false, padded);
-            if (rc) return rc;
             const float *a_tail = layout == ZN_LAYOUT_TN ? a + m_main : a + m_main * lda;
+            // the first part may compute the tail rows too (below); if not, they are a second launch
+            RowTail tail = {a_tail, c + m_main * ldc, m - m_main, false};
+            int rc = gemm_launch_ex(ctx, layout, m_main, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, accumulate, bias,
+                                    act, bias_rows, nullptr, mode, false, padded, &tail);
+            if (rc || tail.folded) return rc;
             return gemm_launch_ex(ctx, layout, m - m_main, n, k, a_tail, lda, 0, b, ldb, 0, c + m_main * ldc, ldc, 0, 1,
                                   accumulate, bias_rows ? bias + m_main : bias, act, bias_rows, nullptr, mode, false,
                                   padded);
@@ -1002,6 +1014,22 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
         part.a = a ? a + b0 * stride_a : nullptr;
         part.b = b ? b + b0 * stride_b : nullptr;
         part.c = c + b0 * stride_c;
+        // A few tail rows go with the unaligned 128x128 tiles when each
+        // workgroup gets at most 4 of their elements and K <= 1024 (two
+        // products per thread): each element a dot product spread over one
+        // workgroup's 512 threads, whose operands load before the main loop.
+        // C4 4097 x 1023 x 777: the one-row tail needs no second launch.
+        if (row_tail && unaligned && batch == 1 && k <= 1024) {
+            const int64_t wgs = ntiles * splits;
+            const int64_t per = cdiv(row_tail->rows * n, wgs);
+            if (per <= 4 && row_tail->rows * n <= INT_MAX) {
+                part.tail_a = row_tail->a;
+                part.tail_c = row_tail->c;
+                part.tail_rows = (int32_t)row_tail->rows;
+                part.tail_per_wg = (int32_t)per;
+                row_tail->folded = true;
+            }
+        }
         const int threads = conv ? ts.threads : ctx->gemm_threads[layout][tile][staging];
         rc = launch(ctx, f, (unsigned)ntiles, (unsigned)nb, (unsigned)threads, &part, (unsigned)splits);
         if (rc) return rc;

@@ -64,6 +64,16 @@ struct ZnGemmArgs {
     // (problem, tile), kCounterStride ints apart, zero between launches (the
     // last workgroup of a tile resets it).
     int32_t *counters;
+    // Row tail folded into the launch (the unaligned 128x128 kernels,
+    // batch 1): tail_rows more rows of C after row m, A's rows (TN: columns)
+    // from tail_a, C's from tail_c (row stride ldc); each element is one
+    // K-long dot product, and workgroup w (over blockIdx.x and .z) computes
+    // elements [w * tail_per_wg, (w + 1) * tail_per_wg) in row-major order.
+    // The bias (by row: entries m ..) and the epilogue are those of the main
+    // rows.  tail_per_wg <= 4, K <= 1024.
+    const float *tail_a;
+    float *tail_c;
+    int32_t tail_rows, tail_per_wg;
 };
 
 // Cross-workgroup arrival counters (the context's counter array): counter i
