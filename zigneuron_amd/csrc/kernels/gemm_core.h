@@ -1105,6 +1105,7 @@ __device__ __forceinline__ void gemm_tile_wide(const ZnGemmArgs &p, int wg = -1)
     const int ktiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     static_assert(!(UA && NHWCW), "unaligned rows: plain operands only");
+    static_assert(!UA || NT == 512, "the folded row tail covers K <= 2 * 512 (the host's bound)");
     constexpr int RU = UA ? 0 : 3;  // whole float4 rows are padded to a multiple of 4 (packed copies)
     const uint32_t a_bytes = (uint32_t)(AK ? (p.m - 1) * lda + ((p.k + RU) & ~RU) : (p.k - 1) * lda + ((p.m + RU) & ~RU)) * 4u;
     const uint32_t b_bytes = NHWCW ? (uint32_t)(p.conv.images * p.conv.channels * p.conv.in_h * p.conv.in_w) * 4u
