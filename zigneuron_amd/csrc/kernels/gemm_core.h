@@ -1557,6 +1557,10 @@ __device__ __forceinline__ void gemm_ksplit(const ZnGemmArgs &p, float *lds, int
 // workgroups share a CU when there are more tiles than CUs.
 // gemm_ksplit16 up to the epilogue: returns the sum (in wave order) of the
 // KS partial values of tile element (threadIdx.x / 16, threadIdx.x % 16).
+//
+// KS = 8 or 16 (the two-layer forward): two or four waves per SIMD, and K's
+// slices dealt out as evenly as whole slices allow (wave w takes slices
+// [w S / KS, (w + 1) S / KS) of S); threads 0..255 return the sums.
 template <int KS, bool AK, bool BKC, int W, int NSMAX = 8>
 __device__ __forceinline__ float gemm_ksplit16_sum(const ZnGemmArgs &p, float *lds, int m0, int n0, int64_t bz) {
     constexpr int BM = 16, BN = 16, BK = 32;
@@ -1565,14 +1569,21 @@ __device__ __forceinline__ float gemm_ksplit16_sum(const ZnGemmArgs &p, float *l
     typedef DmaStage<BN, BK, kWave, BKC, W> SB;
     constexpr int kStage = SA::kFloats + SB::kFloats;
     constexpr int kSliceLoads = SA::kPerWave + SB::kPerWave;
-    static_assert(KS * kWave == 256, "one output element per thread in the epilogue");
+    static_assert(KS == 4 || KS == 8 || KS == 16, "4, 8 or 16 waves; threads 0..255 finish one output element each");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
     float *region = lds + wave * NS * kStage;
 
-    const int chunk = ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
-    const int kbeg = min(p.k, wave * chunk);
-    const int kend = min(p.k, kbeg + chunk);
+    int kbeg, kend;
+    if constexpr (KS > 4) {
+        const int slices = (p.k + BK - 1) / BK;
+        kbeg = min(p.k, wave * slices / KS * BK);
+        kend = min(p.k, (wave + 1) * slices / KS * BK);
+    } else {
+        const int chunk = ((p.k + KS - 1) / KS + BK - 1) / BK * BK;
+        kbeg = min(p.k, wave * chunk);
+        kend = min(p.k, kbeg + chunk);
+    }
     const int ktiles = (kend - kbeg + BK - 1) / BK;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     constexpr int RW = W == 16 ? 3 : 0;
@@ -1631,7 +1642,7 @@ __device__ __forceinline__ float gemm_ksplit16_sum(const ZnGemmArgs &p, float *l
 #pragma unroll
     for (int r = 0; r < 4; ++r) part[r * kWave + lane] = acc[r];
     __syncthreads();
-    const int t = threadIdx.x;
+    const int t = threadIdx.x & 255;
     const int rr = t >> 4, cc = t & 15;
     const int off = (rr & 3) * kWave + (rr >> 2) * 16 + cc;
     float x = lds[off];

@@ -66,7 +66,17 @@ __device__ __forceinline__ int xcd_contiguous(int b) {
 }
 
 // ---------------------------------------------------------------- forward
-// The lower layer runs on gemm_ksplit16's 16x16 tiles (four waves split K)
+// The forward's workgroup: eight waves (two per SIMD) split the lower
+// layer's K over whole 32-slices as evenly as they go, each with one LDS
+// stage (a slice is loaded, waited for and multiplied before the next is
+// requested).  On MI355X, C2's forward (784-128-10, batch 256): four waves
+// with every slice in flight 7.17 us; eight waves 6.44 us with four stages
+// in flight, 6.48 with three, 6.33 with two, 6.18 with one; sixteen waves
+// 6.40 (one stage) and 6.68 (two).  Requests in flight beyond the slice the
+// wave needs next only delay that slice.
+constexpr int kPairFwdWaves = 8;
+constexpr int kPairFwdStages = 1;
+// The lower layer runs on gemm_ksplit16's 16x16 tiles (the waves split K)
 // and stores its block of h = act1(x . W1 + b1).  Each tile then multiplies
 // that block by W2's 16 matching rows (one 16x16x4 MFMA step per 4 of K) into
 // the tile's partial sum of the strip's y, writes the partial to the
@@ -80,12 +90,14 @@ __device__ __forceinline__ int xcd_contiguous(int b) {
 // partials cross workgroups: h itself is written with ordinary stores.
 template <int W, int ACT1>
 __device__ __forceinline__ void pair_forward(const ZnPairFwdArgs &a, float *lds) {
+    constexpr int KS = kPairFwdWaves;
     const ZnGemmArgs &p = a.l1;
     const int pid = xcd_contiguous((int)blockIdx.x);
     const int tm = pid / p.tiles_n, tn = pid - tm * p.tiles_n;
     const int m0 = tm * 16, n0 = tn * 16;
-    const int t = threadIdx.x, lane = t & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int t = threadIdx.x & 255, lane = threadIdx.x & 63;
+    const bool elem = threadIdx.x < 256;  // threads 0..255 own one element of the 16x16 tile each
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int out = a.out;
     // 16x16x4 operands: in step s, lane (i, g = lane / 16) supplies A[i][4g + s]
     // (h) and B[4g + s][i] (W2's rows n0 ..); lane (j, g) receives row 4g + q,
@@ -102,15 +114,15 @@ __device__ __forceinline__ void pair_forward(const ZnPairFwdArgs &a, float *lds)
     const int row = m0 + (t >> 4), col = n0 + (t & 15);
     const float b1v = bload(make_rsrc(p.bias, p.bias ? (uint32_t)p.n * 4u : 0u), col < p.n, col);
     const float b2v = bload(make_rsrc(a.b2, a.b2 ? (uint32_t)out * 4u : 0u), (t & 15) < out, t & 15);
-    float x = gemm_ksplit16_sum<4, true, false, W>(p, lds, m0, n0, 0);
+    float x = gemm_ksplit16_sum<KS, true, false, W, kPairFwdStages>(p, lds, m0, n0, 0);
     float hval = 0.0f;
-    if (row < p.m && col < p.n) {
+    if (elem && row < p.m && col < p.n) {
         if (p.bias) x = x + b1v;
         hval = zn_activate(x, ACT1);
         p.c[(int64_t)row * p.ldc + col] = hval;
     }
-    float *ht = lds + 1024;  // the h block, row stride 20 (gemm_ksplit16_sum's partials sit below)
-    ht[(t >> 4) * 20 + (t & 15)] = hval;
+    float *ht = lds + 4 * KS * 64;  // the h block, row stride 20 (gemm_ksplit16_sum's partials sit below)
+    if (elem) ht[(t >> 4) * 20 + (t & 15)] = hval;
     __syncthreads();
     float *part = a.part + (int64_t)pid * 256;
     if (wave == 0) {
@@ -125,11 +137,11 @@ __device__ __forceinline__ void pair_forward(const ZnPairFwdArgs &a, float *lds)
     __shared__ int last;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is written
     __syncthreads();
-    if (t == 0)
+    if (threadIdx.x == 0)
         last = __hip_atomic_fetch_add(a.counters + tm * kCounterStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                p.tiles_n - 1;
     __syncthreads();
-    if (!last) return;
+    if (!last || !elem) return;
     if (t == 0) __hip_atomic_store(a.counters + tm * kCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // thread t: y element (t / 16, t % 16) of the strip; the partials of the
     // strip's tiles, eight loads in flight at a time, added in tile order
@@ -671,7 +683,7 @@ __device__ __forceinline__ void pair_backward(const ZnPairBwdArgs &a, float *lds
 
 // zn_dense_pair_fwd[_v]: _v stages x and W1 with 16-byte loads.
 #define ZN_PAIR_FWD_KERNEL(SUFFIX, W)                                                            \
-    extern "C" __global__ __launch_bounds__(256, 1) void zn_dense_pair_fwd##SUFFIX(ZnPairFwdArgs a) { \
+    extern "C" __global__ __launch_bounds__(kPairFwdWaves * 64, 1) void zn_dense_pair_fwd##SUFFIX(ZnPairFwdArgs a) { \
         __shared__ __attribute__((aligned(1024))) float lds[4 * 8 * 32 * 32];                     \
         switch (a.l1.act) {                                                                      \
         case 1: pair_forward<W, 1>(a, lds); break;                                               \

@@ -158,6 +158,7 @@ struct zn_ctx {
     hipModule_t attn_module = nullptr;
     hipModule_t mlp_module = nullptr;
     hipFunction_t pair_fwd[2] = {};            // fused two-layer Dense forward [16-byte staging]
+    int pair_fwd_threads[2] = {};              // its workgroup size (the kernel's launch bounds)
     hipFunction_t pair_bwd[4][2][2] = {};      // fused two-layer Dense backward [lower act][non-linear head][16-byte]
     hipFunction_t attn[3][2] = {};             // fused attention [head dim 32/64/128][16-byte I/O]
     hipFunction_t gemm[3][kNumTiles][3] = {};  // [layout][tile][staging: 4-byte, 16-byte, 16-byte unaligned (r only)]
@@ -1699,6 +1700,13 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
     if (hipModuleGetFunction(&ctx->pair_fwd[0], ctx->mlp_module, "zn_dense_pair_fwd") != hipSuccess ||
         hipModuleGetFunction(&ctx->pair_fwd[1], ctx->mlp_module, "zn_dense_pair_fwd_v") != hipSuccess)
         return bail(ZN_ERR_SYMBOL);
+    for (int v = 0; v < 2; ++v) {
+        int threads = 0;
+        if (hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, ctx->pair_fwd[v]) != hipSuccess ||
+            (threads != 256 && threads != 512 && threads != 1024))
+            return bail(ZN_ERR_SYMBOL);
+        ctx->pair_fwd_threads[v] = threads;
+    }
     for (int a1 = 0; a1 < 4; ++a1)
         for (int a2 = 0; a2 < 2; ++a2)
             for (int v = 0; v < 2; ++v) {
@@ -2558,7 +2566,8 @@ int zn_hip_dense_pair_forward(zn_ctx *ctx, int act1, const float *x, const float
     a.out = (int32_t)out_size;
     a.act2 = act2;
     const bool vec = aligned16(x) && aligned16(w1) && in_size % 4 == 0 && hidden % 4 == 0;
-    return launch(ctx, ctx->pair_fwd[vec ? 1 : 0], (unsigned)(tiles_m * tiles_n), 1, 256, &a);
+    return launch(ctx, ctx->pair_fwd[vec ? 1 : 0], (unsigned)(tiles_m * tiles_n), 1,
+                  (unsigned)ctx->pair_fwd_threads[vec ? 1 : 0], &a);
 }
 
 // The backward loop of Network over the same two layers (src/network.zig:
