@@ -82,6 +82,12 @@ def test_code_objects_hold_every_kernel():
             for fam in ("zn_convt_nt", "zn_convw_tn", "zn_convf_nt", "zn_convwn_tn"):
                 assert f"{fam}_{t}{v}".encode() in conv
     assert b"zn_convwn_tn_r_v" in conv  # the NHWC weight gradient on the register-staged 128x128 loop
+    for lay in ("nn", "nt", "tn"):
+        for fam in ("zn_sgemmq4", "zn_sgemmq4m", "zn_sgemmq8"):
+            for v in ("", "_v"):
+                assert f"{fam}_{lay}{v}".encode() in gemm
+        for v in ("_v", "_u"):
+            assert f"zn_sgemm_{lay}_r{v}".encode() in gemm
     for k in ("zn_splitk_reduce", "zn_dense_bwd_m", "zn_dense_bwd_m_v", "zn_dense_bwd_k", "zn_dense_bwd_k_v"):
         assert k.encode() in gemm
     for k in ("zn_fill_f32", "zn_copy_f32", "zn_add_bias", "zn_activation_forward", "zn_activation_backward",

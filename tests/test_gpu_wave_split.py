@@ -169,16 +169,19 @@ Q_CASES = [
     ("nn", 100, 70, 1000, 1, True, "sigmoid", False),  # ragged
     ("tn", 64, 96, 300, 3, False, "linear", False),
     ("nn", 33, 65, 200, 5, False, "linear", False),
-    ("nn", 17, 9, 3000, 1, False, "tanh", False),      # 24 slices per wave through 4 stages (4-byte B)
-    ("nt", 31, 47, 4099, 1, False, "linear", True),    # 4-byte staging, 33 slices per wave
-    ("nn", 64, 64, 2048, 1, False, "linear", False),   # 16 slices per wave through 8 stages
+    ("nn", 17, 9, 3000, 1, False, "tanh", False),      # eight waves, 11-12 slices each through one stage (4-byte B)
+    ("nt", 31, 47, 4099, 1, False, "linear", True),    # 4-byte staging, 16-17 slices per wave
+    ("nn", 64, 64, 2048, 1, False, "linear", False),   # 8 slices per wave through one stage
+    ("nt", 48, 40, 224, 2, False, "linear", False),    # four waves (K < 256), every slice in flight
 ]
 
 
 @pytest.mark.parametrize("layout,m,n,k,batch,bias,act,acc", Q_CASES)
 def test_quarter_tiles_against_oracle(ctx, layout, m, n, k, batch, bias, act, acc):
-    """16x16 tiles whose four waves split K (zn_sgemmq4_*), forced on every
-    case: against the oracle, the same bits on a second run, and the same
+    """16x16 tiles whose waves split K, forced on every case (K < 256: four
+    waves with every slice in flight, zn_sgemmq4_*; else eight waves with
+    one LDS stage each, zn_sgemmq8_*): against the oracle, the same bits on
+    a second run, and the same
     bits as the automatic choice where the policy picks them (64 <= K <=
     4096 and at most one 32x32 tile per CU; at most one 16x16 tile per CU
     and K < 1536 or tiles for at least half the CUs, or two to three 16x16

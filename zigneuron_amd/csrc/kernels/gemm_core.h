@@ -1658,6 +1658,7 @@ __device__ __forceinline__ void gemm_ksplit16(const ZnGemmArgs &p, float *lds) {
     const int m0 = tm * 16, n0 = tn * 16;
     const int64_t bz = blockIdx.y;
     float x = gemm_ksplit16_sum<KS, AK, BKC, W, NSMAX>(p, lds, m0, n0, bz);
+    if (threadIdx.x >= 256) return;  // eight waves: threads 0..255 own the elements
     const int t = threadIdx.x;
     const int row = m0 + (t >> 4), col = n0 + (t & 15);
     if (row < p.m && col < p.n) {

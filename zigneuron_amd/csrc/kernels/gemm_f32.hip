@@ -104,29 +104,41 @@ ZN_GEMMK_LAYOUTS(8, 4, , false, false, )
 ZN_GEMMK_LAYOUTS(4, 16, _v, true, true, s)
 ZN_GEMMK_LAYOUTS(4, 4, , true, true, s)
 
-// The same on 16x16 tiles (gemm_ksplit16): zn_sgemmq4_<layout>[_v] with up
-// to 8 LDS stages per wave, zn_sgemmq4m_<layout>[_v] with 2 (several
-// workgroups per CU).
-#define ZN_GEMMQ_KERNEL(NAME, AK, BKC, W, NSMAX, MINB)                                           \
-    extern "C" __global__ __launch_bounds__(256, MINB) void NAME(ZnGemmArgs p) {                \
+// The same on 16x16 tiles (gemm_ksplit16), at most one workgroup per CU:
+// zn_sgemmq4_<layout>[_v] on four waves with up to 8 LDS stages each (every
+// slice of a wave in flight), zn_sgemmq8_<layout>[_v] on eight waves with
+// one stage each (K's slices dealt out evenly: a wave requests a slice,
+// waits for it and multiplies it before requesting the next); and
+// zn_sgemmq4m_<layout>[_v] on four waves with 2 stages (several workgroups
+// per CU).
+#define ZN_GEMMQ_KERNEL(NAME, AK, BKC, W, KS, NSMAX, MINB)                                       \
+    extern "C" __global__ __launch_bounds__(KS * 64, MINB) void NAME(ZnGemmArgs p) {           \
         constexpr int kStages = NSMAX < (W == 16 ? 8 : 4) ? NSMAX : (W == 16 ? 8 : 4);           \
-        __shared__ __attribute__((aligned(1024))) float lds[4 * kStages * 32 * 32];              \
+        __shared__ __attribute__((aligned(1024))) float lds[KS * kStages * 32 * 32];             \
         switch (p.act) {                                                                         \
-        case 1: gemm_ksplit16<4, AK, BKC, W, 1, NSMAX>(p, lds); break;                           \
-        case 2: gemm_ksplit16<4, AK, BKC, W, 2, NSMAX>(p, lds); break;                           \
-        case 3: gemm_ksplit16<4, AK, BKC, W, 3, NSMAX>(p, lds); break;                           \
-        default: gemm_ksplit16<4, AK, BKC, W, 0, NSMAX>(p, lds); break;                          \
+        case 1: gemm_ksplit16<KS, AK, BKC, W, 1, NSMAX>(p, lds); break;                          \
+        case 2: gemm_ksplit16<KS, AK, BKC, W, 2, NSMAX>(p, lds); break;                          \
+        case 3: gemm_ksplit16<KS, AK, BKC, W, 3, NSMAX>(p, lds); break;                          \
+        default: gemm_ksplit16<KS, AK, BKC, W, 0, NSMAX>(p, lds); break;                         \
         }                                                                                        \
     }
-#define ZN_GEMMQ_LAYOUTS(S, NSMAX, MINB)                                                         \
-    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nn_v, true, false, 16, NSMAX, MINB)                          \
-    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nt_v, true, true, 16, NSMAX, MINB)                           \
-    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_tn_v, false, false, 16, NSMAX, MINB)                         \
-    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nn, true, false, 4, NSMAX, MINB)                             \
-    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nt, true, true, 4, NSMAX, MINB)                              \
-    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_tn, false, false, 4, NSMAX, MINB)
-ZN_GEMMQ_LAYOUTS(, 8, 1)
-ZN_GEMMQ_LAYOUTS(m, 2, 4)
+#define ZN_GEMMQ_LAYOUTS(S, KS, NSMAX, MINB)                                                     \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nn_v, true, false, 16, KS, NSMAX, MINB)                      \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nt_v, true, true, 16, KS, NSMAX, MINB)                       \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_tn_v, false, false, 16, KS, NSMAX, MINB)                     \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nn, true, false, 4, KS, NSMAX, MINB)                         \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_nt, true, true, 4, KS, NSMAX, MINB)                          \
+    ZN_GEMMQ_KERNEL(zn_sgemmq4##S##_tn, false, false, 4, KS, NSMAX, MINB)
+ZN_GEMMQ_LAYOUTS(, 4, 8, 1)
+ZN_GEMMQ_LAYOUTS(m, 4, 2, 4)
+#define ZN_GEMMQ8_LAYOUTS                                                                        \
+    ZN_GEMMQ_KERNEL(zn_sgemmq8_nn_v, true, false, 16, 8, 1, 1)                                   \
+    ZN_GEMMQ_KERNEL(zn_sgemmq8_nt_v, true, true, 16, 8, 1, 1)                                    \
+    ZN_GEMMQ_KERNEL(zn_sgemmq8_tn_v, false, false, 16, 8, 1, 1)                                  \
+    ZN_GEMMQ_KERNEL(zn_sgemmq8_nn, true, false, 4, 8, 1, 1)                                      \
+    ZN_GEMMQ_KERNEL(zn_sgemmq8_nt, true, true, 4, 8, 1, 1)                                       \
+    ZN_GEMMQ_KERNEL(zn_sgemmq8_tn, false, false, 4, 8, 1, 1)
+ZN_GEMMQ8_LAYOUTS
 
 // Persistent plain GEMMs (gemm_persistent), 16-byte staging only:
 // zn_sgemmp_<layout>_<tile>_v, for problems of several rounds of tiles.

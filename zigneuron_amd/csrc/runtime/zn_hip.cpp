@@ -166,7 +166,8 @@ struct zn_ctx {
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
-    hipFunction_t gemmq[3][2][2] = {};         // [layout][2 stages][16-byte]: 16x16 wave-split tiles
+    hipFunction_t gemmq[3][3][2] = {};         // [layout][q4, q4m, q8][16-byte]: 16x16 wave-split tiles
+    int gemmq_threads[3][3][2] = {};           // their workgroup sizes (the kernels' launch bounds)
     hipFunction_t gemmks[3][2] = {};           // [layout][16-byte]: 32x32 wave-split tiles with K split over workgroups too
     hipFunction_t dense_bwd[2] = {};           // grouped Dense backward GEMMs [16-byte staging]
     hipFunction_t dense_bwd_k[2] = {};         // the same on 32x32 tiles with K split over 4 waves [16-byte]
@@ -923,8 +924,13 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
                 part.a = a + b0 * stride_a;
                 part.b = b + b0 * stride_b;
                 part.c = c + b0 * stride_c;
-                rc = launch(ctx, ctx->gemmq[layout][tiles16 > cus ? 1 : 0][vec ? 1 : 0],
-                            (unsigned)(q.tiles_m * q.tiles_n), (unsigned)nb, 256, &part);
+                // one workgroup per CU at most: eight waves of one stage each
+                // once K holds 8 slices or more (C2's 256 x 128 x 784 5.5 ->
+                // 4.65 us, 300 x 200 x 3000 15.3 -> 11.7 us), else four waves
+                // with every slice in flight (256 x 10 x 128: 3.3 against 3.9 us)
+                const int qr = tiles16 > cus ? 1 : k >= 8 * 32 ? 2 : 0, qv = vec ? 1 : 0;
+                rc = launch(ctx, ctx->gemmq[layout][qr][qv], (unsigned)(q.tiles_m * q.tiles_n), (unsigned)nb,
+                            (unsigned)ctx->gemmq_threads[layout][qr][qv], &part);
                 if (rc) return rc;
             }
             return ZN_OK;
@@ -1653,10 +1659,17 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             std::snprintf(name, sizeof(name), "zn_sgemmk4s_%s%s", kLayoutName[l], v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->gemmks[l][v], ctx->gemm_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
-            for (int r = 0; r < 2; ++r) {
-                std::snprintf(name, sizeof(name), "zn_sgemmq4%s_%s%s", r ? "m" : "", kLayoutName[l], v ? "_v" : "");
+            for (int r = 0; r < 3; ++r) {
+                std::snprintf(name, sizeof(name), "zn_sgemmq%s_%s%s", r == 2 ? "8" : r ? "4m" : "4", kLayoutName[l],
+                              v ? "_v" : "");
                 if (hipModuleGetFunction(&ctx->gemmq[l][r][v], ctx->gemm_module, name) != hipSuccess)
                     return bail(ZN_ERR_SYMBOL);
+                int threads = 0;
+                if (hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, ctx->gemmq[l][r][v]) !=
+                        hipSuccess ||
+                    (threads != 256 && threads != 512))
+                    return bail(ZN_ERR_SYMBOL);
+                ctx->gemmq_threads[l][r][v] = threads;
             }
         }
     for (int l = 0; l < 3; ++l)
