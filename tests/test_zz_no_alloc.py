@@ -102,9 +102,11 @@ def test_noalloc_workgroup_split_tiles(ctx):
 
 
 def test_noalloc_unaligned_rows_are_not_packed(ctx):
-    """Rows that are not whole float4s: zn_hip_sgemm packs them into padded
-    rows (a pooled allocation), the no-allocation GEMM stages them with
-    4-byte loads; the zeros past K are the same, so the result is too."""
+    """Rows that are not whole float4s: zn_hip_sgemm may pack them into
+    padded rows (a pooled allocation); the no-allocation GEMM never does and
+    stages them with 4-byte loads (or 16-byte loads of the rows as they lie,
+    on the 128x128 register-staged tile).  The zeros past K are the same, so
+    the result is too."""
     rng = np.random.default_rng(78)
     m, n, k = 1025, 1023, 777
     a, b = uniform(rng, (m, k)), uniform(rng, (k, n))
