@@ -165,6 +165,7 @@ struct zn_ctx {
     int gemm_threads[3][kNumTiles][3] = {};    // their workgroup sizes (the kernels' launch bounds)
     hipFunction_t conv[kNumTiles][2][2] = {};  // implicit-GEMM convolution [tile][16-byte W rows][4-pixel gather]
     hipFunction_t convt[kNumTiles][2] = {};    // stride-1 transposed convolution [tile][16-byte W' rows]
+    int convt_occ[kNumTiles][2] = {};          // their resident workgroups per CU
     hipFunction_t convw[kNumTiles][2] = {};    // implicit weight gradient [tile][16-byte grad_output rows]
     hipFunction_t gemmq[3][3][2] = {};         // [layout][q4, q4m, q8][16-byte]: 16x16 wave-split tiles
     int gemmq_threads[3][3][2] = {};           // their workgroup sizes (the kernels' launch bounds)
@@ -646,6 +647,8 @@ struct RowTail {
     bool folded;
 };
 
+// split_rows: the launch may cut itself into two launches (a row tail; the
+// last problems of a batch), whose calls pass false.
 int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, const float *a, int64_t lda,
                    int64_t stride_a, const float *b, int64_t ldb, int64_t stride_b, float *c, int64_t ldc,
                    int64_t stride_c, int64_t batch, int accumulate, const float *bias, int act, int bias_rows,
@@ -829,6 +832,27 @@ int gemm_launch_ex(zn_ctx *ctx, int layout, int64_t m, int64_t n, int64_t k, con
     args.group_m = 1;
     const int64_t ntiles = tiles_m * tiles_n;
     args.xcd_remap = 0;
+
+    // Batched transposed-convolution GEMMs (the convolution input gradient,
+    // one problem per image) whose tiles overrun the resident workgroups by
+    // a short last round: those few tiles would run nearly alone at the end
+    // (MI355X, C5's 49 tiles per image on 1536 resident workgroups: 147.8 us
+    // for 31 images, 168.8 us for 32).  The last problems go to a launch of
+    // their own, which the split-K policy spreads over every CU.
+    if (conv && mode == kGatherTransposed && split_rows && batch > 1 && !forced && ctx->forced_splits == 0) {
+        const int64_t slots = cus_now(ctx) * ctx->convt_occ[tile][vec ? 1 : 0];
+        const int64_t total = ntiles * batch, rem = total % slots;
+        const int64_t r = cdiv(rem, ntiles);  // problems holding the last round's tiles
+        if (total > slots && rem > 0 && 8 * rem <= slots && r < batch) {
+            const int64_t b1 = batch - r;
+            const int rc = gemm_launch_ex(ctx, layout, m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, b1,
+                                          accumulate, bias, act, bias_rows, conv, mode, false, padded);
+            if (rc) return rc;
+            return gemm_launch_ex(ctx, layout, m, n, k, a + b1 * stride_a, lda, stride_a, b + b1 * stride_b, ldb,
+                                  stride_b, c + b1 * stride_c, ldc, stride_c, r, accumulate, bias, act, bias_rows, conv,
+                                  mode, false, padded);
+        }
+    }
 
     int rc = select_device(ctx);
     if (rc) return rc;
@@ -1632,6 +1656,12 @@ int zn_hip_create(int device, const char *code_object_dir, zn_ctx **out) {
             std::snprintf(name, sizeof(name), "zn_convt_nt_%s%s", kTiles[t].suffix, v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->convt[t][v], ctx->conv_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
+            int occ = 0;
+            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, ctx->convt[t][v], kTiles[t].threads, 0) !=
+                    hipSuccess ||
+                occ < 1)
+                occ = 1;
+            ctx->convt_occ[t][v] = occ;
             std::snprintf(name, sizeof(name), "zn_convw_tn_%s%s", kTiles[t].suffix, v ? "_v" : "");
             if (hipModuleGetFunction(&ctx->convw[t][v], ctx->conv_module, name) != hipSuccess)
                 return bail(ZN_ERR_SYMBOL);
